@@ -1,0 +1,449 @@
+// fh_api.hip -- the extern "C" boundary (include/forge_hip.h): argument checks, context and
+// scratch ownership, the stream, graph capture and the orchestration of the kernels in
+// fh_sort.hip, fh_grid.hip and fh_sph.hip.  No CPU fallback: every compute entry point
+// enqueues HIP kernels or fails with a status code.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "fh_internal.hpp"
+
+using namespace fh;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail((int)e, "%s: %s (%d)", where, hipGetErrorString(e), (int)e);
+}
+
+#define FH_CHECK_HIP(expr)                                  \
+    do {                                                    \
+        hipError_t e_ = (expr);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr);   \
+    } while (0)
+
+int check_ctx(fh_ctx* c) {
+    if (!c) return fail(FH_EINVAL, "null context");
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return FH_OK;
+}
+
+int check_n(fh_ctx* c, uint32_t n, const char* what) {
+    if (n > c->max_n) return fail(FH_ERANGE, "%s: n=%u exceeds max_n=%u", what, n, c->max_n);
+    return FH_OK;
+}
+
+// Validates a grid description and returns its cell count in *cells.
+int check_grid(fh_ctx* c, float cs, const float* origin, const uint32_t* dims, GridDesc* g,
+               uint32_t* cells, const char* what) {
+    if (!dims) return fail(FH_EINVAL, "%s: null dims", what);
+    if (!(cs > 0.0f) || cs != cs || cs > 3.0e38f)
+        return fail(FH_EINVAL, "%s: cell_size must be finite and > 0", what);
+    uint64_t C = 1;
+    for (int q = 0; q < 3; q++) {
+        if (dims[q] == 0 || dims[q] > (1u << 24))
+            return fail(FH_EINVAL, "%s: grid dim %d = %u outside 1..2^24", what, q, dims[q]);
+        C *= dims[q];
+    }
+    if (C > 0xFFFFFFFFull) return fail(FH_EINVAL, "%s: grid has more than 2^32-1 cells", what);
+    if (C > c->max_cells)
+        return fail(FH_ERANGE, "%s: %llu cells exceed max_cells=%u", what,
+                    (unsigned long long)C, c->max_cells);
+    g->cs = cs;
+    g->ox = origin ? origin[0] : 0.0f;
+    g->oy = origin ? origin[1] : 0.0f;
+    g->oz = origin ? origin[2] : 0.0f;
+    g->nx = dims[0];
+    g->ny = dims[1];
+    g->nz = dims[2];
+    *cells = (uint32_t)C;
+    return FH_OK;
+}
+
+int check_sph(fh_ctx* c, const fh_sph_params* p, GridDesc* g, uint32_t* cells, const char* what) {
+    if (!p) return fail(FH_EINVAL, "%s: null params", what);
+    if (!(p->smoothing_radius > 0.0f)) return fail(FH_EINVAL, "%s: smoothing_radius <= 0", what);
+    static const float zero[3] = {0.0f, 0.0f, 0.0f};
+    return check_grid(c, p->cell_size, zero, p->grid_dims, g, cells, what);
+}
+
+template <typename T>
+hipError_t alloc(T** p, size_t count, size_t* total) {
+    size_t bytes = count * sizeof(T);
+    if (bytes == 0) bytes = sizeof(T);
+    *total += bytes;
+    return hipMalloc((void**)p, bytes);
+}
+
+// Rebuild of the SPH grid from the positions: hash + digit histograms + cell counts, CSR
+// cell_start by scan, then the stable sort giving sidx (ascending id within a cell).
+hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
+                       const float* py, const float* pz, uint32_t n) {
+    const uint32_t bits = bits_for_cells(cells);
+    hipError_t e = launch_begin(c);
+    if (e == hipSuccess) e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr, true);
+    if (e == hipSuccess) e = launch_scan_cells(c, cells, c->cell_start);
+    if (e == hipSuccess && n > 0) e = launch_sort_passes(c, c->kb, nullptr, nullptr, c->sidx, n, bits);
+    return e;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fh_abi_version(void) { return FH_ABI_VERSION; }
+
+const char* fh_last_error(void) { return g_err; }
+
+int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_ctx** out) {
+    if (!out) return fail(FH_EINVAL, "fh_create: null out");
+    *out = nullptr;
+    if (max_n == 0 || max_cells == 0) return fail(FH_EINVAL, "fh_create: max_n and max_cells must be > 0");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(FH_ENODEV, "fh_create: no HIP device");
+    if (device < 0 || device >= count) return fail(FH_ENODEV, "fh_create: no device %d", device);
+    hipDeviceProp_t prop;
+    FH_CHECK_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(FH_ENODEV, "fh_create: device %d is %s, this library is built for gfx950",
+                    device, prop.gcnArchName);
+    FH_CHECK_HIP(hipSetDevice(device));
+
+    fh_ctx* c = new fh_ctx();
+    memset(c, 0, sizeof(*c));
+    c->device = device;
+    c->max_n = max_n;
+    c->max_cells = max_cells;
+    c->max_sort_tiles = ceil_div(max_n, (uint32_t)kSortTile);
+    c->max_scan_tiles = ceil_div(max_cells, (uint32_t)kScanTile);
+    size_t tot = 0;
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = alloc(&c->ka, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->va, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->kb, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->vb, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)kMaxPasses * c->max_sort_tiles * 256u, &tot);
+    if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
+    if (e == hipSuccess) e = alloc(&c->cell_count, max_cells, &tot);
+    if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);
+    if (e == hipSuccess) e = alloc(&c->scan_lb, c->max_scan_tiles, &tot);
+    if (e == hipSuccess) e = alloc(&c->sidx, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->spos, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->svel, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->srho, max_n, &tot);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_error, sizeof(uint32_t), hipHostMallocDefault);
+    if (e == hipSuccess) {
+        if (stream) {
+            c->stream = (hipStream_t)stream;
+        } else {
+            e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+            c->own_stream = e == hipSuccess;
+        }
+    }
+    // One-time clears (outside any capture): look-back words start "not ready", cell counts
+    // start at zero and are kept at zero by every scan.
+    if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)kMaxPasses * c->max_sort_tiles * 256u * 8u, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->scan_lb, 0, (size_t)c->max_scan_tiles * 8u, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->cell_count, 0, (size_t)max_cells * 4u, c->stream);
+    for (int q = 0; q < kEvents && e == hipSuccess; q++) e = hipEventCreate(&c->ev[q]);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    c->scratch_bytes = tot;
+    if (e != hipSuccess) {
+        int rc = hip_fail(e, "fh_create");
+        fh_destroy(c);
+        return rc;
+    }
+    *out = c;
+    return FH_OK;
+}
+
+int fh_destroy(fh_ctx* c) {
+    if (!c) return FH_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->exec) (void)hipGraphExecDestroy(c->exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    for (int q = 0; q < kEvents; q++)
+        if (c->ev[q]) (void)hipEventDestroy(c->ev[q]);
+    void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->cell_count,
+                    c->cell_start, c->scan_lb, c->sidx, c->spos, c->svel, c->srho};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (c->h_error) (void)hipHostFree(c->h_error);
+    if (c->own_stream && c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return FH_OK;
+}
+
+void* fh_stream(fh_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+size_t fh_scratch_bytes(const fh_ctx* c) { return c ? c->scratch_bytes : 0; }
+
+int fh_sync(fh_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (c->capturing) return fail(FH_ESTATE, "fh_sync: stream is being captured");
+    FH_CHECK_HIP(hipMemcpyAsync(c->h_error, &c->ctl->error, sizeof(uint32_t),
+                                hipMemcpyDeviceToHost, c->stream));
+    FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+    if (*c->h_error) {
+        uint32_t code = *c->h_error;
+        FH_CHECK_HIP(hipMemsetAsync(&c->ctl->error, 0, sizeof(uint32_t), c->stream));
+        FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+        return fail(FH_ESTATE, "fh_sync: device reported a look-back failure (code %u)", code);
+    }
+    return FH_OK;
+}
+
+int fh_hash_cells(fh_ctx* c, const float* x, const float* y, const float* z, uint32_t stride,
+                  uint32_t n, float cell_size, const float origin[3], const uint32_t dims[3],
+                  uint32_t* keys, uint32_t* vals) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!keys || (n && (!x || !y || !z)) || stride == 0)
+        return fail(FH_EINVAL, "fh_hash_cells: null pointer or zero stride");
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hash_cells"))) return rc;
+    if (n == 0) return FH_OK;
+    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, 0, keys, vals, false));
+    return FH_OK;
+}
+
+int fh_sort_pairs(fh_ctx* c, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_t num_bits) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && (!keys || !vals)) return fail(FH_EINVAL, "fh_sort_pairs: null keys or values");
+    if (num_bits < 1 || num_bits > 32)
+        return fail(FH_EINVAL, "fh_sort_pairs: num_bits=%u outside 1..32", num_bits);
+    if ((rc = check_n(c, n, "fh_sort_pairs"))) return rc;
+    if (n < 2) return FH_OK;
+    FH_CHECK_HIP(launch_begin(c));
+    FH_CHECK_HIP(launch_hist_keys(c, keys, n, num_bits));
+    if (passes_for_bits(num_bits) >= 2) {
+        // The last pass reads scratch and writes the caller's buffers: result in place.
+        FH_CHECK_HIP(launch_sort_passes(c, keys, vals, keys, vals, n, num_bits));
+    } else {
+        // A single pass cannot run in place; sort into scratch and copy back.
+        FH_CHECK_HIP(launch_sort_passes(c, keys, vals, c->ka, c->va, n, num_bits));
+        FH_CHECK_HIP(hipMemcpyAsync(keys, c->ka, (size_t)n * 4u, hipMemcpyDeviceToDevice, c->stream));
+        FH_CHECK_HIP(hipMemcpyAsync(vals, c->va, (size_t)n * 4u, hipMemcpyDeviceToDevice, c->stream));
+    }
+    return FH_OK;
+}
+
+int fh_find_cell_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
+                            uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((n && !sorted_keys) || !cell_start || !cell_end)
+        return fail(FH_EINVAL, "fh_find_cell_boundaries: null pointer");
+    if (num_cells == 0) return fail(FH_EINVAL, "fh_find_cell_boundaries: num_cells == 0");
+    FH_CHECK_HIP(launch_boundaries(c, sorted_keys, n, num_cells, cell_start, cell_end));
+    return FH_OK;
+}
+
+int fh_hashgrid_build(fh_ctx* c, const float* x, const float* y, const float* z,
+                      uint32_t stride, uint32_t n, float cell_size, const float origin[3],
+                      const uint32_t dims[3], uint32_t* cell_start, uint32_t* sorted_indices,
+                      uint32_t* cell_indices) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!cell_start || (n && (!x || !y || !z || !sorted_indices || !cell_indices)) || stride == 0)
+        return fail(FH_EINVAL, "fh_hashgrid_build: null pointer or zero stride");
+    if ((rc = check_n(c, n, "fh_hashgrid_build"))) return rc;
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hashgrid_build"))) return rc;
+    const uint32_t bits = bits_for_cells(cells);
+    FH_CHECK_HIP(launch_begin(c));
+    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr, true));
+    FH_CHECK_HIP(launch_scan_cells(c, cells, cell_start));
+    if (n > 0)
+        FH_CHECK_HIP(launch_sort_passes(c, cell_indices, nullptr, nullptr, sorted_indices, n, bits));
+    return FH_OK;
+}
+
+int fh_neighbor_query(fh_ctx* c, const float* x, const float* y, const float* z,
+                      uint32_t stride, uint32_t n, float cell_size, const float origin[3],
+                      const uint32_t dims[3], const uint32_t* cell_start,
+                      const uint32_t* sorted_indices, float radius, uint32_t* counts,
+                      float* wsum) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!cell_start || (n && (!x || !y || !z || !sorted_indices || !counts)) || stride == 0)
+        return fail(FH_EINVAL, "fh_neighbor_query: null pointer or zero stride");
+    if ((rc = check_n(c, n, "fh_neighbor_query"))) return rc;
+    if (!(radius >= 0.0f)) return fail(FH_EINVAL, "fh_neighbor_query: radius must be >= 0");
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_neighbor_query"))) return rc;
+    FH_CHECK_HIP(launch_neighbor_query(c, x, y, z, stride, n, g, cell_start, sorted_indices,
+                                       radius, counts, wsum));
+    return FH_OK;
+}
+
+int fh_query_neighbors(fh_ctx* c, const float* x, const float* y, const float* z,
+                       uint32_t stride, float cell_size, const float origin[3],
+                       const uint32_t dims[3], const uint32_t* cell_start,
+                       const uint32_t* sorted_indices, const float* qx, const float* qy,
+                       const float* qz, uint32_t qstride, uint32_t nq, float radius,
+                       uint32_t* counts, const uint32_t* offsets, uint32_t* indices) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!x || !y || !z || !cell_start || !sorted_indices || stride == 0 || qstride == 0 ||
+        (nq && (!qx || !qy || !qz || !counts)))
+        return fail(FH_EINVAL, "fh_query_neighbors: null pointer or zero stride");
+    if ((offsets == nullptr) != (indices == nullptr))
+        return fail(FH_EINVAL, "fh_query_neighbors: offsets and indices go together");
+    if (!(radius >= 0.0f)) return fail(FH_EINVAL, "fh_query_neighbors: radius must be >= 0");
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_query_neighbors"))) return rc;
+    FH_CHECK_HIP(launch_query(c, x, y, z, stride, g, cell_start, sorted_indices, qx, qy, qz,
+                              qstride, nq, radius, counts, offsets, indices));
+    return FH_OK;
+}
+
+int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const float* py,
+                   const float* pz, uint32_t n, float* density) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && (!px || !py || !pz || !density)) return fail(FH_EINVAL, "fh_sph_density: null pointer");
+    if ((rc = check_n(c, n, "fh_sph_density"))) return rc;
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_density"))) return rc;
+    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, n));
+    if (n == 0) return FH_OK;
+    FH_CHECK_HIP(launch_gather(c, px, py, pz, nullptr, nullptr, nullptr, n, false));
+    SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
+              prm->rest_density, prm->viscosity_coefficient, 0.0f, n};
+    FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
+    return FH_OK;
+}
+
+int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
+                 float* py, float* pz, float* vx, float* vy, float* vz, float* density,
+                 float* accel, uint32_t n, float dt) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && (!px || !py || !pz || !vx || !vy || !vz || !density))
+        return fail(FH_EINVAL, "fh_sph_fused: null pointer");
+    if ((rc = check_n(c, n, "fh_sph_fused"))) return rc;
+    if (epi && (epi->flags & ~(FH_EPI_GRAVITY | FH_EPI_INTEGRATE | FH_EPI_BOX)))
+        return fail(FH_EINVAL, "fh_sph_fused: unknown epilogue flags 0x%x", epi->flags);
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_fused"))) return rc;
+    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, n));
+    if (n == 0) return FH_OK;
+    FH_CHECK_HIP(launch_gather(c, px, py, pz, vx, vy, vz, n, true));
+    SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
+              prm->rest_density, prm->viscosity_coefficient, dt, n};
+    FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
+    FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
+    return FH_OK;
+}
+
+int fh_gravity(fh_ctx* c, float* vx, float* vy, float* vz, uint32_t n, float gx, float gy,
+               float gz, float dt) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && (!vx || !vy || !vz)) return fail(FH_EINVAL, "fh_gravity: null pointer");
+    FH_CHECK_HIP(launch_gravity(c, vx, vy, vz, n, gx, gy, gz, dt));
+    return FH_OK;
+}
+
+int fh_integrate(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy, float* vz,
+                 uint32_t n, float dt) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && (!px || !py || !pz || !vx || !vy || !vz))
+        return fail(FH_EINVAL, "fh_integrate: null pointer");
+    FH_CHECK_HIP(launch_integrate(c, px, py, pz, vx, vy, vz, n, dt));
+    return FH_OK;
+}
+
+int fh_box_collider(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,
+                    float* vz, uint32_t n, const float box_min[3], const float box_max[3],
+                    float restitution) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!box_min || !box_max || (n && (!px || !py || !pz || !vx || !vy || !vz)))
+        return fail(FH_EINVAL, "fh_box_collider: null pointer");
+    FH_CHECK_HIP(launch_box(c, px, py, pz, vx, vy, vz, n, box_min, box_max, restitution));
+    return FH_OK;
+}
+
+int fh_graph_begin(fh_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (c->capturing) return fail(FH_ESTATE, "fh_graph_begin: already capturing");
+    FH_CHECK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
+    c->capturing = true;
+    return FH_OK;
+}
+
+int fh_graph_end(fh_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!c->capturing) return fail(FH_ESTATE, "fh_graph_end: not capturing");
+    c->capturing = false;
+    hipGraph_t graph = nullptr;
+    FH_CHECK_HIP(hipStreamEndCapture(c->stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    if (c->exec) (void)hipGraphExecDestroy(c->exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->graph = graph;
+    c->exec = exec;
+    FH_CHECK_HIP(hipGraphUpload(c->exec, c->stream));
+    return FH_OK;
+}
+
+int fh_graph_launch(fh_ctx* c, uint32_t count) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!c->exec) return fail(FH_ESTATE, "fh_graph_launch: no captured graph");
+    if (c->capturing) return fail(FH_ESTATE, "fh_graph_launch: stream is being captured");
+    for (uint32_t q = 0; q < count; q++) FH_CHECK_HIP(hipGraphLaunch(c->exec, c->stream));
+    return FH_OK;
+}
+
+int fh_event_record(fh_ctx* c, uint32_t slot) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (slot >= (uint32_t)kEvents) return fail(FH_EINVAL, "fh_event_record: slot %u", slot);
+    FH_CHECK_HIP(hipEventRecord(c->ev[slot], c->stream));
+    return FH_OK;
+}
+
+int fh_event_elapsed_ms(fh_ctx* c, uint32_t a, uint32_t b, float* ms) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (a >= (uint32_t)kEvents || b >= (uint32_t)kEvents || !ms)
+        return fail(FH_EINVAL, "fh_event_elapsed_ms: bad slot or null output");
+    FH_CHECK_HIP(hipEventSynchronize(c->ev[b]));
+    FH_CHECK_HIP(hipEventElapsedTime(ms, c->ev[a], c->ev[b]));
+    return FH_OK;
+}
+
+}  // extern "C"

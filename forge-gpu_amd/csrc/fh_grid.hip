@@ -1,0 +1,302 @@
+// fh_grid.hip -- cell ranges and the 3x3x3 neighbour query for gfx950.
+//
+//   k_scan_cells   CSR cell_start[0..C] = exclusive prefix sum of the per-cell counts
+//                  (hashgrid.rs:95-106), single pass with a decoupled look-back over
+//                  dynamically numbered 4096-cell tiles; it also re-zeroes the counts so the
+//                  next build needs no memset (graph-safe).
+//   k_fill_u32 +   find_cell_boundaries (radix_sort.rs:229-317): sentinel fill, then one
+//   k_boundaries   thread per sorted key marks the first / last index of its run.
+//   k_nbr_query    HashGrid::query_neighbors (hashgrid.rs:145-193) for every point of a built
+//                  grid: the 3 x-adjacent cells of one (dy, dz) row are contiguous in the
+//                  sorted order, so the 27-cell walk is 9 contiguous ranges visited in the
+//                  reference's dz, dy, dx order.
+#include "fh_internal.hpp"
+
+namespace fh {
+
+__global__ __launch_bounds__(kScanThreads) void k_scan_cells(uint32_t* __restrict__ counts,
+                                                             uint32_t* __restrict__ cell_start,
+                                                             uint64_t* __restrict__ lookback,
+                                                             Control* ctl, uint32_t C) {
+    __shared__ uint32_t s_tile;
+    __shared__ uint32_t s_scan[4];
+    __shared__ uint32_t s_prefix;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_tile = atomicAdd(&ctl->scan_ctr, 1u);
+    __syncthreads();
+    const uint32_t tile = s_tile;
+    const uint32_t epoch = ctl->epoch;
+    const uint32_t first = tile * (uint32_t)kScanTile + (uint32_t)tid * kScanItems;
+
+    // Each thread owns kScanItems consecutive cells.
+    uint32_t v[kScanItems];
+    if (first + kScanItems <= C) {
+        const uint4* p4 = reinterpret_cast<const uint4*>(counts + first);
+#pragma unroll
+        for (int q = 0; q < kScanItems / 4; q++) {
+            uint4 t = p4[q];
+            v[4 * q] = t.x;
+            v[4 * q + 1] = t.y;
+            v[4 * q + 2] = t.z;
+            v[4 * q + 3] = t.w;
+        }
+        uint4* w4 = reinterpret_cast<uint4*>(counts + first);
+#pragma unroll
+        for (int q = 0; q < kScanItems / 4; q++) w4[q] = make_uint4(0u, 0u, 0u, 0u);
+    } else {
+#pragma unroll
+        for (int q = 0; q < kScanItems; q++) {
+            uint32_t c = first + q;
+            v[q] = c < C ? counts[c] : 0u;
+            if (c < C) counts[c] = 0u;
+        }
+    }
+    uint32_t sum = 0;
+#pragma unroll
+    for (int q = 0; q < kScanItems; q++) {
+        uint32_t t = v[q];
+        v[q] = sum;  // thread-local exclusive prefix
+        sum += t;
+    }
+    uint32_t total;
+    uint32_t before = block256_exclusive_scan(sum, s_scan, &total);
+
+    if (tid == 0) {
+        uint64_t* my = lookback + tile;
+        uint32_t prefix = 0;
+        if (tile == 0) {
+            lb_store(my, lb_word(kLbInclusive, epoch, total));
+        } else {
+            lb_store(my, lb_word(kLbAggregate, epoch, total));
+            uint32_t t = tile - 1u, spins = 0;
+            for (;;) {
+                uint64_t w = lb_load(lookback + t);
+                uint64_t st = w & (3ull << 62);
+                if (st != 0 && ((uint32_t)(w >> 32) & kEpochMask) == epoch) {
+                    prefix += (uint32_t)w;
+                    if (st == kLbInclusive) break;
+                    if (t == 0) {
+                        atomicOr(&ctl->error, 2u);
+                        break;
+                    }
+                    t--;
+                } else {
+                    if (++spins >= kSpinLimit) {
+                        atomicOr(&ctl->error, 1u);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            lb_store(my, lb_word(kLbInclusive, epoch, prefix + total));
+        }
+        s_prefix = prefix;
+    }
+    __syncthreads();
+    const uint32_t base = s_prefix + before;
+#pragma unroll
+    for (int q = 0; q < kScanItems; q++) {
+        uint32_t c = first + q;
+        if (c < C) cell_start[c] = base + v[q];
+        if (c + 1 == C) cell_start[C] = base + sum;  // = number of hashed particles
+    }
+}
+
+hipError_t launch_scan_cells(fh_ctx* c, uint32_t num_cells, uint32_t* cell_start) {
+    uint32_t tiles = ceil_div(num_cells, (uint32_t)kScanTile);
+    k_scan_cells<<<tiles, kScanThreads, 0, c->stream>>>(c->cell_count, cell_start, c->scan_lb,
+                                                         c->ctl, num_cells);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+__global__ void k_fill_u32(uint32_t* __restrict__ p, uint32_t value, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = value;
+}
+
+hipError_t launch_fill_u32(fh_ctx* c, uint32_t* p, uint32_t value, uint32_t n) {
+    if (n == 0) return hipSuccess;
+    k_fill_u32<<<ceil_div(n, 256u), 256, 0, c->stream>>>(p, value, n);
+    return hipGetLastError();
+}
+
+// radix_sort.rs:451-465
+__global__ void k_boundaries(const uint32_t* __restrict__ keys, uint32_t n, uint32_t C,
+                             uint32_t* __restrict__ cell_start, uint32_t* __restrict__ cell_end) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t cell = keys[i];
+    if (cell >= C) return;
+    if (i == 0 || keys[i - 1] != cell) cell_start[cell] = i;
+    if (i == n - 1 || keys[i + 1] != cell) cell_end[cell] = i + 1;
+}
+
+hipError_t launch_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
+                             uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end) {
+    hipError_t e = launch_fill_u32(c, cell_start, 0xFFFFFFFFu, num_cells);
+    if (e != hipSuccess) return e;
+    e = launch_fill_u32(c, cell_end, 0u, num_cells);
+    if (e != hipSuccess || n == 0) return e;
+    k_boundaries<<<ceil_div(n, 256u), 256, 0, c->stream>>>(sorted_keys, n, num_cells, cell_start,
+                                                           cell_end);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// Rust `f32 as i32` of an already floored value (NaN -> 0, saturating).
+__device__ __forceinline__ int32_t rust_as_i32(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483648.0f) return INT32_MAX;
+    if (f <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)f;
+}
+
+// Gather of the point positions into sorted order (float4), so the query walks contiguous
+// memory.
+__global__ void k_gather_pos(const float* __restrict__ x, const float* __restrict__ y,
+                             const float* __restrict__ z, uint32_t stride,
+                             const uint32_t* __restrict__ sidx, uint32_t n,
+                             float4* __restrict__ spos) {
+    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    uint32_t i = sidx[s];
+    if (i >= n) i = 0;  // never taken for a grid built over these n points
+    size_t o = (size_t)i * stride;
+    spos[s] = make_float4(x[o], y[o], z[o], 0.0f);
+}
+
+// One thread per sorted point.  Arithmetic is exactly the reference's (the library is built
+// with -ffp-contract=off): diff = p_j - q, dist_sq = (dx*dx + dy*dy) + dz*dz, `<=` against
+// radius*radius, weight coeff*diff*diff*diff summed in visiting order, so counts and weight
+// sums are bit-identical to the CPU restatement.
+__global__ __launch_bounds__(256) void k_nbr_query(const float4* __restrict__ spos,
+                                                   const uint32_t* __restrict__ sidx, uint32_t n,
+                                                   GridDesc g,
+                                                   const uint32_t* __restrict__ cell_start,
+                                                   float radius_sq, float coeff,
+                                                   uint32_t* __restrict__ counts,
+                                                   float* __restrict__ wsum) {
+    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const float4 q = spos[s];
+    // Query cell is not clamped (hashgrid.rs:155-157).
+    const int64_t cx = rust_as_i32(floorf((q.x - g.ox) / g.cs));
+    const int64_t cy = rust_as_i32(floorf((q.y - g.oy) / g.cs));
+    const int64_t cz = rust_as_i32(floorf((q.z - g.oz) / g.cs));
+    const int64_t x0 = cx - 1 < 0 ? 0 : cx - 1;
+    const int64_t x1 = cx + 1 > (int64_t)g.nx - 1 ? (int64_t)g.nx - 1 : cx + 1;
+    uint32_t cnt = 0;
+    float w = 0.0f;
+    for (int dz = -1; dz <= 1; dz++) {
+        int64_t nz = cz + dz;
+        if (nz < 0 || nz >= (int64_t)g.nz) continue;
+        for (int dy = -1; dy <= 1; dy++) {
+            int64_t ny = cy + dy;
+            if (ny < 0 || ny >= (int64_t)g.ny) continue;
+            if (x0 > x1) continue;
+            uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
+            uint32_t b = cell_start[row + (uint32_t)x0];
+            uint32_t e = min(cell_start[row + (uint32_t)x1 + 1u], n);
+            for (uint32_t j = b; j < e; j++) {
+                float4 p = spos[j];
+                float dx = p.x - q.x, dy2 = p.y - q.y, dz2 = p.z - q.z;
+                float dist_sq = dx * dx + dy2 * dy2 + dz2 * dz2;
+                if (dist_sq <= radius_sq) {
+                    float diff = radius_sq - dist_sq;
+                    cnt++;
+                    w += coeff * diff * diff * diff;
+                }
+            }
+        }
+    }
+    uint32_t i = sidx[s];
+    if (i >= n) return;
+    counts[i] = cnt;
+    if (wsum) wsum[i] = w;
+}
+
+// Batched HashGrid::query_neighbors: one thread per query, neighbour positions read through
+// sorted_indices from the caller's arrays exactly like hashgrid.rs:176-186.
+__global__ __launch_bounds__(256) void k_query(const float* __restrict__ x,
+                                               const float* __restrict__ y,
+                                               const float* __restrict__ z, uint32_t stride,
+                                               GridDesc g, const uint32_t* __restrict__ cstart,
+                                               const uint32_t* __restrict__ sidx,
+                                               const float* __restrict__ qx,
+                                               const float* __restrict__ qy,
+                                               const float* __restrict__ qz, uint32_t qstride,
+                                               uint32_t nq, float radius_sq,
+                                               uint32_t* __restrict__ counts,
+                                               const uint32_t* __restrict__ offsets,
+                                               uint32_t* __restrict__ indices) {
+    uint32_t qi = blockIdx.x * blockDim.x + threadIdx.x;
+    if (qi >= nq) return;
+    size_t oq = (size_t)qi * qstride;
+    const float px = qx[oq], py = qy[oq], pz = qz[oq];
+    const int64_t cx = rust_as_i32(floorf((px - g.ox) / g.cs));
+    const int64_t cy = rust_as_i32(floorf((py - g.oy) / g.cs));
+    const int64_t cz = rust_as_i32(floorf((pz - g.oz) / g.cs));
+    const int64_t x0 = cx - 1 < 0 ? 0 : cx - 1;
+    const int64_t x1 = cx + 1 > (int64_t)g.nx - 1 ? (int64_t)g.nx - 1 : cx + 1;
+    uint32_t cnt = 0;
+    uint32_t* out = (offsets && indices) ? indices + offsets[qi] : nullptr;
+    const uint32_t room = out ? offsets[qi + 1] - offsets[qi] : 0u;
+    for (int dz = -1; dz <= 1; dz++) {
+        int64_t nz = cz + dz;
+        if (nz < 0 || nz >= (int64_t)g.nz) continue;
+        for (int dy = -1; dy <= 1; dy++) {
+            int64_t ny = cy + dy;
+            if (ny < 0 || ny >= (int64_t)g.ny) continue;
+            if (x0 > x1) continue;
+            uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
+            uint32_t b = cstart[row + (uint32_t)x0];
+            uint32_t e = cstart[row + (uint32_t)x1 + 1u];
+            for (uint32_t j = b; j < e; j++) {
+                uint32_t pi = sidx[j];
+                size_t o = (size_t)pi * stride;
+                float dx = x[o] - px, dy2 = y[o] - py, dz2 = z[o] - pz;
+                float dist_sq = dx * dx + dy2 * dy2 + dz2 * dz2;
+                if (dist_sq <= radius_sq) {
+                    if (cnt < room) out[cnt] = pi;
+                    cnt++;
+                }
+            }
+        }
+    }
+    counts[qi] = cnt;
+}
+
+hipError_t launch_query(fh_ctx* c, const float* x, const float* y, const float* z,
+                        uint32_t stride, const GridDesc& g, const uint32_t* cell_start,
+                        const uint32_t* sorted_indices, const float* qx, const float* qy,
+                        const float* qz, uint32_t qstride, uint32_t nq, float radius,
+                        uint32_t* counts, const uint32_t* offsets, uint32_t* indices) {
+    if (nq == 0) return hipSuccess;
+    k_query<<<ceil_div(nq, 256u), 256, 0, c->stream>>>(x, y, z, stride, g, cell_start,
+                                                       sorted_indices, qx, qy, qz, qstride, nq,
+                                                       radius * radius, counts, offsets, indices);
+    return hipGetLastError();
+}
+
+hipError_t launch_neighbor_query(fh_ctx* c, const float* x, const float* y, const float* z,
+                                 uint32_t stride, uint32_t n, const GridDesc& g,
+                                 const uint32_t* cell_start, const uint32_t* sorted_indices,
+                                 float radius, uint32_t* counts, float* wsum) {
+    if (n == 0) return hipSuccess;
+    k_gather_pos<<<ceil_div(n, 256u), 256, 0, c->stream>>>(x, y, z, stride, sorted_indices, n,
+                                                           c->spos);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // Same float expressions as sph_density.rs:413-416 with h = radius.
+    float h = radius;
+    float h2 = h * h;
+    float h9 = h2 * h2 * h2 * h2 * h;
+    float coeff = 315.0f / (64.0f * 3.14159265f * h9);
+    k_nbr_query<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->spos, sorted_indices, n, g,
+                                                          cell_start, radius * radius, coeff,
+                                                          counts, wsum);
+    return hipGetLastError();
+}
+
+}  // namespace fh

@@ -1,0 +1,200 @@
+// fh_internal.hpp -- context layout, shared device helpers and launcher declarations of the
+// gfx950 SPH / hash-grid library.  Every translation unit of libforge_hip.so includes this.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/forge_hip.h"
+
+namespace fh {
+
+// ---- sizes ----------------------------------------------------------------------------------
+constexpr int kWave = 64;              // CDNA wavefront
+constexpr int kSortThreads = 256;      // 4 waves per sort workgroup
+constexpr int kSortItems = 16;         // keys per thread per tile
+constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys per tile
+constexpr int kMaxPasses = 4;          // 8-bit digits, up to 32-bit keys
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;
+constexpr int kScanTile = kScanThreads * kScanItems;  // 4096 cells per scan tile
+constexpr int kEvents = 16;
+
+// Look-back words: [63:62] status, [61:32] epoch, [31:0] value.  A word whose epoch differs
+// from the current one is "not ready", so the arrays never need clearing between calls.
+constexpr uint64_t kLbAggregate = 1ull << 62;
+constexpr uint64_t kLbInclusive = 2ull << 62;
+constexpr uint32_t kEpochMask = 0x3FFFFFFFu;
+// Bound on look-back polls before a tile gives up and raises the device error flag; keeps
+// every wave finite even if an invariant were broken (each poll sleeps ~64 clocks).
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+// Device-side control block (one per context).
+struct Control {
+    uint32_t epoch;                     // bumped by k_begin before each sort / scan
+    uint32_t tile_ctr[kMaxPasses];      // dynamic tile ids of the sort passes
+    uint32_t scan_ctr;                  // dynamic tile id of the cell scan
+    uint32_t error;                     // nonzero: a look-back spin limit was hit
+    uint32_t pad[9];
+    uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
+};
+
+struct GridDesc {
+    float cs;
+    float ox, oy, oz;
+    uint32_t nx, ny, nz;
+};
+
+}  // namespace fh
+
+struct fh_ctx {
+    int device;
+    hipStream_t stream;
+    bool own_stream;
+    uint32_t max_n, max_cells;
+    uint32_t max_sort_tiles, max_scan_tiles;
+    // sort scratch
+    uint32_t* ka;        // [max_n]
+    uint32_t* va;        // [max_n]
+    uint32_t* kb;        // [max_n]
+    uint32_t* vb;        // [max_n]
+    uint64_t* sort_lb;   // [kMaxPasses][max_sort_tiles][256]
+    fh::Control* ctl;    // device control block
+    // grid scratch
+    uint32_t* cell_count;  // [max_cells], kept all-zero between calls
+    uint32_t* cell_start;  // [max_cells + 1]
+    uint64_t* scan_lb;     // [max_scan_tiles]
+    uint32_t* sidx;        // [max_n] sorted particle ids
+    // SPH scratch (sorted order)
+    float4* spos;        // [max_n] x, y, z, 0
+    float4* svel;        // [max_n] vx, vy, vz, 0
+    float* srho;         // [max_n]
+    uint32_t* h_error;   // pinned host word for the device error flag
+    size_t scratch_bytes;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    bool capturing;
+    hipEvent_t ev[fh::kEvents];
+};
+
+namespace fh {
+
+// ---- shared device helpers -------------------------------------------------------------------
+
+// Cell coordinate along one axis: floor((p - o) / cs) with Rust `as i32` semantics (NaN -> 0,
+// saturating) followed by the clamp to [0, dim - 1] (hashgrid.rs:129-136).  The comparisons
+// run in float so NaN, +-inf and huge values never reach the float->int conversion.  The
+// division is IEEE correctly rounded (the library is built without fast-math), so keys are
+// bit-identical to the CPU definition.  Requires dim <= 2^24 (checked on the host).
+__device__ __forceinline__ uint32_t cell_coord(float p, float o, float cs, uint32_t dim) {
+    float f = floorf((p - o) / cs);
+    if (!(f >= 0.0f)) return 0u;
+    float top = (float)(dim - 1u);
+    if (f >= top) return dim - 1u;
+    return (uint32_t)f;
+}
+
+__device__ __forceinline__ uint32_t cell_of(float x, float y, float z, const GridDesc& g) {
+    uint32_t cx = cell_coord(x, g.ox, g.cs, g.nx);
+    uint32_t cy = cell_coord(y, g.oy, g.cs, g.ny);
+    uint32_t cz = cell_coord(z, g.oz, g.cs, g.nz);
+    return cx + cy * g.nx + cz * g.nx * g.ny;
+}
+
+__device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t lb_word(uint64_t status, uint32_t epoch, uint32_t value) {
+    return status | ((uint64_t)(epoch & kEpochMask) << 32) | (uint64_t)value;
+}
+
+// Inclusive scan of one value per thread across a 64-lane wavefront.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        uint32_t t = __shfl_up(v, off, kWave);
+        if (lane >= off) v += t;
+    }
+    return v;
+}
+
+// Exclusive scan of one value per thread over a 256-thread workgroup; `sm` holds 4 words.
+// Returns the exclusive prefix; *total receives the workgroup sum.  Contains barriers: call
+// from uniform control flow only.
+__device__ __forceinline__ uint32_t block256_exclusive_scan(uint32_t v, uint32_t* sm,
+                                                            uint32_t* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t inc = wave_inclusive_scan(v, lane);
+    if (lane == 63) sm[wave] = inc;
+    __syncthreads();
+    uint32_t w0 = sm[0], w1 = sm[1], w2 = sm[2], w3 = sm[3];
+    uint32_t before = (wave > 0 ? w0 : 0u) + (wave > 1 ? w1 : 0u) + (wave > 2 ? w2 : 0u);
+    *total = w0 + w1 + w2 + w3;
+    __syncthreads();
+    return before + inc - v;
+}
+
+// ---- launchers (host side, enqueue on ctx->stream; return hipError_t) ------------------------
+
+// Sort: bump epoch, clear histograms and tile counters.
+hipError_t launch_begin(fh_ctx* c);
+// Histogram of all digit passes of keys (from a key array).
+hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits);
+// Hash particle positions: keys_out[i] = cell (if non-null), digit histograms of all passes,
+// cell counts (if count_cells).
+hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
+                            uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
+                            uint32_t* keys_out, uint32_t* vals_out, bool count_cells);
+// Run the passes of a sort whose histograms are ready.  Pass 0 reads (k0, v0) (v0 == nullptr:
+// values are the indices 0..n-1); the last pass writes (kfin, vfin) (kfin may be null).
+// Intermediate passes ping-pong through the context's scratch.
+hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
+                              uint32_t* vfin, uint32_t n, uint32_t num_bits);
+// Exclusive scan of c->cell_count[0..C) into cell_start[0..C] and reset of cell_count.
+hipError_t launch_scan_cells(fh_ctx* c, uint32_t num_cells, uint32_t* cell_start);
+hipError_t launch_fill_u32(fh_ctx* c, uint32_t* p, uint32_t value, uint32_t n);
+hipError_t launch_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
+                             uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end);
+hipError_t launch_neighbor_query(fh_ctx* c, const float* x, const float* y, const float* z,
+                                 uint32_t stride, uint32_t n, const GridDesc& g,
+                                 const uint32_t* cell_start, const uint32_t* sorted_indices,
+                                 float radius, uint32_t* counts, float* wsum);
+hipError_t launch_query(fh_ctx* c, const float* x, const float* y, const float* z,
+                        uint32_t stride, const GridDesc& g, const uint32_t* cell_start,
+                        const uint32_t* sorted_indices, const float* qx, const float* qy,
+                        const float* qz, uint32_t qstride, uint32_t nq, float radius,
+                        uint32_t* counts, const uint32_t* offsets, uint32_t* indices);
+// SPH passes over the sorted state held in the context.
+struct SphArgs {
+    GridDesc g;
+    float h, mass, k, rho0, mu, dt;
+    uint32_t n;
+};
+hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const float* pz,
+                         const float* vx, const float* vy, const float* vz, uint32_t n,
+                         bool with_vel);
+hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start,
+                          float* density_out);
+hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
+                        const uint32_t* cell_start, float* px, float* py, float* pz, float* vx,
+                        float* vy, float* vz, float* accel);
+hipError_t launch_gravity(fh_ctx* c, float* vx, float* vy, float* vz, uint32_t n, float gx,
+                          float gy, float gz, float dt);
+hipError_t launch_integrate(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,
+                            float* vz, uint32_t n, float dt);
+hipError_t launch_box(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,
+                      float* vz, uint32_t n, const float* mn, const float* mx, float e);
+
+__host__ __device__ inline uint32_t passes_for_bits(uint32_t bits) { return (bits + 7u) / 8u; }
+inline uint32_t bits_for_cells(uint32_t num_cells) {
+    uint32_t b = 1;
+    while (b < 32 && (1ull << b) < (uint64_t)num_cells) b++;
+    return b;
+}
+inline uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
+
+}  // namespace fh

@@ -1,0 +1,329 @@
+// fh_sph.hip -- SPH density and fused pressure/viscosity passes for gfx950, plus the
+// gravity / integrate / box modules.
+//
+// The passes run over the particles in cell-sorted order (gathered once per substep into
+// float4 arrays), so a particle's 27-cell neighbourhood is 9 contiguous ranges of the same
+// arrays -- the 3 x-adjacent cells of each (dy, dz) row -- and neighbour reads are coalesced
+// and cache-friendly instead of the reference's gathers through sorted_idx into unsorted
+// arrays (sph_density.rs:445-450).  Results are scattered back to the caller's arrays in
+// original particle order, so FieldSet semantics are unchanged.
+//
+// Arithmetic follows the reference expressions term by term (the library is compiled with
+// -ffp-contract=off and IEEE division / square root) and the neighbours of a particle are
+// visited in the reference's order (dz, dy, dx, then ascending particle id within a cell), so
+// density and velocity updates reproduce the CPU restatement of sph_density.rs:409-460 and
+// sph_fused.rs:542-638.
+#include "fh_internal.hpp"
+
+namespace fh {
+
+// Sorted-order copies of the state: spos[s] = pos[sidx[s]], svel[s] = vel[sidx[s]].
+__global__ void k_gather(const float* __restrict__ px, const float* __restrict__ py,
+                         const float* __restrict__ pz, const float* __restrict__ vx,
+                         const float* __restrict__ vy, const float* __restrict__ vz,
+                         const uint32_t* __restrict__ sidx, uint32_t n, float4* __restrict__ spos,
+                         float4* __restrict__ svel) {
+    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    uint32_t i = sidx[s];
+    if (i >= n) i = 0;  // never taken when the sort is consistent
+    spos[s] = make_float4(px[i], py[i], pz[i], 0.0f);
+    if (svel) svel[s] = make_float4(vx[i], vy[i], vz[i], 0.0f);
+}
+
+hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const float* pz,
+                         const float* vx, const float* vy, const float* vz, uint32_t n,
+                         bool with_vel) {
+    if (n == 0) return hipSuccess;
+    k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->sidx, n,
+                                                       c->spos, with_vel ? c->svel : nullptr);
+    return hipGetLastError();
+}
+
+// Clamped cell of a particle in the SPH kernels (sph_density.rs:421-426): grid origin 0.
+struct Cell3 {
+    int cx, cy, cz;
+};
+__device__ __forceinline__ Cell3 sph_cell(const float4& p, const GridDesc& g) {
+    Cell3 c;
+    c.cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
+    c.cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny);
+    c.cz = (int)cell_coord(p.z, 0.0f, g.cs, g.nz);
+    return c;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Density: rho_i = sum_j mass*poly6*(h2 - r2)^3 over r2 < h2, self included.
+__global__ __launch_bounds__(256) void k_density(const float4* __restrict__ spos,
+                                                 const uint32_t* __restrict__ sidx, uint32_t n,
+                                                 GridDesc g, const uint32_t* __restrict__ cstart,
+                                                 float h2, float mc, float* __restrict__ srho,
+                                                 float* __restrict__ density) {
+    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const float4 pi = spos[s];
+    const Cell3 c = sph_cell(pi, g);
+    const int x0 = c.cx > 0 ? c.cx - 1 : 0;
+    const int x1 = c.cx + 1 < (int)g.nx ? c.cx + 1 : (int)g.nx - 1;
+    float rho = 0.0f;
+    for (int dz = -1; dz <= 1; dz++) {
+        int nz = c.cz + dz;
+        if (nz < 0 || nz >= (int)g.nz) continue;
+        for (int dy = -1; dy <= 1; dy++) {
+            int ny = c.cy + dy;
+            if (ny < 0 || ny >= (int)g.ny) continue;
+            uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
+            uint32_t b = cstart[row + (uint32_t)x0], e = min(cstart[row + (uint32_t)x1 + 1u], n);
+            for (uint32_t j = b; j < e; j++) {
+                float4 q = spos[j];
+                float dx2 = pi.x - q.x;
+                float dy2 = pi.y - q.y;
+                float dz2 = pi.z - q.z;
+                float r2 = dx2 * dx2 + dy2 * dy2 + dz2 * dz2;
+                if (r2 < h2) {
+                    float diff = h2 - r2;
+                    rho += mc * diff * diff * diff;
+                }
+            }
+        }
+    }
+    srho[s] = rho;
+    const uint32_t i = sidx[s];
+    if (density && i < n) density[i] = rho;
+}
+
+hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start,
+                          float* density_out) {
+    if (a.n == 0) return hipSuccess;
+    // Same float expressions as sph_density.rs:413-416; mass * coeff is the first product of
+    // `mass * poly6_coeff * diff * diff * diff` (:453).
+    float h2 = a.h * a.h;
+    float h9 = h2 * h2 * h2 * h2 * a.h;
+    float poly6 = 315.0f / (64.0f * 3.14159265f * h9);
+    float mc = a.mass * poly6;
+    k_density<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->sidx, a.n, a.g, cell_start,
+                                                          h2, mc, c->srho, density_out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+struct ForceConsts {
+    float h, h2, mass, k, rho0, mu, gcoef, lcoef, dt;
+    uint32_t flags;
+    float gx, gy, gz;
+    float mn[3], mx[3], e;
+};
+
+// Fused pressure + viscosity (sph_fused.rs:542-638) and the optional epilogue: gravity
+// (gravity.rs:33), integrate with its non-finite guard (integrate.rs:23-29) and the box
+// (box_collider.rs:37-46), written back through sidx to the caller's arrays.
+__global__ __launch_bounds__(256) void k_force(const float4* __restrict__ spos,
+                                               const float4* __restrict__ svel,
+                                               const float* __restrict__ srho,
+                                               const uint32_t* __restrict__ sidx, uint32_t n,
+                                               GridDesc g, const uint32_t* __restrict__ cstart,
+                                               ForceConsts K, float* __restrict__ px,
+                                               float* __restrict__ py, float* __restrict__ pz,
+                                               float* __restrict__ vx, float* __restrict__ vy,
+                                               float* __restrict__ vz,
+                                               float* __restrict__ accel) {
+    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const float4 pi = spos[s];
+    const float4 vi = svel[s];
+    const float rho_i = srho[s];
+    float ax = 0.0f, ay = 0.0f, az = 0.0f;
+    float nvx = vi.x, nvy = vi.y, nvz = vi.z;
+    if (!(rho_i < 1e-6f)) {
+        const float p_i = K.k * (rho_i - K.rho0);
+        float pax = 0.0f, pay = 0.0f, paz = 0.0f;
+        float vax = 0.0f, vay = 0.0f, vaz = 0.0f;
+        const Cell3 c = sph_cell(pi, g);
+        const int x0 = c.cx > 0 ? c.cx - 1 : 0;
+        const int x1 = c.cx + 1 < (int)g.nx ? c.cx + 1 : (int)g.nx - 1;
+        for (int dz = -1; dz <= 1; dz++) {
+            int nz = c.cz + dz;
+            if (nz < 0 || nz >= (int)g.nz) continue;
+            for (int dy = -1; dy <= 1; dy++) {
+                int ny = c.cy + dy;
+                if (ny < 0 || ny >= (int)g.ny) continue;
+                uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
+                uint32_t b = cstart[row + (uint32_t)x0], e = min(cstart[row + (uint32_t)x1 + 1u], n);
+                for (uint32_t j = b; j < e; j++) {
+                    float4 q = spos[j];
+                    float djx = pi.x - q.x;
+                    float djy = pi.y - q.y;
+                    float djz = pi.z - q.z;
+                    float r2 = djx * djx + djy * djy + djz * djz;
+                    if (r2 < K.h2 && r2 > 1e-12f) {
+                        float r = sqrtf(r2);
+                        float rho_j = srho[j];
+                        if (rho_j < 1e-6f) continue;
+                        float diff = K.h - r;
+                        float p_j = K.k * (rho_j - K.rho0);
+                        float grad_scale = K.gcoef * diff * diff / r;
+                        float f_scale = -K.mass * (p_i + p_j) / (2.0f * rho_j) * grad_scale;
+                        pax += f_scale * djx;
+                        pay += f_scale * djy;
+                        paz += f_scale * djz;
+                        float4 vj = svel[j];
+                        float lap = K.lcoef * diff;
+                        float v_scale = K.mu * K.mass / rho_j * lap;
+                        vax += v_scale * (vj.x - vi.x);
+                        vay += v_scale * (vj.y - vi.y);
+                        vaz += v_scale * (vj.z - vi.z);
+                    }
+                }
+            }
+        }
+        float inv_rho = 1.0f / rho_i;
+        ax = (pax + vax) * inv_rho;
+        ay = (pay + vay) * inv_rho;
+        az = (paz + vaz) * inv_rho;
+        nvx = vi.x + ax * K.dt;
+        nvy = vi.y + ay * K.dt;
+        nvz = vi.z + az * K.dt;
+    }
+    const uint32_t i = sidx[s];
+    if (i >= n) return;
+    float npx = pi.x, npy = pi.y, npz = pi.z;
+    if (K.flags & FH_EPI_GRAVITY) {
+        nvx += K.gx * K.dt;
+        nvy += K.gy * K.dt;
+        nvz += K.gz * K.dt;
+    }
+    if (K.flags & FH_EPI_INTEGRATE) {
+        if (!isfinite(nvx)) nvx = 0.0f;
+        if (!isfinite(nvy)) nvy = 0.0f;
+        if (!isfinite(nvz)) nvz = 0.0f;
+        npx += nvx * K.dt;
+        npy += nvy * K.dt;
+        npz += nvz * K.dt;
+    }
+    if (K.flags & FH_EPI_BOX) {
+        if (npx < K.mn[0]) { npx = K.mn[0]; nvx = fabsf(nvx) * K.e; }
+        if (npx > K.mx[0]) { npx = K.mx[0]; nvx = -fabsf(nvx) * K.e; }
+        if (npy < K.mn[1]) { npy = K.mn[1]; nvy = fabsf(nvy) * K.e; }
+        if (npy > K.mx[1]) { npy = K.mx[1]; nvy = -fabsf(nvy) * K.e; }
+        if (npz < K.mn[2]) { npz = K.mn[2]; nvz = fabsf(nvz) * K.e; }
+        if (npz > K.mx[2]) { npz = K.mx[2]; nvz = -fabsf(nvz) * K.e; }
+    }
+    vx[i] = nvx;
+    vy[i] = nvy;
+    vz[i] = nvz;
+    if (K.flags & (FH_EPI_INTEGRATE | FH_EPI_BOX)) {
+        px[i] = npx;
+        py[i] = npy;
+        pz[i] = npz;
+    }
+    if (accel) {
+        accel[i] = ax;
+        accel[(size_t)n + i] = ay;
+        accel[2 * (size_t)n + i] = az;
+    }
+}
+
+hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
+                        const uint32_t* cell_start, float* px, float* py, float* pz, float* vx,
+                        float* vy, float* vz, float* accel) {
+    if (a.n == 0) return hipSuccess;
+    ForceConsts K;
+    K.h = a.h;
+    K.h2 = a.h * a.h;
+    K.mass = a.mass;
+    K.k = a.k;
+    K.rho0 = a.rho0;
+    K.mu = a.mu;
+    // sph_fused.rs:552-555
+    float h6 = K.h2 * K.h2 * K.h2;
+    K.gcoef = -45.0f / (3.14159265f * h6);
+    K.lcoef = 45.0f / (3.14159265f * h6);
+    K.dt = a.dt;
+    K.flags = epi ? epi->flags : 0u;
+    K.gx = epi ? epi->gravity[0] : 0.0f;
+    K.gy = epi ? epi->gravity[1] : 0.0f;
+    K.gz = epi ? epi->gravity[2] : 0.0f;
+    for (int q = 0; q < 3; q++) {
+        K.mn[q] = epi ? epi->box_min[q] : 0.0f;
+        K.mx[q] = epi ? epi->box_max[q] : 0.0f;
+    }
+    K.e = epi ? epi->restitution : 0.0f;
+    k_force<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sidx, a.n,
+                                                        a.g, cell_start, K, px, py, pz, vx, vy,
+                                                        vz, accel);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// gravity.rs:31-34
+__global__ void k_gravity(float* __restrict__ vx, float* __restrict__ vy, float* __restrict__ vz,
+                          float gx, float gy, float gz, float dt, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        vx[i] += gx * dt;
+        vy[i] += gy * dt;
+        vz[i] += gz * dt;
+    }
+}
+
+// integrate.rs:16-31
+__global__ void k_integrate(float* __restrict__ px, float* __restrict__ py,
+                            float* __restrict__ pz, float* __restrict__ vx,
+                            float* __restrict__ vy, float* __restrict__ vz, float dt,
+                            uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float _vx = vx[i], _vy = vy[i], _vz = vz[i];
+    if (!isfinite(_vx)) { _vx = 0.0f; vx[i] = 0.0f; }
+    if (!isfinite(_vy)) { _vy = 0.0f; vy[i] = 0.0f; }
+    if (!isfinite(_vz)) { _vz = 0.0f; vz[i] = 0.0f; }
+    px[i] += _vx * dt;
+    py[i] += _vy * dt;
+    pz[i] += _vz * dt;
+}
+
+// box_collider.rs:26-47
+__global__ void k_box(float* __restrict__ px, float* __restrict__ py, float* __restrict__ pz,
+                      float* __restrict__ vx, float* __restrict__ vy, float* __restrict__ vz,
+                      float mnx, float mny, float mnz, float mxx, float mxy, float mxz, float e,
+                      uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float x = px[i], y = py[i], z = pz[i], u = vx[i], v = vy[i], w = vz[i];
+    if (x < mnx) { x = mnx; u = fabsf(u) * e; }
+    if (x > mxx) { x = mxx; u = -fabsf(u) * e; }
+    if (y < mny) { y = mny; v = fabsf(v) * e; }
+    if (y > mxy) { y = mxy; v = -fabsf(v) * e; }
+    if (z < mnz) { z = mnz; w = fabsf(w) * e; }
+    if (z > mxz) { z = mxz; w = -fabsf(w) * e; }
+    px[i] = x;
+    py[i] = y;
+    pz[i] = z;
+    vx[i] = u;
+    vy[i] = v;
+    vz[i] = w;
+}
+
+hipError_t launch_gravity(fh_ctx* c, float* vx, float* vy, float* vz, uint32_t n, float gx,
+                          float gy, float gz, float dt) {
+    if (n == 0) return hipSuccess;
+    k_gravity<<<ceil_div(n, 256u), 256, 0, c->stream>>>(vx, vy, vz, gx, gy, gz, dt, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_integrate(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,
+                            float* vz, uint32_t n, float dt) {
+    if (n == 0) return hipSuccess;
+    k_integrate<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, dt, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_box(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,
+                      float* vz, uint32_t n, const float* mn, const float* mx, float e) {
+    if (n == 0) return hipSuccess;
+    k_box<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, mn[0], mn[1], mn[2],
+                                                    mx[0], mx[1], mx[2], e, n);
+    return hipGetLastError();
+}
+
+}  // namespace fh

@@ -1,0 +1,23 @@
+"""forge_hip -- MI355X (gfx950) SPH / hash-grid hot path of forge-gpu behind its own API.
+
+The compute path is libforge_hip.so (hand-written HIP kernels behind the C ABI of
+include/forge_hip.h); this package is the host-side mirror of the reference's interfaces for
+the path (HashGrid, RadixSorter, find_cell_boundaries, FieldSet, SimModule, Pipeline and the
+SPH / gravity / integrate / box modules).  Importing it never loads a CPU fallback: there is
+none.
+"""
+from ._lib import (FH_EINVAL, FH_ENODEV, FH_EPI_BOX, FH_EPI_GRAVITY, FH_EPI_INTEGRATE,
+                   FH_ERANGE, FH_ESTATE, FH_OK, ForgeError, LibraryNotBuilt, load)
+from .hashgrid import HashGrid, RadixSorter, find_cell_boundaries
+from .modules import (BoxColliderModule, FieldSet, GravityModule, IntegrateModule, Pipeline,
+                      SimModule, SphDensityModule, SphFusedModule, build_pipeline)
+from .runtime import Context, default_context, from_u32, to_u32, u32_empty
+
+__all__ = [
+    "FH_OK", "FH_EINVAL", "FH_ERANGE", "FH_ESTATE", "FH_ENODEV", "FH_EPI_GRAVITY",
+    "FH_EPI_INTEGRATE", "FH_EPI_BOX", "ForgeError", "LibraryNotBuilt", "load", "HashGrid",
+    "RadixSorter", "find_cell_boundaries", "FieldSet", "SimModule", "Pipeline",
+    "SphDensityModule", "SphFusedModule", "GravityModule", "IntegrateModule",
+    "BoxColliderModule", "build_pipeline", "Context", "default_context", "to_u32", "from_u32",
+    "u32_empty",
+]

@@ -1,0 +1,334 @@
+"""FieldSet / SimModule / Pipeline: host-side mirror of forge-manifest/src/modules/mod.rs and
+the builtin modules on the SPH path, dispatching to the C ABI.
+
+  FieldSet                 modules/mod.rs:12-67   (named SoA device arrays in particle order)
+  SimModule                modules/mod.rs:70-73   (name(), execute(fields, dt))
+  Pipeline                 modules/mod.rs:76-117  (step_async / step / run) + graph capture and
+                           replay of substeps as run_manifest does (manifest_runner.rs:53-77)
+  SphFusedModule           builtins/sph_fused.rs:14-22,410-733
+  SphDensityModule         builtins/sph_density.rs:16-21,385-501
+  GravityModule            builtins/gravity.rs:5-63
+  IntegrateModule          builtins/integrate.rs:5-70
+  BoxColliderModule        builtins/box_collider.rs:6-85
+  build_pipeline           manifest_runner.rs:322-544 (SPH fusion, parameter defaults, order)
+
+Fields stay in original particle order, as the reference keeps them.  The SPH modules create
+`density` on first use (sph_fused.rs:420-422).  When a pipeline holds [sph_fused, gravity,
+integrate, box_collider] in that order, Pipeline fuses the three epilogue modules into the SPH
+force pass (one kernel instead of three); the result equals running them separately.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import FhEpilogue, FhSphParams, check, f3
+from .runtime import Context, default_context, ptr
+
+
+class FieldSet:
+    def __init__(self, particle_count: int, device: int = 0):
+        self.f32_fields: dict[str, torch.Tensor] = {}
+        self.u32_fields: dict[str, torch.Tensor] = {}
+        self.particle_count = int(particle_count)
+        self.device = int(device)
+        self.ctx: Context | None = None
+
+    def add_f32(self, name: str, data) -> None:
+        t = torch.as_tensor(np.asarray(data, dtype=np.float32)).to(f"cuda:{self.device}")
+        self.f32_fields[name] = t.contiguous()
+
+    def add_f32_zeros(self, name: str, n: int) -> None:
+        self.f32_fields[name] = torch.zeros(int(n), dtype=torch.float32,
+                                            device=f"cuda:{self.device}")
+
+    def get_f32(self, name: str):
+        return self.f32_fields.get(name)
+
+    def context(self, max_cells: int = 1) -> Context:
+        """The stream/scratch owner of this field set: the device's default context, grown on
+        first need (grow before capturing a graph: a grown context replaces the old one)."""
+        self.ctx = default_context(max(self.particle_count, 1), max(int(max_cells), 1),
+                                   self.device)
+        return self.ctx
+
+    def _f(self, name: str) -> torch.Tensor:
+        t = self.f32_fields.get(name)
+        if t is None:
+            raise _lib.ForgeError(_lib.FH_EINVAL, f"missing field {name}")
+        return t
+
+    def pos(self):
+        return self._f("pos_x"), self._f("pos_y"), self._f("pos_z")
+
+    def vel(self):
+        return self._f("vel_x"), self._f("vel_y"), self._f("vel_z")
+
+
+class SimModule:
+    def name(self) -> str:
+        raise NotImplementedError
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        raise NotImplementedError
+
+
+def _sph_params(m) -> FhSphParams:
+    p = FhSphParams()
+    p.smoothing_radius = m.smoothing_radius
+    p.cell_size = m.cell_size
+    for q in range(3):
+        p.grid_dims[q] = int(m.grid_dims[q])
+    p.particle_mass = m.particle_mass
+    p.gas_constant = getattr(m, "gas_constant", 0.0)
+    p.rest_density = getattr(m, "rest_density", 0.0)
+    p.viscosity_coefficient = getattr(m, "viscosity_coefficient", 0.0)
+    return p
+
+
+def _cells(dims) -> int:
+    return int(dims[0]) * int(dims[1]) * int(dims[2])
+
+
+class SphDensityModule(SimModule):
+    def __init__(self, smoothing_radius, cell_size, grid_dims, particle_mass):
+        self.smoothing_radius = float(smoothing_radius)
+        self.cell_size = float(cell_size)
+        self.grid_dims = [int(d) for d in grid_dims]
+        self.particle_mass = float(particle_mass)
+
+    def name(self) -> str:
+        return "sph_density"
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        n = fields.particle_count
+        if "density" not in fields.f32_fields:
+            fields.add_f32_zeros("density", n)
+        ctx = fields.context(_cells(self.grid_dims))
+        px, py, pz = fields.pos()
+        check(_lib.load().fh_sph_density(ctx.handle, ctypes.byref(_sph_params(self)), ptr(px),
+                                         ptr(py), ptr(pz), n, ptr(fields.f32_fields["density"])))
+
+
+class SphFusedModule(SimModule):
+    def __init__(self, smoothing_radius, cell_size, grid_dims, particle_mass, gas_constant,
+                 rest_density, viscosity_coefficient):
+        self.smoothing_radius = float(smoothing_radius)
+        self.cell_size = float(cell_size)
+        self.grid_dims = [int(d) for d in grid_dims]
+        self.particle_mass = float(particle_mass)
+        self.gas_constant = float(gas_constant)
+        self.rest_density = float(rest_density)
+        self.viscosity_coefficient = float(viscosity_coefficient)
+        self.epilogue: FhEpilogue | None = None  # set by Pipeline fusion
+        self.accel: torch.Tensor | None = None   # optional (3, N) output of a_i
+
+    def name(self) -> str:
+        return "sph_fused"
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        n = fields.particle_count
+        if "density" not in fields.f32_fields:
+            fields.add_f32_zeros("density", n)
+        ctx = fields.context(_cells(self.grid_dims))
+        px, py, pz = fields.pos()
+        vx, vy, vz = fields.vel()
+        epi = ctypes.byref(self.epilogue) if self.epilogue is not None else None
+        check(_lib.load().fh_sph_fused(ctx.handle, ctypes.byref(_sph_params(self)), epi,
+                                       ptr(px), ptr(py), ptr(pz), ptr(vx), ptr(vy), ptr(vz),
+                                       ptr(fields.f32_fields["density"]), ptr(self.accel), n,
+                                       float(dt)))
+
+
+class GravityModule(SimModule):
+    def __init__(self, gx: float = 0.0, gy: float = -9.81, gz: float = 0.0):
+        self.gx, self.gy, self.gz = float(gx), float(gy), float(gz)
+
+    @staticmethod
+    def default_earth():
+        return GravityModule(0.0, -9.81, 0.0)
+
+    def name(self) -> str:
+        return "gravity"
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        vx, vy, vz = fields.vel()
+        ctx = fields.context()
+        check(_lib.load().fh_gravity(ctx.handle, ptr(vx), ptr(vy), ptr(vz),
+                                     fields.particle_count, self.gx, self.gy, self.gz, float(dt)))
+
+
+class IntegrateModule(SimModule):
+    def name(self) -> str:
+        return "integrate"
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        px, py, pz = fields.pos()
+        vx, vy, vz = fields.vel()
+        ctx = fields.context()
+        check(_lib.load().fh_integrate(ctx.handle, ptr(px), ptr(py), ptr(pz), ptr(vx), ptr(vy),
+                                       ptr(vz), fields.particle_count, float(dt)))
+
+
+class BoxColliderModule(SimModule):
+    def __init__(self, min_x, min_y, min_z, max_x, max_y, max_z, restitution):
+        self.min_x, self.min_y, self.min_z = float(min_x), float(min_y), float(min_z)
+        self.max_x, self.max_y, self.max_z = float(max_x), float(max_y), float(max_z)
+        self.restitution = float(restitution)
+
+    def name(self) -> str:
+        return "box_collider"
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        px, py, pz = fields.pos()
+        vx, vy, vz = fields.vel()
+        ctx = fields.context()
+        check(_lib.load().fh_box_collider(
+            ctx.handle, ptr(px), ptr(py), ptr(pz), ptr(vx), ptr(vy), ptr(vz),
+            fields.particle_count, f3((self.min_x, self.min_y, self.min_z)),
+            f3((self.max_x, self.max_y, self.max_z)), self.restitution))
+
+
+class Pipeline:
+    def __init__(self, fuse_epilogue: bool = True):
+        self.modules: list[SimModule] = []
+        self.fuse_epilogue = fuse_epilogue
+        self._plan: list[SimModule] | None = None
+        self._captured_ctx: Context | None = None
+
+    def add(self, module: SimModule) -> None:
+        self.modules.append(module)
+        self._plan = None
+
+    def __len__(self) -> int:
+        return len(self.modules)
+
+    def _fused_plan(self) -> list[SimModule]:
+        """Fold gravity / integrate / box that directly follow sph_fused into its force pass."""
+        if self._plan is not None:
+            return self._plan
+        plan: list[SimModule] = []
+        mods = self.modules
+        i = 0
+        while i < len(mods):
+            m = mods[i]
+            if self.fuse_epilogue and isinstance(m, SphFusedModule) and m.epilogue is None:
+                epi = FhEpilogue()
+                j = i + 1
+                order = [GravityModule, IntegrateModule, BoxColliderModule]
+                for kind in order:
+                    if j < len(mods) and isinstance(mods[j], kind):
+                        e = mods[j]
+                        if kind is GravityModule:
+                            epi.flags |= _lib.FH_EPI_GRAVITY
+                            epi.gravity[:] = [e.gx, e.gy, e.gz]
+                        elif kind is IntegrateModule:
+                            epi.flags |= _lib.FH_EPI_INTEGRATE
+                        else:
+                            epi.flags |= _lib.FH_EPI_BOX
+                            epi.box_min[:] = [e.min_x, e.min_y, e.min_z]
+                            epi.box_max[:] = [e.max_x, e.max_y, e.max_z]
+                            epi.restitution = e.restitution
+                        j += 1
+                if j > i + 1:
+                    fused = SphFusedModule(m.smoothing_radius, m.cell_size, m.grid_dims,
+                                           m.particle_mass, m.gas_constant, m.rest_density,
+                                           m.viscosity_coefficient)
+                    fused.epilogue = epi
+                    fused.accel = m.accel
+                    plan.append(fused)
+                    i = j
+                    continue
+            plan.append(m)
+            i += 1
+        self._plan = plan
+        return plan
+
+    def step_async(self, fields: FieldSet, dt: float) -> None:
+        """All modules in order, queued on the field set's stream (modules/mod.rs:90-95)."""
+        ctx = fields.context(max((_cells(m.grid_dims) for m in self.modules
+                                  if hasattr(m, "grid_dims")), default=1))
+        if not getattr(ctx, "capturing", False):
+            ctx.torch_stream().wait_stream(torch.cuda.current_stream())
+        for m in self._fused_plan():
+            m.execute(fields, dt)
+
+    def step(self, fields: FieldSet, dt: float) -> None:
+        """step_async, then wait for the stream (modules/mod.rs:98-104)."""
+        self.step_async(fields, dt)
+        fields.context().sync()
+
+    def run(self, fields: FieldSet, dt: float, steps: int) -> None:
+        for _ in range(int(steps)):
+            self.step(fields, dt)
+
+    def capture(self, fields: FieldSet, dt: float, substeps: int) -> None:
+        """Record `substeps` step_async calls into one HIP graph (manifest_runner.rs:57-69)."""
+        ctx = fields.context(max((_cells(m.grid_dims) for m in self.modules
+                                  if hasattr(m, "grid_dims")), default=1))
+        ctx.torch_stream().wait_stream(torch.cuda.current_stream())
+        ctx.sync()
+        ctx.graph_begin()
+        ctx.capturing = True
+        try:
+            for _ in range(int(substeps)):
+                self.step_async(fields, dt)
+        finally:
+            ctx.capturing = False
+            ctx.graph_end()
+        self._captured_ctx = ctx
+
+    def replay(self, count: int = 1) -> None:
+        """Launch the captured graph `count` times (manifest_runner.rs:74-77)."""
+        if self._captured_ctx is None:
+            raise _lib.ForgeError(_lib.FH_ESTATE, "no captured graph")
+        self._captured_ctx.graph_launch(count)
+
+
+def build_pipeline(forces: list[dict], constraints: list[dict], n: int,
+                   spatial: dict | None = None) -> Pipeline:
+    """Pipeline construction of manifest_runner.rs:322-544 for the SPH path.
+
+    forces: dicts with "type" in {"sph_density", "sph_pressure", "sph_viscosity", "gravity"}
+    and the manifest's keys; constraints: {"type": "box", "min": [...], "max": [...],
+    "restitution": e}.  Fusion, defaults (h 0.025, (k, rho0) = (2000, 1000), mu 0.01,
+    cell_size 2h, dims 32^3, mass = rho0 / n * 0.001) and order (fused SPH, other forces,
+    integrate, constraints) follow the reference."""
+    from .workloads import particle_mass
+
+    pipe = Pipeline()
+    kinds = {f["type"] for f in forces}
+    fuse = {"sph_density", "sph_pressure", "sph_viscosity"} <= kinds
+    if fuse:
+        h = next((float(f["smoothing_radius"]) for f in forces if f["type"] == "sph_density"), 0.025)
+        k, rho0 = next(((float(f["gas_constant"]), float(f["rest_density"])) for f in forces
+                        if f["type"] == "sph_pressure"), (2000.0, 1000.0))
+        mu = next((float(f["coefficient"]) for f in forces if f["type"] == "sph_viscosity"), 0.01)
+        cs = float(spatial["cell_size"]) if spatial else h * 2.0
+        dims = list(spatial.get("grid_dims", [32, 32, 32])) if spatial else [32, 32, 32]
+        dims = (dims + [32, 32, 32])[:3]
+        pipe.add(SphFusedModule(h, cs, dims, particle_mass(rho0, n), k, rho0, mu))
+    for f in forces:
+        if f["type"] == "gravity":
+            v = list(f.get("value", [0.0, -9.81, 0.0])) + [0.0, -9.81, 0.0][len(f.get("value", [])):]
+            pipe.add(GravityModule(v[0], v[1], v[2]))
+        elif f["type"] in ("sph_density", "sph_pressure", "sph_viscosity") and fuse:
+            continue
+        elif f["type"] == "sph_density":
+            h = float(f["smoothing_radius"])
+            cs = float(spatial["cell_size"]) if spatial else h * 2.0
+            dims = list(spatial.get("grid_dims", [32, 32, 32])) if spatial else [32, 32, 32]
+            pipe.add(SphDensityModule(h, cs, dims, particle_mass(1000.0, n)))
+        else:
+            raise _lib.ForgeError(_lib.FH_EINVAL, f"force {f['type']} is outside the SPH path")
+    pipe.add(IntegrateModule())
+    for c in constraints:
+        if c["type"] != "box":
+            raise _lib.ForgeError(_lib.FH_EINVAL, f"constraint {c['type']} is outside the SPH path")
+        mn, mx = c.get("min", [0, 0, 0]), c.get("max", [1, 1, 1])
+        pipe.add(BoxColliderModule(mn[0], mn[1], mn[2], mx[0], mx[1], mx[2],
+                                   float(c.get("restitution", 0.5))))
+    return pipe

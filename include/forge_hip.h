@@ -1,0 +1,212 @@
+/*
+ * forge_hip.h -- C ABI of the MI355X (gfx950) SPH / hash-grid hot path.
+ *
+ * This is the drop-in boundary that forge-gpu's host code would bind over FFI in place of its
+ * NVRTC-compiled CUDA kernels.  Every entry point takes plain device pointers and sizes; the
+ * caller owns every particle, key and output buffer, the context owns scratch, the stream and
+ * the captured graph.
+ *
+ * Conventions
+ *  - Return value: 0 = ok, < 0 = invalid argument (FH_E*), > 0 = a hipError_t code.
+ *    Nothing aborts or unwinds across the ABI.  fh_last_error() returns a thread-local message
+ *    describing the last failure on the calling thread.
+ *  - All compute calls are asynchronous on the context stream (fh_stream()); fh_sync() waits.
+ *    Results in caller buffers are visible after fh_sync() or any later work ordered on the
+ *    same stream.
+ *  - All scratch is allocated by fh_create(), so every compute call below is legal inside
+ *    stream capture (no allocation, no memset node, no host synchronisation).
+ *  - A context is used by one host thread at a time; several contexts may coexist.
+ *  - "Position" inputs are three float pointers plus an element stride in floats, so both the
+ *    structure-of-arrays layout of FieldSet (pos_x/pos_y/pos_z, stride 1) and the 12-byte
+ *    Vec3f array-of-structures layout of HashGrid::build (x = p, y = p + 1, z = p + 2,
+ *    stride 3) are accepted without a copy.
+ *
+ * Reference interfaces replaced (huaying/forge-gpu, paths relative to the repository root):
+ *  - forge-runtime/src/hashgrid.rs:21-193      HashGrid::{new, build, position_to_cell, query_neighbors}
+ *  - forge-runtime/src/radix_sort.rs:26-220    RadixSorter::{new, sort}
+ *  - forge-runtime/src/radix_sort.rs:229-317   find_cell_boundaries
+ *  - forge-manifest/src/modules/builtins/sph_density.rs:16-501   SphDensityModule::execute
+ *  - forge-manifest/src/modules/builtins/sph_fused.rs:14-733     SphFusedModule::execute
+ *  - forge-manifest/src/modules/builtins/gravity.rs:23-63        GravityModule::execute
+ *  - forge-manifest/src/modules/builtins/integrate.rs:9-70       IntegrateModule::execute
+ *  - forge-manifest/src/modules/builtins/box_collider.rs:18-85   BoxColliderModule::execute
+ *  - forge-manifest/src/manifest_runner.rs:53-77                 graph capture / replay of substeps
+ *  - forge-runtime/src/cuda.rs:55-63                             the simulation stream
+ *  - forge-runtime/src/error.rs:7-22                             ForgeError (mapped to return codes)
+ */
+#ifndef FORGE_HIP_H
+#define FORGE_HIP_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_ABI_VERSION 1
+
+/* ---- status codes (negative: argument errors detected on the host) ------------------------- */
+#define FH_OK 0
+#define FH_EINVAL -1       /* null pointer, zero-sized grid, bad num_bits, ...                   */
+#define FH_ERANGE -2       /* n > max_n or num_cells > max_cells of the context                 */
+#define FH_ESTATE -3       /* call not legal in the current state (e.g. graph_end w/o begin)     */
+#define FH_ENODEV -4       /* no HIP device, or the device is not gfx950                        */
+
+typedef struct fh_ctx fh_ctx;
+
+/* Parameters of the SPH passes.  Mirrors the fields of SphFusedModule
+ * (forge-manifest/src/modules/builtins/sph_fused.rs:14-22); SphDensityModule uses the first
+ * four (sph_density.rs:16-21).  The grid origin is (0,0,0), as in the reference kernels
+ * (sph_fused.rs:91-93 hash with floorf(p / cell_size)). */
+typedef struct fh_sph_params {
+    float smoothing_radius;      /* h                                                       */
+    float cell_size;             /* cs                                                      */
+    uint32_t grid_dims[3];       /* nx, ny, nz                                              */
+    float particle_mass;         /* m                                                       */
+    float gas_constant;          /* k   (p = k (rho - rho0))                                */
+    float rest_density;          /* rho0                                                    */
+    float viscosity_coefficient; /* mu                                                      */
+} fh_sph_params;
+
+/* Epilogue of one substep, applied after the SPH velocity update in the order of
+ * build_pipeline (manifest_runner.rs:371-393,508,528-537): gravity, integrate, box. */
+#define FH_EPI_GRAVITY 1u
+#define FH_EPI_INTEGRATE 2u
+#define FH_EPI_BOX 4u
+typedef struct fh_epilogue {
+    uint32_t flags;              /* OR of FH_EPI_*                                          */
+    float gravity[3];            /* GravityModule{gx,gy,gz}          (gravity.rs:5-9)       */
+    float box_min[3];            /* BoxColliderModule{min_*}         (box_collider.rs:6-14) */
+    float box_max[3];            /* BoxColliderModule{max_*}                                */
+    float restitution;           /* BoxColliderModule::restitution                          */
+} fh_epilogue;
+
+/* ---- context -------------------------------------------------------------------------------- */
+
+/* Create a context on HIP device `device` for up to `max_n` particles / sort pairs and
+ * `max_cells` grid cells.  `stream` is an existing hipStream_t to run on, or NULL to create a
+ * private default-priority stream.  Allocates every scratch buffer up front (replaces the lazy
+ * scratch creation of sph_fused.rs:43-74 and RadixSorter::new, radix_sort.rs:55-70). */
+int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_ctx** out);
+int fh_destroy(fh_ctx* ctx);
+void* fh_stream(fh_ctx* ctx);                 /* the hipStream_t all calls are queued on       */
+int fh_sync(fh_ctx* ctx);                     /* hipStreamSynchronize (Pipeline::step sync,
+                                                 forge-manifest/src/modules/mod.rs:98-104)     */
+const char* fh_last_error(void);              /* thread-local, never NULL                      */
+int fh_abi_version(void);
+/* Bytes of device scratch the context holds (for capacity planning). */
+size_t fh_scratch_bytes(const fh_ctx* ctx);
+
+/* ---- hashing -------------------------------------------------------------------------------- */
+
+/* keys[i] = cell of particle i, vals[i] = i.  Cell: c = floor((p - origin) / cs) with Rust
+ * `as i32` semantics (NaN -> 0, saturating), clamped to [0, dim-1], linearised
+ * cx + cy*nx + cz*nx*ny (forge-runtime/src/hashgrid.rs:128-139; GPU twin without origin at
+ * sph_fused.rs:84-100).  `vals` may be NULL. */
+int fh_hash_cells(fh_ctx* ctx, const float* x, const float* y, const float* z, uint32_t stride,
+                  uint32_t n, float cell_size, const float origin[3], const uint32_t dims[3],
+                  uint32_t* keys, uint32_t* vals);
+
+/* ---- sorting -------------------------------------------------------------------------------- */
+
+/* Stable LSD radix sort of (key, value) pairs by the low `num_bits` bits of the key (1..32),
+ * result in place in `keys`/`vals`.  Replaces RadixSorter::sort (radix_sort.rs:79-220), which
+ * required num_bits % 4 == 0 and panicked on n > max_n; here any 1..32 is accepted and
+ * n > max_n returns FH_ERANGE.  Equal keys keep their input order. */
+int fh_sort_pairs(fh_ctx* ctx, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_t num_bits);
+
+/* From keys sorted ascending: cell_start[c] = first i with key c, cell_end[c] = last i + 1;
+ * cells with no key keep cell_start = 0xFFFFFFFF, cell_end = 0.  Keys >= num_cells are
+ * ignored.  Replaces find_cell_boundaries (radix_sort.rs:229-317, kernel :444-466). */
+int fh_find_cell_boundaries(fh_ctx* ctx, const uint32_t* sorted_keys, uint32_t n,
+                            uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end);
+
+/* ---- hash grid ------------------------------------------------------------------------------ */
+
+/* HashGrid::build on the GPU (hashgrid.rs:82-125): cell_indices[i] = cell of particle i,
+ * cell_start[0..C] = exclusive prefix sum of the per-cell counts (cell_start[C] = n),
+ * sorted_indices = particle ids ordered by cell, ascending id within a cell (the stable
+ * counting-sort order of hashgrid.rs:109-117).  C = dims[0]*dims[1]*dims[2]. */
+int fh_hashgrid_build(fh_ctx* ctx, const float* x, const float* y, const float* z,
+                      uint32_t stride, uint32_t n, float cell_size, const float origin[3],
+                      const uint32_t dims[3], uint32_t* cell_start, uint32_t* sorted_indices,
+                      uint32_t* cell_indices);
+
+/* For every point i of a grid built by fh_hashgrid_build over the same positions, count the
+ * points j with ((dx*dx + dy*dy) + dz*dz) <= radius^2 (dx = p_j - p_i, self included, the
+ * predicate and neighbourhood walk of HashGrid::query_neighbors, hashgrid.rs:145-193) and sum
+ * their poly6 weights c*(r^2 - d^2)^3 with c = 315/(64*pi*r^9) (sph_density.rs:413-416 with
+ * h = radius, no mass factor).  counts / wsum are in original point order; wsum may be NULL. */
+int fh_neighbor_query(fh_ctx* ctx, const float* x, const float* y, const float* z,
+                      uint32_t stride, uint32_t n, float cell_size, const float origin[3],
+                      const uint32_t dims[3], const uint32_t* cell_start,
+                      const uint32_t* sorted_indices, float radius, uint32_t* counts,
+                      float* wsum);
+
+/* HashGrid::query_neighbors (hashgrid.rs:145-193) for a batch of `nq` arbitrary query points
+ * (qx/qy/qz with element stride qstride) against a grid built over the positions x/y/z.  The
+ * query cell is not clamped; neighbours are visited in the reference's order (dz, dy, dx, then
+ * cell order) and kept when ((dx*dx + dy*dy) + dz*dz) <= radius^2 with dx = p_j - q.
+ * counts[q] receives the number of neighbours.  If `offsets` (nq+1 exclusive prefix sums of a
+ * previous count call) and `indices` are non-NULL, the neighbour ids of query q are also
+ * written to indices[offsets[q] .. offsets[q+1]). */
+int fh_query_neighbors(fh_ctx* ctx, const float* x, const float* y, const float* z,
+                       uint32_t stride, float cell_size, const float origin[3],
+                       const uint32_t dims[3], const uint32_t* cell_start,
+                       const uint32_t* sorted_indices, const float* qx, const float* qy,
+                       const float* qz, uint32_t qstride, uint32_t nq, float radius,
+                       uint32_t* counts, const uint32_t* offsets, uint32_t* indices);
+
+/* ---- SPH modules ---------------------------------------------------------------------------- */
+
+/* SphDensityModule::execute (sph_density.rs:388-501): rebuild the grid from pos and write
+ * density[i] = sum over j in the 27-cell neighbourhood with r^2 < h^2 (self included) of
+ * m * 315/(64*pi*h^9) * (h^2 - r^2)^3, in original particle order. */
+int fh_sph_density(fh_ctx* ctx, const fh_sph_params* prm, const float* px, const float* py,
+                   const float* pz, uint32_t n, float* density);
+
+/* SphFusedModule::execute (sph_fused.rs:413-732): rebuild, density, then the fused pressure +
+ * viscosity pass: v_i += ((a_p + a_v) / rho_i) * dt, all neighbour velocities read from the
+ * state before this call.  density (required) receives rho in original order; accel (may be
+ * NULL) receives a_i = (a_p + a_v) / rho_i as 3 SoA arrays of n floats (accel, accel+n,
+ * accel+2n).  If `epi` is non-NULL its flagged steps are fused into the force pass
+ * (equivalent to running GravityModule, IntegrateModule and BoxColliderModule afterwards). */
+int fh_sph_fused(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
+                 float* py, float* pz, float* vx, float* vy, float* vz, float* density,
+                 float* accel, uint32_t n, float dt);
+
+/* GravityModule (gravity.rs:31-34): v += g * dt. */
+int fh_gravity(fh_ctx* ctx, float* vx, float* vy, float* vz, uint32_t n, float gx, float gy,
+               float gz, float dt);
+/* IntegrateModule (integrate.rs:16-31): non-finite velocity components are zeroed (and
+ * stored), then p += v * dt. */
+int fh_integrate(fh_ctx* ctx, float* px, float* py, float* pz, float* vx, float* vy,
+                 float* vz, uint32_t n, float dt);
+/* BoxColliderModule (box_collider.rs:26-47): per axis, p < min -> (p = min, v = |v| e), then
+ * p > max -> (p = max, v = -|v| e). */
+int fh_box_collider(fh_ctx* ctx, float* px, float* py, float* pz, float* vx, float* vy,
+                    float* vz, uint32_t n, const float box_min[3], const float box_max[3],
+                    float restitution);
+
+/* ---- graphs (run_manifest capture/replay, manifest_runner.rs:53-77) ------------------------- */
+
+/* Begin capturing the context stream; every fh_* compute call until fh_graph_end is recorded
+ * instead of run.  fh_graph_end instantiates (replacing any previous graph of this context);
+ * fh_graph_launch replays it `count` times on the context stream. */
+int fh_graph_begin(fh_ctx* ctx);
+int fh_graph_end(fh_ctx* ctx);
+int fh_graph_launch(fh_ctx* ctx, uint32_t count);
+
+/* ---- timing of the launches on the context stream ------------------------------------------ */
+
+/* Record a HIP event on the context stream into slot `slot` (0..15); fh_event_elapsed_ms gives
+ * the time between two recorded slots after they completed. */
+int fh_event_record(fh_ctx* ctx, uint32_t slot);
+int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGE_HIP_H */

@@ -1,0 +1,128 @@
+"""GPU parity of the radix sort and cell boundaries (C ABI fh_sort_pairs,
+fh_find_cell_boundaries) against the oracle and the reference's known answers.
+Bar: bit-exact keys and values (stable order), tests/radix_sort_test.rs as the model."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+def xorshift32(seed, n, mask):
+    out = np.empty(n, np.uint32)
+    s = seed
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out[i] = s & mask
+    return out
+
+
+def gpu_sort(fh, ctx, keys, vals, bits):
+    k = fh.from_u32(keys)
+    v = fh.from_u32(vals)
+    torch.cuda.synchronize()
+    fh.RadixSorter(max(len(keys), 1), ctx=ctx).sort(k, v, len(keys), bits)
+    return fh.to_u32(k), fh.to_u32(v)
+
+
+def test_radix_sort_small(fh, gpu_ctx):
+    kat = KATS["radix_sort_small"]
+    k, v = gpu_sort(fh, gpu_ctx, kat["keys"], kat["vals"], kat["num_bits"])
+    assert k.tolist() == kat["sorted_keys"]
+    assert v.tolist() == kat["sorted_vals"]
+
+
+@pytest.mark.parametrize("name", ["radix_sort_medium", "radix_sort_compare_cpu"])
+def test_radix_sort_xorshift_streams(fh, gpu_ctx, oracle, name):
+    kat = KATS[name]
+    keys = xorshift32(kat["xorshift_seed"], kat["n"], kat["mask"])
+    assert keys[:8].tolist() == kat["first_keys"]
+    vals = np.arange(kat["n"], dtype=np.uint32)
+    k, v = gpu_sort(fh, gpu_ctx, keys, vals, kat["num_bits"])
+    ok, ov = oracle.stable_sort_pairs(keys, vals, kat["num_bits"])
+    assert np.array_equal(k, ok) and np.array_equal(v, ov)
+    assert np.all(keys[v] == k)  # key/value correspondence (radix_sort_test.rs:84-88)
+
+
+@pytest.mark.parametrize("n,bits", [(0, 8), (1, 32), (2, 1), (3, 5), (4095, 12), (4096, 16),
+                                    (4097, 20), (65537, 8), (100_000, 7), (100_000, 32),
+                                    (1 << 20, 20), (1_000_003, 24), (2_500_000, 31)])
+def test_sort_matches_oracle(fh, gpu_ctx, oracle, n, bits):
+    rng = np.random.default_rng(n * 131 + bits)
+    keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)  # high bits beyond num_bits too
+    vals = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    print(f"sort n={n} bits={bits}", flush=True)
+    k, v = gpu_sort(fh, gpu_ctx, keys, vals, bits)
+    ok, ov = oracle.stable_sort_pairs(keys, vals, bits)
+    assert np.array_equal(k, ok)
+    assert np.array_equal(v, ov)
+
+
+def test_sort_heavy_duplicates_is_stable(fh, gpu_ctx):
+    n = 300_000
+    rng = np.random.default_rng(7)
+    keys = rng.integers(0, 4, n).astype(np.uint32)
+    vals = np.arange(n, dtype=np.uint32)
+    k, v = gpu_sort(fh, gpu_ctx, keys, vals, 32)
+    exp = np.argsort(keys, kind="stable").astype(np.uint32)  # library stable sort
+    assert np.array_equal(v, exp)
+    assert np.array_equal(k, keys[exp])
+
+
+def test_sort_config1_full(fh, gpu_ctx):
+    """c1: 16,777,216 pairs of cell keys, full 32-bit stable sort, vs numpy's stable argsort."""
+    from forge_hip import workloads
+    keys, vals = workloads.config1()
+    print("c1 sort", flush=True)
+    k, v = gpu_sort(fh, gpu_ctx, keys, vals, 32)
+    exp = np.argsort(keys, kind="stable").astype(np.uint32)
+    assert np.array_equal(v, exp)
+    assert np.array_equal(k, keys[exp])
+    assert np.all(np.diff(k.astype(np.int64)) >= 0)
+
+
+def test_sort_errors(fh, gpu_ctx):
+    k = fh.u32_empty(16)
+    v = fh.u32_empty(16)
+    sorter = fh.RadixSorter(16, ctx=gpu_ctx)
+    with pytest.raises(fh.ForgeError) as e:
+        sorter.sort(k, v, 16, 0)
+    assert e.value.code == fh.FH_EINVAL
+    with pytest.raises(fh.ForgeError) as e:
+        sorter.sort(k, v, 16, 33)
+    assert e.value.code == fh.FH_EINVAL
+    small = fh.Context(max_n=8, max_cells=8)
+    with pytest.raises(fh.ForgeError) as e:
+        fh.RadixSorter(1 << 20, ctx=small).sort(k, v, 16, 8)
+    assert e.value.code == fh.FH_ERANGE
+    small.close()
+
+
+def test_find_cell_boundaries_kat(fh, gpu_ctx):
+    kat = KATS["find_cell_boundaries"]
+    ids = fh.from_u32(kat["sorted"])
+    s = fh.u32_empty(kat["num_cells"])
+    e = fh.u32_empty(kat["num_cells"])
+    torch.cuda.synchronize()
+    fh.find_cell_boundaries(ids, s, e, len(kat["sorted"]), kat["num_cells"], ctx=gpu_ctx)
+    assert fh.to_u32(s).tolist() == kat["start"]
+    assert fh.to_u32(e).tolist() == kat["end"]
+
+
+def test_find_cell_boundaries_vs_oracle(fh, gpu_ctx, oracle):
+    rng = np.random.default_rng(3)
+    C = 50_000
+    keys = np.sort(rng.integers(0, C + 100, 200_000).astype(np.uint32))  # some keys >= C
+    s = fh.u32_empty(C)
+    e = fh.u32_empty(C)
+    ids = fh.from_u32(keys)
+    torch.cuda.synchronize()
+    fh.find_cell_boundaries(ids, s, e, keys.size, C, ctx=gpu_ctx)
+    os_, oe = oracle.find_cell_boundaries(keys, C)
+    assert np.array_equal(fh.to_u32(s), os_) and np.array_equal(fh.to_u32(e), oe)

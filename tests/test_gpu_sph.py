@@ -1,0 +1,170 @@
+"""GPU parity of the SPH modules (C ABI fh_sph_fused, fh_sph_density, fh_gravity,
+fh_integrate, fh_box_collider) against the oracle, one Pipeline::step from identical inputs.
+Bar: densities and positions within rel 1e-4; accelerations
+("forces") within 1e-4 * sum_j |pair terms| per component, with the reference acceleration and
+that scale computed in fp64 (or_sph_force_f64)."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+REL = 1e-4
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def fields_from(fh, cfg, vel=None):
+    f = fh.FieldSet(cfg.n)
+    for nm, a in (("pos_x", cfg.x), ("pos_y", cfg.y), ("pos_z", cfg.z)):
+        f.f32_fields[nm] = dev(a)
+    for q, nm in enumerate(("vel_x", "vel_y", "vel_z")):
+        f.f32_fields[nm] = dev(vel[q]) if vel is not None else torch.zeros(cfg.n, device="cuda")
+    return f
+
+
+def sph_pipeline(fh, cfg, fuse=True, accel=None):
+    p = fh.Pipeline(fuse_epilogue=fuse)
+    m = fh.SphFusedModule(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                          cfg.rest_density, cfg.viscosity)
+    m.accel = accel
+    p.add(m)
+    p.add(fh.GravityModule(*cfg.gravity))
+    p.add(fh.IntegrateModule())
+    p.add(fh.BoxColliderModule(*cfg.box_min, *cfg.box_max, cfg.restitution))
+    return p
+
+
+def oracle_step(oracle, cfg, vel=None):
+    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity)
+    v = vel if vel is not None else [np.zeros(cfg.n, np.float32)] * 3
+    return prm, oracle.sph_step(prm, 7, cfg.gravity, cfg.box_min, cfg.box_max, cfg.restitution,
+                                cfg.x, cfg.y, cfg.z, v[0], v[1], v[2], cfg.dt)
+
+
+def rel_err(a, b):
+    return np.abs(a - b) / np.maximum(np.abs(b), 1e-30)
+
+
+def check_step(fh, oracle, cfg, vel=None, fuse=True):
+    accel = torch.zeros((3, cfg.n), dtype=torch.float32, device="cuda")
+    f = fields_from(fh, cfg, vel)
+    p = sph_pipeline(fh, cfg, fuse=fuse, accel=accel)
+    torch.cuda.synchronize()
+    p.step(f, cfg.dt)
+    got = {k: f.f32_fields[k].cpu().numpy() for k in f.f32_fields}
+    prm, (ox, oy, oz, ovx, ovy, ovz, orho, oacc) = oracle_step(oracle, cfg, vel)
+    # density: rel 1e-4
+    assert rel_err(got["density"], orho).max() <= REL
+    # accelerations: |a - a64| <= 1e-4 * sum|terms| (fp64 reference and scale)
+    v0 = vel if vel is not None else [np.zeros(cfg.n, np.float32)] * 3
+    ocs, osi, _ = oracle.hashgrid_build(cfg.x, cfg.y, cfg.z, cfg.cell_size, (0, 0, 0), cfg.dims)
+    a64, s64 = oracle.sph_force_f64(prm, cfg.x, cfg.y, cfg.z, *v0, orho, ocs, osi)
+    ga = accel.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(ga - a64) <= REL * s64 + 1e-30)
+    # positions and velocities after gravity / integrate / box: rel 1e-4
+    for k, o in (("pos_x", ox), ("pos_y", oy), ("pos_z", oz)):
+        assert rel_err(got[k], o).max() <= REL, k
+    for k, o, a in (("vel_x", ovx, 0), ("vel_y", ovy, 1), ("vel_z", ovz, 2)):
+        # velocity error bound: dt * force tolerance (the velocity is v0 + a dt + g dt)
+        tol = REL * np.abs(o) + cfg.dt * REL * s64[a] + 1e-30
+        assert np.all(np.abs(got[k] - o) <= tol), k
+    exact = {k: float(np.mean(got[k] == o)) for k, o in
+             (("density", orho), ("pos_x", ox), ("vel_y", ovy))}
+    return exact
+
+
+def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle):
+    from forge_hip import workloads
+    cfg = workloads.config0()
+    print("c0 step 1", flush=True)
+    exact = check_step(fh, oracle, cfg)
+    print("bit-exact fractions", exact)
+
+
+def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle):
+    """v != 0 exercises the viscosity term (zero at c0's initial state)."""
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=20_000, cols=24)
+    rng = np.random.default_rng(5)
+    vel = [rng.uniform(-0.5, 0.5, cfg.n).astype(np.float32) for _ in range(3)]
+    exact = check_step(fh, oracle, cfg, vel)
+    print("bit-exact fractions", exact)
+
+
+def test_fused_epilogue_equals_separate_modules(fh, gpu_ctx):
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=8192)
+    rng = np.random.default_rng(9)
+    vel = [rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
+    outs = []
+    for fuse in (True, False):
+        f = fields_from(fh, cfg, vel)
+        p = sph_pipeline(fh, cfg, fuse=fuse)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            p.step(f, cfg.dt)
+        outs.append({k: v.cpu().numpy() for k, v in f.f32_fields.items()})
+    for k in outs[0]:
+        assert np.array_equal(outs[0][k], outs[1][k]), k
+
+
+def test_graph_replay_matches_eager(fh, gpu_ctx):
+    """10 captured substeps replayed twice == 20 eager steps, bit for bit; each replay is checked
+    after eager work and synchronisation in between (graph nodes must not go stale)."""
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=16384, cols=32)
+    f_e = fields_from(fh, cfg)
+    f_g = fields_from(fh, cfg)
+    p_e = sph_pipeline(fh, cfg)
+    p_g = sph_pipeline(fh, cfg)
+    torch.cuda.synchronize()
+    p_g.capture(f_g, cfg.dt, 10)
+    for rep in range(2):
+        for _ in range(10):
+            p_e.step(f_e, cfg.dt)
+        p_g.replay(1)
+        f_g.context().sync()
+        for k in f_e.f32_fields:
+            assert torch.equal(f_e.f32_fields[k], f_g.f32_fields[k]), (rep, k)
+
+
+def test_density_module_matches_oracle(fh, gpu_ctx, oracle):
+    from forge_hip import workloads
+    cfg = workloads.config0()
+    f = fields_from(fh, cfg)
+    m = fh.SphDensityModule(cfg.h, cfg.cell_size, cfg.dims, cfg.mass)
+    torch.cuda.synchronize()
+    m.execute(f, cfg.dt)
+    f.context().sync()
+    ocs, osi, _ = oracle.hashgrid_build(cfg.x, cfg.y, cfg.z, cfg.cell_size, (0, 0, 0), cfg.dims)
+    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass)
+    orho = oracle.sph_density(prm, cfg.x, cfg.y, cfg.z, ocs, osi)
+    assert rel_err(f.f32_fields["density"].cpu().numpy(), orho).max() <= REL
+
+
+def test_standalone_modules_match_oracle(fh, gpu_ctx, oracle):
+    rng = np.random.default_rng(1)
+    n = 10_000
+    s = [rng.uniform(-0.2, 1.2, n).astype(np.float32) for _ in range(3)] + \
+        [rng.uniform(-3, 3, n).astype(np.float32) for _ in range(3)]
+    s[3][:7] = [np.nan, np.inf, -np.inf, np.nan, 1.0, 0.0, -0.0]  # integrate's non-finite guard
+    f = fh.FieldSet(n)
+    names = ["pos_x", "pos_y", "pos_z", "vel_x", "vel_y", "vel_z"]
+    for nm, a in zip(names, s):
+        f.f32_fields[nm] = dev(a)
+    g, dt = (0.5, -9.81, 0.25), 1e-3
+    mn, mx, e = (0.0, 0.05, 0.0), (1.0, 0.95, 0.9), 0.3
+    torch.cuda.synchronize()
+    fh.GravityModule(*g).execute(f, dt)
+    fh.IntegrateModule().execute(f, dt)
+    fh.BoxColliderModule(*mn, *mx, e).execute(f, dt)
+    f.context().sync()
+    v = oracle.gravity(s[3], s[4], s[5], g, dt)
+    st = oracle.integrate(s[0], s[1], s[2], v[0], v[1], v[2], dt)
+    st = oracle.box_collider(*st, mn, mx, e)
+    for nm, o in zip(names, st):
+        gpu = f.f32_fields[nm].cpu().numpy()
+        assert np.array_equal(gpu, o), nm
