@@ -1,0 +1,310 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X SPH / hash-grid hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+A "step" is one SPH substep of BASELINE.json configs[3]: 1,048,576 particles (dam-break lattice
+block, h = cell = 0.01, 100^3 cells), re-hash + stable radix sort + cell ranges + density +
+fused pressure/viscosity force + gravity / integrate / box, replayed from a captured HIP graph of
+`--graph-substeps` substeps.  Inputs are resident in HBM before the timed region.
+
+One JSON line on stdout:
+  value        particle-steps/s over the K timed substeps (wall clock between synchronisations)
+  roofline     the dominant kernel of the substep: algorithmic bytes per launch / its mean
+               launch time from HIP events on the context stream (G further substeps launched
+               eagerly with every kernel bracketed by events, right after the timed region)
+  cpu_baseline the single-threaded CPU restatement (oracle/) of the same substep on a bounded
+               sample, timed on this host
+  extra.sort_c1  the standalone 16,777,216-pair 32-bit sort: Gkeys/s and the
+               onesweep pass against the HBM roofline
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "forge-gpu_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+METRIC = "SPH particle-steps/s @1M; radix sort Gkeys/s; achieved HBM GB/s vs peak"
+KERNELS = ["begin", "hash", "sort", "gather", "scan", "plan", "density", "density_heavy",
+           "force", "force_heavy", "finalize"]
+# A "pass" groups the kernels of one stage of the substep; its duration per substep is the sum
+# of its kernels' launch durations (the heavy kernels of a pass process the items its light
+# kernel skips, so the pair moves the pass's bytes together).
+PASSES = {"hash": ["begin", "hash"], "sort": ["sort"], "gather": ["gather"], "scan": ["scan"],
+          "plan": ["plan"], "density": ["density", "density_heavy"],
+          "force": ["force", "force_heavy"], "finalize": ["finalize"]}
+
+
+def algorithmic_bytes(n: int, cells: int, passes: int) -> dict:
+    """Bytes each pass of one substep must move at minimum (neighbour re-reads counted once:
+    they are served from L2/LDS).  See DESIGN.md for the derivation."""
+    return {
+        "hash": 12 * n + 4 * n,                      # positions in, cell keys out
+        # pass 0 reads keys (values are the indices), middle passes read + write (key, value),
+        # the last pass writes (key, value)
+        "sort": 12 * n + 16 * n * max(passes - 2, 0) + 16 * n,
+        "gather": 8 * n + 24 * n + 32 * n,           # sorted (key, id), pos/vel in, float4 out
+        "scan": 8 * cells + 4 * (cells + 1),         # run tags in, cell_start out
+        "plan": 16 * n,                              # sorted positions
+        "density": 16 * n + 12 * n + 4 * (cells + 1),           # positions in, 3 slab partials
+        "force": 32 * n + 12 * n + 36 * n + 4 * (cells + 1),    # pos/vel/density in, 9 partials
+        "finalize": 32 * n + 12 * n + 36 * n + 4 * n + 28 * n,  # + ids; pos, vel, density out
+    }
+
+
+def cpu_info() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def build_fields(fh, cfg, torch):
+    f = fh.FieldSet(cfg.n)
+    for nm, a in (("pos_x", cfg.x), ("pos_y", cfg.y), ("pos_z", cfg.z)):
+        f.f32_fields[nm] = torch.from_numpy(a).cuda()
+    for nm in ("vel_x", "vel_y", "vel_z"):
+        f.f32_fields[nm] = torch.zeros(cfg.n, dtype=torch.float32, device="cuda")
+    f.add_f32_zeros("density", cfg.n)
+    return f
+
+
+def build_pipe(fh, cfg):
+    p = fh.Pipeline()
+    p.add(fh.SphFusedModule(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity))
+    p.add(fh.GravityModule(*cfg.gravity))
+    p.add(fh.IntegrateModule())
+    p.add(fh.BoxColliderModule(*cfg.box_min, *cfg.box_max, cfg.restitution))
+    return p
+
+
+def bench_sph(args, fh, torch, log):
+    from forge_hip import workloads
+
+    cfg = workloads.config3()
+    C = cfg.num_cells
+    passes = (max(1, (C - 1).bit_length()) + 7) // 8
+    G = args.graph_substeps
+    K = max(G, (args.steps // G) * G)
+    W = (args.warmup // G) * G
+    fields = build_fields(fh, cfg, torch)
+    pipe = build_pipe(fh, cfg)
+    ctx = fields.context(C)
+    torch.cuda.synchronize()
+    pipe.capture(fields, cfg.dt, G)  # substeps 1..W are the warm-up replays, then K are timed
+    log(f"captured {G} substeps; warmup {W}")
+    if W:
+        pipe.replay(W // G)
+    ctx.sync()
+    torch.cuda.synchronize()
+    ctx.event_record(0)
+    t0 = time.perf_counter()
+    pipe.replay(K // G)
+    ctx.event_record(1)
+    ctx.sync()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    ev_ms = ctx.event_elapsed_ms(0, 1)
+    log(f"timed {K} substeps: wall {wall * 1e3:.2f} ms, events {ev_ms:.2f} ms")
+
+    # Per-kernel durations: G more substeps launched eagerly on the same stream with every
+    # kernel bracketed by HIP events (events recorded by graph nodes cannot be timed on HIP).
+    for k in KERNELS:
+        ctx.time_kernel(k, (passes if k == "sort" else 1) * G)
+    for _ in range(G):
+        pipe.step_async(fields, cfg.dt)
+    ctx.sync()
+    kern = {}
+    for k in KERNELS:
+        t = ctx.kernel_times_ms(k)
+        kern[k] = {"launches": len(t), "mean_us": 1e3 * sum(t) / max(len(t), 1),
+                   "per_substep_us": 1e3 * sum(t) / G}
+        ctx.time_kernel(k, 0)
+    byts = algorithmic_bytes(cfg.n, C, passes)
+    pas = {}
+    for p, ks in PASSES.items():
+        us = sum(kern[k]["per_substep_us"] for k in ks)
+        pas[p] = {"kernels": ks, "per_substep_us": us, "alg_bytes": byts[p],
+                  "alg_GBs": byts[p] / (us * 1e-6) / 1e9 if us > 0 else None}
+    dom = max(pas, key=lambda p: pas[p]["per_substep_us"])
+    achieved = pas[dom]["alg_GBs"]
+    total_alg = sum(byts.values())
+    return dict(cfg=cfg, C=C, passes=passes, G=G, K=K, W=W, wall=wall, ev_ms=ev_ms, kern=kern,
+                pas=pas, dom=dom, achieved=achieved, total_alg=total_alg, digest=cfg.digest())
+
+
+def bench_sort(args, fh, torch, log):
+    from forge_hip import workloads
+
+    keys, vals = workloads.config1()
+    n = keys.size
+    ctx = fh.Context(max_n=n, max_cells=1)
+    k0, v0 = fh.from_u32(keys), fh.from_u32(vals)
+    k, v = k0.clone(), v0.clone()
+    sorter = fh.RadixSorter(n, ctx=ctx)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        k.copy_(k0)
+        v.copy_(v0)
+        sorter.sort(k, v, n, 32)
+    times = []
+    reps = args.sort_reps
+    ctx.time_kernel("sort", 4 * reps)
+    ctx.time_kernel("hist", reps)
+    for _ in range(reps):
+        k.copy_(k0)
+        v.copy_(v0)
+        ctx.torch_stream().wait_stream(torch.cuda.current_stream())
+        ctx.event_record(2)
+        sorter.sort(k, v, n, 32, sync=False)
+        ctx.event_record(3)
+        times.append(ctx.event_elapsed_ms(2, 3))
+    ctx.sync()
+    passes_ms = ctx.kernel_times_ms("sort")
+    hist_ms = ctx.kernel_times_ms("hist")
+    ctx.close()
+    t = sorted(times)[len(times) // 2]
+    pass_us = 1e3 * sum(passes_ms) / max(len(passes_ms), 1)
+    pass_bytes = 16 * n
+    out = {
+        "workload": "c1: 16,777,216 (u32 cell key, u32 index) pairs, 32-bit stable LSD sort",
+        "median_ms": t, "gkeys_per_s": n / (t * 1e-3) / 1e9,
+        "alg_bytes": 68 * n, "alg_GBs": 68 * n / (t * 1e-3) / 1e9,
+        "frac_of_hbm_peak": 68 * n / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "onesweep_pass_mean_us": pass_us,
+        "onesweep_pass_GBs": pass_bytes / (pass_us * 1e-6) / 1e9,
+        "hist_mean_us": 1e3 * sum(hist_ms) / max(len(hist_ms), 1),
+        "reps": reps,
+    }
+    log(f"sort c1: median {t:.3f} ms, {out['gkeys_per_s']:.2f} Gkeys/s")
+    return out
+
+
+def cpu_baseline(args, log):
+    import numpy as np
+
+    import oracle.oracle as O
+    from forge_hip import workloads
+
+    cfg = workloads.config3()
+    prm = O.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                       cfg.rest_density, cfg.viscosity)
+    z = np.zeros(cfg.n, np.float32)
+    state = [cfg.x, cfg.y, cfg.z, z, z, z]
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        r = O.sph_step(prm, 7, cfg.gravity, cfg.box_min, cfg.box_max, cfg.restitution,
+                       *state, cfg.dt)
+        state = list(r[:6])
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or steps >= 50:
+            break
+    log(f"cpu baseline: {steps} substeps in {el:.2f} s")
+    return {"value": cfg.n * steps / el, "unit": "particle-steps/s", "cores": 1, "kind": "port",
+            "sample": f"{steps} consecutive substeps of configs[3] (1,048,576 particles) through "
+                      f"oracle/oracle.c or_sph_step (single-threaded C, -O2 -ffp-contract=off)",
+            "seconds": el, "cpu": cpu_info(), "host_cpus": os.cpu_count()}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=900)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--graph-substeps", type=int, default=10)
+    ap.add_argument("--sort-reps", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-sort", action="store_true", help="skip the c1 sort line")
+    ap.add_argument("--quiet", action="store_true")
+    args = ap.parse_args(argv)
+
+    def log(msg):
+        if not args.quiet:
+            print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (every GPU box "
+              "here has one GPU); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import forge_hip as fh
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    fh.load()
+    log(f"device {torch.cuda.get_device_name(0)}")
+    s = bench_sph(args, fh, torch, log)
+    sort = None if args.no_sort else bench_sort(args, fh, torch, log)
+    cpu = None if args.no_cpu else cpu_baseline(args, log)
+
+    cfg, K = s["cfg"], s["K"]
+    ms_per_step = s["wall"] * 1e3 / K
+    value = cfg.n * K / s["wall"]
+    dom = s["dom"]
+    kern = s["kern"]
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "particle-steps/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": s["W"],
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "configs[3]: SPH dam-break substep, 1,048,576 particles, h = cell = 0.01, "
+                        "100^3 cells, re-hash + sort every substep, hipGraph of "
+                        f"{s['G']} substeps",
+            "particles": cfg.n, "cells": s["C"], "sort_passes": s["passes"],
+            "graph_substeps": s["G"], "input_sha256": s["digest"], "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": dom + " pass (" + " + ".join(s["pas"][dom]["kernels"]) + ")",
+            "achieved": s["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": s["achieved"] / HBM_PEAK_GBS, "traffic": None,
+            "alg_bytes_per_launch": s["pas"][dom]["alg_bytes"],
+            "mean_launch_us": s["pas"][dom]["per_substep_us"],
+        },
+        "cpu_baseline": cpu,
+        "extra": {
+            "substep_us_events": s["ev_ms"] * 1e3 / K,
+            "substep_alg_bytes": s["total_alg"],
+            "substep_alg_GBs": s["total_alg"] / (ms_per_step * 1e-3) / 1e9,
+            "kernels": {k: {q: (round(v, 3) if isinstance(v, float) else v) for q, v in kern[k].items()}
+                        for k in KERNELS},
+            "passes": {p: {q: (round(v, 3) if isinstance(v, float) else v) for q, v in d.items()}
+                       for p, d in s["pas"].items()},
+            "sort_c1": sort,
+        },
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -86,15 +86,19 @@ hipError_t alloc(T** p, size_t count, size_t* total) {
     return hipMalloc((void**)p, bytes);
 }
 
-// Rebuild of the SPH grid from the positions: hash + digit histograms + cell counts, CSR
-// cell_start by scan, then the stable sort giving sidx (ascending id within a cell).
+// Rebuild of the SPH grid from the positions: hash + digit histograms, the stable sort giving
+// skeys / sidx (ascending id within a cell), the gather into sorted float4 order (which also
+// tags the key runs), and the CSR cell_start scan.
 hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
-                       const float* py, const float* pz, uint32_t n) {
+                       const float* py, const float* pz, const float* vx, const float* vy,
+                       const float* vz, uint32_t n, bool with_vel) {
     const uint32_t bits = bits_for_cells(cells);
     hipError_t e = launch_begin(c);
-    if (e == hipSuccess) e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr, true);
-    if (e == hipSuccess) e = launch_scan_cells(c, cells, c->cell_start);
-    if (e == hipSuccess && n > 0) e = launch_sort_passes(c, c->kb, nullptr, nullptr, c->sidx, n, bits);
+    if (e == hipSuccess) e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr);
+    if (e == hipSuccess && n > 0)
+        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits);
+    if (e == hipSuccess) e = launch_gather(c, px, py, pz, vx, vy, vz, n, with_vel);
+    if (e == hipSuccess) e = launch_scan_starts(c, cells, n, c->cell_start);
     return e;
 }
 
@@ -136,13 +140,18 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->vb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)kMaxPasses * c->max_sort_tiles * 256u, &tot);
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
-    if (e == hipSuccess) e = alloc(&c->cell_count, max_cells, &tot);
+    if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);
     if (e == hipSuccess) e = alloc(&c->scan_lb, c->max_scan_tiles, &tot);
+    if (e == hipSuccess) e = alloc(&c->skeys, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sidx, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->spos, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->svel, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->srho, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->dpart, 3 * (size_t)max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->fpart, 9 * (size_t)max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->heavy, 3 * (size_t)ceil_div(max_n, 64u), &tot);
+    if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_error, sizeof(uint32_t), hipHostMallocDefault);
     if (e == hipSuccess) {
         if (stream) {
@@ -152,12 +161,12 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
             c->own_stream = e == hipSuccess;
         }
     }
-    // One-time clears (outside any capture): look-back words start "not ready", cell counts
-    // start at zero and are kept at zero by every scan.
+    // One-time clears (outside any capture): look-back words and run tags start untagged
+    // (epoch 0 is never current).
     if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)kMaxPasses * c->max_sort_tiles * 256u * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->scan_lb, 0, (size_t)c->max_scan_tiles * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(c->cell_count, 0, (size_t)max_cells * 4u, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->run_tag, 0, (size_t)max_cells * 8u, c->stream);
     for (int q = 0; q < kEvents && e == hipSuccess; q++) e = hipEventCreate(&c->ev[q]);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     c->scratch_bytes = tot;
@@ -178,8 +187,17 @@ int fh_destroy(fh_ctx* c) {
     if (c->graph) (void)hipGraphDestroy(c->graph);
     for (int q = 0; q < kEvents; q++)
         if (c->ev[q]) (void)hipEventDestroy(c->ev[q]);
-    void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->cell_count,
-                    c->cell_start, c->scan_lb, c->sidx, c->spos, c->svel, c->srho};
+    for (int k = 0; k < KID_COUNT; k++) {
+        Timer& t = c->timers[k];
+        if (t.ev) {
+            for (uint32_t q = 0; q < 2 * t.max; q++)
+                if (t.ev[q]) (void)hipEventDestroy(t.ev[q]);
+            delete[] t.ev;
+        }
+    }
+    void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
+                    c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
+                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);
@@ -219,7 +237,7 @@ int fh_hash_cells(fh_ctx* c, const float* x, const float* y, const float* z, uin
     uint32_t cells;
     if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hash_cells"))) return rc;
     if (n == 0) return FH_OK;
-    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, 0, keys, vals, false));
+    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, 0, keys, vals));
     return FH_OK;
 }
 
@@ -270,10 +288,12 @@ int fh_hashgrid_build(fh_ctx* c, const float* x, const float* y, const float* z,
     if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hashgrid_build"))) return rc;
     const uint32_t bits = bits_for_cells(cells);
     FH_CHECK_HIP(launch_begin(c));
-    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr, true));
-    FH_CHECK_HIP(launch_scan_cells(c, cells, cell_start));
-    if (n > 0)
-        FH_CHECK_HIP(launch_sort_passes(c, cell_indices, nullptr, nullptr, sorted_indices, n, bits));
+    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr));
+    if (n > 0) {
+        FH_CHECK_HIP(launch_sort_passes(c, cell_indices, nullptr, c->skeys, sorted_indices, n, bits));
+        FH_CHECK_HIP(launch_runs(c, c->skeys, n));
+    }
+    FH_CHECK_HIP(launch_scan_starts(c, cells, n, cell_start));
     return FH_OK;
 }
 
@@ -327,12 +347,18 @@ int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const f
     GridDesc g;
     uint32_t cells;
     if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_density"))) return rc;
-    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, n));
+    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, nullptr, nullptr, nullptr, n, false));
     if (n == 0) return FH_OK;
-    FH_CHECK_HIP(launch_gather(c, px, py, pz, nullptr, nullptr, nullptr, n, false));
     SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
               prm->rest_density, prm->viscosity_coefficient, 0.0f, n};
-    FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
+    if (c->sph_exact) {
+        FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
+    } else {
+        FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_finalize(c, a, nullptr, true, nullptr, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, density, nullptr));
+    }
     return FH_OK;
 }
 
@@ -349,14 +375,33 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
     GridDesc g;
     uint32_t cells;
     if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_fused"))) return rc;
-    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, n));
+    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, vx, vy, vz, n, true));
     if (n == 0) return FH_OK;
-    FH_CHECK_HIP(launch_gather(c, px, py, pz, vx, vy, vz, n, true));
     SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
               prm->rest_density, prm->viscosity_coefficient, dt, n};
-    FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
-    FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
+    if (c->sph_exact) {
+        FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
+        FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
+    } else {
+        FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_force_fast(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density, accel));
+    }
     return FH_OK;
+}
+
+int fh_set_option(fh_ctx* c, int option, int value) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (c->capturing) return fail(FH_ESTATE, "fh_set_option: stream is being captured");
+    switch (option) {
+        case FH_OPT_SPH_EXACT:
+            c->sph_exact = value != 0;
+            return FH_OK;
+        default:
+            return fail(FH_EINVAL, "fh_set_option: unknown option %d", option);
+    }
 }
 
 int fh_gravity(fh_ctx* c, float* vx, float* vy, float* vz, uint32_t n, float gx, float gy,
@@ -433,6 +478,66 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
     if (rc) return rc;
     if (slot >= (uint32_t)kEvents) return fail(FH_EINVAL, "fh_event_record: slot %u", slot);
     FH_CHECK_HIP(hipEventRecord(c->ev[slot], c->stream));
+    return FH_OK;
+}
+
+static const char* const kKernelNames[KID_COUNT] = {"begin", "hist", "hash", "scan", "sort",
+                                                    "gather", "density", "force", "query",
+                                                    "finalize", "runs", "plan",
+                                                    "density_heavy", "force_heavy"};
+
+static int kernel_id(const char* name) {
+    if (!name) return -1;
+    for (int k = 0; k < KID_COUNT; k++)
+        if (strcmp(name, kKernelNames[k]) == 0) return k;
+    return -1;
+}
+
+static void free_timer(Timer& t) {
+    if (t.ev) {
+        for (uint32_t q = 0; q < 2 * t.max; q++)
+            if (t.ev[q]) (void)hipEventDestroy(t.ev[q]);
+        delete[] t.ev;
+    }
+    t.ev = nullptr;
+    t.max = t.used = 0;
+}
+
+int fh_time_kernel(fh_ctx* c, const char* name, uint32_t max_launches) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    int k = kernel_id(name);
+    if (k < 0) return fail(FH_EINVAL, "fh_time_kernel: unknown kernel '%s'", name ? name : "");
+    if (c->capturing) return fail(FH_ESTATE, "fh_time_kernel: stream is being captured");
+    if (max_launches > 4096) return fail(FH_EINVAL, "fh_time_kernel: at most 4096 launches");
+    FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+    free_timer(c->timers[k]);
+    if (max_launches == 0) return FH_OK;
+    Timer& t = c->timers[k];
+    t.ev = new hipEvent_t[2 * max_launches]();
+    t.max = max_launches;
+    for (uint32_t q = 0; q < 2 * max_launches; q++) {
+        hipError_t e = hipEventCreate(&t.ev[q]);
+        if (e != hipSuccess) {
+            free_timer(t);
+            return hip_fail(e, "hipEventCreate");
+        }
+    }
+    return FH_OK;
+}
+
+int fh_kernel_times(fh_ctx* c, const char* name, float* ms, uint32_t cap, uint32_t* count) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    int k = kernel_id(name);
+    if (k < 0 || !count || (cap && !ms)) return fail(FH_EINVAL, "fh_kernel_times: bad arguments");
+    if (c->capturing) return fail(FH_ESTATE, "fh_kernel_times: stream is being captured");
+    Timer& t = c->timers[k];
+    uint32_t m = t.used < cap ? t.used : cap;
+    if (t.used) FH_CHECK_HIP(hipEventSynchronize(t.ev[2 * t.used - 1]));
+    for (uint32_t q = 0; q < m; q++)
+        FH_CHECK_HIP(hipEventElapsedTime(&ms[q], t.ev[2 * q], t.ev[2 * q + 1]));
+    *count = m;
     return FH_OK;
 }
 

@@ -1,9 +1,10 @@
 // fh_grid.hip -- cell ranges and the 3x3x3 neighbour query for gfx950.
 //
-//   k_scan_cells   CSR cell_start[0..C] = exclusive prefix sum of the per-cell counts
-//                  (hashgrid.rs:95-106), single pass with a decoupled look-back over
-//                  dynamically numbered 4096-cell tiles; it also re-zeroes the counts so the
-//                  next build needs no memset (graph-safe).
+//   k_runs +       CSR cell_start[0..C] (hashgrid.rs:95-106) from the sorted keys: the first
+//   k_scan_starts  index of each key run is tagged at its cell, then a single-pass reverse
+//                  minimum scan with a decoupled look-back fills every cell with the first
+//                  sorted index at or after it (no atomics per particle, no clearing: the tags
+//                  carry the build's epoch, so the build is graph-safe).
 //   k_fill_u32 +   find_cell_boundaries (radix_sort.rs:229-317): sentinel fill, then one
 //   k_boundaries   thread per sorted key marks the first / last index of its run.
 //   k_nbr_query    HashGrid::query_neighbors (hashgrid.rs:145-193) for every point of a built
@@ -14,66 +15,94 @@
 
 namespace fh {
 
-__global__ __launch_bounds__(kScanThreads) void k_scan_cells(uint32_t* __restrict__ counts,
-                                                             uint32_t* __restrict__ cell_start,
-                                                             uint64_t* __restrict__ lookback,
-                                                             Control* ctl, uint32_t C) {
+// Run marking: the first sorted index of every run of equal keys is stored, tagged with the
+// current epoch, at run_tag[key] (untagged cells hold no particle; nothing needs clearing).
+__global__ void k_runs(const uint32_t* __restrict__ keys, uint32_t n,
+                       uint64_t* __restrict__ run_tag, const Control* __restrict__ ctl) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const uint32_t k = keys[s];
+    if (s == 0 || keys[s - 1] != k) run_tag[k] = ((uint64_t)ctl->epoch << 32) | s;
+}
+
+hipError_t launch_runs(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n) {
+    if (n == 0) return hipSuccess;
+    tbeg(c, KID_RUNS);
+    k_runs<<<ceil_div(n, 256u), 256, 0, c->stream>>>(sorted_keys, n, c->run_tag, c->ctl);
+    tend(c, KID_RUNS);
+    return hipGetLastError();
+}
+
+// Suffix minimum (inclusive) of one value per lane over a wavefront.
+__device__ __forceinline__ uint32_t wave_suffix_min(uint32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        uint32_t t = __shfl_down(v, off, kWave);
+        if (lane + off < kWave) v = min(v, t);
+    }
+    return v;
+}
+
+// cell_start[c] = min over cells c' >= c of (first sorted index of c' if c' holds particles),
+// i.e. the first sorted index with key >= c; n where none.  Tiles of 4096 cells are numbered
+// dynamically from the END of the grid, and a decoupled look-back carries the minimum over all
+// later cells; each lane owns 16 consecutive cells.  This equals the exclusive prefix sum of
+// the per-cell counts of hashgrid.rs:102-106.
+__global__ __launch_bounds__(kScanThreads) void k_scan_starts(const uint64_t* __restrict__ run_tag,
+                                                              uint32_t* __restrict__ cell_start,
+                                                              uint64_t* __restrict__ lookback,
+                                                              Control* ctl, uint32_t C, uint32_t n) {
     __shared__ uint32_t s_tile;
-    __shared__ uint32_t s_scan[4];
+    __shared__ uint32_t s_wave[4];
     __shared__ uint32_t s_prefix;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) s_tile = atomicAdd(&ctl->scan_ctr, 1u);
     __syncthreads();
     const uint32_t tile = s_tile;
     const uint32_t epoch = ctl->epoch;
-    const uint32_t first = tile * (uint32_t)kScanTile + (uint32_t)tid * kScanItems;
+    const uint32_t hi = C - tile * (uint32_t)kScanTile;  // cells [hi - 4096, hi), clipped at 0
+    const int64_t first = (int64_t)hi - kScanTile + (int64_t)tid * kScanItems;
 
-    // Each thread owns kScanItems consecutive cells.
     uint32_t v[kScanItems];
-    if (first + kScanItems <= C) {
-        const uint4* p4 = reinterpret_cast<const uint4*>(counts + first);
-#pragma unroll
-        for (int q = 0; q < kScanItems / 4; q++) {
-            uint4 t = p4[q];
-            v[4 * q] = t.x;
-            v[4 * q + 1] = t.y;
-            v[4 * q + 2] = t.z;
-            v[4 * q + 3] = t.w;
-        }
-        uint4* w4 = reinterpret_cast<uint4*>(counts + first);
-#pragma unroll
-        for (int q = 0; q < kScanItems / 4; q++) w4[q] = make_uint4(0u, 0u, 0u, 0u);
-    } else {
-#pragma unroll
-        for (int q = 0; q < kScanItems; q++) {
-            uint32_t c = first + q;
-            v[q] = c < C ? counts[c] : 0u;
-            if (c < C) counts[c] = 0u;
-        }
-    }
-    uint32_t sum = 0;
 #pragma unroll
     for (int q = 0; q < kScanItems; q++) {
-        uint32_t t = v[q];
-        v[q] = sum;  // thread-local exclusive prefix
-        sum += t;
+        const int64_t c = first + q;
+        uint32_t x = 0xFFFFFFFFu;
+        if (c >= 0) {
+            const uint64_t t = run_tag[c];
+            if ((uint32_t)(t >> 32) == epoch) x = (uint32_t)t;
+        }
+        v[q] = x;
     }
-    uint32_t total;
-    uint32_t before = block256_exclusive_scan(sum, s_scan, &total);
+    // lane-local suffix minimum
+    uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = kScanItems - 1; q >= 0; q--) {
+        m = min(m, v[q]);
+        v[q] = m;
+    }
+    // minimum over the later lanes of the workgroup
+    const uint32_t inc = wave_suffix_min(m, lane);
+    uint32_t later = __shfl_down(inc, 1, kWave);
+    if (lane == 63) later = 0xFFFFFFFFu;
+    if (lane == 0) s_wave[wave] = inc;
+    __syncthreads();
+    for (int w = wave + 1; w < 4; w++) later = min(later, s_wave[w]);
+    const uint32_t total = min(min(s_wave[0], s_wave[1]), min(s_wave[2], s_wave[3]));
 
     if (tid == 0) {
         uint64_t* my = lookback + tile;
-        uint32_t prefix = 0;
+        uint32_t prefix = 0xFFFFFFFFu;
         if (tile == 0) {
             lb_store(my, lb_word(kLbInclusive, epoch, total));
         } else {
             lb_store(my, lb_word(kLbAggregate, epoch, total));
             uint32_t t = tile - 1u, spins = 0;
             for (;;) {
-                uint64_t w = lb_load(lookback + t);
-                uint64_t st = w & (3ull << 62);
+                const uint64_t w = lb_load(lookback + t);
+                const uint64_t st = w & (3ull << 62);
                 if (st != 0 && ((uint32_t)(w >> 32) & kEpochMask) == epoch) {
-                    prefix += (uint32_t)w;
+                    prefix = min(prefix, (uint32_t)w);
                     if (st == kLbInclusive) break;
                     if (t == 0) {
                         atomicOr(&ctl->error, 2u);
@@ -88,24 +117,29 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_cells(uint32_t* __restric
                     __builtin_amdgcn_s_sleep(1);
                 }
             }
-            lb_store(my, lb_word(kLbInclusive, epoch, prefix + total));
+            lb_store(my, lb_word(kLbInclusive, epoch, min(prefix, total)));
         }
         s_prefix = prefix;
     }
     __syncthreads();
-    const uint32_t base = s_prefix + before;
+    const uint32_t after = min(later, s_prefix);
 #pragma unroll
     for (int q = 0; q < kScanItems; q++) {
-        uint32_t c = first + q;
-        if (c < C) cell_start[c] = base + v[q];
-        if (c + 1 == C) cell_start[C] = base + sum;  // = number of hashed particles
+        const int64_t c = first + q;
+        if (c >= 0) {
+            const uint32_t x = min(v[q], after);
+            cell_start[c] = x == 0xFFFFFFFFu ? n : x;
+        }
     }
+    if (tile == 0 && tid == 0) cell_start[C] = n;
 }
 
-hipError_t launch_scan_cells(fh_ctx* c, uint32_t num_cells, uint32_t* cell_start) {
-    uint32_t tiles = ceil_div(num_cells, (uint32_t)kScanTile);
-    k_scan_cells<<<tiles, kScanThreads, 0, c->stream>>>(c->cell_count, cell_start, c->scan_lb,
-                                                         c->ctl, num_cells);
+hipError_t launch_scan_starts(fh_ctx* c, uint32_t num_cells, uint32_t n, uint32_t* cell_start) {
+    const uint32_t tiles = ceil_div(num_cells, (uint32_t)kScanTile);
+    tbeg(c, KID_SCAN);
+    k_scan_starts<<<tiles, kScanThreads, 0, c->stream>>>(c->run_tag, cell_start, c->scan_lb,
+                                                         c->ctl, num_cells, n);
+    tend(c, KID_SCAN);
     return hipGetLastError();
 }
 
@@ -293,9 +327,11 @@ hipError_t launch_neighbor_query(fh_ctx* c, const float* x, const float* y, cons
     float h2 = h * h;
     float h9 = h2 * h2 * h2 * h2 * h;
     float coeff = 315.0f / (64.0f * 3.14159265f * h9);
+    tbeg(c, KID_NBR);
     k_nbr_query<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->spos, sorted_indices, n, g,
                                                           cell_start, radius * radius, coeff,
                                                           counts, wsum);
+    tend(c, KID_NBR);
     return hipGetLastError();
 }
 

@@ -36,7 +36,8 @@ struct Control {
     uint32_t tile_ctr[kMaxPasses];      // dynamic tile ids of the sort passes
     uint32_t scan_ctr;                  // dynamic tile id of the cell scan
     uint32_t error;                     // nonzero: a look-back spin limit was hit
-    uint32_t pad[9];
+    uint32_t heavy_count;               // entries in the heavy SPH work list of this substep
+    uint32_t pad[8];
     uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
 };
 
@@ -44,6 +45,18 @@ struct GridDesc {
     float cs;
     float ox, oy, oz;
     uint32_t nx, ny, nz;
+};
+
+// Kernels that can be timed with fh_time_kernel (names in kKernelNames).
+enum KernelId { KID_BEGIN, KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
+                KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_DHEAVY, KID_FHEAVY,
+                KID_COUNT };
+
+// Event pairs bracketing the first `max` launches of one kernel after it was armed; when the
+// launches are captured, every replay of the graph re-records the same events.
+struct Timer {
+    uint32_t max, used;
+    hipEvent_t* ev;  // 2 * max events
 };
 
 }  // namespace fh
@@ -62,20 +75,27 @@ struct fh_ctx {
     uint64_t* sort_lb;   // [kMaxPasses][max_sort_tiles][256]
     fh::Control* ctl;    // device control block
     // grid scratch
-    uint32_t* cell_count;  // [max_cells], kept all-zero between calls
+    uint64_t* run_tag;     // [max_cells] epoch << 32 | first sorted index of the cell's run
     uint32_t* cell_start;  // [max_cells + 1]
     uint64_t* scan_lb;     // [max_scan_tiles]
+    uint32_t* skeys;       // [max_n] sorted keys (cells)
     uint32_t* sidx;        // [max_n] sorted particle ids
     // SPH scratch (sorted order)
     float4* spos;        // [max_n] x, y, z, 0
     float4* svel;        // [max_n] vx, vy, vz, 0
-    float* srho;         // [max_n]
+    float* srho;         // [max_n] density (exact kernels)
+    float* dpart;        // [3][max_n] per-slab density partials (fast kernels)
+    float* fpart;        // [3][3][max_n] per-slab acceleration partials (fast kernels)
+    uint32_t* heavy;     // [3 * ceil(max_n / 64)] heavy (64-particle tile, slab) work items
+    uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1 if the item is on the heavy list
+    bool sph_exact;      // FH_OPT_SPH_EXACT
     uint32_t* h_error;   // pinned host word for the device error flag
     size_t scratch_bytes;
     hipGraph_t graph;
     hipGraphExec_t exec;
     bool capturing;
     hipEvent_t ev[fh::kEvents];
+    fh::Timer timers[fh::KID_COUNT];
 };
 
 namespace fh {
@@ -138,24 +158,40 @@ __device__ __forceinline__ uint32_t block256_exclusive_scan(uint32_t v, uint32_t
     return before + inc - v;
 }
 
+// Bracket a launch with the armed timer's events (no-op when the kernel is not armed).
+inline void tbeg(fh_ctx* c, KernelId k) {
+    Timer& t = c->timers[k];
+    if (t.used < t.max) (void)hipEventRecord(t.ev[2 * t.used], c->stream);
+}
+inline void tend(fh_ctx* c, KernelId k) {
+    Timer& t = c->timers[k];
+    if (t.used < t.max) {
+        (void)hipEventRecord(t.ev[2 * t.used + 1], c->stream);
+        t.used++;
+    }
+}
+
 // ---- launchers (host side, enqueue on ctx->stream; return hipError_t) ------------------------
 
 // Sort: bump epoch, clear histograms and tile counters.
 hipError_t launch_begin(fh_ctx* c);
 // Histogram of all digit passes of keys (from a key array).
 hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits);
-// Hash particle positions: keys_out[i] = cell (if non-null), digit histograms of all passes,
-// cell counts (if count_cells).
+// Hash particle positions: keys_out[i] = cell, vals_out[i] = i (if non-null) and the digit
+// histograms of all passes of a num_bits sort (none for num_bits = 0).
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
-                            uint32_t* keys_out, uint32_t* vals_out, bool count_cells);
+                            uint32_t* keys_out, uint32_t* vals_out);
 // Run the passes of a sort whose histograms are ready.  Pass 0 reads (k0, v0) (v0 == nullptr:
 // values are the indices 0..n-1); the last pass writes (kfin, vfin) (kfin may be null).
 // Intermediate passes ping-pong through the context's scratch.
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits);
-// Exclusive scan of c->cell_count[0..C) into cell_start[0..C] and reset of cell_count.
-hipError_t launch_scan_cells(fh_ctx* c, uint32_t num_cells, uint32_t* cell_start);
+// Mark the first index of every run of equal sorted keys in c->run_tag (epoch-tagged).
+hipError_t launch_runs(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n);
+// CSR cell_start[0..C] from the run tags: cell_start[c] = first sorted index with key >= c
+// (a reverse minimum scan over the cells), cell_start[C] = n.
+hipError_t launch_scan_starts(fh_ctx* c, uint32_t num_cells, uint32_t n, uint32_t* cell_start);
 hipError_t launch_fill_u32(fh_ctx* c, uint32_t* p, uint32_t value, uint32_t n);
 hipError_t launch_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
                              uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end);
@@ -174,9 +210,16 @@ struct SphArgs {
     float h, mass, k, rho0, mu, dt;
     uint32_t n;
 };
+// Gather positions (and velocities) into sorted float4 order and mark the key runs.
 hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const float* pz,
                          const float* vx, const float* vy, const float* vz, uint32_t n,
                          bool with_vel);
+hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
+hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
+hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
+hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
+                           bool density_only, float* px, float* py, float* pz, float* vx,
+                           float* vy, float* vz, float* density, float* accel);
 hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start,
                           float* density_out);
 hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,

@@ -27,11 +27,14 @@ __global__ void k_begin(Control* ctl) {
         ctl->epoch = e ? e : 1u;
         for (int p = 0; p < kMaxPasses; p++) ctl->tile_ctr[p] = 0u;
         ctl->scan_ctr = 0u;
+        ctl->heavy_count = 0u;
     }
 }
 
 hipError_t launch_begin(fh_ctx* c) {
+    tbeg(c, KID_BEGIN);
     k_begin<<<1, 256, 0, c->stream>>>(c->ctl);
+    tend(c, KID_BEGIN);
     return hipGetLastError();
 }
 
@@ -90,7 +93,9 @@ hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_
     uint32_t blocks = ceil_div(n, 256u * 16u);
     if (blocks < 1) blocks = 1;
     if (blocks > 2048) blocks = 2048;
+    tbeg(c, KID_HIST);
     k_hist_keys<<<blocks, 256, 0, c->stream>>>(keys, n, num_bits, c->ctl);
+    tend(c, KID_HIST);
     return hipGetLastError();
 }
 
@@ -100,7 +105,6 @@ __global__ __launch_bounds__(256) void k_hash_hist(const float* __restrict__ x,
                                                    uint32_t n, GridDesc g, uint32_t num_bits,
                                                    uint32_t* __restrict__ keys_out,
                                                    uint32_t* __restrict__ vals_out,
-                                                   uint32_t* __restrict__ cell_count,
                                                    Control* ctl) {
     __shared__ uint32_t sh[4][kMaxPasses][256];
     const int wave = threadIdx.x >> 6;
@@ -117,7 +121,6 @@ __global__ __launch_bounds__(256) void k_hash_hist(const float* __restrict__ x,
             k = cell_of(x[o], y[o], z[o], g);
             if (keys_out) keys_out[i] = k;
             if (vals_out) vals_out[i] = i;
-            if (cell_count) atomicAdd(&cell_count[k], 1u);
         }
         for (uint32_t p = 0; p < passes; p++) {
             uint32_t bits = min(8u, num_bits - 8u * p);
@@ -130,13 +133,14 @@ __global__ __launch_bounds__(256) void k_hash_hist(const float* __restrict__ x,
 
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
-                            uint32_t* keys_out, uint32_t* vals_out, bool count_cells) {
+                            uint32_t* keys_out, uint32_t* vals_out) {
     uint32_t blocks = ceil_div(n, 256u * 8u);
     if (blocks < 1) blocks = 1;
     if (blocks > 2048) blocks = 2048;
+    tbeg(c, KID_HASH);
     k_hash_hist<<<blocks, 256, 0, c->stream>>>(x, y, z, stride, n, g, num_bits, keys_out,
-                                               vals_out, count_cells ? c->cell_count : nullptr,
-                                               c->ctl);
+                                               vals_out, c->ctl);
+    tend(c, KID_HASH);
     return hipGetLastError();
 }
 
@@ -280,8 +284,10 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
         uint32_t* vout = last ? vfin : ((p & 1u) ? c->vb : c->va);
         uint32_t pbits = min(8u, num_bits - 8u * p);
         uint64_t* lb = c->sort_lb + (size_t)p * c->max_sort_tiles * 256u;
+        tbeg(c, KID_SORT);
         k_onesweep<<<tiles, kSortThreads, 0, c->stream>>>(kin, vin, kout, vout, c->ctl, p, lb, n,
                                                           8u * p, pbits);
+        tend(c, KID_SORT);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         kin = kout;

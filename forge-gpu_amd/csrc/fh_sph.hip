@@ -17,14 +17,18 @@
 
 namespace fh {
 
-// Sorted-order copies of the state: spos[s] = pos[sidx[s]], svel[s] = vel[sidx[s]].
+// Sorted-order copies of the state: spos[s] = pos[sidx[s]], svel[s] = vel[sidx[s]], and the
+// run tags of the sorted keys (first index of each cell's run, see k_runs).
 __global__ void k_gather(const float* __restrict__ px, const float* __restrict__ py,
                          const float* __restrict__ pz, const float* __restrict__ vx,
                          const float* __restrict__ vy, const float* __restrict__ vz,
-                         const uint32_t* __restrict__ sidx, uint32_t n, float4* __restrict__ spos,
-                         float4* __restrict__ svel) {
+                         const uint32_t* __restrict__ sidx, const uint32_t* __restrict__ skeys,
+                         uint32_t n, float4* __restrict__ spos, float4* __restrict__ svel,
+                         uint64_t* __restrict__ run_tag, const Control* __restrict__ ctl) {
     uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
+    const uint32_t k = skeys[s];
+    if (s == 0 || skeys[s - 1] != k) run_tag[k] = ((uint64_t)ctl->epoch << 32) | s;
     uint32_t i = sidx[s];
     if (i >= n) i = 0;  // never taken when the sort is consistent
     spos[s] = make_float4(px[i], py[i], pz[i], 0.0f);
@@ -35,8 +39,11 @@ hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const floa
                          const float* vx, const float* vy, const float* vz, uint32_t n,
                          bool with_vel) {
     if (n == 0) return hipSuccess;
-    k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->sidx, n,
-                                                       c->spos, with_vel ? c->svel : nullptr);
+    tbeg(c, KID_GATHER);
+    k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->sidx, c->skeys,
+                                                       n, c->spos, with_vel ? c->svel : nullptr,
+                                                       c->run_tag, c->ctl);
+    tend(c, KID_GATHER);
     return hipGetLastError();
 }
 
@@ -101,8 +108,10 @@ hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_star
     float h9 = h2 * h2 * h2 * h2 * a.h;
     float poly6 = 315.0f / (64.0f * 3.14159265f * h9);
     float mc = a.mass * poly6;
+    tbeg(c, KID_DENSITY);
     k_density<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->sidx, a.n, a.g, cell_start,
                                                           h2, mc, c->srho, density_out);
+    tend(c, KID_DENSITY);
     return hipGetLastError();
 }
 
@@ -248,9 +257,11 @@ hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
         K.mx[q] = epi ? epi->box_max[q] : 0.0f;
     }
     K.e = epi ? epi->restitution : 0.0f;
+    tbeg(c, KID_FORCE);
     k_force<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sidx, a.n,
                                                         a.g, cell_start, K, px, py, pz, vx, vy,
                                                         vz, accel);
+    tend(c, KID_FORCE);
     return hipGetLastError();
 }
 

@@ -24,6 +24,8 @@ FH_EPI_GRAVITY = 1
 FH_EPI_INTEGRATE = 2
 FH_EPI_BOX = 4
 
+FH_OPT_SPH_EXACT = 1
+
 
 class LibraryNotBuilt(RuntimeError):
     """libforge_hip.so has not been built (run ``python -c 'import __graft_entry__ as g; g.build()'``)."""
@@ -90,6 +92,7 @@ SIGNATURES = {
     "fh_sph_density": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _U32, _P]),
     "fh_sph_fused": (_I, [_P, ctypes.POINTER(FhSphParams), ctypes.POINTER(FhEpilogue),
                           _P, _P, _P, _P, _P, _P, _P, _P, _U32, _F32]),
+    "fh_set_option": (_I, [_P, _I, _I]),
     "fh_gravity": (_I, [_P, _P, _P, _P, _U32, _F32, _F32, _F32, _F32]),
     "fh_integrate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _F32]),
     "fh_box_collider": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _F3, _F3, _F32]),
@@ -98,6 +101,9 @@ SIGNATURES = {
     "fh_graph_launch": (_I, [_P, _U32]),
     "fh_event_record": (_I, [_P, _U32]),
     "fh_event_elapsed_ms": (_I, [_P, _U32, _U32, ctypes.POINTER(ctypes.c_float)]),
+    "fh_time_kernel": (_I, [_P, ctypes.c_char_p, _U32]),
+    "fh_kernel_times": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), _U32,
+                             ctypes.POINTER(ctypes.c_uint32)]),
 }
 
 _lib = None

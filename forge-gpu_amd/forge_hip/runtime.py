@@ -97,6 +97,21 @@ class Context:
         check(_lib.load().fh_event_elapsed_ms(self.handle, int(a), int(b), ctypes.byref(ms)))
         return float(ms.value)
 
+    def set_option(self, option: int, value: int) -> None:
+        """fh_set_option, e.g. set_option(FH_OPT_SPH_EXACT, 1) for the bit-exact SPH passes."""
+        check(_lib.load().fh_set_option(self.handle, int(option), int(value)))
+
+    def time_kernel(self, name: str, max_launches: int) -> None:
+        """Bracket the next `max_launches` launches of kernel `name` with HIP events (captured
+        launches re-record them on every graph replay)."""
+        check(_lib.load().fh_time_kernel(self.handle, name.encode(), int(max_launches)))
+
+    def kernel_times_ms(self, name: str, cap: int = 4096) -> list:
+        buf = (ctypes.c_float * cap)()
+        cnt = ctypes.c_uint32()
+        check(_lib.load().fh_kernel_times(self.handle, name.encode(), buf, cap, ctypes.byref(cnt)))
+        return [float(buf[q]) for q in range(cnt.value)]
+
     def close(self) -> None:
         if getattr(self, "_h", None) is not None:
             _lib.load().fh_destroy(self._h)

@@ -176,6 +176,14 @@ int fh_sph_fused(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, 
                  float* py, float* pz, float* vx, float* vy, float* vz, float* density,
                  float* accel, uint32_t n, float dt);
 
+/* Context options.  FH_OPT_SPH_EXACT = 1 makes fh_sph_density / fh_sph_fused evaluate the
+ * reference's float expressions term by term in the reference's neighbour order (one thread per
+ * particle, no FMA, IEEE division and square root: bit-identical to the CPU restatement, slower);
+ * 0 (default) uses the LDS-tiled passes (fused multiply-adds, hardware reciprocal square root,
+ * deterministic per-slab partial sums; within rel 1e-4). */
+#define FH_OPT_SPH_EXACT 1
+int fh_set_option(fh_ctx* ctx, int option, int value);
+
 /* GravityModule (gravity.rs:31-34): v += g * dt. */
 int fh_gravity(fh_ctx* ctx, float* vx, float* vy, float* vz, uint32_t n, float gx, float gy,
                float gz, float dt);
@@ -204,6 +212,15 @@ int fh_graph_launch(fh_ctx* ctx, uint32_t count);
  * the time between two recorded slots after they completed. */
 int fh_event_record(fh_ctx* ctx, uint32_t slot);
 int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
+
+/* Per-kernel timing.  Arm kernel `name` (one of "begin", "hist", "hash", "scan", "sort",
+ * "gather", "density", "force", "query", "finalize", "runs") so that its next `max_launches` launches on the
+ * context stream are bracketed by HIP events; launches captured into a graph record the events
+ * on every replay.  max_launches = 0 disarms.  Arming allocates events: call outside capture.
+ * fh_kernel_times waits for the last armed launch and writes the durations (ms) of the armed
+ * launches made so far (up to `cap`) into ms[], their number into *count. */
+int fh_time_kernel(fh_ctx* ctx, const char* name, uint32_t max_launches);
+int fh_kernel_times(fh_ctx* ctx, const char* name, float* ms, uint32_t cap, uint32_t* count);
 
 #ifdef __cplusplus
 }
