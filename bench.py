@@ -62,6 +62,42 @@ def algorithmic_bytes(n: int, cells: int, passes: int) -> dict:
     }
 
 
+def survey_step_bytes(n: int, cells: int, passes: int) -> int:
+    """Whole-substep algorithmic bytes with the neighbour re-reads counted once:
+    N·(168 + 16p) + 24C for p 8-bit sort passes (hash 20, sort 4 + 16p, bounds 4, gather 60,
+    density 20, force + epilogue 60 bytes per particle; the cell table written once, read twice)."""
+    return n * (168 + 16 * passes) + 24 * cells
+
+
+def read_traffic(kernel_pass: str):
+    """HBM bytes per launch of a pass, from the committed rocprofv3 PMC summary
+    (profiles/traffic_c3.txt, lines `<pass> fetch_bytes=<B> write_bytes=<B>`), or None."""
+    f = REPO / "profiles" / "traffic_c3.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 3 and parts[0] == kernel_pass:
+            kv = dict(q.split("=", 1) for q in parts[1:] if "=" in q)
+            try:
+                return int(float(kv["fetch_bytes"]) + float(kv["write_bytes"]))
+            except (KeyError, ValueError):
+                return None
+    return None
+
+
+def copy_calibration(torch, log, mib: int = 1024) -> None:
+    """A plain copy kernel of known size (reads and writes `mib` MiB each) for scaling the PMC
+    FETCH_SIZE / WRITE_SIZE readings; run alone under rocprofv3 --pmc."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 launches, {mib} MiB read + {mib} MiB written each")
+
+
 def cpu_info() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -234,6 +270,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sort", action="store_true", help="skip the c1 sort line")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--sort-only", action="store_true",
+                    help="only the c1 sort line (for a profile of the sort alone)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB copy kernel (scale for PMC byte counters)")
     args = ap.parse_args(argv)
 
     def log(msg):
@@ -252,8 +292,15 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        copy_calibration(torch, log)
+        return 0
     fh.load()
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.sort_only:
+        print(json.dumps({"metric": "radix sort Gkeys/s (configs[1])", "sort_c1":
+                          bench_sort(args, fh, torch, log)}), flush=True)
+        return 0
     s = bench_sph(args, fh, torch, log)
     sort = None if args.no_sort else bench_sort(args, fh, torch, log)
     cpu = None if args.no_cpu else cpu_baseline(args, log)
@@ -286,7 +333,7 @@ def main(argv=None) -> int:
         "roofline": {
             "bound": "hbm", "kernel": dom + " pass (" + " + ".join(s["pas"][dom]["kernels"]) + ")",
             "achieved": s["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": s["achieved"] / HBM_PEAK_GBS, "traffic": None,
+            "frac": s["achieved"] / HBM_PEAK_GBS, "traffic": read_traffic(dom),
             "alg_bytes_per_launch": s["pas"][dom]["alg_bytes"],
             "mean_launch_us": s["pas"][dom]["per_substep_us"],
         },
@@ -295,6 +342,9 @@ def main(argv=None) -> int:
             "substep_us_events": s["ev_ms"] * 1e3 / K,
             "substep_alg_bytes": s["total_alg"],
             "substep_alg_GBs": s["total_alg"] / (ms_per_step * 1e-3) / 1e9,
+            "substep_survey_bytes": survey_step_bytes(cfg.n, s["C"], s["passes"]),
+            "substep_survey_frac": survey_step_bytes(cfg.n, s["C"], s["passes"])
+            / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "kernels": {k: {q: (round(v, 3) if isinstance(v, float) else v) for q, v in kern[k].items()}
                         for k in KERNELS},
             "passes": {p: {q: (round(v, 3) if isinstance(v, float) else v) for q, v in d.items()}

@@ -71,6 +71,20 @@ def build_library(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_cpp_mirror_test(verbose: bool = False) -> Path:
+    """Compile tests/cpp/test_mirror.cpp (the C++ host mirror, include/forge_hip.hpp, exercised
+    against the reference's tests) into _build/test_mirror, linked to the library and the oracle."""
+    out = OBJ / "test_mirror"
+    OBJ.mkdir(exist_ok=True)
+    _run([_hipcc(), "-std=c++17", "-O2", f"-I{REPO / 'include'}",
+          str(REPO / "tests" / "cpp" / "test_mirror.cpp"), "-o", str(out),
+          f"-L{LIB.parent}", "-lforge_hip", f"-L{ORACLE_DIR}", "-loracle",
+          "-Wl,-rpath,$ORIGIN/../lib", "-Wl,-rpath,$ORIGIN/../../oracle"])
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 def build_oracle(verbose: bool = False) -> Path:
     """Compile the CPU checker (oracle/liboracle.so).  Test infrastructure, not the product."""
     _run(["make", "-s", "-C", str(ORACLE_DIR), "liboracle.so"])
@@ -87,6 +101,7 @@ def main(argv=None) -> int:
     build_library(verbose=True)
     if not a.lib:
         build_oracle(verbose=True)
+        build_cpp_mirror_test(verbose=True)
     return 0
 
 

@@ -72,6 +72,10 @@ class SimModule:
     def name(self) -> str:
         raise NotImplementedError
 
+    def prepare(self, fields: FieldSet) -> None:
+        """Create the fields execute() writes but the caller may not have added; this allocates,
+        so Pipeline.capture calls it before recording starts."""
+
     def execute(self, fields: FieldSet, dt: float) -> None:
         raise NotImplementedError
 
@@ -103,10 +107,13 @@ class SphDensityModule(SimModule):
     def name(self) -> str:
         return "sph_density"
 
+    def prepare(self, fields: FieldSet) -> None:
+        if "density" not in fields.f32_fields:
+            fields.add_f32_zeros("density", fields.particle_count)
+
     def execute(self, fields: FieldSet, dt: float) -> None:
         n = fields.particle_count
-        if "density" not in fields.f32_fields:
-            fields.add_f32_zeros("density", n)
+        self.prepare(fields)
         ctx = fields.context(_cells(self.grid_dims))
         px, py, pz = fields.pos()
         check(_lib.load().fh_sph_density(ctx.handle, ctypes.byref(_sph_params(self)), ptr(px),
@@ -129,10 +136,13 @@ class SphFusedModule(SimModule):
     def name(self) -> str:
         return "sph_fused"
 
+    def prepare(self, fields: FieldSet) -> None:
+        if "density" not in fields.f32_fields:
+            fields.add_f32_zeros("density", fields.particle_count)
+
     def execute(self, fields: FieldSet, dt: float) -> None:
         n = fields.particle_count
-        if "density" not in fields.f32_fields:
-            fields.add_f32_zeros("density", n)
+        self.prepare(fields)
         ctx = fields.context(_cells(self.grid_dims))
         px, py, pz = fields.pos()
         vx, vy, vz = fields.vel()
@@ -269,6 +279,8 @@ class Pipeline:
         """Record `substeps` step_async calls into one HIP graph (manifest_runner.rs:57-69)."""
         ctx = fields.context(max((_cells(m.grid_dims) for m in self.modules
                                   if hasattr(m, "grid_dims")), default=1))
+        for m in self._fused_plan():
+            m.prepare(fields)
         ctx.torch_stream().wait_stream(torch.cuda.current_stream())
         ctx.sync()
         ctx.graph_begin()

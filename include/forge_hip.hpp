@@ -1,0 +1,425 @@
+// forge_hip.hpp -- C++ host-side mirror of forge-gpu's interfaces for the SPH / hash-grid path,
+// header-only, on top of the C ABI in forge_hip.h.
+//
+// The reference host code is Rust; its toolchain is not available here, so this header restates
+// the same interfaces in C++ (same names, argument meaning and error behaviour) for C++ callers
+// and for the parity tests that read like the reference's own tests:
+//   forge::Array<T>              forge-runtime/src/array.rs:81-107,193-214,366-406 (device buffer,
+//                                synchronous from_vec / to_vec)
+//   forge::Error                 forge-runtime/src/error.rs:7-22 (thrown instead of Result::Err)
+//   forge::HashGrid              forge-runtime/src/hashgrid.rs:21-193 (build runs on the GPU)
+//   forge::RadixSorter           forge-runtime/src/radix_sort.rs:26-220
+//   forge::find_cell_boundaries  forge-runtime/src/radix_sort.rs:229-317
+//   forge::FieldSet, SimModule, Pipeline
+//                                forge-manifest/src/modules/mod.rs:12-117
+//   forge::SphFusedModule, SphDensityModule, GravityModule, IntegrateModule, BoxColliderModule
+//                                forge-manifest/src/modules/builtins/{sph_fused,sph_density,
+//                                gravity,integrate,box_collider}.rs
+// Exceptions stay on this side of the ABI: every C call returns a status that is turned into a
+// forge::Error here.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "forge_hip.h"
+
+namespace forge {
+
+class Error : public std::runtime_error {
+   public:
+    Error(int code, const std::string& msg) : std::runtime_error(msg), code_(code) {}
+    int code() const { return code_; }
+
+   private:
+    int code_;
+};
+
+inline void check(int rc) {
+    if (rc != FH_OK) throw Error(rc, fh_last_error());
+}
+
+inline void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error((int)e, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Owns an fh_ctx (stream + scratch), the counterpart of the reference's per-ordinal context and
+// simulation stream (forge-runtime/src/cuda.rs:13-63).
+class Context {
+   public:
+    Context(uint32_t max_n, uint32_t max_cells, int device = 0) {
+        check(fh_create(device, max_n, max_cells, nullptr, &ctx_));
+        max_n_ = max_n;
+        max_cells_ = max_cells;
+    }
+    ~Context() {
+        if (ctx_) fh_destroy(ctx_);
+    }
+    Context(const Context&) = delete;
+    Context& operator=(const Context&) = delete;
+    fh_ctx* get() const { return ctx_; }
+    hipStream_t stream() const { return (hipStream_t)fh_stream(ctx_); }
+    void sync() const { check(fh_sync(ctx_)); }
+    uint32_t max_n() const { return max_n_; }
+    uint32_t max_cells() const { return max_cells_; }
+
+   private:
+    fh_ctx* ctx_ = nullptr;
+    uint32_t max_n_ = 0, max_cells_ = 0;
+};
+
+// Typed device buffer (Array<T>): RAII hipMalloc, synchronous host transfers.
+template <typename T>
+class Array {
+   public:
+    Array() = default;
+    explicit Array(size_t n) : n_(n) {
+        if (n) check_hip(hipMalloc((void**)&p_, n * sizeof(T)), "hipMalloc");
+    }
+    static Array zeros(size_t n) {
+        Array a(n);
+        if (n) check_hip(hipMemset(a.p_, 0, n * sizeof(T)), "hipMemset");
+        return a;
+    }
+    static Array from_vec(const std::vector<T>& v) {
+        Array a(v.size());
+        if (!v.empty())
+            check_hip(hipMemcpy(a.p_, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice),
+                      "hipMemcpy");
+        return a;
+    }
+    std::vector<T> to_vec() const {
+        std::vector<T> v(n_);
+        if (n_) check_hip(hipMemcpy(v.data(), p_, n_ * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy");
+        return v;
+    }
+    ~Array() {
+        if (p_) (void)hipFree(p_);
+    }
+    Array(Array&& o) noexcept : p_(o.p_), n_(o.n_) {
+        o.p_ = nullptr;
+        o.n_ = 0;
+    }
+    Array& operator=(Array&& o) noexcept {
+        std::swap(p_, o.p_);
+        std::swap(n_, o.n_);
+        return *this;
+    }
+    Array(const Array&) = delete;
+    Array& operator=(const Array&) = delete;
+    T* data() { return p_; }
+    const T* data() const { return p_; }
+    size_t len() const { return n_; }
+
+   private:
+    T* p_ = nullptr;
+    size_t n_ = 0;
+};
+
+struct Vec3f {  // forge-core Vec3f: #[repr(C)] 3 x f32, 12 bytes (forge-core/src/vec.rs:137-139)
+    float x, y, z;
+};
+static_assert(sizeof(Vec3f) == 12, "Vec3f must be 12 bytes");
+
+class HashGrid {
+   public:
+    HashGrid(Context& ctx, float cell_size, uint32_t dim_x, uint32_t dim_y, uint32_t dim_z,
+             Vec3f origin, size_t max_particles)
+        : ctx_(ctx), cell_size(cell_size), dim_x(dim_x), dim_y(dim_y), dim_z(dim_z),
+          origin(origin), cell_start(Array<uint32_t>::zeros(num_cells() + 1)),
+          sorted_indices(Array<uint32_t>::zeros(max_particles)),
+          cell_indices(Array<uint32_t>::zeros(max_particles)) {}
+
+    size_t num_cells() const { return (size_t)dim_x * dim_y * dim_z; }
+
+    // Build from device-resident Vec3f positions (stride 3 floats).
+    void build(const Array<Vec3f>& positions) {
+        const size_t n = positions.len();
+        if (n > sorted_indices.len()) {
+            sorted_indices = Array<uint32_t>(n);
+            cell_indices = Array<uint32_t>(n);
+        }
+        const float* p = reinterpret_cast<const float*>(positions.data());
+        const float o[3] = {origin.x, origin.y, origin.z};
+        const uint32_t d[3] = {dim_x, dim_y, dim_z};
+        check(fh_hashgrid_build(ctx_.get(), p, p + 1, p + 2, 3, (uint32_t)n, cell_size, o, d,
+                                cell_start.data(), sorted_indices.data(), cell_indices.data()));
+        ctx_.sync();
+        num_particles = n;
+    }
+
+    uint32_t position_to_cell(Vec3f pos) const {
+        Array<Vec3f> p = Array<Vec3f>::from_vec({pos});
+        Array<uint32_t> k(1);
+        const float* f = reinterpret_cast<const float*>(p.data());
+        const float o[3] = {origin.x, origin.y, origin.z};
+        const uint32_t d[3] = {dim_x, dim_y, dim_z};
+        check(fh_hash_cells(ctx_.get(), f, f + 1, f + 2, 3, 1, cell_size, o, d, k.data(), nullptr));
+        ctx_.sync();
+        return k.to_vec()[0];
+    }
+
+    // Neighbour ids of `pos` within `radius` (dist^2 <= r^2, visiting order of the reference).
+    std::vector<uint32_t> query_neighbors(Vec3f pos, float radius,
+                                          const Array<Vec3f>& positions) const {
+        Array<Vec3f> q = Array<Vec3f>::from_vec({pos});
+        Array<uint32_t> count(1), offsets = Array<uint32_t>::zeros(2);
+        const float* p = reinterpret_cast<const float*>(positions.data());
+        const float* qf = reinterpret_cast<const float*>(q.data());
+        const float o[3] = {origin.x, origin.y, origin.z};
+        const uint32_t d[3] = {dim_x, dim_y, dim_z};
+        check(fh_query_neighbors(ctx_.get(), p, p + 1, p + 2, 3, cell_size, o, d, cell_start.data(),
+                                 sorted_indices.data(), qf, qf + 1, qf + 2, 3, 1, radius,
+                                 count.data(), nullptr, nullptr));
+        ctx_.sync();
+        const uint32_t c = count.to_vec()[0];
+        std::vector<uint32_t> off = {0u, c};
+        offsets = Array<uint32_t>::from_vec(off);
+        Array<uint32_t> idx(c ? c : 1);
+        check(fh_query_neighbors(ctx_.get(), p, p + 1, p + 2, 3, cell_size, o, d, cell_start.data(),
+                                 sorted_indices.data(), qf, qf + 1, qf + 2, 3, 1, radius,
+                                 count.data(), offsets.data(), idx.data()));
+        ctx_.sync();
+        std::vector<uint32_t> out = idx.to_vec();
+        out.resize(c);
+        return out;
+    }
+
+   private:
+    Context& ctx_;
+
+   public:
+    float cell_size;
+    uint32_t dim_x, dim_y, dim_z;
+    Vec3f origin;
+    Array<uint32_t> cell_start;
+    Array<uint32_t> sorted_indices;
+    Array<uint32_t> cell_indices;
+    size_t num_particles = 0;
+};
+
+class RadixSorter {
+   public:
+    RadixSorter(Context& ctx, size_t max_n) : ctx_(ctx), max_n_(max_n) {}
+    // Stable sort of (keys, values) by the low num_bits bits, in place.
+    void sort(Array<uint32_t>& keys, Array<uint32_t>& values, size_t n, uint32_t num_bits) {
+        if (n > max_n_) throw Error(FH_ERANGE, "n exceeds max_n");
+        check(fh_sort_pairs(ctx_.get(), keys.data(), values.data(), (uint32_t)n, num_bits));
+    }
+
+   private:
+    Context& ctx_;
+    size_t max_n_;
+};
+
+inline void find_cell_boundaries(Context& ctx, const Array<uint32_t>& sorted_cell_ids,
+                                 Array<uint32_t>& cell_start, Array<uint32_t>& cell_end, size_t n,
+                                 size_t num_cells) {
+    check(fh_find_cell_boundaries(ctx.get(), sorted_cell_ids.data(), (uint32_t)n,
+                                  (uint32_t)num_cells, cell_start.data(), cell_end.data()));
+}
+
+// Named SoA particle fields in original particle order (modules/mod.rs:12-67).
+class FieldSet {
+   public:
+    FieldSet(Context& ctx, size_t particle_count) : ctx(ctx), particle_count(particle_count) {}
+    void add_f32(const std::string& name, const std::vector<float>& data) {
+        f32_fields[name] = Array<float>::from_vec(data);
+    }
+    void add_f32_zeros(const std::string& name, size_t n) {
+        f32_fields[name] = Array<float>::zeros(n);
+    }
+    Array<float>& f(const std::string& name) {
+        auto it = f32_fields.find(name);
+        if (it == f32_fields.end()) throw Error(FH_EINVAL, "missing field " + name);
+        return it->second;
+    }
+    Context& ctx;
+    size_t particle_count;
+    std::map<std::string, Array<float>> f32_fields;
+};
+
+class SimModule {
+   public:
+    virtual ~SimModule() = default;
+    virtual const char* name() const = 0;
+    // Creates the fields execute() writes but the caller may not have added (allocation and a
+    // memset, so it must not run while a graph is being captured).
+    virtual void prepare(FieldSet&) {}
+    virtual void execute(FieldSet& fields, float dt) = 0;
+};
+
+struct SphFusedModule : SimModule {
+    float smoothing_radius, cell_size;
+    uint32_t grid_dims[3];
+    float particle_mass, gas_constant, rest_density, viscosity_coefficient;
+    bool has_epilogue = false;
+    fh_epilogue epilogue{};
+    SphFusedModule(float h, float cs, uint32_t nx, uint32_t ny, uint32_t nz, float m, float k,
+                   float rho0, float mu)
+        : smoothing_radius(h), cell_size(cs), grid_dims{nx, ny, nz}, particle_mass(m),
+          gas_constant(k), rest_density(rho0), viscosity_coefficient(mu) {}
+    const char* name() const override { return "sph_fused"; }
+    void prepare(FieldSet& fs) override {
+        if (!fs.f32_fields.count("density")) fs.add_f32_zeros("density", fs.particle_count);
+    }
+    void execute(FieldSet& fs, float dt) override {
+        prepare(fs);
+        fh_sph_params p{smoothing_radius, cell_size, {grid_dims[0], grid_dims[1], grid_dims[2]},
+                        particle_mass, gas_constant, rest_density, viscosity_coefficient};
+        check(fh_sph_fused(fs.ctx.get(), &p, has_epilogue ? &epilogue : nullptr,
+                           fs.f("pos_x").data(), fs.f("pos_y").data(), fs.f("pos_z").data(),
+                           fs.f("vel_x").data(), fs.f("vel_y").data(), fs.f("vel_z").data(),
+                           fs.f("density").data(), nullptr, (uint32_t)fs.particle_count, dt));
+    }
+};
+
+struct SphDensityModule : SimModule {
+    float smoothing_radius, cell_size;
+    uint32_t grid_dims[3];
+    float particle_mass;
+    SphDensityModule(float h, float cs, uint32_t nx, uint32_t ny, uint32_t nz, float m)
+        : smoothing_radius(h), cell_size(cs), grid_dims{nx, ny, nz}, particle_mass(m) {}
+    const char* name() const override { return "sph_density"; }
+    void prepare(FieldSet& fs) override {
+        if (!fs.f32_fields.count("density")) fs.add_f32_zeros("density", fs.particle_count);
+    }
+    void execute(FieldSet& fs, float) override {
+        prepare(fs);
+        fh_sph_params p{smoothing_radius, cell_size, {grid_dims[0], grid_dims[1], grid_dims[2]},
+                        particle_mass, 0.0f, 0.0f, 0.0f};
+        check(fh_sph_density(fs.ctx.get(), &p, fs.f("pos_x").data(), fs.f("pos_y").data(),
+                             fs.f("pos_z").data(), (uint32_t)fs.particle_count,
+                             fs.f("density").data()));
+    }
+};
+
+struct GravityModule : SimModule {
+    float gx, gy, gz;
+    GravityModule(float gx, float gy, float gz) : gx(gx), gy(gy), gz(gz) {}
+    static GravityModule default_earth() { return GravityModule(0.0f, -9.81f, 0.0f); }
+    const char* name() const override { return "gravity"; }
+    void execute(FieldSet& fs, float dt) override {
+        check(fh_gravity(fs.ctx.get(), fs.f("vel_x").data(), fs.f("vel_y").data(),
+                         fs.f("vel_z").data(), (uint32_t)fs.particle_count, gx, gy, gz, dt));
+    }
+};
+
+struct IntegrateModule : SimModule {
+    const char* name() const override { return "integrate"; }
+    void execute(FieldSet& fs, float dt) override {
+        check(fh_integrate(fs.ctx.get(), fs.f("pos_x").data(), fs.f("pos_y").data(),
+                           fs.f("pos_z").data(), fs.f("vel_x").data(), fs.f("vel_y").data(),
+                           fs.f("vel_z").data(), (uint32_t)fs.particle_count, dt));
+    }
+};
+
+struct BoxColliderModule : SimModule {
+    float min_x, min_y, min_z, max_x, max_y, max_z, restitution;
+    BoxColliderModule(float x0, float y0, float z0, float x1, float y1, float z1, float e)
+        : min_x(x0), min_y(y0), min_z(z0), max_x(x1), max_y(y1), max_z(z1), restitution(e) {}
+    const char* name() const override { return "box_collider"; }
+    void execute(FieldSet& fs, float) override {
+        const float mn[3] = {min_x, min_y, min_z}, mx[3] = {max_x, max_y, max_z};
+        check(fh_box_collider(fs.ctx.get(), fs.f("pos_x").data(), fs.f("pos_y").data(),
+                              fs.f("pos_z").data(), fs.f("vel_x").data(), fs.f("vel_y").data(),
+                              fs.f("vel_z").data(), (uint32_t)fs.particle_count, mn, mx,
+                              restitution));
+    }
+};
+
+// Modules run in order; a sph_fused followed by gravity / integrate / box is fused into one
+// force pass with the same result (the build_pipeline fusion idea, manifest_runner.rs:334-379).
+class Pipeline {
+   public:
+    void add(std::unique_ptr<SimModule> m) {
+        modules_.push_back(std::move(m));
+        fused_ = false;
+    }
+    size_t len() const { return modules_.size(); }
+    void step_async(FieldSet& fs, float dt) {
+        plan();
+        for (SimModule* m : plan_) m->execute(fs, dt);
+    }
+    void step(FieldSet& fs, float dt) {
+        step_async(fs, dt);
+        fs.ctx.sync();
+    }
+    void run(FieldSet& fs, float dt, size_t steps) {
+        for (size_t i = 0; i < steps; i++) step(fs, dt);
+    }
+    // Record `substeps` step_async calls into the context's graph (manifest_runner.rs:57-69)
+    // and replay it (manifest_runner.rs:74-77).
+    void capture(FieldSet& fs, float dt, size_t substeps) {
+        plan();
+        for (SimModule* m : plan_) m->prepare(fs);
+        fs.ctx.sync();
+        check(fh_graph_begin(fs.ctx.get()));
+        for (size_t i = 0; i < substeps; i++)
+            for (SimModule* m : plan_) m->execute(fs, dt);
+        check(fh_graph_end(fs.ctx.get()));
+    }
+    void replay(FieldSet& fs, uint32_t count) { check(fh_graph_launch(fs.ctx.get(), count)); }
+
+   private:
+    void plan() {
+        if (fused_) return;
+        plan_.clear();
+        fused_mods_.clear();
+        for (size_t i = 0; i < modules_.size(); i++) {
+            auto* sph = dynamic_cast<SphFusedModule*>(modules_[i].get());
+            if (sph && !sph->has_epilogue) {
+                auto f = std::make_unique<SphFusedModule>(*sph);
+                size_t j = i + 1;
+                if (j < modules_.size()) {
+                    if (auto* g = dynamic_cast<GravityModule*>(modules_[j].get())) {
+                        f->epilogue.flags |= FH_EPI_GRAVITY;
+                        f->epilogue.gravity[0] = g->gx;
+                        f->epilogue.gravity[1] = g->gy;
+                        f->epilogue.gravity[2] = g->gz;
+                        j++;
+                    }
+                }
+                if (j < modules_.size() && dynamic_cast<IntegrateModule*>(modules_[j].get())) {
+                    f->epilogue.flags |= FH_EPI_INTEGRATE;
+                    j++;
+                }
+                if (j < modules_.size()) {
+                    if (auto* b = dynamic_cast<BoxColliderModule*>(modules_[j].get())) {
+                        f->epilogue.flags |= FH_EPI_BOX;
+                        f->epilogue.box_min[0] = b->min_x;
+                        f->epilogue.box_min[1] = b->min_y;
+                        f->epilogue.box_min[2] = b->min_z;
+                        f->epilogue.box_max[0] = b->max_x;
+                        f->epilogue.box_max[1] = b->max_y;
+                        f->epilogue.box_max[2] = b->max_z;
+                        f->epilogue.restitution = b->restitution;
+                        j++;
+                    }
+                }
+                if (j > i + 1) {
+                    f->has_epilogue = true;
+                    plan_.push_back(f.get());
+                    fused_mods_.push_back(std::move(f));
+                    i = j - 1;
+                    continue;
+                }
+            }
+            plan_.push_back(modules_[i].get());
+        }
+        fused_ = true;
+    }
+    std::vector<std::unique_ptr<SimModule>> modules_;
+    std::vector<std::unique_ptr<SimModule>> fused_mods_;
+    std::vector<SimModule*> plan_;
+    bool fused_ = false;
+};
+
+}  // namespace forge

@@ -1,0 +1,331 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker of the HIP path.
+
+Every oracle function is checked against something other than a retyping of its own formula:
+the reference's known-answer tests (tests/golden/reference_kats.json), library routines (numpy's
+stable argsort, searchsorted, bincount), brute force over all pairs, and closed forms of the SPH
+kernels (Mueller et al. 2003: poly6 density, spiky pressure gradient, viscosity Laplacian).  The
+checks are chosen so that plausible slips (a dropped self term, `<=` for `<`, a sign, a swapped
+operand, an off-by-one cell) fail at least one of them.  CPU only.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+PI = math.pi
+
+
+def xorshift32(seed, n, mask):
+    out = np.empty(n, np.uint32)
+    s = seed
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out[i] = s & mask
+    return out
+
+
+# ---- hashing (hashgrid.rs:128-139) -----------------------------------------------------------
+
+def test_f32_as_i32_matches_rust_semantics(oracle):
+    assert oracle.f32_as_i32(float("nan")) == 0
+    assert oracle.f32_as_i32(float("inf")) == 2**31 - 1
+    assert oracle.f32_as_i32(float("-inf")) == -(2**31)
+    assert oracle.f32_as_i32(3e9) == 2**31 - 1
+    assert oracle.f32_as_i32(-3e9) == -(2**31)
+    assert oracle.f32_as_i32(-2.0) == -2
+    assert oracle.f32_as_i32(7.0) == 7
+
+
+def test_position_to_cell_closed_forms(oracle):
+    dims, o = (10, 20, 30), (0.0, 0.0, 0.0)
+    # cell centres of a power-of-two cell size are exact: cell (i, j, k) -> i + 10 j + 200 k
+    cs = 0.125
+    for (i, j, k) in [(0, 0, 0), (9, 19, 29), (3, 7, 11), (5, 0, 29)]:
+        p = ((i + 0.5) * cs, (j + 0.5) * cs, (k + 0.5) * cs)
+        assert oracle.position_to_cell(p, cs, o, dims) == i + 10 * j + 200 * k
+    # exact lower faces belong to the cell
+    assert oracle.position_to_cell((3 * cs, 4 * cs, 5 * cs), cs, o, dims) == 3 + 40 + 1000
+    # below the grid / NaN -> 0, above -> dim - 1 (clamp after the saturating cast)
+    assert oracle.position_to_cell((-5.0, float("nan"), -0.0), cs, o, dims) == 0
+    assert oracle.position_to_cell((1e30, float("inf"), 100.0), cs, o, dims) == 9 + 10 * 19 + 200 * 29
+    assert oracle.position_to_cell((float("-inf"), 1e-30, 2.0), cs, o, dims) == 0 + 0 + 200 * 16
+    # origin is subtracted before dividing
+    assert oracle.position_to_cell((1.0 + 0.3, 2.0, 3.0), 0.25, (1.0, 2.0, 3.0), dims) == 1
+
+
+def test_hash_of_config1_points_is_exact(oracle):
+    """c1: cs = 1/256, so floor(x / cs) = floor(256 x) exactly; checked on the 24-bit mantissas."""
+    from forge_hip import workloads
+    n = 100_000
+    m = [workloads.u32_stream(7, a, n) >> np.uint32(8) for a in range(3)]
+    x, y, z = [(mm.astype(np.float64) * 2.0**-24).astype(np.float32) for mm in m]
+    keys, vals = oracle.hash_cells(x, y, z, 1.0 / 256.0, (0, 0, 0), (256, 256, 256))
+    exp = (m[0] >> 16) + (m[1] >> 16) * 256 + (m[2] >> 16) * 65536
+    assert np.array_equal(keys, exp.astype(np.uint32))
+    assert np.array_equal(vals, np.arange(n, dtype=np.uint32))
+
+
+# ---- sorting (radix_sort.rs:79-220 contract) ------------------------------------------------
+
+def test_sort_known_answer(oracle):
+    kat = KATS["radix_sort_small"]
+    k, v = oracle.stable_sort_pairs(kat["keys"], kat["vals"], kat["num_bits"])
+    assert k.tolist() == kat["sorted_keys"] and v.tolist() == kat["sorted_vals"]
+
+
+@pytest.mark.parametrize("name", ["radix_sort_medium", "radix_sort_compare_cpu"])
+def test_sort_reference_streams_vs_numpy_stable(oracle, name):
+    kat = KATS[name]
+    keys = xorshift32(kat["xorshift_seed"], kat["n"], kat["mask"])
+    assert keys[:8].tolist() == kat["first_keys"]
+    vals = np.arange(kat["n"], dtype=np.uint32)
+    k, v = oracle.stable_sort_pairs(keys, vals, kat["num_bits"])
+    order = np.argsort(keys, kind="stable")
+    assert np.array_equal(v, order.astype(np.uint32)) and np.array_equal(k, keys[order])
+
+
+@pytest.mark.parametrize("bits", [1, 5, 12, 16, 31, 32])
+def test_sort_masked_keys_vs_numpy(oracle, bits):
+    rng = np.random.default_rng(bits)
+    keys = rng.integers(0, 2**32, 20_000, dtype=np.uint64).astype(np.uint32)
+    vals = rng.integers(0, 2**32, 20_000, dtype=np.uint64).astype(np.uint32)
+    mask = np.uint32(0xFFFFFFFF if bits == 32 else (1 << bits) - 1)
+    order = np.argsort(keys & mask, kind="stable")
+    k, v = oracle.stable_sort_pairs(keys, vals, bits)
+    assert np.array_equal(k, keys[order]) and np.array_equal(v, vals[order])
+
+
+# ---- cell ranges ----------------------------------------------------------------------------
+
+def test_find_cell_boundaries_known_answer(oracle):
+    kat = KATS["find_cell_boundaries"]
+    s, e = oracle.find_cell_boundaries(kat["sorted"], kat["num_cells"])
+    assert s.tolist() == kat["start"] and e.tolist() == kat["end"]
+
+
+def test_cell_ranges_vs_searchsorted(oracle):
+    rng = np.random.default_rng(2)
+    C = 5000
+    keys = np.sort(rng.integers(0, C + 50, 40_000).astype(np.uint32))  # some keys >= C
+    csr = oracle.cell_start_csr(keys, C)
+    assert np.array_equal(csr, np.searchsorted(keys, np.arange(C + 1), side="left").astype(np.uint32)
+                          .clip(max=int(np.searchsorted(keys, C))))
+    s, e = oracle.find_cell_boundaries(keys, C)
+    nonempty = csr[1:] > csr[:-1]
+    assert np.array_equal(s[nonempty], csr[:-1][nonempty]) and np.array_equal(e[nonempty], csr[1:][nonempty])
+    assert np.all(s[~nonempty] == 0xFFFFFFFF) and np.all(e[~nonempty] == 0)
+
+
+def test_hashgrid_build_vs_library_counting_sort(oracle):
+    rng = np.random.default_rng(4)
+    p = rng.uniform(-0.1, 1.1, (30_000, 3)).astype(np.float32)
+    cs, dims = 0.05, (20, 22, 24)
+    start, sidx, cell = oracle.hashgrid_build(p[:, 0], p[:, 1], p[:, 2], cs, (0, 0, 0), dims)
+    keys, _ = oracle.hash_cells(p[:, 0], p[:, 1], p[:, 2], cs, (0, 0, 0), dims)
+    assert np.array_equal(cell, keys)
+    C = dims[0] * dims[1] * dims[2]
+    counts = np.bincount(keys, minlength=C)
+    assert start[0] == 0 and np.array_equal(np.diff(start.astype(np.int64)), counts)
+    assert np.array_equal(sidx, np.argsort(keys, kind="stable").astype(np.uint32))
+
+
+# ---- neighbour queries (hashgrid.rs:145-193) ------------------------------------------------
+
+def test_query_neighbors_known_answers(oracle):
+    kat = KATS["hashgrid_basic"]
+    p = np.asarray(kat["positions"], np.float32)
+    st, si, _ = oracle.hashgrid_build(p[:, 0], p[:, 1], p[:, 2], kat["cell_size"], kat["origin"], kat["dims"])
+    nb = oracle.query_neighbors(kat["query"], kat["radius"], p[:, 0], p[:, 1], p[:, 2],
+                                kat["cell_size"], kat["origin"], kat["dims"], st, si)
+    assert nb.tolist() == kat["neighbors"]
+    kat = KATS["hashgrid_uniform"]
+    i = np.arange(1000)
+    p = np.stack([(i % 10) + 0.5, ((i // 10) % 10) + 0.5, (i // 100) + 0.5], 1).astype(np.float32)
+    st, si, _ = oracle.hashgrid_build(p[:, 0], p[:, 1], p[:, 2], kat["cell_size"], kat["origin"], kat["dims"])
+    nb = oracle.query_neighbors(kat["query"], kat["radius"], p[:, 0], p[:, 1], p[:, 2],
+                                kat["cell_size"], kat["origin"], kat["dims"], st, si)
+    assert sorted(nb.tolist()) == kat["neighbors_sorted"] and len(nb) == kat["count"] == 8
+
+
+def brute_counts(p, r):
+    d = p[None, :, :] - p[:, None, :]
+    dist = (d[..., 0] * d[..., 0] + d[..., 1] * d[..., 1]) + d[..., 2] * d[..., 2]
+    return dist, dist <= np.float32(r) * np.float32(r)
+
+
+def test_neighbor_counts_vs_brute_force(oracle):
+    rng = np.random.default_rng(8)
+    n, cs, dims = 2000, 0.1, (10, 10, 10)
+    p = rng.uniform(0, 1, (n, 3)).astype(np.float32)
+    st, si, _ = oracle.hashgrid_build(p[:, 0], p[:, 1], p[:, 2], cs, (0, 0, 0), dims)
+    r = 0.1
+    cnt, w = oracle.neighbor_counts(p[:, 0], p[:, 1], p[:, 2], cs, (0, 0, 0), dims, st, si, r)
+    dist, hit = brute_counts(p, r)
+    assert np.array_equal(cnt, hit.sum(1).astype(np.uint32))
+    c = 315.0 / (64.0 * PI * r**9)
+    w64 = np.where(hit, c * (r * r - dist.astype(np.float64)) ** 3, 0.0).sum(1)
+    assert np.allclose(w, w64, rtol=2e-5, atol=0)
+    for q in (0, 17, 999):  # per-query lists equal the brute-force sets
+        nb = oracle.query_neighbors(p[q], r, p[:, 0], p[:, 1], p[:, 2], cs, (0, 0, 0), dims, st, si)
+        assert sorted(nb.tolist()) == np.nonzero(hit[q])[0].tolist()
+
+
+# ---- SPH (sph_density.rs:401-461, sph_fused.rs:542-638) -------------------------------------
+
+# parameters are float32 in the reference; the closed forms use their exact float32 values
+H, MASS, K, RHO0, MU = (float(np.float32(v)) for v in (0.025, 2e-5, 2000.0, 1000.0, 0.01))
+
+
+def prm(oracle, dims=(40, 40, 40)):
+    return oracle.sph_params(H, H, dims, MASS, K, RHO0, MU)
+
+
+def grid(oracle, x, y, z, dims=(40, 40, 40)):
+    st, si, _ = oracle.hashgrid_build(x, y, z, H, (0, 0, 0), dims)
+    return st, si
+
+
+def poly6(r):
+    return 315.0 / (64.0 * PI * H**9) * (H * H - r * r) ** 3 if r < H else 0.0
+
+
+def test_density_closed_forms(oracle):
+    # isolated particle: rho = m * W(0) = m * 315 / (64 pi h^3)
+    x, y, z = (np.array([0.5], np.float32),) * 3
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(prm(oracle), x, y, z, st, si)
+    assert rho[0] == pytest.approx(MASS * 315.0 / (64.0 * PI * H**3), rel=2e-6)
+    # two particles at distance d in neighbouring cells: rho = m (W(0) + W(d)) each
+    d = 0.6 * H
+    x = np.array([0.5 - 0.01, 0.5 - 0.01 + d], np.float32)
+    y = z = np.array([0.5, 0.5], np.float32)
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(prm(oracle), x, y, z, st, si)
+    dd = float(x[1]) - float(x[0])
+    assert rho == pytest.approx([MASS * (poly6(0) + poly6(dd))] * 2, rel=2e-6)
+    # at distance >= h the neighbour contributes nothing (strict r^2 < h^2)
+    x = np.array([0.5, 0.5 + H], np.float32)
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(prm(oracle), x, y, z, st, si)
+    assert rho == pytest.approx([MASS * poly6(0)] * 2, rel=2e-6)
+
+
+def test_density_vs_brute_force(oracle):
+    rng = np.random.default_rng(12)
+    p = rng.uniform(0.2, 0.5, (3000, 3)).astype(np.float32)
+    st, si = grid(oracle, p[:, 0], p[:, 1], p[:, 2])
+    rho = oracle.sph_density(prm(oracle), p[:, 0], p[:, 1], p[:, 2], st, si)
+    d = p[None, :, :].astype(np.float64) - p[:, None, :]
+    r2 = (d * d).sum(-1)
+    c = 315.0 / (64.0 * PI * H**9)
+    rho64 = MASS * c * np.where(r2 < H * H, (H * H - r2) ** 3, 0.0).sum(1)
+    assert np.allclose(rho, rho64, rtol=5e-5)
+
+
+def pair_accel(xi, xj, vi, vj, rho_i, rho_j):
+    """Mueller 2003 forms as the reference applies them: pressure with the spiky gradient
+    grad W = -45/(pi h^6) (h - r)^2 r_hat, symmetrised as -(m (p_i + p_j) / (2 rho_j)) grad W;
+    viscosity mu m (v_j - v_i) / rho_j * lap W with lap W = 45/(pi h^6) (h - r); both / rho_i."""
+    rv = np.asarray(xi, np.float64) - np.asarray(xj, np.float64)
+    r = np.linalg.norm(rv)
+    if not (r < H and r * r > 1e-12):
+        return np.zeros(3)
+    grad = -45.0 / (PI * H**6) * (H - r) ** 2 * rv / r
+    pi_, pj = K * (rho_i - RHO0), K * (rho_j - RHO0)
+    a_p = -MASS * (pi_ + pj) / (2.0 * rho_j) * grad
+    a_v = MU * MASS * (np.asarray(vj, np.float64) - vi) / rho_j * 45.0 / (PI * H**6) * (H - r)
+    return (a_p + a_v) / rho_i
+
+
+def test_force_closed_forms(oracle):
+    p = prm(oracle)
+    # isolated particle: no force
+    x = y = z = np.array([0.5], np.float32)
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(p, x, y, z, st, si)
+    _, acc = oracle.sph_force(p, x, y, z, x * 0 + 1, y * 0, z * 0, rho, st, si, 1e-4)
+    assert np.all(acc == 0)
+    # two particles with velocities: against the textbook pair terms
+    x = np.array([0.5, 0.512], np.float32)
+    y = np.array([0.4, 0.405], np.float32)
+    z = np.array([0.3, 0.296], np.float32)
+    vx, vy, vz = (np.array([0.1, -0.3], np.float32), np.array([0.0, 0.2], np.float32),
+                  np.array([0.5, 0.5], np.float32))
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(p, x, y, z, st, si)
+    vout, acc = oracle.sph_force(p, x, y, z, vx, vy, vz, rho, st, si, 1e-4)
+    a64, s64 = oracle.sph_force_f64(p, x, y, z, vx, vy, vz, rho, st, si)
+    for i, j in ((0, 1), (1, 0)):
+        exp = pair_accel((x[i], y[i], z[i]), (x[j], y[j], z[j]), (vx[i], vy[i], vz[i]),
+                         (vx[j], vy[j], vz[j]), float(rho[i]), float(rho[j]))
+        assert np.allclose(acc[:, i], exp, rtol=1e-5, atol=0)
+        assert np.allclose(a64[:, i], exp, rtol=1e-12, atol=0)
+        # attraction: rho << rho0 makes p negative, so particle i accelerates towards j
+        # (pressure part only: compare with zero velocities)
+    _, acc0 = oracle.sph_force(p, x, y, z, vx * 0, vy * 0, vz * 0, rho, st, si, 1e-4)
+    d01 = np.array([x[1] - x[0], y[1] - y[0], z[1] - z[0]], np.float64)
+    assert np.dot(acc0[:, 0], d01) > 0 and np.dot(acc0[:, 1], d01) < 0
+    # v_out = v + a dt
+    assert np.allclose(vout[0], vx + acc[0] * np.float32(1e-4), rtol=0, atol=1e-7)
+
+
+def test_force_vs_brute_force_and_f64(oracle):
+    rng = np.random.default_rng(14)
+    n = 2500
+    P = rng.uniform(0.3, 0.45, (n, 3)).astype(np.float32)
+    V = rng.uniform(-1, 1, (n, 3)).astype(np.float32)
+    p = prm(oracle)
+    st, si = grid(oracle, P[:, 0], P[:, 1], P[:, 2])
+    rho = oracle.sph_density(p, P[:, 0], P[:, 1], P[:, 2], st, si)
+    _, acc = oracle.sph_force(p, *P.T, *V.T, rho, st, si, 1e-4)
+    a64, s64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
+    bf = np.zeros((3, n))
+    for i in range(0, n, 97):  # brute force over all particles for a sample of i
+        for j in range(n):
+            if j != i:
+                bf[:, i] += pair_accel(P[i], P[j], V[i], V[j], float(rho[i]), float(rho[j]))
+        assert np.all(np.abs(bf[:, i] - a64[:, i]) <= 1e-9 * s64[:, i] + 1e-12)
+        assert np.all(np.abs(acc[:, i] - a64[:, i]) <= 1e-5 * s64[:, i] + 1e-12)
+
+
+def test_epilogue_closed_forms(oracle):
+    vx, vy, vz = (np.array([1.0, np.nan, -2.0], np.float32), np.array([0.0, 1.0, np.inf], np.float32),
+                  np.array([3.0, -1.0, 0.5], np.float32))
+    g, dt = (0.5, -9.81, 0.0), 0.01
+    v = oracle.gravity(vx, vy, vz, g, dt)
+    assert v[0][0] == np.float32(1.0) + np.float32(0.5) * np.float32(dt)
+    assert v[1][0] == np.float32(-9.81) * np.float32(dt)
+    x = np.array([0.5, 0.5, 0.5], np.float32)
+    s = oracle.integrate(x, x, x, vx, vy, vz, dt)
+    assert s[3][1] == 0.0 and s[0][1] == 0.5           # NaN velocity zeroed, no motion
+    assert s[4][2] == 0.0 and s[1][2] == 0.5           # inf likewise
+    assert s[0][0] == np.float32(0.5) + np.float32(1.0) * np.float32(dt)
+    b = oracle.box_collider(np.array([-0.1, 1.2, 0.5], np.float32), x, x,
+                            np.array([-2.0, 3.0, 1.0], np.float32), vy, vz, (0, 0, 0), (1, 1, 1), 0.3)
+    assert b[0].tolist() == [0.0, 1.0, 0.5]
+    assert b[3][0] == np.float32(2.0) * np.float32(0.3) and b[3][1] == -np.float32(3.0) * np.float32(0.3)
+
+
+def test_sph_step_is_the_module_sequence(oracle):
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=3000, cols=16)
+    rng = np.random.default_rng(3)
+    V = [rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
+    p = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                          cfg.rest_density, cfg.viscosity)
+    out = oracle.sph_step(p, 7, cfg.gravity, cfg.box_min, cfg.box_max, cfg.restitution,
+                          cfg.x, cfg.y, cfg.z, *V, cfg.dt)
+    st, si = grid(oracle, cfg.x, cfg.y, cfg.z, cfg.dims)
+    rho = oracle.sph_density(p, cfg.x, cfg.y, cfg.z, st, si)
+    vout, acc = oracle.sph_force(p, cfg.x, cfg.y, cfg.z, *V, rho, st, si, cfg.dt)
+    v = oracle.gravity(*vout, cfg.gravity, cfg.dt)
+    s = oracle.integrate(cfg.x, cfg.y, cfg.z, *v, cfg.dt)
+    s = oracle.box_collider(*s, cfg.box_min, cfg.box_max, cfg.restitution)
+    for a, b in zip(out[:6], s):
+        assert np.array_equal(a, b)
+    assert np.array_equal(out[6], rho) and np.array_equal(out[7], acc)
