@@ -93,7 +93,7 @@ hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float
                        const float* py, const float* pz, const float* vx, const float* vy,
                        const float* vz, uint32_t n, bool with_vel) {
     const uint32_t bits = bits_for_cells(cells);
-    hipError_t e = launch_begin(c);
+    hipError_t e = launch_begin(c, n, bits);
     if (e == hipSuccess) e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr);
     if (e == hipSuccess && n > 0)
         e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits);
@@ -114,6 +114,8 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (!out) return fail(FH_EINVAL, "fh_create: null out");
     *out = nullptr;
     if (max_n == 0 || max_cells == 0) return fail(FH_EINVAL, "fh_create: max_n and max_cells must be > 0");
+    if (max_n > kMaxSortN)
+        return fail(FH_ERANGE, "fh_create: max_n=%u exceeds the supported 2^30", max_n);
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
         return fail(FH_ENODEV, "fh_create: no HIP device");
@@ -139,6 +141,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->kb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->vb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)kMaxPasses * c->max_sort_tiles * 256u, &tot);
+    if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)kHistBlocks * kMaxPasses * 256u, &tot);
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
     if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);
@@ -163,7 +166,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     }
     // One-time clears (outside any capture): look-back words and run tags start untagged
     // (epoch 0 is never current).
-    if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)kMaxPasses * c->max_sort_tiles * 256u * 8u, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)kMaxPasses * c->max_sort_tiles * 256u * 4u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->scan_lb, 0, (size_t)c->max_scan_tiles * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->run_tag, 0, (size_t)max_cells * 8u, c->stream);
@@ -214,12 +217,12 @@ int fh_sync(fh_ctx* c) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (c->capturing) return fail(FH_ESTATE, "fh_sync: stream is being captured");
-    FH_CHECK_HIP(hipMemcpyAsync(c->h_error, &c->ctl->error, sizeof(uint32_t),
+    FH_CHECK_HIP(hipMemcpyAsync(c->h_error, &c->ctl->error.v, sizeof(uint32_t),
                                 hipMemcpyDeviceToHost, c->stream));
     FH_CHECK_HIP(hipStreamSynchronize(c->stream));
     if (*c->h_error) {
         uint32_t code = *c->h_error;
-        FH_CHECK_HIP(hipMemsetAsync(&c->ctl->error, 0, sizeof(uint32_t), c->stream));
+        FH_CHECK_HIP(hipMemsetAsync(&c->ctl->error.v, 0, sizeof(uint32_t), c->stream));
         FH_CHECK_HIP(hipStreamSynchronize(c->stream));
         return fail(FH_ESTATE, "fh_sync: device reported a look-back failure (code %u)", code);
     }
@@ -249,17 +252,11 @@ int fh_sort_pairs(fh_ctx* c, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_
         return fail(FH_EINVAL, "fh_sort_pairs: num_bits=%u outside 1..32", num_bits);
     if ((rc = check_n(c, n, "fh_sort_pairs"))) return rc;
     if (n < 2) return FH_OK;
-    FH_CHECK_HIP(launch_begin(c));
+    FH_CHECK_HIP(launch_begin(c, n, num_bits));
     FH_CHECK_HIP(launch_hist_keys(c, keys, n, num_bits));
-    if (passes_for_bits(num_bits) >= 2) {
-        // The last pass reads scratch and writes the caller's buffers: result in place.
-        FH_CHECK_HIP(launch_sort_passes(c, keys, vals, keys, vals, n, num_bits));
-    } else {
-        // A single pass cannot run in place; sort into scratch and copy back.
-        FH_CHECK_HIP(launch_sort_passes(c, keys, vals, c->ka, c->va, n, num_bits));
-        FH_CHECK_HIP(hipMemcpyAsync(keys, c->ka, (size_t)n * 4u, hipMemcpyDeviceToDevice, c->stream));
-        FH_CHECK_HIP(hipMemcpyAsync(vals, c->va, (size_t)n * 4u, hipMemcpyDeviceToDevice, c->stream));
-    }
+    // In place: the last pass that moves keys writes the caller's buffers (a single such pass
+    // writes scratch and the finishing kernel copies back).
+    FH_CHECK_HIP(launch_sort_passes(c, keys, vals, keys, vals, n, num_bits));
     return FH_OK;
 }
 
@@ -287,7 +284,7 @@ int fh_hashgrid_build(fh_ctx* c, const float* x, const float* y, const float* z,
     uint32_t cells;
     if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hashgrid_build"))) return rc;
     const uint32_t bits = bits_for_cells(cells);
-    FH_CHECK_HIP(launch_begin(c));
+    FH_CHECK_HIP(launch_begin(c, n, bits));
     FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr));
     if (n > 0) {
         FH_CHECK_HIP(launch_sort_passes(c, cell_indices, nullptr, c->skeys, sorted_indices, n, bits));

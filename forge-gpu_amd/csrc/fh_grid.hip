@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_starts(const uint64_t* __
     __shared__ uint32_t s_wave[4];
     __shared__ uint32_t s_prefix;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_tile = atomicAdd(&ctl->scan_ctr, 1u);
+    if (tid == 0) s_tile = atomicAdd(&ctl->scan_ctr.v, 1u);
     __syncthreads();
     const uint32_t tile = s_tile;
     const uint32_t epoch = ctl->epoch;
@@ -105,13 +105,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_starts(const uint64_t* __
                     prefix = min(prefix, (uint32_t)w);
                     if (st == kLbInclusive) break;
                     if (t == 0) {
-                        atomicOr(&ctl->error, 2u);
+                        atomicOr(&ctl->error.v, 2u);
                         break;
                     }
                     t--;
                 } else {
                     if (++spins >= kSpinLimit) {
-                        atomicOr(&ctl->error, 1u);
+                        atomicOr(&ctl->error.v, 1u);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);

@@ -12,17 +12,28 @@ namespace fh {
 
 // ---- sizes ----------------------------------------------------------------------------------
 constexpr int kWave = 64;              // CDNA wavefront
-constexpr int kSortThreads = 256;      // 4 waves per sort workgroup
+constexpr int kSortThreads = 512;      // 8 waves per sort workgroup
+constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kSortItems = 16;         // keys per thread per tile
-constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys per tile
+constexpr int kSortTile = kSortThreads * kSortItems;  // 8192 keys per tile
 constexpr int kMaxPasses = 4;          // 8-bit digits, up to 32-bit keys
+constexpr int kHistThreads = 256;
+constexpr int kHistItems = 16;
+constexpr int kHistChunk = kHistThreads * kHistItems;  // keys per histogram chunk
+constexpr int kHistBlocks = 1024;      // rows of per-block partial histograms
+constexpr int kHistRowsPerReduce = 8;  // partial rows summed by one reduce workgroup
+constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;  // 4096 cells per scan tile
 constexpr int kEvents = 16;
 
-// Look-back words: [63:62] status, [61:32] epoch, [31:0] value.  A word whose epoch differs
-// from the current one is "not ready", so the arrays never need clearing between calls.
+// Look-back words of the cell scan: [63:62] status, [61:32] epoch, [31:0] value.  A word whose
+// epoch differs from the current one is "not ready", so the array never needs clearing.
+// (The sort's look-back words are 32-bit, [31:30] status, [29:0] value, and are zeroed by
+// k_begin: half the bytes per poll, which is what the look-back walk is bound by.)
+constexpr uint32_t kLb32Aggregate = 1u << 30;
+constexpr uint32_t kLb32Inclusive = 2u << 30;
 constexpr uint64_t kLbAggregate = 1ull << 62;
 constexpr uint64_t kLbInclusive = 2ull << 62;
 constexpr uint32_t kEpochMask = 0x3FFFFFFFu;
@@ -30,14 +41,21 @@ constexpr uint32_t kEpochMask = 0x3FFFFFFFu;
 // every wave finite even if an invariant were broken (each poll sleeps ~64 clocks).
 constexpr uint32_t kSpinLimit = 1u << 22;
 
-// Device-side control block (one per context).
+// Device-side control block (one per context).  Every word that is the target of atomics from
+// many workgroups sits alone on its own 128-byte line: a line under atomic traffic that also
+// holds data every workgroup reads slows those reads down by tens of microseconds per kernel.
+struct Line {
+    uint32_t v;
+    uint32_t pad[31];
+};
 struct Control {
     uint32_t epoch;                     // bumped by k_begin before each sort / scan
-    uint32_t tile_ctr[kMaxPasses];      // dynamic tile ids of the sort passes
-    uint32_t scan_ctr;                  // dynamic tile id of the cell scan
-    uint32_t error;                     // nonzero: a look-back spin limit was hit
-    uint32_t heavy_count;               // entries in the heavy SPH work list of this substep
-    uint32_t pad[8];
+    uint32_t plan;                      // bit p: sort pass p moves keys (not all digits equal)
+    uint32_t pad0[30];
+    Line error;                         // nonzero: a look-back spin limit was hit
+    Line tile_ctr[kMaxPasses];          // dynamic tile ids of the sort passes
+    Line scan_ctr;                      // dynamic tile id of the cell scan
+    Line heavy_count;                   // entries in the heavy SPH work list of this substep
     uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
 };
 
@@ -72,7 +90,8 @@ struct fh_ctx {
     uint32_t* va;        // [max_n]
     uint32_t* kb;        // [max_n]
     uint32_t* vb;        // [max_n]
-    uint64_t* sort_lb;   // [kMaxPasses][max_sort_tiles][256]
+    uint32_t* sort_lb;   // [kMaxPasses][max_sort_tiles][256] 32-bit look-back words
+    uint32_t* hist_part; // [kHistBlocks][kMaxPasses * 256] per-block digit histograms
     fh::Control* ctl;    // device control block
     // grid scratch
     uint64_t* run_tag;     // [max_cells] epoch << 32 | first sorted index of the cell's run
@@ -142,20 +161,30 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int lane) {
     return v;
 }
 
-// Exclusive scan of one value per thread over a 256-thread workgroup; `sm` holds 4 words.
+// Exclusive scan of one value per thread over a workgroup of NW waves; `sm` holds NW words.
 // Returns the exclusive prefix; *total receives the workgroup sum.  Contains barriers: call
 // from uniform control flow only.
-__device__ __forceinline__ uint32_t block256_exclusive_scan(uint32_t v, uint32_t* sm,
-                                                            uint32_t* total) {
+template <int NW>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* sm,
+                                                         uint32_t* total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t inc = wave_inclusive_scan(v, lane);
+    const uint32_t inc = wave_inclusive_scan(v, lane);
     if (lane == 63) sm[wave] = inc;
     __syncthreads();
-    uint32_t w0 = sm[0], w1 = sm[1], w2 = sm[2], w3 = sm[3];
-    uint32_t before = (wave > 0 ? w0 : 0u) + (wave > 1 ? w1 : 0u) + (wave > 2 ? w2 : 0u);
-    *total = w0 + w1 + w2 + w3;
+    uint32_t before = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        const uint32_t x = sm[w];
+        if (w < wave) before += x;
+        sum += x;
+    }
+    *total = sum;
     __syncthreads();
     return before + inc - v;
+}
+__device__ __forceinline__ uint32_t block256_exclusive_scan(uint32_t v, uint32_t* sm,
+                                                            uint32_t* total) {
+    return block_exclusive_scan<4>(v, sm, total);
 }
 
 // Bracket a launch with the armed timer's events (no-op when the kernel is not armed).
@@ -173,18 +202,21 @@ inline void tend(fh_ctx* c, KernelId k) {
 
 // ---- launchers (host side, enqueue on ctx->stream; return hipError_t) ------------------------
 
-// Sort: bump epoch, clear histograms and tile counters.
-hipError_t launch_begin(fh_ctx* c);
-// Histogram of all digit passes of keys (from a key array).
+// Bump the epoch, clear histograms and counters, and zero the look-back words of a sort of n
+// keys with num_bits-bit digits (n = 0: no sort follows).
+hipError_t launch_begin(fh_ctx* c, uint32_t n, uint32_t num_bits);
+// Digit histograms of all passes of a num_bits sort of a key array (per-block partials, then
+// the reduce that also decides which passes move keys).
 hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits);
-// Hash particle positions: keys_out[i] = cell, vals_out[i] = i (if non-null) and the digit
-// histograms of all passes of a num_bits sort (none for num_bits = 0).
+// Hash particle positions: keys_out[i] = cell, vals_out[i] = i (if non-null) and, for
+// num_bits > 0, the digit histograms of all passes of a num_bits sort.
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
                             uint32_t* keys_out, uint32_t* vals_out);
-// Run the passes of a sort whose histograms are ready.  Pass 0 reads (k0, v0) (v0 == nullptr:
-// values are the indices 0..n-1); the last pass writes (kfin, vfin) (kfin may be null).
-// Intermediate passes ping-pong through the context's scratch.
+// Run a sort whose histograms are ready: reads (k0, v0) (v0 == nullptr: values are the indices
+// 0..n-1), leaves the result in (kfin, vfin).  kfin may equal k0 (in place) and may be null
+// (values only).  Passes whose digit is the same for every key are skipped on the device;
+// the others ping-pong through the context's scratch, and a final kernel copies when needed.
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits);
 // Mark the first index of every run of equal sorted keys in c->run_tag (epoch-tagged).
@@ -238,6 +270,6 @@ inline uint32_t bits_for_cells(uint32_t num_cells) {
     while (b < 32 && (1ull << b) < (uint64_t)num_cells) b++;
     return b;
 }
-inline uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
+__host__ __device__ inline uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
 
 }  // namespace fh

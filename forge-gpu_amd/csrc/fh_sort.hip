@@ -2,273 +2,477 @@
 //
 // Replaces RadixSorter::sort (forge-runtime/src/radix_sort.rs:79-220), whose 4-bit passes
 // re-read every earlier block's histogram per block and every earlier key per key.  Design:
-//   k_begin        bump the look-back epoch, clear the digit histograms and tile counters
-//   k_hist_keys /  one read of the keys builds the 256-bin histograms of ALL 8-bit passes
-//   k_hash_hist    (k_hash_hist computes the keys from positions on the fly: the hash of
-//                  HashGrid::build, hashgrid.rs:89-92, fused with the histogram)
-//   k_onesweep     one kernel per 8-bit pass: a 4096-key tile per workgroup, ranked with
-//                  64-lane ballot match-any, digit offsets from a decoupled look-back over
-//                  dynamically numbered tiles, then staged in LDS in digit order so the
-//                  global scatter writes contiguous runs.
+//   k_begin        bump the look-back epoch, clear histograms and counters, zero the 32-bit
+//                  look-back words of the coming sort
+//   k_hist_keys /  one read of the keys builds the 256-bin histograms of ALL 8-bit passes into
+//   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
+//                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
+//   k_hist_reduce  sums the partial rows into the histograms
+//   k_sort_plan    marks which passes move keys (a pass whose digit is equal for every key is
+//                  the identity and is skipped)
+//   k_onesweep     one kernel per 8-bit pass: an 8192-key tile per 512-lane workgroup, ranked
+//                  with 64-lane ballot match-any, digit offsets from a decoupled look-back over
+//                  dynamically numbered tiles, then staged in LDS in digit order (keys, then
+//                  values through the same buffer) so the global scatter writes contiguous runs
+//   k_sort_finish  copies the result into place when the number of passes that moved keys
+//                  left it in scratch
 // Stability: within a tile the rank of a key counts the equal digits before it in input order
 // (earlier items, earlier lanes, earlier waves); across tiles the look-back prefix counts the
 // equal digits of all earlier tiles.  Equal keys therefore keep their input order, which is
 // the `sort_by_key` contract of tests/radix_sort_test.rs:111-127.
+//
+// Device-wide atomics are performed past the per-XCD L2 on this part, so the design keeps them
+// few and apart: per-workgroup histogram rows instead of global bin atomics, 32-bit look-back
+// words (a poll moves half the bytes of a 64-bit epoch word), and every hot counter on a line
+// of its own (Control).
 #include "fh_internal.hpp"
 
 namespace fh {
 
 // ---------------------------------------------------------------------------------------------
-__global__ void k_begin(Control* ctl) {
-    const int t = threadIdx.x;
-    for (int i = t; i < kMaxPasses * 256; i += blockDim.x) (&ctl->hist[0][0])[i] = 0u;
-    if (t == 0) {
-        uint32_t e = (ctl->epoch + 1u) & kEpochMask;
-        ctl->epoch = e ? e : 1u;
-        for (int p = 0; p < kMaxPasses; p++) ctl->tile_ctr[p] = 0u;
-        ctl->scan_ctr = 0u;
-        ctl->heavy_count = 0u;
+__global__ void k_begin(Control* ctl, uint32_t* __restrict__ lb, uint32_t lb_words) {
+    const uint32_t t = threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (uint32_t i = t; i < (uint32_t)kMaxPasses * 256u; i += blockDim.x)
+            (&ctl->hist[0][0])[i] = 0u;
+        if (t == 0) {
+            uint32_t e = (ctl->epoch + 1u) & kEpochMask;
+            ctl->epoch = e ? e : 1u;
+            ctl->plan = 0u;
+            for (int p = 0; p < kMaxPasses; p++) ctl->tile_ctr[p].v = 0u;
+            ctl->scan_ctr.v = 0u;
+            ctl->heavy_count.v = 0u;
+        }
     }
+    for (uint32_t i = blockIdx.x * blockDim.x + t; i < lb_words; i += gridDim.x * blockDim.x)
+        lb[i] = 0u;
 }
 
-hipError_t launch_begin(fh_ctx* c) {
+hipError_t launch_begin(fh_ctx* c, uint32_t n, uint32_t num_bits) {
+    const uint32_t words = n ? passes_for_bits(num_bits) * ceil_div(n, (uint32_t)kSortTile) * 256u : 0u;
+    uint32_t blocks = ceil_div(words, 256u * 4u);
+    if (blocks < 1) blocks = 1;
+    if (blocks > 1024) blocks = 1024;
     tbeg(c, KID_BEGIN);
-    k_begin<<<1, 256, 0, c->stream>>>(c->ctl);
+    k_begin<<<blocks, 256, 0, c->stream>>>(c->ctl, c->sort_lb, words);
     tend(c, KID_BEGIN);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------------
-// Add one digit per lane to a per-wave LDS histogram.  When the whole wave holds the same digit
-// (skewed top digits: c1's top byte is always 0) one lane adds the population instead of 64
-// conflicting LDS atomics.
-__device__ __forceinline__ void wave_hist_add(uint32_t* h, uint32_t d, bool valid) {
-    uint64_t act = __ballot(valid);
-    if (act == 0) return;
-    uint32_t d0 = __shfl(d, __ffsll((unsigned long long)act) - 1, kWave);
-    bool same = __all(!valid || d == d0);
-    if (same) {
-        if ((threadIdx.x & 63) == __ffsll((unsigned long long)act) - 1)
-            atomicAdd(&h[d0], (uint32_t)__popcll(act));
+// Histograms.  Each workgroup counts into per-wave LDS histograms; a wave whose valid lanes all
+// hold the same digit (skewed digits: c1's top byte is always 0) adds its population with one
+// LDS atomic instead of 64 conflicting ones.  Digit p of key k is (k >> 8p) & mask_p.
+__device__ __forceinline__ void hist_add(uint32_t* h, uint32_t d, bool valid) {
+    const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
+    const uint64_t other = __ballot(valid && d != d0);
+    if (other == 0ull) {
+        const uint64_t act = __ballot(valid);
+        if ((threadIdx.x & 63u) == 0u && act) atomicAdd(&h[d0], (uint32_t)__popcll(act));
     } else if (valid) {
         atomicAdd(&h[d], 1u);
     }
 }
 
-// Shared tail of the histogram kernels: reduce the 4 per-wave histograms and add the nonzero
-// bins to the global ones.
-__device__ __forceinline__ void flush_hist(uint32_t (*sh)[kMaxPasses][256], Control* ctl,
-                                           uint32_t passes) {
-    __syncthreads();
-    for (uint32_t p = 0; p < passes; p++) {
-        uint32_t d = threadIdx.x;  // 256 threads, one bin each
-        uint32_t s = sh[0][p][d] + sh[1][p][d] + sh[2][p][d] + sh[3][p][d];
-        if (s) atomicAdd(&ctl->hist[p][d], s);
-    }
+// P = number of passes (compile time, so the pass loop unrolls); top = mask of the last pass.
+template <int P>
+__device__ __forceinline__ void count_key(uint32_t (*sh)[256], uint32_t k, bool valid,
+                                          uint32_t top) {
+#pragma unroll
+    for (int p = 0; p < P; p++)
+        hist_add(sh[p], (k >> (8 * p)) & (p == P - 1 ? top : 255u), valid);
 }
 
-__global__ __launch_bounds__(256) void k_hist_keys(const uint32_t* __restrict__ keys, uint32_t n,
-                                                   uint32_t num_bits, Control* ctl) {
-    __shared__ uint32_t sh[4][kMaxPasses][256];
-    const int wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < 4 * kMaxPasses * 256; i += 256) (&sh[0][0][0])[i] = 0u;
+// Write this workgroup's row of partial histograms (all 256 bins of every pass).
+__device__ __forceinline__ void write_row(uint32_t (*sh)[kMaxPasses][256], uint32_t* part,
+                                          uint32_t passes) {
     __syncthreads();
-    const uint32_t passes = passes_for_bits(num_bits);
-    const uint32_t stride = gridDim.x * 256u;
-    // Trip count is uniform across the block (it depends only on the loop base).
-    for (uint32_t base = blockIdx.x * 256u; base < n; base += stride) {
-        uint32_t i = base + threadIdx.x;
-        bool valid = i < n;
-        uint32_t k = valid ? keys[i] : 0u;
-        for (uint32_t p = 0; p < passes; p++) {
-            uint32_t bits = min(8u, num_bits - 8u * p);
-            uint32_t d = (k >> (8u * p)) & ((1u << bits) - 1u);
-            wave_hist_add(sh[wave][p], d, valid);
+    const uint32_t d = threadIdx.x;  // kHistThreads == 256: one bin per thread
+    for (uint32_t p = 0; p < passes; p++)
+        part[(size_t)blockIdx.x * (kMaxPasses * 256u) + p * 256u + d] =
+            sh[0][p][d] + sh[1][p][d] + sh[2][p][d] + sh[3][p][d];
+}
+
+template <int P>
+__global__ __launch_bounds__(kHistThreads) void k_hist_keys(const uint32_t* __restrict__ keys,
+                                                            uint32_t n, uint32_t top,
+                                                            uint32_t* __restrict__ part) {
+    __shared__ uint32_t sh[4][kMaxPasses][256];
+    const uint32_t wave = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < 4u * kMaxPasses * 256u; i += kHistThreads)
+        (&sh[0][0][0])[i] = 0u;
+    __syncthreads();
+    const uint32_t chunks = ceil_div(n, (uint32_t)kHistChunk);
+    // Striped chunk loads (item j of thread t is key base + 256 j + t); the loads of the next
+    // chunk are issued before the current one is counted.
+    uint32_t cur[kHistItems], nxt[kHistItems];
+    uint32_t c = blockIdx.x;
+#pragma unroll
+    for (int j = 0; j < kHistItems; j++) {
+        const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
+        cur[j] = (c < chunks && i < n) ? keys[i] : 0u;
+    }
+    for (; c < chunks; c += gridDim.x) {
+        const uint32_t cn = c + gridDim.x;
+#pragma unroll
+        for (int j = 0; j < kHistItems; j++) {
+            const uint32_t i = cn * kHistChunk + j * kHistThreads + threadIdx.x;
+            nxt[j] = (cn < chunks && i < n) ? keys[i] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kHistItems; j++) {
+            const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
+            count_key<P>(sh[wave], cur[j], i < n, top);
+        }
+#pragma unroll
+        for (int j = 0; j < kHistItems; j++) cur[j] = nxt[j];
+    }
+    write_row(sh, part, P);
+}
+
+template <int P>
+__global__ __launch_bounds__(kHistThreads) void k_hash_hist(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ z,
+    uint32_t stride, uint32_t n, GridDesc g, uint32_t top, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, uint32_t* __restrict__ part) {
+    __shared__ uint32_t sh[4][kMaxPasses][256];
+    const uint32_t wave = threadIdx.x >> 6;
+    if (P > 0) {
+        for (uint32_t i = threadIdx.x; i < 4u * kMaxPasses * 256u; i += kHistThreads)
+            (&sh[0][0][0])[i] = 0u;
+        __syncthreads();
+    }
+    const uint32_t chunks = ceil_div(n, (uint32_t)kHistChunk);
+    for (uint32_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        uint32_t k[kHistItems];
+#pragma unroll
+        for (int j = 0; j < kHistItems; j++) {
+            const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
+            k[j] = 0u;
+            if (i < n) {
+                const size_t o = (size_t)i * stride;
+                k[j] = cell_of(x[o], y[o], z[o], g);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kHistItems; j++) {
+            const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
+            if (i < n) {
+                if (keys_out) keys_out[i] = k[j];
+                if (vals_out) vals_out[i] = i;
+            }
+            if (P > 0) count_key<P>(sh[wave], k[j], i < n, top);
         }
     }
-    flush_hist(sh, ctl, passes);
+    if (P > 0) write_row(sh, part, P);
 }
 
-hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits) {
-    uint32_t blocks = ceil_div(n, 256u * 16u);
-    if (blocks < 1) blocks = 1;
-    if (blocks > 2048) blocks = 2048;
-    tbeg(c, KID_HIST);
-    k_hist_keys<<<blocks, 256, 0, c->stream>>>(keys, n, num_bits, c->ctl);
-    tend(c, KID_HIST);
+// Sum the partial rows: workgroup (p, r) adds rows r*R .. r*R+R-1 of pass p into the global
+// histogram.  (No fence / last-workgroup election here: an agent-scope release on this part
+// writes the L2 back, which costs tens of microseconds per workgroup; the decision about the
+// passes is a separate one-workgroup kernel, the kernel boundary gives the visibility.)
+__global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict__ part,
+                                                     uint32_t rows, Control* ctl) {
+    const uint32_t d = threadIdx.x;
+    const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
+    const uint32_t p = blockIdx.x / groups, r0 = (blockIdx.x % groups) * kHistRowsPerReduce;
+    const uint32_t r1 = min(rows, r0 + (uint32_t)kHistRowsPerReduce);
+    uint32_t s = 0;
+#pragma unroll 8
+    for (uint32_t r = r0; r < r1; r++) s += part[(size_t)r * (kMaxPasses * 256u) + p * 256u + d];
+    if (s) atomicAdd(&ctl->hist[p][d], s);
+}
+
+// Decide which passes move keys: a pass whose digit is equal for every key is the identity.
+__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t n, Control* ctl) {
+    __shared__ uint32_t s_trivial[kMaxPasses];
+    const uint32_t d = threadIdx.x;
+    if (d < kMaxPasses) s_trivial[d] = 0u;
+    __syncthreads();
+    for (uint32_t q = 0; q < passes; q++)
+        if (ctl->hist[q][d] == n) s_trivial[q] = 1u;
+    __syncthreads();
+    if (d == 0) {
+        uint32_t plan = 0;
+        for (uint32_t q = 0; q < passes; q++)
+            if (!s_trivial[q]) plan |= 1u << q;
+        ctl->plan = plan;
+    }
+}
+
+hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t passes, uint32_t n) {
+    const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
+    k_hist_reduce<<<passes * groups, 256, 0, c->stream>>>(c->hist_part, rows, c->ctl);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_sort_plan<<<1, 256, 0, c->stream>>>(passes, n, c->ctl);
     return hipGetLastError();
 }
 
-__global__ __launch_bounds__(256) void k_hash_hist(const float* __restrict__ x,
-                                                   const float* __restrict__ y,
-                                                   const float* __restrict__ z, uint32_t stride,
-                                                   uint32_t n, GridDesc g, uint32_t num_bits,
-                                                   uint32_t* __restrict__ keys_out,
-                                                   uint32_t* __restrict__ vals_out,
-                                                   Control* ctl) {
-    __shared__ uint32_t sh[4][kMaxPasses][256];
-    const int wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < 4 * kMaxPasses * 256; i += 256) (&sh[0][0][0])[i] = 0u;
-    __syncthreads();
-    const uint32_t passes = passes_for_bits(num_bits);
-    const uint32_t gstride = gridDim.x * 256u;
-    for (uint32_t base = blockIdx.x * 256u; base < n; base += gstride) {
-        uint32_t i = base + threadIdx.x;
-        bool valid = i < n;
-        uint32_t k = 0;
-        if (valid) {
-            size_t o = (size_t)i * stride;
-            k = cell_of(x[o], y[o], z[o], g);
-            if (keys_out) keys_out[i] = k;
-            if (vals_out) vals_out[i] = i;
-        }
-        for (uint32_t p = 0; p < passes; p++) {
-            uint32_t bits = min(8u, num_bits - 8u * p);
-            uint32_t d = (k >> (8u * p)) & ((1u << bits) - 1u);
-            wave_hist_add(sh[wave][p], d, valid);
-        }
+static uint32_t hist_blocks(uint32_t n) {
+    uint32_t b = ceil_div(n, (uint32_t)kHistChunk);
+    if (b < 1) b = 1;
+    if (b > (uint32_t)kHistBlocks) b = kHistBlocks;
+    return b;
+}
+
+// Mask of the digit of the last pass of a num_bits sort.
+static uint32_t top_mask(uint32_t num_bits) {
+    const uint32_t b = num_bits - 8u * (passes_for_bits(num_bits) - 1u);
+    return (1u << b) - 1u;
+}
+
+hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits) {
+    const uint32_t blocks = hist_blocks(n), top = top_mask(num_bits);
+    tbeg(c, KID_HIST);
+    switch (passes_for_bits(num_bits)) {
+        case 1: k_hist_keys<1><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
+        case 2: k_hist_keys<2><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
+        case 3: k_hist_keys<3><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
+        default: k_hist_keys<4><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
     }
-    flush_hist(sh, ctl, passes);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits), n);
+    tend(c, KID_HIST);
+    return e;
 }
 
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
                             uint32_t* keys_out, uint32_t* vals_out) {
-    uint32_t blocks = ceil_div(n, 256u * 8u);
-    if (blocks < 1) blocks = 1;
-    if (blocks > 2048) blocks = 2048;
+    const uint32_t blocks = hist_blocks(n), top = num_bits ? top_mask(num_bits) : 0u;
+    uint32_t* part = c->hist_part;
     tbeg(c, KID_HASH);
-    k_hash_hist<<<blocks, 256, 0, c->stream>>>(x, y, z, stride, n, g, num_bits, keys_out,
-                                               vals_out, c->ctl);
+    switch (passes_for_bits(num_bits)) {
+        case 0: k_hash_hist<0><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
+        case 1: k_hash_hist<1><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
+        case 2: k_hash_hist<2><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
+        case 3: k_hash_hist<3><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
+        default: k_hash_hist<4><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && num_bits > 0)
+        e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits), n);
     tend(c, KID_HASH);
-    return hipGetLastError();
+    return e;
 }
 
 // ---------------------------------------------------------------------------------------------
-// One 8-bit (or narrower, for the last pass) digit pass.
-__global__ __launch_bounds__(kSortThreads) void k_onesweep(
-    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
-    uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, Control* ctl, uint32_t pass,
-    uint64_t* __restrict__ lookback, uint32_t n, uint32_t shift, uint32_t pbits) {
-    __shared__ uint32_t s_keys[kSortTile];
-    __shared__ uint32_t s_vals[kSortTile];
-    __shared__ uint32_t s_wcnt[4][256];  // per-wave digit counts, then per-wave digit offsets
-    __shared__ uint32_t s_dstart[256];   // first slot of digit d in the tile's digit order
-    __shared__ uint32_t s_gbase[256];    // global index of slot 0 of digit d's run, minus s_dstart
-    __shared__ uint32_t s_scan[4];
+// Buffers of one sort.  Pass j of the passes that move keys (those in ctl->plan) reads the
+// output of pass j-1 (pass 0: k0 / v0) and writes, alternately, scratch a and b; the last one
+// writes (kfin, vfin) unless it reads kfin itself (a single pass in place), in which case it
+// writes a and k_sort_finish copies back.
+struct SortIO {
+    const uint32_t* k0;
+    const uint32_t* v0;  // null: values are the indices 0..n-1
+    uint32_t* ka;
+    uint32_t* va;
+    uint32_t* kb;
+    uint32_t* vb;
+    uint32_t* kfin;      // null: keys are not needed in the output
+    uint32_t* vfin;
+};
+
+struct PassBufs {
+    const uint32_t* kin;
+    const uint32_t* vin;
+    uint32_t* kout;
+    uint32_t* vout;
+};
+
+__device__ __forceinline__ PassBufs pass_bufs(SortIO io, uint32_t plan, uint32_t pass) {
+    const uint32_t j = (uint32_t)__popc(plan & ((1u << pass) - 1u));
+    const bool last = (plan >> (pass + 1u)) == 0u;
+    PassBufs b;
+    b.kin = j == 0 ? io.k0 : ((j & 1u) ? io.ka : io.kb);
+    b.vin = j == 0 ? io.v0 : ((j & 1u) ? io.va : io.vb);
+    if (last && !(j == 0 && io.kfin == io.k0 && io.kfin)) {
+        b.kout = io.kfin;
+        b.vout = io.vfin;
+    } else {
+        b.kout = (j & 1u) ? io.kb : io.ka;
+        b.vout = (j & 1u) ? io.vb : io.va;
+    }
+    return b;
+}
+
+// Branch-free 64-lane match of an 8-bit digit: bit l of the result is set iff lane l holds the
+// same digit.  m is 0 or all ones per lane (sign-extended digit bit); ~(ballot ^ m) keeps the
+// lanes that agree with this lane on that bit.
+__device__ __forceinline__ void match8(uint32_t d, uint32_t& lo, uint32_t& hi) {
+    lo = 0xFFFFFFFFu;
+    hi = 0xFFFFFFFFu;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const int32_t m = ((int32_t)(d << (31 - b))) >> 31;
+        const uint64_t bal = __ballot(m != 0);
+        lo &= ~((uint32_t)bal ^ (uint32_t)m);
+        hi &= ~((uint32_t)(bal >> 32) ^ (uint32_t)m);
+    }
+}
+
+__global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control* ctl,
+                                                              uint32_t pass,
+                                                              uint32_t* __restrict__ lookback,
+                                                              uint32_t n, uint32_t shift,
+                                                              uint32_t pbits) {
+    __shared__ uint32_t s_buf[kSortTile];
+    __shared__ uint32_t s_wcnt[kSortWaves][256];  // per-wave digit counts, then wave offsets
+    __shared__ uint32_t s_gbase[256];             // global index of tile slot 0 of digit d
+    __shared__ uint32_t s_scan[kSortWaves];
     __shared__ uint32_t s_tile;
+
+    const uint32_t plan = ctl->plan;
+    if (!((plan >> pass) & 1u)) return;  // every key has the same digit: identity pass
+    const PassBufs bf = pass_bufs(io, plan, pass);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t mask = (1u << pbits) - 1u;
-    if (tid == 0) s_tile = atomicAdd(&ctl->tile_ctr[pass], 1u);
-    for (int i = tid; i < 4 * 256; i += kSortThreads) (&s_wcnt[0][0])[i] = 0u;
+    if (tid == 0) s_tile = atomicAdd(&ctl->tile_ctr[pass].v, 1u);
+    for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_wcnt[0][0])[i] = 0u;
     __syncthreads();
     const uint32_t tile = s_tile;
-    const uint32_t epoch = ctl->epoch;
     const uint32_t tile_base = tile * (uint32_t)kSortTile;
     const uint32_t wbase = tile_base + (uint32_t)wave * (kWave * kSortItems);
 
-    // Striped load: item k of lane l is element wbase + 64k + l, so (k, l) order = input order.
-    uint32_t keys[kSortItems], vals[kSortItems], rank[kSortItems];
+    // Striped key loads: item k of lane l is element wbase + 64k + l, so (k, l) order = input
+    // order.  Slots past n hold digit `mask` and rank after every real key of the tile.
+    uint32_t keys[kSortItems], vals[kSortItems], pos[kSortItems];
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) {
-        uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
-        bool v = idx < n;
-        keys[k] = v ? kin[idx] : 0u;
-        vals[k] = v ? (vin ? vin[idx] : idx) : 0u;
+        const uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
+        keys[k] = idx < n ? bf.kin[idx] : 0xFFFFFFFFu;
     }
-
-    // Rank within the wave.  Out-of-range slots take the largest digit so they sort after every
-    // real key of the tile and never shift a real key's rank.
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t lt_lo = lane >= 32 ? 0xFFFFFFFFu : ((1u << lane) - 1u);
+    const uint32_t lt_hi = lane <= 32 ? 0u : (0xFFFFFFFFu >> (64 - lane));
+    const uint32_t gt_lo = lane >= 31 ? 0u : (0xFFFFFFFFu << (lane + 1));
+    const uint32_t gt_hi = lane < 31 ? 0xFFFFFFFFu : (lane == 63 ? 0u : (0xFFFFFFFFu << (lane - 31)));
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) {
-        uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
-        uint32_t d = idx < n ? (keys[k] >> shift) & mask : mask;
-        uint64_t peers = ~0ull;
-        for (uint32_t b = 0; b < pbits; b++) {
-            bool bit = (d >> b) & 1u;
-            uint64_t bal = __ballot(bit);
-            peers &= bit ? bal : ~bal;
-        }
-        uint32_t before = s_wcnt[wave][d];
-        uint32_t below = (uint32_t)__popcll(peers & lt);
-        bool leader = (peers >> lane) == 1ull;  // highest lane of its digit group
-        rank[k] = before + below;
-        if (leader) s_wcnt[wave][d] = before + (uint32_t)__popcll(peers);
+        const uint32_t d = (keys[k] >> shift) & mask;
+        uint32_t lo, hi;
+        match8(d, lo, hi);
+        const uint32_t before = s_wcnt[wave][d];
+        pos[k] = before + (uint32_t)(__popc(lo & lt_lo) + __popc(hi & lt_hi));
+        if (((lo & gt_lo) | (hi & gt_hi)) == 0u)  // highest lane of its digit group
+            s_wcnt[wave][d] = before + (uint32_t)(__popc(lo) + __popc(hi));
+        // Materialise the rank here: left alone, the compiler defers the popcounts to the
+        // staging loop and keeps every item's 64-bit match mask alive across the look-back
+        // (32 extra VGPRs, one workgroup less per CU).
+        asm volatile("" : "+v"(pos[k]));
     }
     __syncthreads();
 
-    // Per digit (one thread each): tile count, per-wave offsets, tile-local digit start, global
-    // digit start, look-back.
-    const uint32_t d = (uint32_t)tid;
-    uint32_t c0 = s_wcnt[0][d], c1 = s_wcnt[1][d], c2 = s_wcnt[2][d], c3 = s_wcnt[3][d];
-    uint32_t cnt = c0 + c1 + c2 + c3;
-    uint64_t* my = lookback + (size_t)tile * 256u + d;
-    if (tile == 0) lb_store(my, lb_word(kLbInclusive, epoch, cnt));
-    else lb_store(my, lb_word(kLbAggregate, epoch, cnt));
-    __syncthreads();  // everyone has read s_wcnt before it is overwritten
-    s_wcnt[0][d] = 0u;
-    s_wcnt[1][d] = c0;
-    s_wcnt[2][d] = c0 + c1;
-    s_wcnt[3][d] = c0 + c1 + c2;
+    // Per digit (threads 0..255): tile count and aggregate, wave offsets, tile-local digit
+    // start, global digit start, look-back.
+    const uint32_t d = (uint32_t)tid & 255u;
+    uint32_t cnt = 0, wc[kSortWaves];
+    if (tid < 256) {
+#pragma unroll
+        for (int w = 0; w < kSortWaves; w++) {
+            wc[w] = s_wcnt[w][d];
+            cnt += wc[w];
+        }
+        __hip_atomic_store(lookback + (size_t)tile * 256u + d,
+                           (tile == 0 ? kLb32Inclusive : kLb32Aggregate) | cnt,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     uint32_t total;
-    uint32_t dstart = block256_exclusive_scan(cnt, s_scan, &total);
-    uint32_t ghist = d <= mask ? ctl->hist[pass][d] : 0u;
-    uint32_t gstart = block256_exclusive_scan(ghist, s_scan, &total);
+    const uint32_t dstart = block_exclusive_scan<kSortWaves>(tid < 256 ? cnt : 0u, s_scan, &total);
+    if (tid < 256) {
+        uint32_t run = dstart;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; w++) {
+            s_wcnt[w][d] = run;
+            run += wc[w];
+        }
+    }
+    const uint32_t ghist = (tid < 256 && d <= mask) ? ctl->hist[pass][d] : 0u;
+    const uint32_t gstart = block_exclusive_scan<kSortWaves>(ghist, s_scan, &total);
 
     uint32_t prefix = 0;
-    if (tile > 0) {
+    if (tid < 256 && tile > 0) {
         uint32_t t = tile - 1u, spins = 0;
         for (;;) {
-            uint64_t w = lb_load(lookback + (size_t)t * 256u + d);
-            uint64_t st = w & (3ull << 62);
-            if (st != 0 && ((uint32_t)(w >> 32) & kEpochMask) == epoch) {
-                prefix += (uint32_t)w;
-                if (st == kLbInclusive) break;
+            const uint32_t w = __hip_atomic_load(lookback + (size_t)t * 256u + d,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t st = w & (3u << 30);
+            if (st != 0u) {
+                prefix += w & 0x3FFFFFFFu;
+                if (st == kLb32Inclusive) break;
                 if (t == 0) {  // tile 0 always publishes inclusive; never walk below it
-                    atomicOr(&ctl->error, 2u);
+                    atomicOr(&ctl->error.v, 2u);
                     break;
                 }
                 t--;
             } else {
                 if (++spins >= kSpinLimit) {
-                    atomicOr(&ctl->error, 1u);
+                    atomicOr(&ctl->error.v, 1u);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
         }
-        lb_store(my, lb_word(kLbInclusive, epoch, prefix + cnt));
+        __hip_atomic_store(lookback + (size_t)tile * 256u + d, kLb32Inclusive | (prefix + cnt),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    s_dstart[d] = dstart;
-    s_gbase[d] = gstart + prefix - dstart;
+    if (tid < 256) s_gbase[d] = gstart + prefix - dstart;
     __syncthreads();
 
-    // Stage the tile in digit order.
+    // Stage the keys in digit order, scatter them; then the values through the same buffer.
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) {
-        uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
-        uint32_t dk = idx < n ? (keys[k] >> shift) & mask : mask;
-        uint32_t pos = s_dstart[dk] + s_wcnt[wave][dk] + rank[k];
-        s_keys[pos] = keys[k];
-        s_vals[pos] = vals[k];
+        pos[k] += s_wcnt[wave][(keys[k] >> shift) & mask];
+        s_buf[pos[k]] = keys[k];
     }
     __syncthreads();
-
-    // Coalesced scatter: consecutive slots of one digit go to consecutive global indices.
-    const uint32_t valid = n - tile_base < (uint32_t)kSortTile ? n - tile_base : (uint32_t)kSortTile;
+    const uint32_t valid = min(n - tile_base, (uint32_t)kSortTile);
+    uint32_t dst[kSortItems];
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) {
-        uint32_t i = (uint32_t)(k * kSortThreads + tid);
-        if (i < valid) {
-            uint32_t key = s_keys[i];
-            uint32_t dst = s_gbase[(key >> shift) & mask] + i;
-            if (dst < n) {  // always true when the histograms are consistent
-                if (kout) kout[dst] = key;
-                vout[dst] = s_vals[i];
-            }
-        }
+        const uint32_t i = (uint32_t)(k * kSortThreads + tid);
+        const uint32_t key = s_buf[i];
+        dst[k] = s_gbase[(key >> shift) & mask] + i;
+        if (i < valid && dst[k] < n && bf.kout) bf.kout[dst[k]] = key;
+    }
+    // Values are loaded only now: holding them through ranking and look-back would cost 16
+    // VGPRs and with them a third workgroup per CU; the other workgroups hide the latency.
+#pragma unroll
+    for (int k = 0; k < kSortItems; k++) {
+        const uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
+        vals[k] = idx < n ? (bf.vin ? bf.vin[idx] : idx) : 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kSortItems; k++) s_buf[pos[k]] = vals[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kSortItems; k++) {
+        const uint32_t i = (uint32_t)(k * kSortThreads + tid);
+        if (i < valid && dst[k] < n) bf.vout[dst[k]] = s_buf[i];
+    }
+}
+
+// When no pass moved keys the input is the result; when one pass ran in place it wrote
+// scratch.  Copy into (kfin, vfin) in those cases; otherwise do nothing.
+__global__ __launch_bounds__(256) void k_sort_finish(SortIO io, const Control* ctl, uint32_t n) {
+    const uint32_t plan = ctl->plan;
+    const uint32_t moved = (uint32_t)__popc(plan);
+    const uint32_t* ks;
+    const uint32_t* vs;
+    if (moved == 0u) {
+        ks = io.k0;
+        vs = io.v0;
+        if (ks == io.kfin && vs == io.vfin && vs) return;
+    } else if (moved == 1u && io.kfin && io.kfin == io.k0) {
+        ks = io.ka;
+        vs = io.va;
+    } else {
+        return;
+    }
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
+        if (io.kfin && io.kfin != ks) io.kfin[i] = ks[i];
+        io.vfin[i] = vs ? vs[i] : i;
     }
 }
 
@@ -276,24 +480,21 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits) {
     const uint32_t passes = passes_for_bits(num_bits);
     const uint32_t tiles = ceil_div(n, (uint32_t)kSortTile);
-    const uint32_t* kin = k0;
-    const uint32_t* vin = v0;
+    SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin};
     for (uint32_t p = 0; p < passes; p++) {
-        bool last = p + 1 == passes;
-        uint32_t* kout = last ? kfin : ((p & 1u) ? c->kb : c->ka);
-        uint32_t* vout = last ? vfin : ((p & 1u) ? c->vb : c->va);
-        uint32_t pbits = min(8u, num_bits - 8u * p);
-        uint64_t* lb = c->sort_lb + (size_t)p * c->max_sort_tiles * 256u;
+        const uint32_t pbits = min(8u, num_bits - 8u * p);
+        uint32_t* lb = c->sort_lb + (size_t)p * tiles * 256u;
         tbeg(c, KID_SORT);
-        k_onesweep<<<tiles, kSortThreads, 0, c->stream>>>(kin, vin, kout, vout, c->ctl, p, lb, n,
-                                                          8u * p, pbits);
+        k_onesweep<<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb, n, 8u * p, pbits);
         tend(c, KID_SORT);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        kin = kout;
-        vin = vout;
     }
-    return hipSuccess;
+    uint32_t blocks = ceil_div(n, 256u * 8u);
+    if (blocks > 1024) blocks = 1024;
+    if (blocks < 1) blocks = 1;
+    k_sort_finish<<<blocks, 256, 0, c->stream>>>(io, c->ctl, n);
+    return hipGetLastError();
 }
 
 }  // namespace fh

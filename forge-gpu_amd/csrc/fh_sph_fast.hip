@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void k_plan(const float4* __restrict__ spos, u
             const uint32_t item = sub * 3u + (uint32_t)slab;
             const bool hv = w > kHeavyWork;
             flag[item] = hv ? 1 : 0;
-            if (hv) heavy[atomicAdd(&ctl->heavy_count, 1u)] = item;
+            if (hv) heavy[atomicAdd(&ctl->heavy_count.v, 1u)] = item;
         }
     }
 }
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kHeavyThreads) void k_density_heavy(
     __shared__ float4 s_p[2][kHeavyStage];
     __shared__ float s_acc[kHeavyWaves][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = ctl->heavy_count;
+    const uint32_t count = ctl->heavy_count.v;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
         const uint32_t item = heavy[it];
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kHeavyThreads) void k_force_heavy(
     __shared__ float4 s_v[2][kHeavyStage];
     __shared__ float s_acc[3][kHeavyWaves][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = ctl->heavy_count;
+    const uint32_t count = ctl->heavy_count.v;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
         const uint32_t item = heavy[it];

@@ -84,8 +84,8 @@ typedef struct fh_epilogue {
 
 /* ---- context -------------------------------------------------------------------------------- */
 
-/* Create a context on HIP device `device` for up to `max_n` particles / sort pairs and
- * `max_cells` grid cells.  `stream` is an existing hipStream_t to run on, or NULL to create a
+/* Create a context on HIP device `device` for up to `max_n` (<= 2^30, else FH_ERANGE)
+ * particles / sort pairs and `max_cells` grid cells.  `stream` is an existing hipStream_t to run on, or NULL to create a
  * private default-priority stream.  Allocates every scratch buffer up front (replaces the lazy
  * scratch creation of sph_fused.rs:43-74 and RadixSorter::new, radix_sort.rs:55-70). */
 int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_ctx** out);

@@ -43,6 +43,7 @@ def test_create_argument_errors(fh):
     out = ctypes.c_void_p()
     assert lib.fh_create(0, 0, 10, None, ctypes.byref(out)) == fh.FH_EINVAL
     assert lib.fh_create(0, 10, 10, None, None) == fh.FH_EINVAL
+    assert lib.fh_create(0, (1 << 30) + 1, 10, None, ctypes.byref(out)) == fh.FH_ERANGE
 
 
 def test_create_without_gpu_reports_nodev(fh):

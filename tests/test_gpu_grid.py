@@ -57,6 +57,8 @@ def edge_positions(n, rng, lo=-0.2, hi=1.2):
     (100_000, 0.0122, (82, 82, 82), (0.0, 0.0, 0.0)),
     (70_001, 0.1, (7, 13, 3), (-0.1, 0.2, 0.05)),
     (1, 1.0, (1, 1, 1), (0.0, 0.0, 0.0)),
+    (20_000, 1.0, (1, 1, 1), (0.0, 0.0, 0.0)),      # one cell: no sort pass moves keys
+    (20_000, 0.5, (2, 1, 1), (0.0, 0.0, 0.0)),      # one 1-bit pass
 ])
 def test_build_matches_oracle(fh, gpu_ctx, oracle, layout, n, cs, dims, origin):
     rng = np.random.default_rng(n)

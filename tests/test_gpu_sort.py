@@ -75,6 +75,37 @@ def test_sort_heavy_duplicates_is_stable(fh, gpu_ctx):
     assert np.array_equal(k, keys[exp])
 
 
+@pytest.mark.parametrize("case", ["all_equal", "one_moving_pass", "trivial_middle_passes",
+                                  "trivial_first_pass", "two_values"])
+def test_sort_skips_identity_passes(fh, gpu_ctx, oracle, case):
+    """Passes whose digit is the same for every key are skipped on the device; the result must
+    still be the stable sort, in place, whatever number of passes actually moved keys."""
+    n = 50_000
+    rng = np.random.default_rng(11)
+    r = rng.integers(0, 256, n).astype(np.uint32)
+    keys = {"all_equal": np.full(n, 0xA5A5A5A5, np.uint32),
+            "one_moving_pass": r,                                  # bytes 1..3 are zero
+            "trivial_middle_passes": r | (r[::-1] << 24),          # bytes 1, 2 zero
+            "trivial_first_pass": (r << 8) | 7,                    # byte 0 constant
+            "two_values": np.where(r < 128, 3, 0x70000).astype(np.uint32)}[case]
+    vals = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    print(f"sort skip case {case}", flush=True)
+    k, v = gpu_sort(fh, gpu_ctx, keys, vals, 32)
+    ok, ov = oracle.stable_sort_pairs(keys, vals, 32)
+    assert np.array_equal(k, ok) and np.array_equal(v, ov)
+
+
+def test_sort_back_to_back_sizes(fh, gpu_ctx, oracle):
+    """Consecutive sorts of different sizes on one context (look-back words are re-zeroed)."""
+    rng = np.random.default_rng(5)
+    for n, bits in [(1_000_000, 24), (10_000, 32), (300_000, 16), (8193, 9), (1_000_000, 24)]:
+        keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        vals = np.arange(n, dtype=np.uint32)
+        k, v = gpu_sort(fh, gpu_ctx, keys, vals, bits)
+        ok, ov = oracle.stable_sort_pairs(keys, vals, bits)
+        assert np.array_equal(k, ok) and np.array_equal(v, ov), (n, bits)
+
+
 def test_sort_config1_full(fh, gpu_ctx):
     """c1: 16,777,216 pairs of cell keys, full 32-bit stable sort, vs numpy's stable argsort."""
     from forge_hip import workloads
