@@ -155,6 +155,11 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->fpart, 9 * (size_t)max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
+    if (e == hipSuccess) e = alloc(&c->cell_grp, max_cells, &tot);
+    if (e == hipSuccess) e = alloc(&c->big, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
+    if (e == hipSuccess) e = alloc(&c->collapsed, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
+    if (e == hipSuccess) e = alloc(&c->wpart, 3 * (size_t)max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->vrep, max_n, &tot);
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_error, sizeof(uint32_t), hipHostMallocDefault);
     if (e == hipSuccess) {
         if (stream) {
@@ -170,6 +175,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = hipMemsetAsync(c->scan_lb, 0, (size_t)c->max_scan_tiles * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->run_tag, 0, (size_t)max_cells * 8u, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->cell_grp, 0, (size_t)max_cells * 8u, c->stream);
     for (int q = 0; q < kEvents && e == hipSuccess; q++) e = hipEventCreate(&c->ev[q]);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     c->scratch_bytes = tot;
@@ -200,7 +206,8 @@ int fh_destroy(fh_ctx* c) {
     }
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
-                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag};
+                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hist_part,
+                    c->cell_grp, c->big, c->collapsed, c->wpart, c->vrep};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);
@@ -351,6 +358,7 @@ int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const f
     if (c->sph_exact) {
         FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
     } else {
+        FH_CHECK_HIP(launch_group(c, n, false));
         FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
         FH_CHECK_HIP(launch_finalize(c, a, nullptr, true, nullptr, nullptr, nullptr, nullptr,
@@ -380,8 +388,10 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
         FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
         FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
     } else {
+        FH_CHECK_HIP(launch_group(c, n, true));
         FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_broadcast(c, n));
         FH_CHECK_HIP(launch_force_fast(c, a, c->cell_start));
         FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density, accel));
     }
@@ -395,6 +405,10 @@ int fh_set_option(fh_ctx* c, int option, int value) {
     switch (option) {
         case FH_OPT_SPH_EXACT:
             c->sph_exact = value != 0;
+            return FH_OK;
+        case FH_OPT_HEAVY_WORK:
+            if (value < 0) return fail(FH_EINVAL, "fh_set_option: heavy work %d < 0", value);
+            c->heavy_work = (uint32_t)value;
             return FH_OK;
         default:
             return fail(FH_EINVAL, "fh_set_option: unknown option %d", option);
@@ -481,7 +495,7 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
 static const char* const kKernelNames[KID_COUNT] = {"begin", "hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
                                                     "finalize", "runs", "plan",
-                                                    "density_heavy", "force_heavy"};
+                                                    "density_heavy", "force_heavy", "group"};
 
 static int kernel_id(const char* name) {
     if (!name) return -1;

@@ -23,6 +23,14 @@ constexpr int kHistChunk = kHistThreads * kHistItems;  // keys per histogram chu
 constexpr int kHistBlocks = 1024;      // rows of per-block partial histograms
 constexpr int kHistRowsPerReduce = 8;  // partial rows summed by one reduce workgroup
 constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
+// Co-located particles: when at least kCollapseMin particles of a cell sit at one position (the
+// box corners of a dam break collect thousands, next to a few hundred others), the cell is
+// reordered so they come first.  The first of them (the representative) stands for the group:
+// as a home particle it is computed once for all, as a neighbour it is one candidate of weight
+// M carrying the summed velocity of the group.  spos[s].w holds raw bits: s for an ordinary
+// particle, M | kRepFlag for a representative, the representative's index for the others.
+constexpr uint32_t kCollapseMin = 64;
+constexpr uint32_t kRepFlag = 0x80000000u;
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;  // 4096 cells per scan tile
@@ -56,6 +64,8 @@ struct Control {
     Line tile_ctr[kMaxPasses];          // dynamic tile ids of the sort passes
     Line scan_ctr;                      // dynamic tile id of the cell scan
     Line heavy_count;                   // entries in the heavy SPH work list of this substep
+    Line collapse_count;                // entries in the list of co-located cells
+    Line big_count;                     // entries in the list of cells of >= kCollapseMin
     uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
 };
 
@@ -68,7 +78,7 @@ struct GridDesc {
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
 enum KernelId { KID_BEGIN, KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
                 KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_DHEAVY, KID_FHEAVY,
-                KID_COUNT };
+                KID_GROUP, KID_COUNT };
 
 // Event pairs bracketing the first `max` launches of one kernel after it was armed; when the
 // launches are captured, every replay of the graph re-records the same events.
@@ -106,8 +116,14 @@ struct fh_ctx {
     float* dpart;        // [3][max_n] per-slab density partials (fast kernels)
     float* fpart;        // [3][3][max_n] per-slab acceleration partials (fast kernels)
     uint32_t* heavy;     // [3 * ceil(max_n / 64)] heavy (64-particle tile, slab) work items
-    uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1 if the item is on the heavy list
+    uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
+    uint64_t* cell_grp;  // [max_cells] epoch << 32 | number of co-located leading particles
+    uint2* big;          // [ceil(max_n / 64) + 1] (first, count) of cells of >= kCollapseMin
+    uint2* collapsed;    // [ceil(max_n / 64) + 1] (representative, count) of co-located groups
+    float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
+    float4* vrep;        // [max_n] summed velocity of the group, at representative indices
     bool sph_exact;      // FH_OPT_SPH_EXACT
+    uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
     uint32_t* h_error;   // pinned host word for the device error flag
     size_t scratch_bytes;
     hipGraph_t graph;
@@ -249,6 +265,12 @@ hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const floa
 hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
+// Copy the density partials of each co-located cell's representative to its other particles.
+hipError_t launch_broadcast(fh_ctx* c, uint32_t n);
+// Fast passes only: list the cells of >= kCollapseMin particles and move the particles that
+// share the position of the cell's middle particle to the front of the cell when they are at
+// least kCollapseMin (cell_grp).  Reorders spos / svel / sidx inside those cells.
+hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel);
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
                            bool density_only, float* px, float* py, float* pz, float* vx,
                            float* vy, float* vz, float* density, float* accel);

@@ -42,6 +42,8 @@ __global__ void k_begin(Control* ctl, uint32_t* __restrict__ lb, uint32_t lb_wor
             for (int p = 0; p < kMaxPasses; p++) ctl->tile_ctr[p].v = 0u;
             ctl->scan_ctr.v = 0u;
             ctl->heavy_count.v = 0u;
+            ctl->collapse_count.v = 0u;
+            ctl->big_count.v = 0u;
         }
     }
     for (uint32_t i = blockIdx.x * blockDim.x + t; i < lb_words; i += gridDim.x * blockDim.x)

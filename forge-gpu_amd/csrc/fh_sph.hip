@@ -17,21 +17,21 @@
 
 namespace fh {
 
-// Sorted-order copies of the state: spos[s] = pos[sidx[s]], svel[s] = vel[sidx[s]], and the
-// run tags of the sorted keys (first index of each cell's run, see k_runs).
-__global__ void k_gather(const float* __restrict__ px, const float* __restrict__ py,
-                         const float* __restrict__ pz, const float* __restrict__ vx,
-                         const float* __restrict__ vy, const float* __restrict__ vz,
-                         const uint32_t* __restrict__ sidx, const uint32_t* __restrict__ skeys,
-                         uint32_t n, float4* __restrict__ spos, float4* __restrict__ svel,
-                         uint64_t* __restrict__ run_tag, const Control* __restrict__ ctl) {
-    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+// Sorted-order copies of the state: spos[s] = (pos[sidx[s]], bits of s), svel[s] =
+// vel[sidx[s]], and the run tags of the sorted keys (first index of each cell's run, k_runs).
+__global__ __launch_bounds__(256) void k_gather(
+    const float* __restrict__ px, const float* __restrict__ py, const float* __restrict__ pz,
+    const float* __restrict__ vx, const float* __restrict__ vy, const float* __restrict__ vz,
+    const uint32_t* __restrict__ sidx, const uint32_t* __restrict__ skeys, uint32_t n,
+    float4* __restrict__ spos, float4* __restrict__ svel, uint64_t* __restrict__ run_tag,
+    const Control* __restrict__ ctl) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const uint32_t k = skeys[s];
     if (s == 0 || skeys[s - 1] != k) run_tag[k] = ((uint64_t)ctl->epoch << 32) | s;
     uint32_t i = sidx[s];
     if (i >= n) i = 0;  // never taken when the sort is consistent
-    spos[s] = make_float4(px[i], py[i], pz[i], 0.0f);
+    spos[s] = make_float4(px[i], py[i], pz[i], __uint_as_float(s));
     if (svel) svel[s] = make_float4(vx[i], vy[i], vz[i], 0.0f);
 }
 

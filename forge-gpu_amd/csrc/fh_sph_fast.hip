@@ -79,8 +79,7 @@ __device__ __forceinline__ void slab_ranges(const float4& p, bool live, const Gr
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
 constexpr int kHeavyThreads = 1024;     // 16 waves per heavy workgroup
 constexpr int kHeavyWaves = kHeavyThreads / kWave;
-constexpr int kHeavyStage = 1024;       // staged candidates per chunk (64 per wave)
-constexpr uint32_t kHeavyWork = 1024;   // candidates per particle and slab
+constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
 constexpr uint32_t kHeavyGrid = 512;    // heavy workgroups (grid-stride over the list)
 
 // Candidate density accumulation of one lane over [jb, je) of a staged chunk, four candidates
@@ -114,74 +113,252 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
     return acc + ((a0 + a1) + (a2 + a3));
 }
 
-// Plan: per (sub-tile, slab) the largest per-particle candidate count decides light / heavy.
-__global__ __launch_bounds__(256) void k_plan(const float4* __restrict__ spos, uint32_t n,
-                                              GridDesc g, const uint32_t* __restrict__ cstart,
+// Co-located groups.  k_big lists the cells of >= kCollapseMin particles.  k_group, one
+// workgroup per listed cell, takes the position P of the cell's middle particle, counts the
+// particles at exactly P (M) and, when M >= kCollapseMin, moves them to the front of the cell:
+// the misplaced particles on both sides are ranked and swapped pairwise, in place.  The order
+// inside such a cell then differs from ascending particle id (sums only change by rounding).
+__global__ __launch_bounds__(256) void k_big(const uint32_t* __restrict__ skeys,
+                                             const uint32_t* __restrict__ cstart, uint32_t n,
+                                             uint2* __restrict__ big, uint32_t cap,
+                                             Control* ctl) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const uint32_t c = skeys[s];
+    if (cstart[c] != s) return;  // not the first particle of its cell
+    const uint32_t cnt = min(cstart[c + 1u], n) - s;
+    if (cnt < kCollapseMin) return;
+    const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
+    if (slot < cap) big[slot] = make_uint2(s, cnt);
+}
+
+__device__ __forceinline__ bool same_pos(const float4& a, const float4& b) {
+    return __float_as_uint(a.x) == __float_as_uint(b.x) &&
+           __float_as_uint(a.y) == __float_as_uint(b.y) &&
+           __float_as_uint(a.z) == __float_as_uint(b.z);
+}
+
+__device__ __forceinline__ void swap4(float4* p, uint32_t a, uint32_t b) {
+    const float4 t = p[a];
+    p[a] = p[b];
+    p[b] = t;
+}
+
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupWaves = kGroupThreads / kWave;
+
+// Workgroup sum of one value per thread, added in a fixed order (deterministic).
+__device__ __forceinline__ float group_sum(float v, float* s_w) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < kGroupWaves; w++) t += s_w[w];
+    __syncthreads();
+    return t;
+}
+
+// Blocked layout: thread t owns particles [f + t L, f + (t + 1) L) of the cell, L = ceil(cnt / 1024).
+__global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict__ big,
+                                                         uint32_t cap,
+                                                         const uint32_t* __restrict__ skeys,
+                                                         float4* __restrict__ spos,
+                                                         float4* __restrict__ svel,
+                                                         uint32_t* __restrict__ sidx,
+                                                         uint32_t* __restrict__ scratch,
+                                                         uint64_t* __restrict__ cell_grp,
+                                                         float4* __restrict__ vrep,
+                                                         const Control* __restrict__ ctl) {
+    __shared__ uint32_t s_scan[kGroupWaves];
+    __shared__ float s_w[kGroupWaves];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t count = min(ctl->big_count.v, cap);
+    const uint32_t epoch = ctl->epoch;
+    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform
+        const uint32_t f = big[q].x, cnt = big[q].y, end = f + cnt;
+        const float4 P = spos[f + cnt / 2u];
+        const uint32_t L = ceil_div(cnt, (uint32_t)kGroupThreads);
+        const uint32_t t0 = min(f + tid * L, end), t1 = min(t0 + L, end);
+        uint32_t mine = 0, M;
+        for (uint32_t t = t0; t < t1; t++) mine += same_pos(spos[t], P) ? 1u : 0u;
+        (void)block_exclusive_scan<kGroupWaves>(mine, s_scan, &M);
+        if (M < kCollapseMin) continue;  // uniform
+        // misplaced particles: non-members before f + M, members from f + M on
+        uint32_t nm = 0, mm = 0;
+        for (uint32_t t = t0; t < t1; t++) {
+            const bool m = same_pos(spos[t], P);
+            if (t < f + M) nm += m ? 0u : 1u;
+            else mm += m ? 1u : 0u;
+        }
+        uint32_t tot;
+        uint32_t knm = block_exclusive_scan<kGroupWaves>(nm, s_scan, &tot);
+        uint32_t kmm = block_exclusive_scan<kGroupWaves>(mm, s_scan, &tot);
+        for (uint32_t t = t0; t < t1 && t < f + M; t++)
+            if (!same_pos(spos[t], P)) scratch[f + knm++] = t;
+        __threadfence_block();
+        __syncthreads();
+        for (uint32_t t = max(t0, f + M); t < t1; t++) {
+            if (!same_pos(spos[t], P)) continue;
+            const uint32_t u = scratch[f + kmm++];
+            // positions move, the .w index bits stay with the slot
+            const float4 pt = spos[t], pu = spos[u];
+            spos[t] = make_float4(pu.x, pu.y, pu.z, pt.w);
+            spos[u] = make_float4(pt.x, pt.y, pt.z, pu.w);
+            if (svel) swap4(svel, t, u);
+            const uint32_t ti = sidx[t];
+            sidx[t] = sidx[u];
+            sidx[u] = ti;
+        }
+        __threadfence_block();
+        __syncthreads();
+        if (svel) {  // summed velocity of the group (fixed order)
+            float vx = 0.0f, vy = 0.0f, vz = 0.0f;
+            for (uint32_t t = t0; t < t1 && t < f + M; t++) {
+                const float4 v = svel[t];
+                vx += v.x;
+                vy += v.y;
+                vz += v.z;
+            }
+            vx = group_sum(vx, s_w);
+            vy = group_sum(vy, s_w);
+            vz = group_sum(vz, s_w);
+            if (tid == 0) vrep[f] = make_float4(vx, vy, vz, 0.0f);
+        }
+        if (tid == 0) cell_grp[skeys[f]] = ((uint64_t)epoch << 32) | M;
+        __syncthreads();
+    }
+}
+
+// Candidates of the grouped cells among the 9 cells of a slab, as a count to subtract: a group
+// of M particles is one candidate.
+__device__ __forceinline__ uint32_t grouped_excess(const float4& p, const GridDesc& g,
+                                                   const uint64_t* __restrict__ cell_grp,
+                                                   uint32_t epoch, int dz) {
+    const int cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
+    const int cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny);
+    const int cz = (int)cell_coord(p.z, 0.0f, g.cs, g.nz) + dz;
+    if (cz < 0 || cz >= (int)g.nz) return 0u;
+    uint32_t ex = 0;
+    for (int y = cy - 1; y <= cy + 1; y++) {
+        if (y < 0 || y >= (int)g.ny) continue;
+        for (int x = cx - 1; x <= cx + 1; x++) {
+            if (x < 0 || x >= (int)g.nx) continue;
+            const uint64_t grp = cell_grp[(uint32_t)x + (uint32_t)y * g.nx + (uint32_t)cz * g.nx * g.ny];
+            if ((uint32_t)(grp >> 32) == epoch) ex += (uint32_t)grp - 1u;
+        }
+    }
+    return ex;
+}
+
+// Weight of a candidate from its spos.w bits: 1 for an ordinary particle, M for a group
+// representative, 0 for the other members of a group (they are counted by the representative).
+__device__ __forceinline__ float candidate_weight(float wbits, uint32_t j) {
+    const uint32_t w = __float_as_uint(wbits);
+    if (w & kRepFlag) return (float)(w & ~kRepFlag);
+    return w == j ? 1.0f : 0.0f;
+}
+
+// density_run over candidates staged with their weight in .w (heavy kernels: groups staged
+// in full, members with weight 0).
+__device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, uint32_t c0,
+                                               uint32_t jb, uint32_t je, float4 pi, float h2,
+                                               float acc) {
+    float a0 = 0.0f, a1 = 0.0f;
+    uint32_t j = jb;
+    for (; j + 2 <= je; j += 2) {
+        const float4 q0 = sp[j - c0], q1 = sp[j + 1 - c0];
+        float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
+        float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        a0 = fmaf(q0.w * d, d * d, a0);
+        dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
+        d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        a1 = fmaf(q1.w * d, d * d, a1);
+    }
+    if (j < je) {
+        const float4 q = sp[j - c0];
+        const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
+        const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        a0 = fmaf(q.w * d, d * d, a0);
+    }
+    return acc + (a0 + a1);
+}
+
+// Plan.  First the co-located groups (k_group): particles f+1 .. f+M-1 of a grouped cell are
+// tagged in spos[s].w with their representative f (which gets kRepFlag and appends the group
+// to the collapsed list).  A sub-tile made only of such non-representative particles is
+// skipped by both passes (flag 2): its particles take the representative's density, and its
+// acceleration up to the viscosity term that depends on the particle's own velocity
+// (k_finalize).  Then, per (sub-tile, slab), the largest per-particle candidate count decides
+// light / heavy.
+__global__ __launch_bounds__(256) void k_plan(float4* __restrict__ spos, uint32_t n, GridDesc g,
+                                              const uint32_t* __restrict__ cstart,
+                                              const uint64_t* __restrict__ cell_grp,
                                               uint8_t* __restrict__ flag,
-                                              uint32_t* __restrict__ heavy, Control* ctl) {
+                                              uint32_t* __restrict__ heavy,
+                                              uint2* __restrict__ collapsed, uint32_t cap,
+                                              uint32_t heavy_work, Control* ctl) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     const uint32_t sub = s / kSub;
     const bool live = s < n;
     if (sub * kSub >= n) return;  // whole wave beyond the particles
     const float4 pi = live ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    bool member = false;
+    if (live) {
+        const uint32_t c = cell_of(pi.x, pi.y, pi.z, g);
+        const uint64_t grp = cell_grp[c];
+        if ((uint32_t)(grp >> 32) == ctl->epoch) {
+            const uint32_t f = cstart[c], M = (uint32_t)grp;
+            float* w = reinterpret_cast<float*>(spos + s) + 3;
+            if (s == f) {
+                *w = __uint_as_float(M | kRepFlag);
+                const uint32_t slot = atomicAdd(&ctl->collapse_count.v, 1u);
+                if (slot < cap) collapsed[slot] = make_uint2(f, M);
+            } else if (s < f + M) {
+                *w = __uint_as_float(f);
+                member = true;
+            }
+        }
+    }
+    if (__ballot(live && !member) == 0ull) {  // every particle of the sub-tile is co-located
+        if ((threadIdx.x & 63) == 0)
+            for (int slab = 0; slab < 3; slab++) flag[sub * 3u + (uint32_t)slab] = 2;
+        return;
+    }
+    const uint32_t epoch = ctl->epoch;
     for (int slab = 0; slab < 3; slab++) {
         uint32_t b[3], e[3];
         slab_ranges(pi, live, g, cstart, n, slab - 1, b, e);
-        const uint32_t w = wave_max((e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]));
+        uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
+        if (cand > heavy_work) cand -= grouped_excess(pi, g, cell_grp, epoch, slab - 1);
+        const uint32_t w = wave_max(cand);
         if ((threadIdx.x & 63) == 0) {
             const uint32_t item = sub * 3u + (uint32_t)slab;
-            const bool hv = w > kHeavyWork;
+            const bool hv = w > heavy_work;
             flag[item] = hv ? 1 : 0;
             if (hv) heavy[atomicAdd(&ctl->heavy_count.v, 1u)] = item;
         }
     }
 }
 
-// ---------------------------------------------------------------------------------------------
-// The staged chunk sequence of one slab: the union [lo[r], hi[r]) of each of the 3 rows, cut
-// into chunks of `ch` candidates, rows in dy order.  Chunks are double-buffered in LDS: chunk
-// q + 1 is fetched into registers while chunk q is consumed, so one barrier per chunk suffices
-// and global latency overlaps the pair work.
-struct ChunkSeq {
-    uint32_t lo[3], n[3], total, ch;
-    __device__ __forceinline__ ChunkSeq(const uint32_t l[3], const uint32_t h[3], uint32_t c) {
-        ch = c;
-        total = 0;
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-            lo[r] = l[r];
-            n[r] = l[r] < h[r] ? (h[r] - l[r] + c - 1) / c : 0u;
-            total += n[r];
+// After the density pass: every particle of a co-located cell takes its representative's
+// density partials (the force pass reads them for candidates and home particles alike).
+__global__ __launch_bounds__(256) void k_broadcast(const uint2* __restrict__ collapsed,
+                                                   uint32_t cap, const Control* __restrict__ ctl,
+                                                   float* __restrict__ dpart, uint32_t stride) {
+    const uint32_t count = min(ctl->collapse_count.v, cap);
+    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {
+        const uint2 fc = collapsed[q];
+        const float d0 = dpart[fc.x], d1 = dpart[stride + fc.x], d2 = dpart[2u * stride + fc.x];
+        for (uint32_t t = fc.x + 1u + threadIdx.x; t < fc.x + fc.y; t += blockDim.x) {
+            dpart[t] = d0;
+            dpart[stride + t] = d1;
+            dpart[2u * stride + t] = d2;
         }
-        hi0 = h[0];
-        hi1 = h[1];
-        hi2 = h[2];
     }
-    uint32_t hi0, hi1, hi2;
-    // chunk q -> row r, first candidate c0, size m
-    __device__ __forceinline__ void at(uint32_t q, int& r, uint32_t& c0, uint32_t& m) const {
-        uint32_t hi;
-        if (q < n[0]) {
-            r = 0;
-            c0 = lo[0] + q * ch;
-            hi = hi0;
-        } else if (q < n[0] + n[1]) {
-            r = 1;
-            c0 = lo[1] + (q - n[0]) * ch;
-            hi = hi1;
-        } else {
-            r = 2;
-            c0 = lo[2] + (q - n[0] - n[1]) * ch;
-            hi = hi2;
-        }
-        m = min(ch, hi - c0);
-    }
-};
-
-__device__ __forceinline__ uint32_t pick3(const uint32_t v[3], int r) {
-    return r == 0 ? v[0] : (r == 1 ? v[1] : v[2]);
 }
 
+// ---------------------------------------------------------------------------------------------
 // Home-row segments.  A wave owns 64 consecutive sorted particles (a sub-tile); the particles of
 // one home row (cy, cz) are consecutive lanes, and for each of the slab's 3 rows the union of
 // their neighbour ranges is one short contiguous range (x-adjacent cells of that row only).
@@ -226,64 +403,181 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
             // non-decreasing ranges: the union is [b of the first lane, e of the last lane)
             const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
             const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
-            for (uint32_t c0 = lo; c0 < hi; c0 += kWave) {
+            uint32_t c0 = lo;
+            while (c0 < hi) {  // wave-uniform
                 const uint32_t m = min((uint32_t)kWave, hi - c0);
+                const float4 q = (uint32_t)lane < m ? spos[c0 + lane] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                // A group representative ends the chunk; its members (which follow it) are
+                // skipped and it counts for all of them.
+                const uint32_t wb = __float_as_uint(q.w);
+                const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
+                uint32_t mm = m, gm = 0;
+                if (reps) {
+                    const int rl = __ffsll((unsigned long long)reps) - 1;
+                    mm = (uint32_t)rl;
+                    gm = (uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag;
+                }
                 __builtin_amdgcn_wave_barrier();
-                buf[lane] = (uint32_t)lane < m ? spos[c0 + lane] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                buf[lane] = q;
                 __builtin_amdgcn_wave_barrier();
-                if (mine) acc = density_run(buf, c0, max(b[r], c0), min(e[r], c0 + m), pi, h2, acc);
+                if (mine) {
+                    acc = density_run(buf, c0, max(b[r], c0), min(e[r], c0 + mm), pi, h2, acc);
+                    const uint32_t jr = c0 + mm;
+                    if (gm && jr >= b[r] && jr < e[r]) {
+                        const float4 g4 = buf[mm];
+                        const float dx = pi.x - g4.x, dy = pi.y - g4.y, dz = pi.z - g4.z;
+                        const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+                        acc = fmaf((float)gm * d, d * d, acc);
+                    }
+                }
+                c0 += gm ? mm + gm : m;
             }
         }
     }
     if (live) dpart[(size_t)slab * stride + s] = acc;
 }
 
-// Heavy items: 16 waves share the 64 particles of one (sub-tile, slab); wave w walks slots
-// [64 w, 64 w + 64) of every staged 1024-candidate chunk.
+// Heavy items: the 16 waves of a workgroup hold the same 64 particles of one (sub-tile, slab)
+// and walk the same home-row segments as k_density_wave, but split each segment row's chunks
+// round-robin (wave w takes chunks w, w + 16, ...), each through its own LDS slice (no
+// workgroup barrier until the final reduction in wave order).  The members of co-located groups
+// in a segment row are cut out of its candidate range (the representative stays, with weight M).
+constexpr int kMaxCut = 4;  // groups cut out per segment row (further ones are staged, weight 0)
+
+struct RowPlan {
+    uint32_t lo[kMaxCut + 1], hi[kMaxCut + 1];
+    uint32_t k, total;  // sub-ranges, chunks
+};
+
+// Sub-ranges of one segment row [lo, hi), which covers cells xa..xb of the row at rowbase.
+__device__ __forceinline__ void row_plan(RowPlan& R, uint32_t lo, uint32_t hi, uint32_t rowbase,
+                                         int xa, int xb, const uint32_t* __restrict__ cstart,
+                                         const uint64_t* __restrict__ cell_grp, uint32_t epoch,
+                                         int lane) {
+    R.k = 0;
+    uint32_t cur = lo;
+    for (int x0 = xa; x0 <= xb; x0 += kWave) {  // uniform
+        const int x = x0 + lane;
+        bool grp = false;
+        uint32_t f = 0, M = 0;
+        if (x <= xb) {
+            const uint64_t gv = cell_grp[rowbase + (uint32_t)x];
+            if ((uint32_t)(gv >> 32) == epoch) {
+                grp = true;
+                M = (uint32_t)gv;
+                f = cstart[rowbase + (uint32_t)x];
+            }
+        }
+        uint64_t bal = __ballot(grp);
+        while (bal) {  // uniform
+            const int l = __ffsll((unsigned long long)bal) - 1;
+            bal &= bal - 1ull;
+            const uint32_t fl = (uint32_t)__builtin_amdgcn_readlane((int)f, l);
+            const uint32_t ml = (uint32_t)__builtin_amdgcn_readlane((int)M, l);
+            if (R.k < (uint32_t)kMaxCut) {
+#pragma unroll
+                for (int i = 0; i < kMaxCut; i++)
+                    if ((uint32_t)i == R.k) {
+                        R.lo[i] = cur;
+                        R.hi[i] = fl + 1u;
+                    }
+                R.k++;
+                cur = fl + ml;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i <= kMaxCut; i++)
+        if ((uint32_t)i == R.k) {
+            R.lo[i] = cur;
+            R.hi[i] = hi;
+        }
+    R.k++;
+    R.total = 0;
+#pragma unroll
+    for (int i = 0; i <= kMaxCut; i++)
+        if ((uint32_t)i < R.k) R.total += (R.hi[i] - R.lo[i] + kWave - 1) / kWave;
+}
+
+__device__ __forceinline__ void row_chunk(const RowPlan& R, uint32_t q, uint32_t& c0,
+                                          uint32_t& m) {
+    c0 = 0;
+    m = 0;
+#pragma unroll
+    for (int i = 0; i <= kMaxCut; i++) {
+        if ((uint32_t)i < R.k && m == 0) {
+            const uint32_t nc = (R.hi[i] - R.lo[i] + kWave - 1) / kWave;
+            if (q < nc) {
+                c0 = R.lo[i] + q * kWave;
+                m = min((uint32_t)kWave, R.hi[i] - c0);
+            } else {
+                q -= nc;
+            }
+        }
+    }
+}
+
+// Cells xa..xb and base index of row r of slab dz for a lane at p (valid = row inside the grid).
+__device__ __forceinline__ bool seg_row(const float4& p, const GridDesc& g, int dz, int r,
+                                        uint32_t& rowbase, int& cx) {
+    cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
+    const int cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny) + r - 1;
+    const int cz = (int)cell_coord(p.z, 0.0f, g.cs, g.nz) + dz;
+    rowbase = (uint32_t)cy * g.nx + (uint32_t)cz * g.nx * g.ny;
+    return cy >= 0 && cy < (int)g.ny && cz >= 0 && cz < (int)g.nz;
+}
+
 __global__ __launch_bounds__(kHeavyThreads) void k_density_heavy(
     const float4* __restrict__ spos, uint32_t n, GridDesc g, const uint32_t* __restrict__ cstart,
-    float h2, float* __restrict__ dpart, uint32_t stride, const uint32_t* __restrict__ heavy,
-    const Control* __restrict__ ctl) {
-    __shared__ float4 s_p[2][kHeavyStage];
+    const uint64_t* __restrict__ cell_grp, float h2, float* __restrict__ dpart, uint32_t stride,
+    const uint32_t* __restrict__ heavy, const Control* __restrict__ ctl) {
+    __shared__ float4 s_p[kHeavyWaves][kWave];
     __shared__ float s_acc[kHeavyWaves][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = ctl->heavy_count.v;
+    const uint32_t count = ctl->heavy_count.v, epoch = ctl->epoch;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4* buf = s_p[wave];
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
         const uint32_t item = heavy[it];
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool live = s < n;
         const float4 pi = live ? spos[s] : z4;
-        uint32_t b[3], e[3], lo[3], hi[3];
+        uint32_t b[3], e[3];
         slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
-#pragma unroll
-        for (int q = 0; q < 3; q++) {  // every wave holds the same particles: wave-local unions
-            lo[q] = wave_min(b[q] < e[q] ? b[q] : kEmpty);
-            hi[q] = wave_max(b[q] < e[q] ? e[q] : 0u);
-        }
-        const ChunkSeq cq(lo, hi, kHeavyStage);
-        int r;
-        uint32_t c0, m;
-        float4 fa = z4;
-        if (cq.total) {
-            cq.at(0, r, c0, m);
-            if ((uint32_t)tid < m) fa = spos[c0 + tid];
-        }
+        const uint32_t hr = home_row(pi, g);
         float acc = 0.0f;
-        for (uint32_t q = 0; q < cq.total; q++) {
-            float4* buf = s_p[q & 1u];
-            buf[tid] = fa;
-            __syncthreads();
-            if (q + 1 < cq.total) {
-                cq.at(q + 1, r, c0, m);
-                fa = (uint32_t)tid < m ? spos[c0 + tid] : z4;
+        uint64_t pending = __ballot(live);
+        while (pending) {  // uniform, identical in every wave
+            const int leader = __ffsll((unsigned long long)pending) - 1;
+            const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
+            const bool mine = live && hr == row;
+            const uint64_t seg = __ballot(mine);
+            pending &= ~seg;
+            const int last = 63 - __clzll((long long)seg);
+            for (int r = 0; r < 3; r++) {
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
+                if (lo >= hi) continue;
+                uint32_t rowbase;
+                int cx;
+                (void)seg_row(pi, g, (int)slab - 1, r, rowbase, cx);
+                rowbase = (uint32_t)__builtin_amdgcn_readlane((int)rowbase, leader);
+                const int xa = max(__builtin_amdgcn_readlane(cx, leader) - 1, 0);
+                const int xb = min(__builtin_amdgcn_readlane(cx, last) + 1, (int)g.nx - 1);
+                RowPlan R;
+                row_plan(R, lo, hi, rowbase, xa, xb, cstart, cell_grp, epoch, lane);
+                for (uint32_t q = (uint32_t)wave; q < R.total; q += kHeavyWaves) {
+                    uint32_t c0, m;
+                    row_chunk(R, q, c0, m);
+                    const uint32_t j = c0 + (uint32_t)lane;
+                    const float4 v = (uint32_t)lane < m ? spos[j] : z4;
+                    __builtin_amdgcn_wave_barrier();
+                    buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
+                    __builtin_amdgcn_wave_barrier();
+                    if (mine) acc = density_run_w(buf, c0, max(b[r], c0), min(e[r], c0 + m), pi, h2, acc);
+                }
             }
-            cq.at(q, r, c0, m);
-            const uint32_t sb = c0 + (uint32_t)wave * kSub;
-            const uint32_t se = min(sb + (uint32_t)kSub, c0 + m);
-            const uint32_t jb = max(pick3(b, r), sb), je = min(pick3(e, r), se);
-            acc = density_run(buf, c0, jb, je, pi, h2, acc);
         }
         s_acc[wave][lane] = acc;
         __syncthreads();
@@ -308,22 +602,28 @@ __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_
     return mc * ((dpart[j] + dpart[stride + j]) + dpart[2u * stride + j]);
 }
 
-// One prefetched candidate of the force pass: position, velocity and its three density
-// partials; converted at store time to (x, y, z, p_j) and (vx, vy, vz, 1/rho_j), where 1/rho_j
-// is 0 when rho_j < 1e-6 -- that removes the pair exactly like the skip of sph_fused.rs:607.
+// One prefetched candidate of the force pass: position (with its spos.w bits), velocity, the
+// group's summed velocity when it is a representative, and its three density partials;
+// converted at store time to (x, y, z, p_j) and (u/rho_j, w/rho_j) with w the candidate weight
+// (1, M for a representative, 0 for the other members of a group) and u = w * v_j (the group's
+// summed velocity for a representative).  1/rho_j is taken as 0 when rho_j < 1e-6, which removes
+// the pair exactly like the skip of sph_fused.rs:607.
 struct ForceSlot {
-    float4 q, w;
+    float4 q, w, g;
     float d0, d1, d2;
 };
 
 __device__ __forceinline__ ForceSlot force_fetch(const float4* __restrict__ spos,
                                                  const float4* __restrict__ svel,
+                                                 const float4* __restrict__ vrep,
                                                  const float* __restrict__ dpart,
                                                  uint32_t stride, uint32_t j, bool ok) {
     ForceSlot f;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     f.q = ok ? spos[j] : z4;
     f.w = ok ? svel[j] : z4;
+    f.g = z4;
+    if (ok && (__float_as_uint(f.q.w) & kRepFlag)) f.g = vrep[j];
     f.d0 = ok ? dpart[j] : 0.0f;
     f.d1 = ok ? dpart[stride + j] : 0.0f;
     f.d2 = ok ? dpart[2u * stride + j] : 0.0f;
@@ -331,18 +631,31 @@ __device__ __forceinline__ ForceSlot force_fetch(const float4* __restrict__ spos
 }
 
 __device__ __forceinline__ void force_store(float4* __restrict__ sp, float4* __restrict__ sv,
-                                            uint32_t t, const ForceSlot& f, const FastForce& K) {
+                                            uint32_t t, uint32_t j, const ForceSlot& f,
+                                            const FastForce& K) {
     const float rj = K.mc * ((f.d0 + f.d1) + f.d2);
+    const float inv = rj < 1e-6f ? 0.0f : 1.0f / rj;
+    const uint32_t wb = __float_as_uint(f.q.w);
+    float wt = 1.0f;
+    float4 u = f.w;
+    if (wb & kRepFlag) {
+        wt = (float)(wb & ~kRepFlag);
+        u = f.g;
+    } else if (wb != j) {
+        wt = 0.0f;
+        u = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     sp[t] = make_float4(f.q.x, f.q.y, f.q.z, K.k * (rj - K.rho0));
-    sv[t] = make_float4(f.w.x, f.w.y, f.w.z, rj < 1e-6f ? 0.0f : 1.0f / rj);
+    sv[t] = make_float4(u.x * inv, u.y * inv, u.z * inv, wt * inv);
 }
 
-// Pressure + viscosity pair terms of one lane over [jb, je) of a staged chunk.
+// Pressure + viscosity pair terms of one lane over [jb, je) of a staged chunk: per candidate
+// w/rho_j * [fp (p_i + p_j) (h - r)^2 / r (x_i - x_j)] + fv (h - r) (u/rho_j - w/rho_j v_i).
 __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
                                           const float4* __restrict__ sv, uint32_t c0,
                                           uint32_t jb, uint32_t je, float4 pi, float4 vi,
                                           float p_i, const FastForce& K, float& ax, float& ay,
-                                          float& az) {
+                                          float& az, float& wv) {
 #pragma unroll 2
     for (uint32_t j = jb; j < je; j++) {
         const float4 q = sp[j - c0];
@@ -353,10 +666,11 @@ __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
             const float rinv = __builtin_amdgcn_rsqf(r2);
             const float diff = K.h - r2 * rinv;
             const float fs = K.fp * (p_i + q.w) * w.w * (diff * diff) * rinv;
-            const float vs = K.fv * w.w * diff;
-            ax = fmaf(vs, w.x - vi.x, fmaf(fs, dx, ax));
-            ay = fmaf(vs, w.y - vi.y, fmaf(fs, dy, ay));
-            az = fmaf(vs, w.z - vi.z, fmaf(fs, dz, az));
+            const float vs = K.fv * diff;
+            wv = fmaf(vs, w.w, wv);  // a_i depends on v_i only through -wv * v_i
+            ax = fmaf(vs, fmaf(-w.w, vi.x, w.x), fmaf(fs, dx, ax));
+            ay = fmaf(vs, fmaf(-w.w, vi.y, w.y), fmaf(fs, dy, ay));
+            az = fmaf(vs, fmaf(-w.w, vi.z, w.z), fmaf(fs, dz, az));
         }
     }
 }
@@ -366,10 +680,12 @@ __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
 // home-row segments as k_density_wave.
 __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict__ spos,
                                                        const float4* __restrict__ svel,
+                                                       const float4* __restrict__ vrep,
                                                        const float* __restrict__ dpart,
                                                        uint32_t n, GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
                                                        FastForce K, float* __restrict__ fpart,
+                                                       float* __restrict__ wpart,
                                                        uint32_t stride, uint32_t items,
                                                        const uint8_t* __restrict__ flag) {
     __shared__ float4 s_p[kTileP / kWave][kWave];  // x, y, z, p_j
@@ -391,7 +707,7 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     const uint32_t hr = home_row(pi, g);
     float4* bp = s_p[wave];
     float4* bv = s_v[wave];
-    float ax = 0.0f, ay = 0.0f, az = 0.0f;
+    float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
     uint64_t pending = __ballot(live);
     while (pending) {
         const int leader = __ffsll((unsigned long long)pending) - 1;
@@ -404,16 +720,28 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         for (int r = 0; r < 3; r++) {
             const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
             const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
-            for (uint32_t c0 = lo; c0 < hi; c0 += kWave) {
+            uint32_t c0 = lo;
+            while (c0 < hi) {  // wave-uniform
                 const uint32_t m = min((uint32_t)kWave, hi - c0);
-                const ForceSlot f = force_fetch(spos, svel, dpart, stride, c0 + lane,
+                const ForceSlot f = force_fetch(spos, svel, vrep, dpart, stride, c0 + lane,
                                                 (uint32_t)lane < m);
+                // a group representative (staged with its weight) ends the chunk; its members
+                // follow it and are skipped
+                const uint32_t wb = __float_as_uint(f.q.w);
+                const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
+                uint32_t mm = m, skip = 0;
+                if (reps) {
+                    const int rl = __ffsll((unsigned long long)reps) - 1;
+                    mm = (uint32_t)rl + 1u;
+                    skip = ((uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag) - 1u;
+                }
                 __builtin_amdgcn_wave_barrier();
-                force_store(bp, bv, lane, f, K);
+                force_store(bp, bv, lane, c0 + lane, f, K);
                 __builtin_amdgcn_wave_barrier();
                 if (mine)
-                    force_run(bp, bv, c0, max(b[r], c0), min(e[r], c0 + m), pi, vi, p_i, K, ax,
-                              ay, az);
+                    force_run(bp, bv, c0, max(b[r], c0), min(e[r], c0 + mm), pi, vi, p_i, K, ax,
+                              ay, az, wv);
+                c0 += mm + skip;
             }
         }
     }
@@ -422,20 +750,24 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         o[s] = ax;
         o[stride + s] = ay;
         o[2u * (size_t)stride + s] = az;
+        if (__float_as_uint(pi.w) & kRepFlag) wpart[(size_t)slab * stride + s] = wv;
     }
 }
 
 __global__ __launch_bounds__(kHeavyThreads) void k_force_heavy(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
-    const float* __restrict__ dpart, uint32_t n, GridDesc g, const uint32_t* __restrict__ cstart,
-    FastForce K, float* __restrict__ fpart, uint32_t stride, const uint32_t* __restrict__ heavy,
-    const Control* __restrict__ ctl) {
-    __shared__ float4 s_p[2][kHeavyStage];
-    __shared__ float4 s_v[2][kHeavyStage];
-    __shared__ float s_acc[3][kHeavyWaves][kSub];
+    const float4* __restrict__ vrep, const float* __restrict__ dpart, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
+    float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
+    const uint32_t* __restrict__ heavy, const Control* __restrict__ ctl) {
+    __shared__ float4 s_p[kHeavyWaves][kWave];
+    __shared__ float4 s_v[kHeavyWaves][kWave];
+    __shared__ float s_acc[4][kHeavyWaves][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = ctl->heavy_count.v;
+    const uint32_t count = ctl->heavy_count.v, epoch = ctl->epoch;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4* bp = s_p[wave];
+    float4* bv = s_v[wave];
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
         const uint32_t item = heavy[it];
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
@@ -446,46 +778,57 @@ __global__ __launch_bounds__(kHeavyThreads) void k_force_heavy(
         const float rho_i = in ? rho_of(dpart, stride, s, K.mc) : 0.0f;
         const bool live = in && !(rho_i < 1e-6f);
         const float p_i = K.k * (rho_i - K.rho0);
-        uint32_t b[3], e[3], lo[3], hi[3];
+        uint32_t b[3], e[3];
         slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
-#pragma unroll
-        for (int q = 0; q < 3; q++) {
-            lo[q] = wave_min(b[q] < e[q] ? b[q] : kEmpty);
-            hi[q] = wave_max(b[q] < e[q] ? e[q] : 0u);
-        }
-        const ChunkSeq cq(lo, hi, kHeavyStage);
-        int r;
-        uint32_t c0, m;
-        ForceSlot fa;
-        {
-            uint32_t c = 0, mm = 0;
-            if (cq.total) cq.at(0, r, c, mm);
-            fa = force_fetch(spos, svel, dpart, stride, c + tid, (uint32_t)tid < mm);
-        }
-        float ax = 0.0f, ay = 0.0f, az = 0.0f;
-        for (uint32_t q = 0; q < cq.total; q++) {
-            float4* bp = s_p[q & 1u];
-            float4* bv = s_v[q & 1u];
-            force_store(bp, bv, tid, fa, K);
-            __syncthreads();
-            if (q + 1 < cq.total) {
-                cq.at(q + 1, r, c0, m);
-                fa = force_fetch(spos, svel, dpart, stride, c0 + tid, (uint32_t)tid < m);
+        const uint32_t hr = home_row(pi, g);
+        float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
+        uint64_t pending = __ballot(live);
+        while (pending) {  // uniform, identical in every wave
+            const int leader = __ffsll((unsigned long long)pending) - 1;
+            const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
+            const bool mine = live && hr == row;
+            const uint64_t seg = __ballot(mine);
+            pending &= ~seg;
+            const int last = 63 - __clzll((long long)seg);
+            for (int r = 0; r < 3; r++) {
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
+                if (lo >= hi) continue;
+                uint32_t rowbase;
+                int cx;
+                (void)seg_row(pi, g, (int)slab - 1, r, rowbase, cx);
+                rowbase = (uint32_t)__builtin_amdgcn_readlane((int)rowbase, leader);
+                const int xa = max(__builtin_amdgcn_readlane(cx, leader) - 1, 0);
+                const int xb = min(__builtin_amdgcn_readlane(cx, last) + 1, (int)g.nx - 1);
+                RowPlan R;
+                row_plan(R, lo, hi, rowbase, xa, xb, cstart, cell_grp, epoch, lane);
+                for (uint32_t q = (uint32_t)wave; q < R.total; q += kHeavyWaves) {
+                    uint32_t c0, m;
+                    row_chunk(R, q, c0, m);
+                    const uint32_t j = c0 + (uint32_t)lane;
+                    const ForceSlot f = force_fetch(spos, svel, vrep, dpart, stride, j, (uint32_t)lane < m);
+                    __builtin_amdgcn_wave_barrier();
+                    force_store(bp, bv, lane, j, f, K);
+                    __builtin_amdgcn_wave_barrier();
+                    if (mine)
+                        force_run(bp, bv, c0, max(b[r], c0), min(e[r], c0 + m), pi, vi, p_i, K,
+                                  ax, ay, az, wv);
+                }
             }
-            cq.at(q, r, c0, m);
-            const uint32_t sb = c0 + (uint32_t)wave * kSub;
-            const uint32_t se = min(sb + (uint32_t)kSub, c0 + m);
-            const uint32_t jb = max(pick3(b, r), sb), je = min(pick3(e, r), se);
-            force_run(bp, bv, c0, jb, je, pi, vi, p_i, K, ax, ay, az);
         }
         s_acc[0][wave][lane] = ax;
         s_acc[1][wave][lane] = ay;
         s_acc[2][wave][lane] = az;
+        s_acc[3][wave][lane] = wv;
         __syncthreads();
         if (wave < 3) {  // wave c reduces component c in wave order
             float t = 0.0f;
             for (int w = 0; w < kHeavyWaves; w++) t += s_acc[wave][w][lane];
             if (in) fpart[((size_t)slab * 3u + (uint32_t)wave) * stride + s] = t;
+        } else if (wave == 3 && in && (__float_as_uint(pi.w) & kRepFlag)) {
+            float t = 0.0f;
+            for (int w = 0; w < kHeavyWaves; w++) t += s_acc[3][w][lane];
+            wpart[(size_t)slab * stride + s] = t;
         }
         __syncthreads();
     }
@@ -506,6 +849,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
                                                   const float4* __restrict__ svel,
                                                   const float* __restrict__ dpart,
                                                   const float* __restrict__ fpart,
+                                                  const float* __restrict__ wpart,
                                                   const uint32_t* __restrict__ sidx, uint32_t n,
                                                   uint32_t stride, Finish F,
                                                   float* __restrict__ px, float* __restrict__ py,
@@ -517,19 +861,35 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     if (s >= n) return;
     const uint32_t i = sidx[s];
     if (i >= n) return;
-    const float rho = rho_of(dpart, stride, s, F.mc);
+    const float4 p = spos[s];
+    // Co-located particle: its density, and its acceleration up to the viscosity term, are
+    // those of its representative r; sum_j w_j (v_j - v_s) = [sum_j w_j (v_j - v_r)] + W (v_r - v_s)
+    // with W = sum_j w_j, which the force pass kept for r.
+    const uint32_t wb = __float_as_uint(p.w);
+    uint32_t r = (wb & kRepFlag) ? s : wb;
+    if (r >= n) r = s;
+    const float rho = rho_of(dpart, stride, r, F.mc);
     if (density) density[i] = rho;
     if (F.flags & kDensityOnly) return;
-    const float4 p = spos[s];
     const float4 v = svel[s];
     float ax = 0.0f, ay = 0.0f, az = 0.0f;
     float nvx = v.x, nvy = v.y, nvz = v.z;
     if (!(rho < 1e-6f)) {
         const float inv = 1.0f / rho;
         const size_t S = stride;
-        ax = ((fpart[s] + fpart[3 * S + s]) + fpart[6 * S + s]) * inv;
-        ay = ((fpart[S + s] + fpart[4 * S + s]) + fpart[7 * S + s]) * inv;
-        az = ((fpart[2 * S + s] + fpart[5 * S + s]) + fpart[8 * S + s]) * inv;
+        float fx = (fpart[r] + fpart[3 * S + r]) + fpart[6 * S + r];
+        float fy = (fpart[S + r] + fpart[4 * S + r]) + fpart[7 * S + r];
+        float fz = (fpart[2 * S + r] + fpart[5 * S + r]) + fpart[8 * S + r];
+        if (r != s) {
+            const float W = (wpart[r] + wpart[S + r]) + wpart[2 * S + r];
+            const float4 vr = svel[r];
+            fx = fmaf(W, vr.x - v.x, fx);
+            fy = fmaf(W, vr.y - v.y, fy);
+            fz = fmaf(W, vr.z - v.z, fz);
+        }
+        ax = fx * inv;
+        ay = fy * inv;
+        az = fz * inv;
         nvx = v.x + ax * F.dt;
         nvy = v.y + ay * F.dt;
         nvz = v.z + az * F.dt;
@@ -590,7 +950,10 @@ hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) 
     if (a.n == 0) return hipSuccess;
     tbeg(c, KID_PLAN);
     k_plan<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, a.n, a.g, cell_start,
-                                                       c->heavy_flag, c->heavy, c->ctl);
+                                                       c->cell_grp, c->heavy_flag, c->heavy,
+                                                       c->collapsed, ceil_div(c->max_n, 64u) + 1u,
+                                                       c->heavy_work ? c->heavy_work : kHeavyWork,
+                                                       c->ctl);
     tend(c, KID_PLAN);
     return hipGetLastError();
 }
@@ -607,8 +970,34 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     if (e != hipSuccess) return e;
     tbeg(c, KID_DHEAVY);
     k_density_heavy<<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
-        c->spos, a.n, a.g, cell_start, a.h * a.h, c->dpart, c->max_n, c->heavy, c->ctl);
+        c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
+        c->ctl);
     tend(c, KID_DHEAVY);
+    return hipGetLastError();
+}
+
+hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
+    if (n == 0) return hipSuccess;
+    const uint32_t cap = ceil_div(c->max_n, 64u) + 1u;
+    tbeg(c, KID_GROUP);
+    k_big<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->skeys, c->cell_start, n, c->big, cap,
+                                                    c->ctl);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) {
+        // scratch: the sort's key buffer, free after the sort (disjoint ranges per cell)
+        k_group<<<256, kGroupThreads, 0, c->stream>>>(c->big, cap, c->skeys, c->spos,
+                                                      with_vel ? c->svel : nullptr, c->sidx,
+                                                      c->ka, c->cell_grp, c->vrep, c->ctl);
+        e = hipGetLastError();
+    }
+    tend(c, KID_GROUP);
+    return e;
+}
+
+hipError_t launch_broadcast(fh_ctx* c, uint32_t n) {
+    if (n == 0) return hipSuccess;
+    k_broadcast<<<64, 256, 0, c->stream>>>(c->collapsed, ceil_div(c->max_n, 64u) + 1u, c->ctl,
+                                           c->dpart, c->max_n);
     return hipGetLastError();
 }
 
@@ -628,15 +1017,16 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_FORCE);
-    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->dpart, a.n, a.g,
-                                                 cell_start, K, c->fpart, c->max_n, items,
-                                                 c->heavy_flag);
+    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n, a.g,
+                                                 cell_start, K, c->fpart, c->wpart, c->max_n,
+                                                 items, c->heavy_flag);
     tend(c, KID_FORCE);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     tbeg(c, KID_FHEAVY);
     k_force_heavy<<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
-        c->spos, c->svel, c->dpart, a.n, a.g, cell_start, K, c->fpart, c->max_n, c->heavy, c->ctl);
+        c->spos, c->svel, c->vrep, c->dpart, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
+        c->wpart, c->max_n, c->heavy, c->ctl);
     tend(c, KID_FHEAVY);
     return hipGetLastError();
 }
@@ -659,8 +1049,8 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     F.e = epi ? epi->restitution : 0.0f;
     tbeg(c, KID_FINAL);
     k_finalize<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
-                                                           c->sidx, a.n, c->max_n, F, px, py, pz,
-                                                           vx, vy, vz, density, accel);
+                                                           c->wpart, c->sidx, a.n, c->max_n, F,
+                                                           px, py, pz, vx, vy, vz, density, accel);
     tend(c, KID_FINAL);
     return hipGetLastError();
 }

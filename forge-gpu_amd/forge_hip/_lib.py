@@ -25,6 +25,7 @@ FH_EPI_INTEGRATE = 2
 FH_EPI_BOX = 4
 
 FH_OPT_SPH_EXACT = 1
+FH_OPT_HEAVY_WORK = 2
 
 
 class LibraryNotBuilt(RuntimeError):

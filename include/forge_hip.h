@@ -182,6 +182,11 @@ int fh_sph_fused(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, 
  * 0 (default) uses the LDS-tiled passes (fused multiply-adds, hardware reciprocal square root,
  * deterministic per-slab partial sums; within rel 1e-4). */
 #define FH_OPT_SPH_EXACT 1
+/* FH_OPT_HEAVY_WORK = 2: work split of the fast passes.  A (64-particle, z-slab) item whose
+ * particles face more than `value` candidates (a co-located group counting as one) is processed
+ * by a 1024-lane workgroup instead of one wavefront; value 0 restores the default (384).
+ * Results differ only by rounding. */
+#define FH_OPT_HEAVY_WORK 2
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
 /* GravityModule (gravity.rs:31-34): v += g * dt. */
@@ -214,7 +219,8 @@ int fh_event_record(fh_ctx* ctx, uint32_t slot);
 int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
 
 /* Per-kernel timing.  Arm kernel `name` (one of "begin", "hist", "hash", "scan", "sort",
- * "gather", "density", "force", "query", "finalize", "runs") so that its next `max_launches` launches on the
+ * "gather", "density", "force", "query", "finalize", "runs", "plan", "density_heavy",
+ * "force_heavy", "group") so that its next `max_launches` launches on the
  * context stream are bracketed by HIP events; launches captured into a graph record the events
  * on every replay.  max_launches = 0 disarms.  Arming allocates events: call outside capture.
  * fh_kernel_times waits for the last armed launch and writes the durations (ms) of the armed

@@ -49,7 +49,11 @@ def rel_err(a, b):
 
 
 def set_mode(fh, f, cfg, mode):
-    f.context(cfg.num_cells).set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
+    """fast: default work split; heavy: every (sub-tile, slab) item through the 1024-lane
+    kernels; light: none of them (one wavefront per item); exact: the bit-exact passes."""
+    ctx = f.context(cfg.num_cells)
+    ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
+    ctx.set_option(fh.FH_OPT_HEAVY_WORK, {"heavy": 1, "light": 1 << 30}.get(mode, 0))
 
 
 def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast"):
@@ -106,7 +110,7 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "exact"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
     from forge_hip import workloads
@@ -126,7 +130,8 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle):
+@pytest.mark.parametrize("mode", ["fast", "heavy", "light"])
+def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
     from forge_hip import workloads
@@ -140,9 +145,59 @@ def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle):
     cfg.y[k:k + 500] = 1.0
     cfg.z[k:k + 500] = 1.0
     vel = [rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
-    print("dense clumps", flush=True)
-    exact = check_step(fh, oracle, cfg, vel)
+    print(f"dense clumps ({mode})", flush=True)
+    exact = check_step(fh, oracle, cfg, vel, mode=mode)
     print("bit-exact fractions", exact)
+
+
+def colocated_cfg(n=40_000, seed=33):
+    """Clumps of particles at bitwise-identical positions (the box corners of c3 hold ~5600
+    each): cells of >= 64 such particles are computed once by their first particle."""
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=n, cols=24)
+    rng = np.random.default_rng(seed)
+    spots = [((0.0, 0.0, 0.0), 5600), ((1.0, 1.0, 1.0), 1000), ((0.3, 0.41, 0.27), 200),
+             ((0.6, 0.2, 0.7), 65), ((0.62, 0.52, 0.12), 64), ((0.2, 0.8, 0.5), 63)]
+    at = 0
+    for (x, y, z), k in spots:
+        cfg.x[at:at + k] = x
+        cfg.y[at:at + k] = y
+        cfg.z[at:at + k] = z
+        at += k
+    # 200 particles at one point but one of them 1 ulp away: that cell must not be collapsed
+    cfg.x[at:at + 200] = 0.45
+    cfg.y[at:at + 200] = 0.55
+    cfg.z[at:at + 200] = 0.65
+    cfg.x[at + 137] = np.nextafter(np.float32(0.45), np.float32(1.0))
+    at += 200
+    # shuffle so clump members are spread over the particle order
+    perm = rng.permutation(cfg.n)
+    for a in ("x", "y", "z"):
+        setattr(cfg, a, np.ascontiguousarray(getattr(cfg, a)[perm]))
+    vel = [rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
+    return cfg, vel
+
+
+@pytest.mark.parametrize("mode", ["fast", "heavy", "light"])
+def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
+    cfg, vel = colocated_cfg()
+    print(f"co-located cells ({mode})", flush=True)
+    exact = check_step(fh, oracle, cfg, vel, mode=mode)
+    print("bit-exact fractions", exact)
+
+
+def test_colocated_density_module_matches_oracle(fh, gpu_ctx, oracle):
+    cfg, _ = colocated_cfg(seed=34)
+    f = fields_from(fh, cfg, None)
+    p = fh.Pipeline()
+    p.add(fh.SphDensityModule(cfg.h, cfg.cell_size, cfg.dims, cfg.mass))
+    torch.cuda.synchronize()
+    p.step(f, cfg.dt)
+    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity)
+    ocs, osi, _ = oracle.hashgrid_build(cfg.x, cfg.y, cfg.z, cfg.cell_size, (0, 0, 0), cfg.dims)
+    orho = oracle.sph_density(prm, cfg.x, cfg.y, cfg.z, ocs, osi)
+    assert rel_err(f.f32_fields["density"].cpu().numpy(), orho).max() <= REL
 
 
 def test_fused_epilogue_equals_separate_modules(fh, gpu_ctx):
