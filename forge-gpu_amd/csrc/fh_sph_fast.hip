@@ -77,10 +77,17 @@ __device__ __forceinline__ void slab_ranges(const float4& p, bool live, const Gr
 // candidates of the same 64 particles and reduce their partial sums in wave order.  The light
 // kernels skip those items.  The plan is made once per substep and serves both passes.
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
-constexpr int kHeavyThreads = 1024;     // 16 waves per heavy workgroup
-constexpr int kHeavyWaves = kHeavyThreads / kWave;
+#ifndef FH_HW
+#define FH_HW 8
+#endif
+constexpr int kHeavyWaves = FH_HW;      // waves per heavy workgroup (one item at a time)
+constexpr int kHeavyThreads = kHeavyWaves * kWave;
 constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
-constexpr uint32_t kHeavyGrid = 512;    // heavy workgroups (grid-stride over the list)
+constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
+#ifndef FH_HGRID
+#define FH_HGRID 1024
+#endif
+constexpr uint32_t kHeavyGrid = FH_HGRID;  // heavy workgroups (grid-stride over the list)
 
 // Candidate density accumulation of one lane over [jb, je) of a staged chunk, four candidates
 // per iteration with independent accumulators so LDS latency and the FMA chain overlap.
@@ -330,13 +337,18 @@ __global__ __launch_bounds__(256) void k_plan(float4* __restrict__ spos, uint32_
         uint32_t b[3], e[3];
         slab_ranges(pi, live, g, cstart, n, slab - 1, b, e);
         uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
-        if (cand > heavy_work) cand -= grouped_excess(pi, g, cell_grp, epoch, slab - 1);
+        uint32_t excess = 0;
+        if (cand > heavy_work) {
+            excess = grouped_excess(pi, g, cell_grp, epoch, slab - 1);
+            cand -= excess;
+        }
         const uint32_t w = wave_max(cand);
+        const bool touches = __ballot(excess > 0u) != 0ull;
         if ((threadIdx.x & 63) == 0) {
             const uint32_t item = sub * 3u + (uint32_t)slab;
             const bool hv = w > heavy_work;
             flag[item] = hv ? 1 : 0;
-            if (hv) heavy[atomicAdd(&ctl->heavy_count.v, 1u)] = item;
+            if (hv) heavy[atomicAdd(&ctl->heavy_count.v, 1u)] = item | (touches ? kCutFlag : 0u);
         }
     }
 }
@@ -359,6 +371,27 @@ __global__ __launch_bounds__(256) void k_broadcast(const uint2* __restrict__ col
 }
 
 // ---------------------------------------------------------------------------------------------
+// Lane `lane` of a chunk of m (>= 1) candidates starting at c0: a global load from a clamped,
+// always valid index, zeroed past the chunk.  (A conditional load written as `lane < m ?
+// spos[c0 + lane] : zero` selects between two addresses and compiles to a FLAT load, which
+// also counts against the LDS wait counter and so serialises with the LDS staging.)
+__device__ __forceinline__ float4 chunk_load(const float4* __restrict__ spos, uint32_t c0,
+                                             uint32_t m, int lane) {
+    const float4 v = spos[c0 + min((uint32_t)lane, m - 1u)];
+    return (uint32_t)lane < m ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+__device__ __forceinline__ uint32_t pick3(const uint32_t v[3], int r) {
+    return r == 0 ? v[0] : (r == 1 ? v[1] : v[2]);
+}
+
+// Next non-empty row after r (3 if none) of a segment whose row r spans [lo[r], hi[r]).
+__device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[3], int r) {
+    for (r = r + 1; r < 3; r++)
+        if (pick3(lo, r) < pick3(hi, r)) break;
+    return r;
+}
+
 // Home-row segments.  A wave owns 64 consecutive sorted particles (a sub-tile); the particles of
 // one home row (cy, cz) are consecutive lanes, and for each of the slab's 3 rows the union of
 // their neighbour ranges is one short contiguous range (x-adjacent cells of that row only).
@@ -388,6 +421,7 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
     const uint32_t hr = home_row(pi, g);
     float4* buf = s_p[wave];
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float acc = 0.0f;
     uint64_t pending = __ballot(live);
     while (pending) {  // wave-uniform
@@ -397,41 +431,58 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
         const uint64_t seg = __ballot(mine);
         pending &= ~seg;
         const int last = 63 - __clzll((long long)seg);
+        // The segment's lanes share the home row (so the same valid rows) and have
+        // non-decreasing ranges: the union of row r is [b of the first lane, e of the last lane).
+        // Its rows are walked as one chunk stream; the next chunk is fetched before the current
+        // one is evaluated.
+        uint32_t lo[3], hi[3];
 #pragma unroll
-        for (int r = 0; r < 3; r++) {
-            // the segment's lanes share the home row (so the same valid rows) and have
-            // non-decreasing ranges: the union is [b of the first lane, e of the last lane)
-            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
-            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
-            uint32_t c0 = lo;
-            while (c0 < hi) {  // wave-uniform
-                const uint32_t m = min((uint32_t)kWave, hi - c0);
-                const float4 q = (uint32_t)lane < m ? spos[c0 + lane] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                // A group representative ends the chunk; its members (which follow it) are
-                // skipped and it counts for all of them.
-                const uint32_t wb = __float_as_uint(q.w);
-                const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
-                uint32_t mm = m, gm = 0;
-                if (reps) {
-                    const int rl = __ffsll((unsigned long long)reps) - 1;
-                    mm = (uint32_t)rl;
-                    gm = (uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag;
-                }
-                __builtin_amdgcn_wave_barrier();
-                buf[lane] = q;
-                __builtin_amdgcn_wave_barrier();
-                if (mine) {
-                    acc = density_run(buf, c0, max(b[r], c0), min(e[r], c0 + mm), pi, h2, acc);
-                    const uint32_t jr = c0 + mm;
-                    if (gm && jr >= b[r] && jr < e[r]) {
-                        const float4 g4 = buf[mm];
-                        const float dx = pi.x - g4.x, dy = pi.y - g4.y, dz = pi.z - g4.z;
-                        const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
-                        acc = fmaf((float)gm * d, d * d, acc);
-                    }
-                }
-                c0 += gm ? mm + gm : m;
+        for (int q = 0; q < 3; q++) {
+            lo[q] = (uint32_t)__builtin_amdgcn_readlane((int)b[q], leader);
+            hi[q] = (uint32_t)__builtin_amdgcn_readlane((int)e[q], last);
+        }
+        int r = next_row(lo, hi, -1);
+        uint32_t c0 = r < 3 ? pick3(lo, r) : 0u;
+        float4 cur = z4;
+        if (r < 3) cur = chunk_load(spos, c0, min((uint32_t)kWave, pick3(hi, r) - c0), lane);
+        while (r < 3) {  // wave-uniform
+            const uint32_t hr_end = pick3(hi, r);
+            const uint32_t m = min((uint32_t)kWave, hr_end - c0);
+            // A group representative ends the chunk; its members (which follow it) are skipped
+            // and it counts for all of them.
+            const uint32_t wb = __float_as_uint(cur.w);
+            const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
+            uint32_t mm = m, gm = 0;
+            if (reps) {
+                const int rl = __ffsll((unsigned long long)reps) - 1;
+                mm = (uint32_t)rl;
+                gm = (uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag;
             }
+            int nr = r;
+            uint32_t nc0 = gm ? c0 + mm + gm : c0 + m;
+            if (nc0 >= hr_end) {
+                nr = next_row(lo, hi, r);
+                nc0 = nr < 3 ? pick3(lo, nr) : 0u;
+            }
+            float4 nq = z4;
+            if (nr < 3) nq = chunk_load(spos, nc0, min((uint32_t)kWave, pick3(hi, nr) - nc0), lane);
+            __builtin_amdgcn_wave_barrier();
+            buf[lane] = cur;
+            __builtin_amdgcn_wave_barrier();
+            if (mine) {
+                const uint32_t br = pick3(b, r), er = pick3(e, r);
+                acc = density_run(buf, c0, max(br, c0), min(er, c0 + mm), pi, h2, acc);
+                const uint32_t jr = c0 + mm;
+                if (gm && jr >= br && jr < er) {
+                    const float4 g4 = buf[mm];
+                    const float dx = pi.x - g4.x, dy = pi.y - g4.y, dz = pi.z - g4.z;
+                    const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+                    acc = fmaf((float)gm * d, d * d, acc);
+                }
+            }
+            r = nr;
+            c0 = nc0;
+            cur = nq;
         }
     }
     if (live) dpart[(size_t)slab * stride + s] = acc;
@@ -527,18 +578,73 @@ __device__ __forceinline__ bool seg_row(const float4& p, const GridDesc& g, int 
     return cy >= 0 && cy < (int)g.ny && cz >= 0 && cz < (int)g.nz;
 }
 
-__global__ __launch_bounds__(kHeavyThreads) void k_density_heavy(
+// Chunk t of a segment whose rows r = 0..2 have the plans R[r] (rows in order): row, first
+// candidate and size; r = 3 past the end.
+__device__ __forceinline__ void seg_chunk(const RowPlan R[3], uint32_t t, int& r, uint32_t& c0,
+                                          uint32_t& m) {
+    r = 3;
+    c0 = 0;
+    m = 0;
+    if (t < R[0].total) {
+        r = 0;
+    } else if (t < R[0].total + R[1].total) {
+        r = 1;
+        t -= R[0].total;
+    } else if (t < R[0].total + R[1].total + R[2].total) {
+        r = 2;
+        t -= R[0].total + R[1].total;
+    } else {
+        return;
+    }
+    if (r == 0) row_chunk(R[0], t, c0, m);  // constant indices: the plans stay in registers
+    else if (r == 1) row_chunk(R[1], t, c0, m);
+    else row_chunk(R[2], t, c0, m);
+}
+
+// The plans of the 3 rows of a segment (leader / last lane of the segment): the row union,
+// cut around co-located groups when the item touches any (`cut`).
+__device__ __forceinline__ void seg_plans(RowPlan R[3], const float4& pi, const GridDesc& g,
+                                          int dz, const uint32_t b[3], const uint32_t e[3],
+                                          int leader, int last, bool cut,
+                                          const uint32_t* __restrict__ cstart,
+                                          const uint64_t* __restrict__ cell_grp, uint32_t epoch,
+                                          int lane) {
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
+        R[r].k = 1;
+        R[r].lo[0] = lo;
+        R[r].hi[0] = lo < hi ? hi : lo;
+        R[r].total = lo < hi ? (hi - lo + kWave - 1) / kWave : 0u;
+        if (cut && lo < hi) {
+            uint32_t rowbase;
+            int cx;
+            (void)seg_row(pi, g, dz, r, rowbase, cx);
+            rowbase = (uint32_t)__builtin_amdgcn_readlane((int)rowbase, leader);
+            const int xa = max(__builtin_amdgcn_readlane(cx, leader) - 1, 0);
+            const int xb = min(__builtin_amdgcn_readlane(cx, last) + 1, (int)g.nx - 1);
+            row_plan(R[r], lo, hi, rowbase, xa, xb, cstart, cell_grp, epoch, lane);
+        }
+    }
+}
+
+
+template <int HW>
+__global__ __launch_bounds__(HW * kWave) void k_density_heavy(
     const float4* __restrict__ spos, uint32_t n, GridDesc g, const uint32_t* __restrict__ cstart,
     const uint64_t* __restrict__ cell_grp, float h2, float* __restrict__ dpart, uint32_t stride,
     const uint32_t* __restrict__ heavy, const Control* __restrict__ ctl) {
-    __shared__ float4 s_p[kHeavyWaves][kWave];
-    __shared__ float s_acc[kHeavyWaves][kSub];
+    __shared__ float4 s_p[HW][kWave];
+    __shared__ float s_acc[HW][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t count = ctl->heavy_count.v, epoch = ctl->epoch;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float4* buf = s_p[wave];
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
-        const uint32_t item = heavy[it];
+        const uint32_t entry = heavy[it];
+        const bool cut = (entry & kCutFlag) != 0u;  // the item touches a co-located group
+        const uint32_t item = entry & ~kCutFlag;
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool live = s < n;
@@ -555,35 +661,40 @@ __global__ __launch_bounds__(kHeavyThreads) void k_density_heavy(
             const uint64_t seg = __ballot(mine);
             pending &= ~seg;
             const int last = 63 - __clzll((long long)seg);
-            for (int r = 0; r < 3; r++) {
-                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
-                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
-                if (lo >= hi) continue;
-                uint32_t rowbase;
-                int cx;
-                (void)seg_row(pi, g, (int)slab - 1, r, rowbase, cx);
-                rowbase = (uint32_t)__builtin_amdgcn_readlane((int)rowbase, leader);
-                const int xa = max(__builtin_amdgcn_readlane(cx, leader) - 1, 0);
-                const int xb = min(__builtin_amdgcn_readlane(cx, last) + 1, (int)g.nx - 1);
-                RowPlan R;
-                row_plan(R, lo, hi, rowbase, xa, xb, cstart, cell_grp, epoch, lane);
-                for (uint32_t q = (uint32_t)wave; q < R.total; q += kHeavyWaves) {
-                    uint32_t c0, m;
-                    row_chunk(R, q, c0, m);
-                    const uint32_t j = c0 + (uint32_t)lane;
-                    const float4 v = (uint32_t)lane < m ? spos[j] : z4;
-                    __builtin_amdgcn_wave_barrier();
-                    buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
-                    __builtin_amdgcn_wave_barrier();
-                    if (mine) acc = density_run_w(buf, c0, max(b[r], c0), min(e[r], c0 + m), pi, h2, acc);
-                }
+            RowPlan R[3];
+            seg_plans(R, pi, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
+                      lane);
+            // chunks wave, wave + HW, ... of the segment's three rows; the next is fetched
+            // before the current one is evaluated
+            uint32_t t = (uint32_t)wave;
+            int r;
+            uint32_t c0, m;
+            seg_chunk(R, t, r, c0, m);
+            float4 v = r < 3 ? chunk_load(spos, c0, m, lane) : z4;
+            while (r < 3) {  // uniform within the wave
+                int nr;
+                uint32_t nc0, nm;
+                seg_chunk(R, t + HW, nr, nc0, nm);
+                const float4 nv = nr < 3 ? chunk_load(spos, nc0, nm, lane) : z4;
+                const uint32_t j = c0 + (uint32_t)lane;
+                __builtin_amdgcn_wave_barrier();
+                buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
+                __builtin_amdgcn_wave_barrier();
+                if (mine)
+                    acc = density_run_w(buf, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m),
+                                        pi, h2, acc);
+                t += HW;
+                r = nr;
+                c0 = nc0;
+                m = nm;
+                v = nv;
             }
         }
         s_acc[wave][lane] = acc;
         __syncthreads();
         if (wave == 0) {
             float t = 0.0f;
-            for (int w = 0; w < kHeavyWaves; w++) t += s_acc[w][lane];
+            for (int w = 0; w < HW; w++) t += s_acc[w][lane];
             if (live) dpart[(size_t)slab * stride + s] = t;
         }
         __syncthreads();
@@ -716,33 +827,47 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         const uint64_t seg = __ballot(mine);
         pending &= ~seg;
         const int last = 63 - __clzll((long long)seg);
+        uint32_t lo[3], hi[3];
 #pragma unroll
-        for (int r = 0; r < 3; r++) {
-            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
-            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
-            uint32_t c0 = lo;
-            while (c0 < hi) {  // wave-uniform
-                const uint32_t m = min((uint32_t)kWave, hi - c0);
-                const ForceSlot f = force_fetch(spos, svel, vrep, dpart, stride, c0 + lane,
-                                                (uint32_t)lane < m);
-                // a group representative (staged with its weight) ends the chunk; its members
-                // follow it and are skipped
-                const uint32_t wb = __float_as_uint(f.q.w);
-                const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
-                uint32_t mm = m, skip = 0;
-                if (reps) {
-                    const int rl = __ffsll((unsigned long long)reps) - 1;
-                    mm = (uint32_t)rl + 1u;
-                    skip = ((uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag) - 1u;
-                }
-                __builtin_amdgcn_wave_barrier();
-                force_store(bp, bv, lane, c0 + lane, f, K);
-                __builtin_amdgcn_wave_barrier();
-                if (mine)
-                    force_run(bp, bv, c0, max(b[r], c0), min(e[r], c0 + mm), pi, vi, p_i, K, ax,
-                              ay, az, wv);
-                c0 += mm + skip;
+        for (int q = 0; q < 3; q++) {
+            lo[q] = (uint32_t)__builtin_amdgcn_readlane((int)b[q], leader);
+            hi[q] = (uint32_t)__builtin_amdgcn_readlane((int)e[q], last);
+        }
+        int r = next_row(lo, hi, -1);
+        uint32_t c0 = r < 3 ? pick3(lo, r) : 0u;
+        ForceSlot cur = force_fetch(spos, svel, vrep, dpart, stride, c0 + lane,
+                                    r < 3 && (uint32_t)lane < min((uint32_t)kWave, pick3(hi, r) - c0));
+        while (r < 3) {  // wave-uniform
+            const uint32_t hr_end = pick3(hi, r);
+            const uint32_t m = min((uint32_t)kWave, hr_end - c0);
+            // a group representative (staged with its weight) ends the chunk; its members
+            // follow it and are skipped
+            const uint32_t wb = __float_as_uint(cur.q.w);
+            const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
+            uint32_t mm = m, skip = 0;
+            if (reps) {
+                const int rl = __ffsll((unsigned long long)reps) - 1;
+                mm = (uint32_t)rl + 1u;
+                skip = ((uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag) - 1u;
             }
+            int nr = r;
+            uint32_t nc0 = c0 + mm + skip;
+            if (nc0 >= hr_end) {
+                nr = next_row(lo, hi, r);
+                nc0 = nr < 3 ? pick3(lo, nr) : 0u;
+            }
+            const ForceSlot nxt = force_fetch(
+                spos, svel, vrep, dpart, stride, nc0 + lane,
+                nr < 3 && (uint32_t)lane < min((uint32_t)kWave, pick3(hi, nr) - nc0));
+            __builtin_amdgcn_wave_barrier();
+            force_store(bp, bv, lane, c0 + lane, cur, K);
+            __builtin_amdgcn_wave_barrier();
+            if (mine)
+                force_run(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + mm), pi, vi,
+                          p_i, K, ax, ay, az, wv);
+            r = nr;
+            c0 = nc0;
+            cur = nxt;
         }
     }
     if (in) {
@@ -754,22 +879,25 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     }
 }
 
-__global__ __launch_bounds__(kHeavyThreads) void k_force_heavy(
+template <int HW>
+__global__ __launch_bounds__(HW * kWave) void k_force_heavy(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
     const float4* __restrict__ vrep, const float* __restrict__ dpart, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
     float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
     const uint32_t* __restrict__ heavy, const Control* __restrict__ ctl) {
-    __shared__ float4 s_p[kHeavyWaves][kWave];
-    __shared__ float4 s_v[kHeavyWaves][kWave];
-    __shared__ float s_acc[4][kHeavyWaves][kSub];
+    __shared__ float4 s_p[HW][kWave];
+    __shared__ float4 s_v[HW][kWave];
+    __shared__ float s_acc[4][HW][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t count = ctl->heavy_count.v, epoch = ctl->epoch;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float4* bp = s_p[wave];
     float4* bv = s_v[wave];
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
-        const uint32_t item = heavy[it];
+        const uint32_t entry = heavy[it];
+        const bool cut = (entry & kCutFlag) != 0u;
+        const uint32_t item = entry & ~kCutFlag;
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool in = s < n;
@@ -790,30 +918,32 @@ __global__ __launch_bounds__(kHeavyThreads) void k_force_heavy(
             const uint64_t seg = __ballot(mine);
             pending &= ~seg;
             const int last = 63 - __clzll((long long)seg);
-            for (int r = 0; r < 3; r++) {
-                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
-                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], last);
-                if (lo >= hi) continue;
-                uint32_t rowbase;
-                int cx;
-                (void)seg_row(pi, g, (int)slab - 1, r, rowbase, cx);
-                rowbase = (uint32_t)__builtin_amdgcn_readlane((int)rowbase, leader);
-                const int xa = max(__builtin_amdgcn_readlane(cx, leader) - 1, 0);
-                const int xb = min(__builtin_amdgcn_readlane(cx, last) + 1, (int)g.nx - 1);
-                RowPlan R;
-                row_plan(R, lo, hi, rowbase, xa, xb, cstart, cell_grp, epoch, lane);
-                for (uint32_t q = (uint32_t)wave; q < R.total; q += kHeavyWaves) {
-                    uint32_t c0, m;
-                    row_chunk(R, q, c0, m);
-                    const uint32_t j = c0 + (uint32_t)lane;
-                    const ForceSlot f = force_fetch(spos, svel, vrep, dpart, stride, j, (uint32_t)lane < m);
-                    __builtin_amdgcn_wave_barrier();
-                    force_store(bp, bv, lane, j, f, K);
-                    __builtin_amdgcn_wave_barrier();
-                    if (mine)
-                        force_run(bp, bv, c0, max(b[r], c0), min(e[r], c0 + m), pi, vi, p_i, K,
-                                  ax, ay, az, wv);
-                }
+            RowPlan R[3];
+            seg_plans(R, pi, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
+                      lane);
+            uint32_t t = (uint32_t)wave;
+            int r;
+            uint32_t c0, m;
+            seg_chunk(R, t, r, c0, m);
+            ForceSlot f = force_fetch(spos, svel, vrep, dpart, stride, c0 + lane,
+                                      r < 3 && (uint32_t)lane < m);
+            while (r < 3) {  // uniform within the wave
+                int nr;
+                uint32_t nc0, nm;
+                seg_chunk(R, t + HW, nr, nc0, nm);
+                const ForceSlot nf = force_fetch(spos, svel, vrep, dpart, stride, nc0 + lane,
+                                                 nr < 3 && (uint32_t)lane < nm);
+                __builtin_amdgcn_wave_barrier();
+                force_store(bp, bv, lane, c0 + lane, f, K);  // members of a group: weight 0
+                __builtin_amdgcn_wave_barrier();
+                if (mine)
+                    force_run(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m), pi, vi,
+                              p_i, K, ax, ay, az, wv);
+                t += HW;
+                r = nr;
+                c0 = nc0;
+                m = nm;
+                f = nf;
             }
         }
         s_acc[0][wave][lane] = ax;
@@ -823,11 +953,11 @@ __global__ __launch_bounds__(kHeavyThreads) void k_force_heavy(
         __syncthreads();
         if (wave < 3) {  // wave c reduces component c in wave order
             float t = 0.0f;
-            for (int w = 0; w < kHeavyWaves; w++) t += s_acc[wave][w][lane];
+            for (int w = 0; w < HW; w++) t += s_acc[wave][w][lane];
             if (in) fpart[((size_t)slab * 3u + (uint32_t)wave) * stride + s] = t;
         } else if (wave == 3 && in && (__float_as_uint(pi.w) & kRepFlag)) {
             float t = 0.0f;
-            for (int w = 0; w < kHeavyWaves; w++) t += s_acc[3][w][lane];
+            for (int w = 0; w < HW; w++) t += s_acc[3][w][lane];
             wpart[(size_t)slab * stride + s] = t;
         }
         __syncthreads();
@@ -969,7 +1099,7 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     tbeg(c, KID_DHEAVY);
-    k_density_heavy<<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
+    k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
         c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
         c->ctl);
     tend(c, KID_DHEAVY);
@@ -1024,7 +1154,7 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     tbeg(c, KID_FHEAVY);
-    k_force_heavy<<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
+    k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
         c->spos, c->svel, c->vrep, c->dpart, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
         c->wpart, c->max_n, c->heavy, c->ctl);
     tend(c, KID_FHEAVY);
