@@ -160,6 +160,8 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->collapsed, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
     if (e == hipSuccess) e = alloc(&c->wpart, 3 * (size_t)max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->vrep, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->rank, max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->sout, 3 * (size_t)max_n, &tot);
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_error, sizeof(uint32_t), hipHostMallocDefault);
     if (e == hipSuccess) {
         if (stream) {
@@ -207,7 +209,7 @@ int fh_destroy(fh_ctx* c) {
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
                     c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hist_part,
-                    c->cell_grp, c->big, c->collapsed, c->wpart, c->vrep};
+                    c->cell_grp, c->big, c->collapsed, c->wpart, c->vrep, c->rank, c->sout};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);

@@ -122,6 +122,9 @@ struct fh_ctx {
     uint2* collapsed;    // [ceil(max_n / 64) + 1] (representative, count) of co-located groups
     float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
     float4* vrep;        // [max_n] summed velocity of the group, at representative indices
+    uint32_t* rank;      // [max_n] sorted position of each particle (inverse of sidx)
+    float4* sout;        // [3][max_n] new state in sorted order: (x, y, z, rho), (vx, vy, vz, .),
+                         // (ax, ay, az, .) before it is moved to particle order
     bool sph_exact;      // FH_OPT_SPH_EXACT
     uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
     uint32_t* h_error;   // pinned host word for the device error flag

@@ -17,22 +17,35 @@
 
 namespace fh {
 
-// Sorted-order copies of the state: spos[s] = (pos[sidx[s]], bits of s), svel[s] =
-// vel[sidx[s]], and the run tags of the sorted keys (first index of each cell's run, k_runs).
-__global__ __launch_bounds__(256) void k_gather(
-    const float* __restrict__ px, const float* __restrict__ py, const float* __restrict__ pz,
-    const float* __restrict__ vx, const float* __restrict__ vy, const float* __restrict__ vz,
-    const uint32_t* __restrict__ sidx, const uint32_t* __restrict__ skeys, uint32_t n,
-    float4* __restrict__ spos, float4* __restrict__ svel, uint64_t* __restrict__ run_tag,
-    const Control* __restrict__ ctl) {
+// Sorted-order copies of the state, in two passes.  k_rank (sorted order): the run tags of the
+// sorted keys (first index of each cell's run, see k_runs) and rank[sidx[s]] = s.  k_gather
+// (particle order): spos[rank[i]] = (pos[i], bits of rank[i]), svel[rank[i]] = vel[i] -- the
+// caller's arrays are read in order and each particle costs two 16-byte stores, instead of six
+// 4-byte reads from scattered lines.
+__global__ __launch_bounds__(256) void k_rank(const uint32_t* __restrict__ sidx,
+                                              const uint32_t* __restrict__ skeys, uint32_t n,
+                                              uint32_t* __restrict__ rank,
+                                              uint64_t* __restrict__ run_tag,
+                                              const Control* __restrict__ ctl) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const uint32_t k = skeys[s];
     if (s == 0 || skeys[s - 1] != k) run_tag[k] = ((uint64_t)ctl->epoch << 32) | s;
-    uint32_t i = sidx[s];
-    if (i >= n) i = 0;  // never taken when the sort is consistent
-    spos[s] = make_float4(px[i], py[i], pz[i], __uint_as_float(s));
-    if (svel) svel[s] = make_float4(vx[i], vy[i], vz[i], 0.0f);
+    const uint32_t i = sidx[s];
+    if (i < n) rank[i] = s;
+}
+
+__global__ __launch_bounds__(256) void k_gather(
+    const float* __restrict__ px, const float* __restrict__ py, const float* __restrict__ pz,
+    const float* __restrict__ vx, const float* __restrict__ vy, const float* __restrict__ vz,
+    const uint32_t* __restrict__ rank, uint32_t n, float4* __restrict__ spos,
+    float4* __restrict__ svel) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t r = rank[i];
+    if (r >= n) return;  // never taken when the sort is consistent
+    spos[r] = make_float4(px[i], py[i], pz[i], __uint_as_float(r));
+    if (svel) svel[r] = make_float4(vx[i], vy[i], vz[i], 0.0f);
 }
 
 hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const float* pz,
@@ -40,11 +53,16 @@ hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const floa
                          bool with_vel) {
     if (n == 0) return hipSuccess;
     tbeg(c, KID_GATHER);
-    k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->sidx, c->skeys,
-                                                       n, c->spos, with_vel ? c->svel : nullptr,
-                                                       c->run_tag, c->ctl);
+    k_rank<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->sidx, c->skeys, n, c->rank, c->run_tag,
+                                                     c->ctl);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) {
+        k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->rank, n,
+                                                           c->spos, with_vel ? c->svel : nullptr);
+        e = hipGetLastError();
+    }
     tend(c, KID_GATHER);
-    return hipGetLastError();
+    return e;
 }
 
 // Clamped cell of a particle in the SPH kernels (sph_density.rs:421-426): grid origin 0.

@@ -173,6 +173,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict
                                                          float4* __restrict__ spos,
                                                          float4* __restrict__ svel,
                                                          uint32_t* __restrict__ sidx,
+                                                         uint32_t* __restrict__ rank,
                                                          uint32_t* __restrict__ scratch,
                                                          uint64_t* __restrict__ cell_grp,
                                                          float4* __restrict__ vrep,
@@ -213,9 +214,11 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict
             spos[t] = make_float4(pu.x, pu.y, pu.z, pt.w);
             spos[u] = make_float4(pt.x, pt.y, pt.z, pu.w);
             if (svel) swap4(svel, t, u);
-            const uint32_t ti = sidx[t];
-            sidx[t] = sidx[u];
+            const uint32_t ti = sidx[t], ui = sidx[u];
+            sidx[t] = ui;
             sidx[u] = ti;
+            rank[ui] = t;
+            rank[ti] = u;
         }
         __threadfence_block();
         __syncthreads();
@@ -974,23 +977,18 @@ struct Finish {
 constexpr uint32_t kDensityOnly = 1u << 31;
 
 // Sum the slab partials, apply v += a dt and the fused epilogue (gravity.rs:33,
-// integrate.rs:23-29, box_collider.rs:37-46), scatter everything back to particle order.
+// integrate.rs:23-29, box_collider.rs:37-46), in sorted order: the new state goes to
+// sout[0][s] = (x, y, z, rho), sout[1][s] = (vx, vy, vz, 0) and, when accelerations are asked
+// for, sout[2][s] = (ax, ay, az, 0).  k_scatter then moves it to particle order.
 __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spos,
                                                   const float4* __restrict__ svel,
                                                   const float* __restrict__ dpart,
                                                   const float* __restrict__ fpart,
-                                                  const float* __restrict__ wpart,
-                                                  const uint32_t* __restrict__ sidx, uint32_t n,
-                                                  uint32_t stride, Finish F,
-                                                  float* __restrict__ px, float* __restrict__ py,
-                                                  float* __restrict__ pz, float* __restrict__ vx,
-                                                  float* __restrict__ vy, float* __restrict__ vz,
-                                                  float* __restrict__ density,
-                                                  float* __restrict__ accel) {
+                                                  const float* __restrict__ wpart, uint32_t n,
+                                                  uint32_t stride, Finish F, bool want_accel,
+                                                  float4* __restrict__ sout) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
-    const uint32_t i = sidx[s];
-    if (i >= n) return;
     const float4 p = spos[s];
     // Co-located particle: its density, and its acceleration up to the viscosity term, are
     // those of its representative r; sum_j w_j (v_j - v_s) = [sum_j w_j (v_j - v_r)] + W (v_r - v_s)
@@ -999,8 +997,10 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     uint32_t r = (wb & kRepFlag) ? s : wb;
     if (r >= n) r = s;
     const float rho = rho_of(dpart, stride, r, F.mc);
-    if (density) density[i] = rho;
-    if (F.flags & kDensityOnly) return;
+    if (F.flags & kDensityOnly) {
+        sout[s] = make_float4(p.x, p.y, p.z, rho);
+        return;
+    }
     const float4 v = svel[s];
     float ax = 0.0f, ay = 0.0f, az = 0.0f;
     float nvx = v.x, nvy = v.y, nvz = v.z;
@@ -1046,18 +1046,43 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
         if (npz < F.mn[2]) { npz = F.mn[2]; nvz = fabsf(nvz) * F.e; }
         if (npz > F.mx[2]) { npz = F.mx[2]; nvz = -fabsf(nvz) * F.e; }
     }
-    vx[i] = nvx;
-    vy[i] = nvy;
-    vz[i] = nvz;
-    if (F.flags & (FH_EPI_INTEGRATE | FH_EPI_BOX)) {
-        px[i] = npx;
-        py[i] = npy;
-        pz[i] = npz;
+    sout[s] = make_float4(npx, npy, npz, rho);
+    sout[(size_t)stride + s] = make_float4(nvx, nvy, nvz, 0.0f);
+    if (want_accel) sout[2 * (size_t)stride + s] = make_float4(ax, ay, az, 0.0f);
+}
+
+// Particle order: particle i reads its new state at its sorted position rank[i] (16-byte
+// reads) and writes the caller's arrays coalesced.  Positions are written only when the
+// epilogue moves them.
+__global__ __launch_bounds__(256) void k_scatter(const float4* __restrict__ sout,
+                                                 const uint32_t* __restrict__ rank, uint32_t n,
+                                                 uint32_t stride, uint32_t flags,
+                                                 float* __restrict__ px, float* __restrict__ py,
+                                                 float* __restrict__ pz, float* __restrict__ vx,
+                                                 float* __restrict__ vy, float* __restrict__ vz,
+                                                 float* __restrict__ density,
+                                                 float* __restrict__ accel) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t r = rank[i];
+    if (r >= n) return;  // never taken when the sort is consistent
+    const float4 o0 = sout[r];
+    if (density) density[i] = o0.w;
+    if (flags & kDensityOnly) return;
+    const float4 o1 = sout[(size_t)stride + r];
+    vx[i] = o1.x;
+    vy[i] = o1.y;
+    vz[i] = o1.z;
+    if (flags & (FH_EPI_INTEGRATE | FH_EPI_BOX)) {
+        px[i] = o0.x;
+        py[i] = o0.y;
+        pz[i] = o0.z;
     }
     if (accel) {
-        accel[i] = ax;
-        accel[(size_t)n + i] = ay;
-        accel[2 * (size_t)n + i] = az;
+        const float4 o2 = sout[2 * (size_t)stride + r];
+        accel[i] = o2.x;
+        accel[(size_t)n + i] = o2.y;
+        accel[2 * (size_t)n + i] = o2.z;
     }
 }
 
@@ -1117,7 +1142,8 @@ hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
         // scratch: the sort's key buffer, free after the sort (disjoint ranges per cell)
         k_group<<<256, kGroupThreads, 0, c->stream>>>(c->big, cap, c->skeys, c->spos,
                                                       with_vel ? c->svel : nullptr, c->sidx,
-                                                      c->ka, c->cell_grp, c->vrep, c->ctl);
+                                                      c->rank, c->ka, c->cell_grp, c->vrep,
+                                                      c->ctl);
         e = hipGetLastError();
     }
     tend(c, KID_GROUP);
@@ -1179,10 +1205,17 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     F.e = epi ? epi->restitution : 0.0f;
     tbeg(c, KID_FINAL);
     k_finalize<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
-                                                           c->wpart, c->sidx, a.n, c->max_n, F,
-                                                           px, py, pz, vx, vy, vz, density, accel);
+                                                           c->wpart, a.n, c->max_n, F,
+                                                           accel != nullptr, c->sout);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) {
+        k_scatter<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->sout, c->rank, a.n, c->max_n,
+                                                              F.flags, px, py, pz, vx, vy, vz,
+                                                              density, accel);
+        e = hipGetLastError();
+    }
     tend(c, KID_FINAL);
-    return hipGetLastError();
+    return e;
 }
 
 }  // namespace fh
