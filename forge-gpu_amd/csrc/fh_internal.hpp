@@ -31,6 +31,15 @@ constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
 // particle, M | kRepFlag for a representative, the representative's index for the others.
 constexpr uint32_t kCollapseMin = 64;
 constexpr uint32_t kRepFlag = 0x80000000u;
+// A cell of >= kCollapseMin particles is examined in full only when at least kGroupHits of
+// kGroupSamples evenly spaced particles sit at the position of its middle particle (groups that
+// are a small minority of their cell are not collapsed; results are the same either way).
+constexpr uint32_t kGroupSamples = 16;
+constexpr uint32_t kGroupHits = 4;
+// The heavy SPH work list is split into kHeavyLists sub-lists with counters on separate lines,
+// so that appends from different workgroups do not serialise on one address.
+constexpr int kHeavyLists = 8;
+constexpr int kPlanThreads = 1024;  // k_plan workgroup: 16 sub-tiles, 48 (sub-tile, slab) items
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;  // 4096 cells per scan tile
@@ -63,7 +72,7 @@ struct Control {
     Line error;                         // nonzero: a look-back spin limit was hit
     Line tile_ctr[kMaxPasses];          // dynamic tile ids of the sort passes
     Line scan_ctr;                      // dynamic tile id of the cell scan
-    Line heavy_count;                   // entries in the heavy SPH work list of this substep
+    Line heavy_count[kHeavyLists];      // entries in each heavy SPH work sub-list
     Line collapse_count;                // entries in the list of co-located cells
     Line big_count;                     // entries in the list of cells of >= kCollapseMin
     uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
@@ -115,7 +124,8 @@ struct fh_ctx {
     float* srho;         // [max_n] density (exact kernels)
     float* dpart;        // [3][max_n] per-slab density partials (fast kernels)
     float* fpart;        // [3][3][max_n] per-slab acceleration partials (fast kernels)
-    uint32_t* heavy;     // [3 * ceil(max_n / 64)] heavy (64-particle tile, slab) work items
+    uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
+    uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
     uint64_t* cell_grp;  // [max_cells] epoch << 32 | number of co-located leading particles
     uint2* big;          // [ceil(max_n / 64) + 1] (first, count) of cells of >= kCollapseMin
@@ -123,8 +133,8 @@ struct fh_ctx {
     float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
     float4* vrep;        // [max_n] summed velocity of the group, at representative indices
     uint32_t* rank;      // [max_n] sorted position of each particle (inverse of sidx)
-    float4* sout;        // [3][max_n] new state in sorted order: (x, y, z, rho), (vx, vy, vz, .),
-                         // (ax, ay, az, .) before it is moved to particle order
+    float4* sout;        // [3 * max_n] new state in sorted order before it is moved to particle
+                         // order: pairs (x, y, z, rho), (vx, vy, vz, .), then (ax, ay, az, .)
     bool sph_exact;      // FH_OPT_SPH_EXACT
     uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
     uint32_t* h_error;   // pinned host word for the device error flag

@@ -41,7 +41,7 @@ __global__ void k_begin(Control* ctl, uint32_t* __restrict__ lb, uint32_t lb_wor
             ctl->plan = 0u;
             for (int p = 0; p < kMaxPasses; p++) ctl->tile_ctr[p].v = 0u;
             ctl->scan_ctr.v = 0u;
-            ctl->heavy_count.v = 0u;
+            for (int q = 0; q < kHeavyLists; q++) ctl->heavy_count[q].v = 0u;
             ctl->collapse_count.v = 0u;
             ctl->big_count.v = 0u;
         }

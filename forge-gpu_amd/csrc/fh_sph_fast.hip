@@ -120,13 +120,21 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
     return acc + ((a0 + a1) + (a2 + a3));
 }
 
-// Co-located groups.  k_big lists the cells of >= kCollapseMin particles.  k_group, one
-// workgroup per listed cell, takes the position P of the cell's middle particle, counts the
-// particles at exactly P (M) and, when M >= kCollapseMin, moves them to the front of the cell:
-// the misplaced particles on both sides are ranked and swapped pairwise, in place.  The order
-// inside such a cell then differs from ascending particle id (sums only change by rounding).
+// Co-located groups.  k_big lists the cells of >= kCollapseMin particles in which at least
+// kGroupHits of kGroupSamples evenly spaced particles sit at the position P of the middle
+// particle.  k_group, one workgroup per listed cell, counts the particles at exactly P (M) and,
+// when M >= kCollapseMin, moves them to the front of the cell: the misplaced particles on both
+// sides are ranked and swapped pairwise, in place.  The order inside such a cell then differs
+// from ascending particle id (sums only change by rounding).
+__device__ __forceinline__ bool same_pos(const float4& a, const float4& b) {
+    return __float_as_uint(a.x) == __float_as_uint(b.x) &&
+           __float_as_uint(a.y) == __float_as_uint(b.y) &&
+           __float_as_uint(a.z) == __float_as_uint(b.z);
+}
+
 __global__ __launch_bounds__(256) void k_big(const uint32_t* __restrict__ skeys,
-                                             const uint32_t* __restrict__ cstart, uint32_t n,
+                                             const uint32_t* __restrict__ cstart,
+                                             const float4* __restrict__ spos, uint32_t n,
                                              uint2* __restrict__ big, uint32_t cap,
                                              Control* ctl) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
@@ -135,14 +143,17 @@ __global__ __launch_bounds__(256) void k_big(const uint32_t* __restrict__ skeys,
     if (cstart[c] != s) return;  // not the first particle of its cell
     const uint32_t cnt = min(cstart[c + 1u], n) - s;
     if (cnt < kCollapseMin) return;
+    const float4 P = spos[s + cnt / 2u];
+    float4 v[kGroupSamples];
+#pragma unroll
+    for (uint32_t k = 0; k < kGroupSamples; k++)
+        v[k] = spos[s + (uint32_t)(((uint64_t)k * cnt) / kGroupSamples)];
+    uint32_t hits = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kGroupSamples; k++) hits += same_pos(v[k], P) ? 1u : 0u;
+    if (hits < kGroupHits) return;
     const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
     if (slot < cap) big[slot] = make_uint2(s, cnt);
-}
-
-__device__ __forceinline__ bool same_pos(const float4& a, const float4& b) {
-    return __float_as_uint(a.x) == __float_as_uint(b.x) &&
-           __float_as_uint(a.y) == __float_as_uint(b.y) &&
-           __float_as_uint(a.z) == __float_as_uint(b.z);
 }
 
 __device__ __forceinline__ void swap4(float4* p, uint32_t a, uint32_t b) {
@@ -153,6 +164,7 @@ __device__ __forceinline__ void swap4(float4* p, uint32_t a, uint32_t b) {
 
 constexpr int kGroupThreads = 1024;
 constexpr int kGroupWaves = kGroupThreads / kWave;
+constexpr uint32_t kGroupUnroll = 8;  // particles loaded per thread before they are examined
 
 // Workgroup sum of one value per thread, added in a fixed order (deterministic).
 __device__ __forceinline__ float group_sum(float v, float* s_w) {
@@ -164,6 +176,20 @@ __device__ __forceinline__ float group_sum(float v, float* s_w) {
     for (int w = 0; w < kGroupWaves; w++) t += s_w[w];
     __syncthreads();
     return t;
+}
+
+// Bit k of the result: particle t + k (< t1) sits at P.  The loads are issued together from
+// clamped indices.
+__device__ __forceinline__ uint32_t match_bits(const float4* __restrict__ spos, uint32_t t,
+                                               uint32_t t1, const float4& P) {
+    float4 v[kGroupUnroll];
+#pragma unroll
+    for (uint32_t k = 0; k < kGroupUnroll; k++) v[k] = spos[min(t + k, t1 - 1u)];
+    uint32_t m = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kGroupUnroll; k++)
+        m |= (t + k < t1 && same_pos(v[k], P)) ? (1u << k) : 0u;
+    return m;
 }
 
 // Blocked layout: thread t owns particles [f + t L, f + (t + 1) L) of the cell, L = ceil(cnt / 1024).
@@ -188,47 +214,73 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict
         const float4 P = spos[f + cnt / 2u];
         const uint32_t L = ceil_div(cnt, (uint32_t)kGroupThreads);
         const uint32_t t0 = min(f + tid * L, end), t1 = min(t0 + L, end);
-        uint32_t mine = 0, M;
-        for (uint32_t t = t0; t < t1; t++) mine += same_pos(spos[t], P) ? 1u : 0u;
+        // Membership bits of the thread's particles (L <= 32 kept in a register word; larger
+        // cells are re-read in the later phases).
+        const bool fits = L <= 32u;
+        uint32_t bits = 0, mine = 0, M;
+        for (uint32_t t = t0; t < t1; t += kGroupUnroll) {
+            const uint32_t m = match_bits(spos, t, t1, P);
+            mine += (uint32_t)__popc(m);
+            if (fits) bits |= m << (t - t0);
+        }
         (void)block_exclusive_scan<kGroupWaves>(mine, s_scan, &M);
         if (M < kCollapseMin) continue;  // uniform
         // misplaced particles: non-members before f + M, members from f + M on
         uint32_t nm = 0, mm = 0;
-        for (uint32_t t = t0; t < t1; t++) {
-            const bool m = same_pos(spos[t], P);
-            if (t < f + M) nm += m ? 0u : 1u;
-            else mm += m ? 1u : 0u;
+        for (uint32_t t = t0; t < t1; t += kGroupUnroll) {
+            const uint32_t m = fits ? (bits >> (t - t0)) & 0xFFu : match_bits(spos, t, t1, P);
+            for (uint32_t k = 0; k < kGroupUnroll && t + k < t1; k++) {
+                const bool is = (m >> k) & 1u;
+                if (t + k < f + M) nm += is ? 0u : 1u;
+                else mm += is ? 1u : 0u;
+            }
         }
         uint32_t tot;
         uint32_t knm = block_exclusive_scan<kGroupWaves>(nm, s_scan, &tot);
         uint32_t kmm = block_exclusive_scan<kGroupWaves>(mm, s_scan, &tot);
-        for (uint32_t t = t0; t < t1 && t < f + M; t++)
-            if (!same_pos(spos[t], P)) scratch[f + knm++] = t;
+        if (nm) {
+            for (uint32_t t = t0; t < t1 && t < f + M; t += kGroupUnroll) {
+                const uint32_t m = fits ? (bits >> (t - t0)) & 0xFFu : match_bits(spos, t, t1, P);
+                for (uint32_t k = 0; k < kGroupUnroll && t + k < t1 && t + k < f + M; k++)
+                    if (!((m >> k) & 1u)) scratch[f + knm++] = t + k;
+            }
+        }
         __threadfence_block();
         __syncthreads();
-        for (uint32_t t = max(t0, f + M); t < t1; t++) {
-            if (!same_pos(spos[t], P)) continue;
-            const uint32_t u = scratch[f + kmm++];
-            // positions move, the .w index bits stay with the slot
-            const float4 pt = spos[t], pu = spos[u];
-            spos[t] = make_float4(pu.x, pu.y, pu.z, pt.w);
-            spos[u] = make_float4(pt.x, pt.y, pt.z, pu.w);
-            if (svel) swap4(svel, t, u);
-            const uint32_t ti = sidx[t], ui = sidx[u];
-            sidx[t] = ui;
-            sidx[u] = ti;
-            rank[ui] = t;
-            rank[ti] = u;
+        if (mm) {
+            for (uint32_t t = max(t0, f + M); t < t1; t++) {
+                const bool is = fits ? (bits >> (t - t0)) & 1u : same_pos(spos[t], P);
+                if (!is) continue;
+                const uint32_t u = scratch[f + kmm++];
+                // positions move, the .w index bits stay with the slot
+                const float4 pt = spos[t], pu = spos[u];
+                spos[t] = make_float4(pu.x, pu.y, pu.z, pt.w);
+                spos[u] = make_float4(pt.x, pt.y, pt.z, pu.w);
+                if (svel) swap4(svel, t, u);
+                const uint32_t ti = sidx[t], ui = sidx[u];
+                sidx[t] = ui;
+                sidx[u] = ti;
+                rank[ui] = t;
+                rank[ti] = u;
+            }
         }
         __threadfence_block();
         __syncthreads();
         if (svel) {  // summed velocity of the group (fixed order)
             float vx = 0.0f, vy = 0.0f, vz = 0.0f;
-            for (uint32_t t = t0; t < t1 && t < f + M; t++) {
-                const float4 v = svel[t];
-                vx += v.x;
-                vy += v.y;
-                vz += v.z;
+            const uint32_t e1 = min(t1, f + M);
+            for (uint32_t t = t0; t < e1; t += kGroupUnroll) {
+                float4 v[kGroupUnroll];
+#pragma unroll
+                for (uint32_t k = 0; k < kGroupUnroll; k++) v[k] = svel[min(t + k, e1 - 1u)];
+#pragma unroll
+                for (uint32_t k = 0; k < kGroupUnroll; k++) {
+                    if (t + k < e1) {
+                        vx += v[k].x;
+                        vy += v[k].y;
+                        vz += v[k].z;
+                    }
+                }
             }
             vx = group_sum(vx, s_w);
             vy = group_sum(vy, s_w);
@@ -301,59 +353,108 @@ __device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, ui
 // acceleration up to the viscosity term that depends on the particle's own velocity
 // (k_finalize).  Then, per (sub-tile, slab), the largest per-particle candidate count decides
 // light / heavy.
-__global__ __launch_bounds__(256) void k_plan(float4* __restrict__ spos, uint32_t n, GridDesc g,
-                                              const uint32_t* __restrict__ cstart,
-                                              const uint64_t* __restrict__ cell_grp,
-                                              uint8_t* __restrict__ flag,
-                                              uint32_t* __restrict__ heavy,
-                                              uint2* __restrict__ collapsed, uint32_t cap,
-                                              uint32_t heavy_work, Control* ctl) {
+__global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos, uint32_t n,
+                                                       GridDesc g,
+                                                       const uint32_t* __restrict__ cstart,
+                                                       const uint64_t* __restrict__ cell_grp,
+                                                       uint8_t* __restrict__ flag,
+                                                       uint32_t* __restrict__ heavy,
+                                                       uint32_t heavy_cap,
+                                                       uint2* __restrict__ collapsed, uint32_t cap,
+                                                       uint32_t heavy_work, Control* ctl) {
+    constexpr int kWaves = kPlanThreads / kWave;
+    __shared__ uint32_t s_item[kWaves * 3];
+    __shared__ uint32_t s_count[kWaves];
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     const uint32_t sub = s / kSub;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const bool live = s < n;
-    if (sub * kSub >= n) return;  // whole wave beyond the particles
-    const float4 pi = live ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    bool member = false;
-    if (live) {
-        const uint32_t c = cell_of(pi.x, pi.y, pi.z, g);
-        const uint64_t grp = cell_grp[c];
-        if ((uint32_t)(grp >> 32) == ctl->epoch) {
-            const uint32_t f = cstart[c], M = (uint32_t)grp;
-            float* w = reinterpret_cast<float*>(spos + s) + 3;
-            if (s == f) {
-                *w = __uint_as_float(M | kRepFlag);
-                const uint32_t slot = atomicAdd(&ctl->collapse_count.v, 1u);
-                if (slot < cap) collapsed[slot] = make_uint2(f, M);
-            } else if (s < f + M) {
-                *w = __uint_as_float(f);
-                member = true;
+    uint32_t nh = 0;  // heavy items of this wave, kept in s_item[wave * 3 ...]
+    if (sub * kSub < n) {  // wave-uniform
+        const float4 pi = live ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        bool member = false;
+        if (live) {
+            const uint32_t c = cell_of(pi.x, pi.y, pi.z, g);
+            const uint64_t grp = cell_grp[c];
+            if ((uint32_t)(grp >> 32) == ctl->epoch) {
+                const uint32_t f = cstart[c], M = (uint32_t)grp;
+                float* w = reinterpret_cast<float*>(spos + s) + 3;
+                if (s == f) {
+                    *w = __uint_as_float(M | kRepFlag);
+                    const uint32_t slot = atomicAdd(&ctl->collapse_count.v, 1u);
+                    if (slot < cap) collapsed[slot] = make_uint2(f, M);
+                } else if (s < f + M) {
+                    *w = __uint_as_float(f);
+                    member = true;
+                }
+            }
+        }
+        if (__ballot(live && !member) == 0ull) {  // every particle of the sub-tile is co-located
+            if (lane == 0)
+                for (int slab = 0; slab < 3; slab++) flag[sub * 3u + (uint32_t)slab] = 2;
+        } else {
+            const uint32_t epoch = ctl->epoch;
+            for (int slab = 0; slab < 3; slab++) {
+                uint32_t b[3], e[3];
+                slab_ranges(pi, live, g, cstart, n, slab - 1, b, e);
+                uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
+                uint32_t excess = 0;
+                if (cand > heavy_work) {
+                    excess = grouped_excess(pi, g, cell_grp, epoch, slab - 1);
+                    cand -= excess;
+                }
+                const uint32_t w = wave_max(cand);
+                const bool touches = __ballot(excess > 0u) != 0ull;
+                const bool hv = w > heavy_work;
+                if (lane == 0) {
+                    const uint32_t item = sub * 3u + (uint32_t)slab;
+                    flag[item] = hv ? 1 : 0;
+                    if (hv) s_item[wave * 3 + (int)nh] = item | (touches ? kCutFlag : 0u);
+                }
+                nh += hv ? 1u : 0u;
             }
         }
     }
-    if (__ballot(live && !member) == 0ull) {  // every particle of the sub-tile is co-located
-        if ((threadIdx.x & 63) == 0)
-            for (int slab = 0; slab < 3; slab++) flag[sub * 3u + (uint32_t)slab] = 2;
-        return;
+    if (lane == 0) s_count[wave] = nh;
+    __syncthreads();
+    // one append per workgroup, to sub-list blockIdx % kHeavyLists, in wave order
+    __shared__ uint32_t s_base;
+    if (threadIdx.x == 0) {
+        uint32_t tot = 0;
+        for (int w = 0; w < kWaves; w++) tot += s_count[w];
+        s_base = tot ? atomicAdd(&ctl->heavy_count[blockIdx.x % kHeavyLists].v, tot) : 0u;
     }
-    const uint32_t epoch = ctl->epoch;
-    for (int slab = 0; slab < 3; slab++) {
-        uint32_t b[3], e[3];
-        slab_ranges(pi, live, g, cstart, n, slab - 1, b, e);
-        uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
-        uint32_t excess = 0;
-        if (cand > heavy_work) {
-            excess = grouped_excess(pi, g, cell_grp, epoch, slab - 1);
-            cand -= excess;
-        }
-        const uint32_t w = wave_max(cand);
-        const bool touches = __ballot(excess > 0u) != 0ull;
-        if ((threadIdx.x & 63) == 0) {
-            const uint32_t item = sub * 3u + (uint32_t)slab;
-            const bool hv = w > heavy_work;
-            flag[item] = hv ? 1 : 0;
-            if (hv) heavy[atomicAdd(&ctl->heavy_count.v, 1u)] = item | (touches ? kCutFlag : 0u);
+    __syncthreads();
+    if (threadIdx.x < kWaves * 3) {
+        const int w = threadIdx.x / 3, k = threadIdx.x - 3 * (threadIdx.x / 3);
+        uint32_t off = 0;
+        for (int v = 0; v < w; v++) off += s_count[v];
+        if ((uint32_t)k < s_count[w]) {
+            const uint32_t pos = s_base + off + (uint32_t)k;
+            if (pos < heavy_cap)
+                heavy[(size_t)(blockIdx.x % kHeavyLists) * heavy_cap + pos] = s_item[w * 3 + k];
         }
     }
+}
+
+// The heavy work lists of this substep as one sequence: entry q of the concatenation of the
+// kHeavyLists sub-lists.  heavy_total() is their total length.
+__device__ __forceinline__ uint32_t heavy_total(const Control* __restrict__ ctl, uint32_t cap) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int q = 0; q < kHeavyLists; q++) t += min(ctl->heavy_count[q].v, cap);
+    return t;
+}
+__device__ __forceinline__ uint32_t heavy_entry(const uint32_t* __restrict__ heavy,
+                                                const Control* __restrict__ ctl, uint32_t cap,
+                                                uint32_t q) {
+    int k = 0;
+    for (; k < kHeavyLists - 1; k++) {
+        const uint32_t c = min(ctl->heavy_count[k].v, cap);
+        if (q < c) break;
+        q -= c;
+    }
+    return heavy[(size_t)k * cap + q];
 }
 
 // After the density pass: every particle of a co-located cell takes its representative's
@@ -637,15 +738,15 @@ template <int HW>
 __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
     const float4* __restrict__ spos, uint32_t n, GridDesc g, const uint32_t* __restrict__ cstart,
     const uint64_t* __restrict__ cell_grp, float h2, float* __restrict__ dpart, uint32_t stride,
-    const uint32_t* __restrict__ heavy, const Control* __restrict__ ctl) {
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const Control* __restrict__ ctl) {
     __shared__ float4 s_p[HW][kWave];
     __shared__ float s_acc[HW][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = ctl->heavy_count.v, epoch = ctl->epoch;
+    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float4* buf = s_p[wave];
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
-        const uint32_t entry = heavy[it];
+        const uint32_t entry = heavy_entry(heavy, ctl, heavy_cap, it);
         const bool cut = (entry & kCutFlag) != 0u;  // the item touches a co-located group
         const uint32_t item = entry & ~kCutFlag;
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
@@ -888,17 +989,17 @@ __global__ __launch_bounds__(HW * kWave) void k_force_heavy(
     const float4* __restrict__ vrep, const float* __restrict__ dpart, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
     float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
-    const uint32_t* __restrict__ heavy, const Control* __restrict__ ctl) {
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const Control* __restrict__ ctl) {
     __shared__ float4 s_p[HW][kWave];
     __shared__ float4 s_v[HW][kWave];
     __shared__ float s_acc[4][HW][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = ctl->heavy_count.v, epoch = ctl->epoch;
+    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float4* bp = s_p[wave];
     float4* bv = s_v[wave];
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
-        const uint32_t entry = heavy[it];
+        const uint32_t entry = heavy_entry(heavy, ctl, heavy_cap, it);
         const bool cut = (entry & kCutFlag) != 0u;
         const uint32_t item = entry & ~kCutFlag;
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
@@ -977,9 +1078,10 @@ struct Finish {
 constexpr uint32_t kDensityOnly = 1u << 31;
 
 // Sum the slab partials, apply v += a dt and the fused epilogue (gravity.rs:33,
-// integrate.rs:23-29, box_collider.rs:37-46), in sorted order: the new state goes to
-// sout[0][s] = (x, y, z, rho), sout[1][s] = (vx, vy, vz, 0) and, when accelerations are asked
-// for, sout[2][s] = (ax, ay, az, 0).  k_scatter then moves it to particle order.
+// integrate.rs:23-29, box_collider.rs:37-46), in sorted order: the new state of particle s goes
+// to sout[2 s] = (x, y, z, rho) and sout[2 s + 1] = (vx, vy, vz, 0) (32 contiguous bytes) and,
+// when accelerations are asked for, to sout[2 stride + s] = (ax, ay, az, 0).  k_scatter then
+// moves it to particle order.
 __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spos,
                                                   const float4* __restrict__ svel,
                                                   const float* __restrict__ dpart,
@@ -998,7 +1100,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     if (r >= n) r = s;
     const float rho = rho_of(dpart, stride, r, F.mc);
     if (F.flags & kDensityOnly) {
-        sout[s] = make_float4(p.x, p.y, p.z, rho);
+        sout[2u * s] = make_float4(p.x, p.y, p.z, rho);
         return;
     }
     const float4 v = svel[s];
@@ -1046,13 +1148,13 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
         if (npz < F.mn[2]) { npz = F.mn[2]; nvz = fabsf(nvz) * F.e; }
         if (npz > F.mx[2]) { npz = F.mx[2]; nvz = -fabsf(nvz) * F.e; }
     }
-    sout[s] = make_float4(npx, npy, npz, rho);
-    sout[(size_t)stride + s] = make_float4(nvx, nvy, nvz, 0.0f);
+    sout[2u * s] = make_float4(npx, npy, npz, rho);
+    sout[2u * s + 1u] = make_float4(nvx, nvy, nvz, 0.0f);
     if (want_accel) sout[2 * (size_t)stride + s] = make_float4(ax, ay, az, 0.0f);
 }
 
-// Particle order: particle i reads its new state at its sorted position rank[i] (16-byte
-// reads) and writes the caller's arrays coalesced.  Positions are written only when the
+// Particle order: particle i reads its new state at its sorted position rank[i] (one 32-byte
+// read) and writes the caller's arrays coalesced.  Positions are written only when the
 // epilogue moves them.
 __global__ __launch_bounds__(256) void k_scatter(const float4* __restrict__ sout,
                                                  const uint32_t* __restrict__ rank, uint32_t n,
@@ -1066,10 +1168,10 @@ __global__ __launch_bounds__(256) void k_scatter(const float4* __restrict__ sout
     if (i >= n) return;
     const uint32_t r = rank[i];
     if (r >= n) return;  // never taken when the sort is consistent
-    const float4 o0 = sout[r];
+    const float4 o0 = sout[2u * r];
     if (density) density[i] = o0.w;
     if (flags & kDensityOnly) return;
-    const float4 o1 = sout[(size_t)stride + r];
+    const float4 o1 = sout[2u * r + 1u];
     vx[i] = o1.x;
     vy[i] = o1.y;
     vz[i] = o1.z;
@@ -1104,11 +1206,10 @@ static float poly6_mc(float h, float mass) {
 hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
     if (a.n == 0) return hipSuccess;
     tbeg(c, KID_PLAN);
-    k_plan<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, a.n, a.g, cell_start,
-                                                       c->cell_grp, c->heavy_flag, c->heavy,
-                                                       c->collapsed, ceil_div(c->max_n, 64u) + 1u,
-                                                       c->heavy_work ? c->heavy_work : kHeavyWork,
-                                                       c->ctl);
+    k_plan<<<ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0, c->stream>>>(
+        c->spos, a.n, a.g, cell_start, c->cell_grp, c->heavy_flag, c->heavy, c->heavy_cap,
+        c->collapsed, ceil_div(c->max_n, 64u) + 1u, c->heavy_work ? c->heavy_work : kHeavyWork,
+        c->ctl);
     tend(c, KID_PLAN);
     return hipGetLastError();
 }
@@ -1126,7 +1227,7 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     tbeg(c, KID_DHEAVY);
     k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
         c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
-        c->ctl);
+        c->heavy_cap, c->ctl);
     tend(c, KID_DHEAVY);
     return hipGetLastError();
 }
@@ -1135,8 +1236,8 @@ hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
     if (n == 0) return hipSuccess;
     const uint32_t cap = ceil_div(c->max_n, 64u) + 1u;
     tbeg(c, KID_GROUP);
-    k_big<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->skeys, c->cell_start, n, c->big, cap,
-                                                    c->ctl);
+    k_big<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->skeys, c->cell_start, c->spos, n, c->big,
+                                                    cap, c->ctl);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) {
         // scratch: the sort's key buffer, free after the sort (disjoint ranges per cell)
@@ -1182,7 +1283,7 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     tbeg(c, KID_FHEAVY);
     k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
         c->spos, c->svel, c->vrep, c->dpart, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
-        c->wpart, c->max_n, c->heavy, c->ctl);
+        c->wpart, c->max_n, c->heavy, c->heavy_cap, c->ctl);
     tend(c, KID_FHEAVY);
     return hipGetLastError();
 }
