@@ -174,6 +174,9 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
             c->own_stream = e == hipSuccess;
         }
     }
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming);
     // One-time clears (outside any capture): look-back words and run tags start untagged
     // (epoch 0 is never current).
     if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)kMaxPasses * c->max_sort_tiles * 256u * 4u, c->stream);
@@ -197,6 +200,7 @@ int fh_destroy(fh_ctx* c) {
     if (!c) return FH_OK;
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->side) (void)hipStreamSynchronize(c->side);
     if (c->exec) (void)hipGraphExecDestroy(c->exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
     for (int q = 0; q < kEvents; q++)
@@ -217,6 +221,9 @@ int fh_destroy(fh_ctx* c) {
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);
     if (c->own_stream && c->stream) (void)hipStreamDestroy(c->stream);
+    if (c->side) (void)hipStreamDestroy(c->side);
+    if (c->fork_ev) (void)hipEventDestroy(c->fork_ev);
+    if (c->join_ev) (void)hipEventDestroy(c->join_ev);
     delete c;
     return FH_OK;
 }

@@ -102,6 +102,10 @@ struct fh_ctx {
     int device;
     hipStream_t stream;
     bool own_stream;
+    // The heavy SPH kernels run on `side`, forked from and joined back into `stream` with the
+    // two events, so they overlap the light kernels (default priority, like `stream`).
+    hipStream_t side;
+    hipEvent_t fork_ev, join_ev;
     uint32_t max_n, max_cells;
     uint32_t max_sort_tiles, max_scan_tiles;
     // sort scratch
@@ -217,14 +221,14 @@ __device__ __forceinline__ uint32_t block256_exclusive_scan(uint32_t v, uint32_t
 }
 
 // Bracket a launch with the armed timer's events (no-op when the kernel is not armed).
-inline void tbeg(fh_ctx* c, KernelId k) {
+inline void tbeg(fh_ctx* c, KernelId k, hipStream_t s = nullptr) {
     Timer& t = c->timers[k];
-    if (t.used < t.max) (void)hipEventRecord(t.ev[2 * t.used], c->stream);
+    if (t.used < t.max) (void)hipEventRecord(t.ev[2 * t.used], s ? s : c->stream);
 }
-inline void tend(fh_ctx* c, KernelId k) {
+inline void tend(fh_ctx* c, KernelId k, hipStream_t s = nullptr) {
     Timer& t = c->timers[k];
     if (t.used < t.max) {
-        (void)hipEventRecord(t.ev[2 * t.used + 1], c->stream);
+        (void)hipEventRecord(t.ev[2 * t.used + 1], s ? s : c->stream);
         t.used++;
     }
 }

@@ -27,7 +27,14 @@
 
 namespace fh {
 
-constexpr int kTileP = 256;   // home particles per workgroup
+#ifndef FH_LW
+#define FH_LW 1
+#endif
+// Light kernels: waves per workgroup.  One: a workgroup's LDS is released as soon as its item
+// is done, however unequal the items (with several waves per workgroup the short items would
+// hold LDS while the longest one runs).
+constexpr int kLightWaves = FH_LW;
+constexpr int kTileP = kLightWaves * 64;  // home particles per light workgroup
 constexpr int kStage = 512;   // neighbour particles staged per chunk
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 
@@ -351,8 +358,8 @@ __device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, ui
 // to the collapsed list).  A sub-tile made only of such non-representative particles is
 // skipped by both passes (flag 2): its particles take the representative's density, and its
 // acceleration up to the viscosity term that depends on the particle's own velocity
-// (k_finalize).  Then, per (sub-tile, slab), the largest per-particle candidate count decides
-// light / heavy.
+// (k_finalize).  Then a (sub-tile, slab) item is heavy when its largest per-particle candidate
+// count (a group counting once) exceeds heavy_work or when it touches a co-located group.
 __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos, uint32_t n,
                                                        GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
@@ -399,13 +406,13 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
                 slab_ranges(pi, live, g, cstart, n, slab - 1, b, e);
                 uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
                 uint32_t excess = 0;
-                if (cand > heavy_work) {
+                if (cand >= kCollapseMin) {  // a grouped cell holds at least kCollapseMin
                     excess = grouped_excess(pi, g, cell_grp, epoch, slab - 1);
                     cand -= excess;
                 }
                 const uint32_t w = wave_max(cand);
                 const bool touches = __ballot(excess > 0u) != 0ull;
-                const bool hv = w > heavy_work;
+                const bool hv = w > heavy_work || touches;  // light items hold no group
                 if (lane == 0) {
                     const uint32_t item = sub * 3u + (uint32_t)slab;
                     flag[item] = hv ? 1 : 0;
@@ -498,98 +505,134 @@ __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[
 
 // Home-row segments.  A wave owns 64 consecutive sorted particles (a sub-tile); the particles of
 // one home row (cy, cz) are consecutive lanes, and for each of the slab's 3 rows the union of
-// their neighbour ranges is one short contiguous range (x-adjacent cells of that row only).
-// The wave walks its segments one at a time and stages each union through its own LDS slice
-// 64 candidates at a time: no workgroup barrier anywhere, so waves never wait for each other
-// and a sparse sub-tile spanning many rows never stages the unrelated cells between them.
+// their neighbour ranges is one contiguous range (x-adjacent cells of that row only): from the
+// first lane's begin to the last lane's end.
 __device__ __forceinline__ uint32_t home_row(const float4& p, const GridDesc& g) {
     return cell_coord(p.y, 0.0f, g.cs, g.ny) + cell_coord(p.z, 0.0f, g.cs, g.nz) * g.ny;
 }
 
+// Light items.  The candidates of a wave are laid out as one stream: for each home-row segment
+// in lane order, the unions of its rows 0, 1, 2.  Every lane's own range of row r is then one
+// contiguous interval [S[r], S[r] + cnt[r]) of the stream.  The stream is staged through the
+// wave's LDS slice kWin candidates at a time, and all lanes (of every segment at once) evaluate
+// their own intervals clipped to the window: segments no longer take turns.
+constexpr int kWin = 256;  // candidates staged per window
+constexpr int kWinLoads = kWin / kWave;
+
+struct LightStream {
+    uint32_t S[3], cnt[3];  // the lane's own intervals
+    uint32_t T;             // stream length (wave-uniform)
+    int nin;                // lanes holding a particle (a prefix of the wave)
+    // the lane's segment: first stream position, row unions [lo[r], lo[r] + L[r])
+    uint32_t base, lo0, lo1, lo2, L0, L1;
+};
+
+__device__ __forceinline__ void light_stream(LightStream& L, const uint32_t b[3],
+                                             const uint32_t e[3], uint32_t hr, bool in, int lane) {
+    L.nin = __popcll(__ballot(in));
+    const uint32_t hprev = (uint32_t)__shfl_up((int)hr, 1u, kWave);
+    const uint64_t starts = __ballot(in && (lane == 0 || hprev != hr));
+    const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+    const uint64_t before = starts & upto, after = starts & ~upto;
+    const int leader = before ? 63 - __clzll((long long)before) : 0;
+    const int last = after ? __ffsll((unsigned long long)after) - 2 : L.nin - 1;
+    const uint32_t lo0 = (uint32_t)__shfl((int)b[0], leader, kWave);
+    const uint32_t lo1 = (uint32_t)__shfl((int)b[1], leader, kWave);
+    const uint32_t lo2 = (uint32_t)__shfl((int)b[2], leader, kWave);
+    const uint32_t hi0 = (uint32_t)__shfl((int)e[0], last < 0 ? 0 : last, kWave);
+    const uint32_t hi1 = (uint32_t)__shfl((int)e[1], last < 0 ? 0 : last, kWave);
+    const uint32_t hi2 = (uint32_t)__shfl((int)e[2], last < 0 ? 0 : last, kWave);
+    L.lo0 = lo0;
+    L.lo1 = lo1;
+    L.lo2 = lo2;
+    L.L0 = hi0 - lo0;
+    L.L1 = hi1 - lo1;
+    const uint32_t len = L.L0 + L.L1 + (hi2 - lo2);
+    // inclusive scan of the segment lengths, counted at their leaders
+    uint32_t x = (in && lane == leader) ? len : 0u;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)x, (unsigned)d, kWave);
+        if (lane >= d) x += y;
+    }
+    L.T = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+    const uint32_t excl = x - ((in && lane == leader) ? len : 0u);
+    L.base = (uint32_t)__shfl((int)excl, leader, kWave);
+    L.S[0] = L.base + (b[0] - lo0);
+    L.S[1] = L.base + L.L0 + (b[1] - lo1);
+    L.S[2] = L.base + L.L0 + L.L1 + (b[2] - lo2);
+#pragma unroll
+    for (int r = 0; r < 3; r++) L.cnt[r] = in ? e[r] - b[r] : 0u;
+}
+
+// Sorted index of stream position t (< T): the last lane whose segment starts at or before t
+// (segment bases are non-decreasing over the lanes) gives the segment, then the row.
+__device__ __forceinline__ uint32_t stream_index(const LightStream& L, uint32_t t) {
+    int pos = 0;
+#pragma unroll
+    for (int step = 32; step >= 1; step >>= 1) {
+        const int c = pos + step;
+        const uint32_t sb = (uint32_t)__shfl((int)L.base, c < 64 ? c : 63, kWave);
+        if (c < L.nin && sb <= t) pos = c;
+    }
+    const uint32_t base = (uint32_t)__shfl((int)L.base, pos, kWave);
+    const uint32_t lo0 = (uint32_t)__shfl((int)L.lo0, pos, kWave);
+    const uint32_t lo1 = (uint32_t)__shfl((int)L.lo1, pos, kWave);
+    const uint32_t lo2 = (uint32_t)__shfl((int)L.lo2, pos, kWave);
+    const uint32_t L0 = (uint32_t)__shfl((int)L.L0, pos, kWave);
+    const uint32_t L1 = (uint32_t)__shfl((int)L.L1, pos, kWave);
+    const uint32_t u = t - base;
+    return u < L0 ? lo0 + u : (u < L0 + L1 ? lo1 + (u - L0) : lo2 + (u - L0 - L1));
+}
+
+// Sorted indices of the window's staging slots: slot k * 64 + lane holds stream position
+// w0 + k * 64 + lane; positions past the stream repeat its last element.
+__device__ __forceinline__ void window_indices(const LightStream& L, uint32_t w0, int lane,
+                                               uint32_t j[kWinLoads]) {
+#pragma unroll
+    for (int k = 0; k < kWinLoads; k++)
+        j[k] = stream_index(L, min(w0 + (uint32_t)(k * kWave + lane), L.T - 1u));
+}
+
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
+// Light items hold no co-located group (k_plan sends those to the heavy list).
 __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restrict__ spos,
                                                          uint32_t n, GridDesc g,
                                                          const uint32_t* __restrict__ cstart,
                                                          float h2, float* __restrict__ dpart,
                                                          uint32_t stride, uint32_t items,
                                                          const uint8_t* __restrict__ flag) {
-    __shared__ float4 s_p[kTileP / kWave][kWave];
+    __shared__ float4 s_p[kTileP / kWave][kWin];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
-    if (item >= items) return;  // whole wave
+    if (item >= items || flag[item]) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     const uint32_t s = sub * kSub + (uint32_t)lane;
-    const bool live = s < n && !flag[item];
-    const float4 pi = live ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const bool in = s < n;
+    const float4 pi = in ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     uint32_t b[3], e[3];
-    slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
-    const uint32_t hr = home_row(pi, g);
+    slab_ranges(pi, in, g, cstart, n, (int)slab - 1, b, e);
+    LightStream L;
+    light_stream(L, b, e, home_row(pi, g), in, lane);
     float4* buf = s_p[wave];
-    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float acc = 0.0f;
-    uint64_t pending = __ballot(live);
-    while (pending) {  // wave-uniform
-        const int leader = __ffsll((unsigned long long)pending) - 1;
-        const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
-        const bool mine = live && hr == row;
-        const uint64_t seg = __ballot(mine);
-        pending &= ~seg;
-        const int last = 63 - __clzll((long long)seg);
-        // The segment's lanes share the home row (so the same valid rows) and have
-        // non-decreasing ranges: the union of row r is [b of the first lane, e of the last lane).
-        // Its rows are walked as one chunk stream; the next chunk is fetched before the current
-        // one is evaluated.
-        uint32_t lo[3], hi[3];
+    for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
+        uint32_t j[kWinLoads];
+        window_indices(L, w0, lane, j);
+        float4 v[kWinLoads];
 #pragma unroll
-        for (int q = 0; q < 3; q++) {
-            lo[q] = (uint32_t)__builtin_amdgcn_readlane((int)b[q], leader);
-            hi[q] = (uint32_t)__builtin_amdgcn_readlane((int)e[q], last);
-        }
-        int r = next_row(lo, hi, -1);
-        uint32_t c0 = r < 3 ? pick3(lo, r) : 0u;
-        float4 cur = z4;
-        if (r < 3) cur = chunk_load(spos, c0, min((uint32_t)kWave, pick3(hi, r) - c0), lane);
-        while (r < 3) {  // wave-uniform
-            const uint32_t hr_end = pick3(hi, r);
-            const uint32_t m = min((uint32_t)kWave, hr_end - c0);
-            // A group representative ends the chunk; its members (which follow it) are skipped
-            // and it counts for all of them.
-            const uint32_t wb = __float_as_uint(cur.w);
-            const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
-            uint32_t mm = m, gm = 0;
-            if (reps) {
-                const int rl = __ffsll((unsigned long long)reps) - 1;
-                mm = (uint32_t)rl;
-                gm = (uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag;
-            }
-            int nr = r;
-            uint32_t nc0 = gm ? c0 + mm + gm : c0 + m;
-            if (nc0 >= hr_end) {
-                nr = next_row(lo, hi, r);
-                nc0 = nr < 3 ? pick3(lo, nr) : 0u;
-            }
-            float4 nq = z4;
-            if (nr < 3) nq = chunk_load(spos, nc0, min((uint32_t)kWave, pick3(hi, nr) - nc0), lane);
-            __builtin_amdgcn_wave_barrier();
-            buf[lane] = cur;
-            __builtin_amdgcn_wave_barrier();
-            if (mine) {
-                const uint32_t br = pick3(b, r), er = pick3(e, r);
-                acc = density_run(buf, c0, max(br, c0), min(er, c0 + mm), pi, h2, acc);
-                const uint32_t jr = c0 + mm;
-                if (gm && jr >= br && jr < er) {
-                    const float4 g4 = buf[mm];
-                    const float dx = pi.x - g4.x, dy = pi.y - g4.y, dz = pi.z - g4.z;
-                    const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
-                    acc = fmaf((float)gm * d, d * d, acc);
-                }
-            }
-            r = nr;
-            c0 = nc0;
-            cur = nq;
+        for (int k = 0; k < kWinLoads; k++) v[k] = spos[j[k]];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < kWinLoads; k++) buf[k * kWave + lane] = v[k];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const uint32_t jb = max(L.S[r], w0), je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin);
+            if (jb < je) acc = density_run(buf, w0, jb, je, pi, h2, acc);
         }
     }
-    if (live) dpart[(size_t)slab * stride + s] = acc;
+    if (in) dpart[(size_t)slab * stride + s] = acc;
 }
 
 // Heavy items: the 16 waves of a workgroup hold the same 64 particles of one (sub-tile, slab)
@@ -891,26 +934,25 @@ __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
 }
 
 // Acceleration partials: fpart[slab][c][s] = sum over the slab's neighbours j of the pressure
-// and viscosity pair terms (sph_fused.rs:604-623), not yet divided by rho_i.  Same wave-private
-// home-row segments as k_density_wave.
+// and viscosity pair terms (sph_fused.rs:604-623), not yet divided by rho_i.  Same windowed
+// stream as k_density_wave; light items hold no co-located group, so every candidate has weight
+// 1 and is staged as (x, y, z, p_j), (v_j / rho_j, 1 / rho_j).
 __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict__ spos,
                                                        const float4* __restrict__ svel,
-                                                       const float4* __restrict__ vrep,
                                                        const float* __restrict__ dpart,
                                                        uint32_t n, GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
                                                        FastForce K, float* __restrict__ fpart,
-                                                       float* __restrict__ wpart,
                                                        uint32_t stride, uint32_t items,
                                                        const uint8_t* __restrict__ flag) {
-    __shared__ float4 s_p[kTileP / kWave][kWave];  // x, y, z, p_j
-    __shared__ float4 s_v[kTileP / kWave][kWave];  // vx, vy, vz, 1/rho_j
+    __shared__ float4 s_p[kTileP / kWave][kWin];  // x, y, z, p_j
+    __shared__ float4 s_v[kTileP / kWave][kWin];  // vx, vy, vz, 1/rho_j
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
-    if (item >= items) return;
+    if (item >= items || flag[item]) return;  // whole wave; heavy items: k_force_heavy
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     const uint32_t s = sub * kSub + (uint32_t)lane;
-    const bool in = s < n && !flag[item];  // heavy items: k_force_heavy
+    const bool in = s < n;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const float4 pi = in ? spos[s] : z4;
     const float4 vi = in ? svel[s] : z4;
@@ -918,60 +960,41 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     const bool live = in && !(rho_i < 1e-6f);  // sph_fused.rs:550
     const float p_i = K.k * (rho_i - K.rho0);
     uint32_t b[3], e[3];
-    slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
-    const uint32_t hr = home_row(pi, g);
+    slab_ranges(pi, in, g, cstart, n, (int)slab - 1, b, e);
+    LightStream L;
+    light_stream(L, b, e, home_row(pi, g), in, lane);
     float4* bp = s_p[wave];
     float4* bv = s_v[wave];
     float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
-    uint64_t pending = __ballot(live);
-    while (pending) {
-        const int leader = __ffsll((unsigned long long)pending) - 1;
-        const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
-        const bool mine = live && hr == row;
-        const uint64_t seg = __ballot(mine);
-        pending &= ~seg;
-        const int last = 63 - __clzll((long long)seg);
-        uint32_t lo[3], hi[3];
+    for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
+        uint32_t j[kWinLoads];
+        window_indices(L, w0, lane, j);
+        float4 q[kWinLoads], w[kWinLoads];
+        float d0[kWinLoads], d1[kWinLoads], d2[kWinLoads];
 #pragma unroll
-        for (int q = 0; q < 3; q++) {
-            lo[q] = (uint32_t)__builtin_amdgcn_readlane((int)b[q], leader);
-            hi[q] = (uint32_t)__builtin_amdgcn_readlane((int)e[q], last);
+        for (int k = 0; k < kWinLoads; k++) {
+            q[k] = spos[j[k]];
+            w[k] = svel[j[k]];
+            d0[k] = dpart[j[k]];
+            d1[k] = dpart[stride + j[k]];
+            d2[k] = dpart[2u * stride + j[k]];
         }
-        int r = next_row(lo, hi, -1);
-        uint32_t c0 = r < 3 ? pick3(lo, r) : 0u;
-        ForceSlot cur = force_fetch(spos, svel, vrep, dpart, stride, c0 + lane,
-                                    r < 3 && (uint32_t)lane < min((uint32_t)kWave, pick3(hi, r) - c0));
-        while (r < 3) {  // wave-uniform
-            const uint32_t hr_end = pick3(hi, r);
-            const uint32_t m = min((uint32_t)kWave, hr_end - c0);
-            // a group representative (staged with its weight) ends the chunk; its members
-            // follow it and are skipped
-            const uint32_t wb = __float_as_uint(cur.q.w);
-            const uint64_t reps = __ballot((uint32_t)lane < m && (wb & kRepFlag));
-            uint32_t mm = m, skip = 0;
-            if (reps) {
-                const int rl = __ffsll((unsigned long long)reps) - 1;
-                mm = (uint32_t)rl + 1u;
-                skip = ((uint32_t)__builtin_amdgcn_readlane((int)wb, rl) & ~kRepFlag) - 1u;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < kWinLoads; k++) {
+            const float rj = K.mc * ((d0[k] + d1[k]) + d2[k]);
+            const float inv = rj < 1e-6f ? 0.0f : 1.0f / rj;
+            bp[k * kWave + lane] = make_float4(q[k].x, q[k].y, q[k].z, K.k * (rj - K.rho0));
+            bv[k * kWave + lane] = make_float4(w[k].x * inv, w[k].y * inv, w[k].z * inv, inv);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (live) {
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                const uint32_t jb = max(L.S[r], w0);
+                const uint32_t je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin);
+                if (jb < je) force_run(bp, bv, w0, jb, je, pi, vi, p_i, K, ax, ay, az, wv);
             }
-            int nr = r;
-            uint32_t nc0 = c0 + mm + skip;
-            if (nc0 >= hr_end) {
-                nr = next_row(lo, hi, r);
-                nc0 = nr < 3 ? pick3(lo, nr) : 0u;
-            }
-            const ForceSlot nxt = force_fetch(
-                spos, svel, vrep, dpart, stride, nc0 + lane,
-                nr < 3 && (uint32_t)lane < min((uint32_t)kWave, pick3(hi, nr) - nc0));
-            __builtin_amdgcn_wave_barrier();
-            force_store(bp, bv, lane, c0 + lane, cur, K);
-            __builtin_amdgcn_wave_barrier();
-            if (mine)
-                force_run(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + mm), pi, vi,
-                          p_i, K, ax, ay, az, wv);
-            r = nr;
-            c0 = nc0;
-            cur = nxt;
         }
     }
     if (in) {
@@ -979,7 +1002,6 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         o[s] = ax;
         o[stride + s] = ay;
         o[2u * (size_t)stride + s] = az;
-        if (__float_as_uint(pi.w) & kRepFlag) wpart[(size_t)slab * stride + s] = wv;
     }
 }
 
@@ -1214,22 +1236,35 @@ hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) 
     return hipGetLastError();
 }
 
+// Fork the side stream off the main one (heavy kernels go there), and join it back.
+static hipError_t fork_side(fh_ctx* c) {
+    hipError_t e = hipEventRecord(c->fork_ev, c->stream);
+    return e == hipSuccess ? hipStreamWaitEvent(c->side, c->fork_ev, 0) : e;
+}
+static hipError_t join_side(fh_ctx* c) {
+    hipError_t e = hipEventRecord(c->join_ev, c->side);
+    return e == hipSuccess ? hipStreamWaitEvent(c->stream, c->join_ev, 0) : e;
+}
+
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
     if (a.n == 0) return hipSuccess;
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
+    hipError_t e = fork_side(c);
+    if (e != hipSuccess) return e;
+    tbeg(c, KID_DHEAVY, c->side);
+    k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
+        c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
+        c->heavy_cap, c->ctl);
+    tend(c, KID_DHEAVY, c->side);
+    e = hipGetLastError();
     tbeg(c, KID_DENSITY);
     k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, a.n, a.g, cell_start, a.h * a.h,
                                                    c->dpart, c->max_n, items, c->heavy_flag);
     tend(c, KID_DENSITY);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    tbeg(c, KID_DHEAVY);
-    k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
-        c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
-        c->heavy_cap, c->ctl);
-    tend(c, KID_DHEAVY);
-    return hipGetLastError();
+    if (e == hipSuccess) e = hipGetLastError();
+    const hipError_t j = join_side(c);  // joined even after a failed launch
+    return e != hipSuccess ? e : j;
 }
 
 hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
@@ -1273,19 +1308,21 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     K.fv = a.mu * a.mass * lcoef;
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
-    tbeg(c, KID_FORCE);
-    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n, a.g,
-                                                 cell_start, K, c->fpart, c->wpart, c->max_n,
-                                                 items, c->heavy_flag);
-    tend(c, KID_FORCE);
-    hipError_t e = hipGetLastError();
+    hipError_t e = fork_side(c);
     if (e != hipSuccess) return e;
-    tbeg(c, KID_FHEAVY);
-    k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->stream>>>(
+    tbeg(c, KID_FHEAVY, c->side);
+    k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
         c->spos, c->svel, c->vrep, c->dpart, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
         c->wpart, c->max_n, c->heavy, c->heavy_cap, c->ctl);
-    tend(c, KID_FHEAVY);
-    return hipGetLastError();
+    tend(c, KID_FHEAVY, c->side);
+    e = hipGetLastError();
+    tbeg(c, KID_FORCE);
+    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->dpart, a.n, a.g, cell_start,
+                                                 K, c->fpart, c->max_n, items, c->heavy_flag);
+    tend(c, KID_FORCE);
+    if (e == hipSuccess) e = hipGetLastError();
+    const hipError_t j = join_side(c);
+    return e != hipSuccess ? e : j;
 }
 
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, bool density_only,
