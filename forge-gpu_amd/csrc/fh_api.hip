@@ -355,7 +355,8 @@ int fh_query_neighbors(fh_ctx* c, const float* x, const float* y, const float* z
 }
 
 int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const float* py,
-                   const float* pz, uint32_t n, float* density) {
+                   const float* pz, uint32_t n, float* density, uint32_t* cell_start,
+                   uint32_t* sorted_indices) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (n && (!px || !py || !pz || !density)) return fail(FH_EINVAL, "fh_sph_density: null pointer");
@@ -364,6 +365,8 @@ int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const f
     uint32_t cells;
     if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_density"))) return rc;
     FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, nullptr, nullptr, nullptr, n, false));
+    // the grid as rebuilt (ascending id within a cell), before the fast passes regroup cells
+    FH_CHECK_HIP(launch_copy_grid(c, cells, n, cell_start, sorted_indices));
     if (n == 0) return FH_OK;
     SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
               prm->rest_density, prm->viscosity_coefficient, 0.0f, n};
@@ -408,6 +411,42 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
         FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density, accel));
     }
     return FH_OK;
+}
+
+static int unfused(fh_ctx* c, bool viscosity, const fh_sph_params* prm, const float* px,
+                   const float* py, const float* pz, float* vx, float* vy, float* vz,
+                   const float* density, const uint32_t* cell_start,
+                   const uint32_t* sorted_indices, uint32_t n, float dt) {
+    const char* what = viscosity ? "fh_sph_viscosity" : "fh_sph_pressure";
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!cell_start || (n && (!px || !py || !pz || !vx || !vy || !vz || !density || !sorted_indices)))
+        return fail(FH_EINVAL, "%s: null pointer", what);
+    if ((rc = check_n(c, n, what))) return rc;
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_sph(c, prm, &g, &cells, what))) return rc;
+    SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
+              prm->rest_density, prm->viscosity_coefficient, dt, n};
+    FH_CHECK_HIP(launch_unfused(c, viscosity, a, px, py, pz, vx, vy, vz, density, cell_start,
+                                sorted_indices));
+    return FH_OK;
+}
+
+int fh_sph_pressure(fh_ctx* c, const fh_sph_params* prm, const float* px, const float* py,
+                    const float* pz, float* vx, float* vy, float* vz, const float* density,
+                    const uint32_t* cell_start, const uint32_t* sorted_indices, uint32_t n,
+                    float dt) {
+    return unfused(c, false, prm, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices,
+                   n, dt);
+}
+
+int fh_sph_viscosity(fh_ctx* c, const fh_sph_params* prm, const float* px, const float* py,
+                     const float* pz, float* vx, float* vy, float* vz, const float* density,
+                     const uint32_t* cell_start, const uint32_t* sorted_indices, uint32_t n,
+                     float dt) {
+    return unfused(c, true, prm, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices,
+                   n, dt);
 }
 
 int fh_set_option(fh_ctx* c, int option, int value) {

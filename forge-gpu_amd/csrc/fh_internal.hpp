@@ -296,6 +296,15 @@ hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_star
 hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
                         const uint32_t* cell_start, float* px, float* py, float* pz, float* vx,
                         float* vy, float* vz, float* accel);
+// Unfused pressure (viscosity = false) or viscosity pass over a caller grid, updating v in place
+// (the viscosity pass first copies v into c->svel: every neighbour reads the state before it).
+hipError_t launch_unfused(fh_ctx* c, bool viscosity, const SphArgs& a, const float* px,
+                          const float* py, const float* pz, float* vx, float* vy, float* vz,
+                          const float* density, const uint32_t* cell_start,
+                          const uint32_t* sorted_indices);
+// Copy c->cell_start[0..cells] and c->sidx[0..n) to caller arrays (either may be null).
+hipError_t launch_copy_grid(fh_ctx* c, uint32_t cells, uint32_t n, uint32_t* cell_start,
+                            uint32_t* sorted_indices);
 hipError_t launch_gravity(fh_ctx* c, float* vx, float* vy, float* vz, uint32_t n, float gx,
                           float gy, float gz, float dt);
 hipError_t launch_integrate(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,

@@ -284,6 +284,188 @@ hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
 }
 
 // ---------------------------------------------------------------------------------------------
+// Unfused modules (sph_pressure.rs:28-112, sph_viscosity.rs:27-106): one thread per particle i
+// in original order, neighbours through the caller's grid (cell_start[C+1], sorted_indices[n]
+// left in the FieldSet by the density module), visited cell by cell in the reference's order
+// (dz, dy, dx, then the cell's range), j == i skipped.  The reference expressions are kept term
+// by term (no contraction, IEEE division and square root), so each velocity equals the CPU
+// restatement's bit for bit.  Ranges and ids are clamped to n so a malformed grid cannot read
+// out of bounds.
+struct UnfusedConsts {
+    float h, h2, mass, k, rho0, mu, coef, dt;
+    uint32_t n;
+};
+
+template <class Pair>
+__device__ __forceinline__ void unfused_walk(const float* __restrict__ px,
+                                             const float* __restrict__ py,
+                                             const float* __restrict__ pz,
+                                             const float* __restrict__ density,
+                                             const uint32_t* __restrict__ cstart,
+                                             const uint32_t* __restrict__ sidx, GridDesc g,
+                                             const UnfusedConsts& K, uint32_t i, float xi,
+                                             float yi, float zi, Pair&& pair) {
+    const int cx = (int)cell_coord(xi, 0.0f, g.cs, g.nx);
+    const int cy = (int)cell_coord(yi, 0.0f, g.cs, g.ny);
+    const int cz = (int)cell_coord(zi, 0.0f, g.cs, g.nz);
+    for (int dz = -1; dz <= 1; dz++) {
+        const int nzz = cz + dz;
+        if (nzz < 0 || nzz >= (int)g.nz) continue;
+        for (int dy = -1; dy <= 1; dy++) {
+            const int nyy = cy + dy;
+            if (nyy < 0 || nyy >= (int)g.ny) continue;
+            for (int dx = -1; dx <= 1; dx++) {
+                const int nxx = cx + dx;
+                if (nxx < 0 || nxx >= (int)g.nx) continue;
+                const uint32_t cell = (uint32_t)nxx + (uint32_t)nyy * g.nx +
+                                      (uint32_t)nzz * g.nx * g.ny;
+                const uint32_t end = min(cstart[cell + 1u], K.n);
+                for (uint32_t s = cstart[cell]; s < end; s++) {
+                    const uint32_t j = sidx[s];
+                    if (j == i || j >= K.n) continue;
+                    float djx = xi - px[j];
+                    float djy = yi - py[j];
+                    float djz = zi - pz[j];
+                    float r2 = djx * djx + djy * djy + djz * djz;
+                    if (r2 < K.h2 && r2 > 1e-12f) {
+                        float r = sqrtf(r2);
+                        float rho_j = density[j];
+                        if (rho_j < 1e-6f) continue;
+                        pair(j, djx, djy, djz, r, rho_j);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// sph_pressure.rs:34-111; K.coef = -45 / (pi h^6).  Pressure terms read positions and
+// densities only, so v_i is updated in place.
+__global__ __launch_bounds__(256) void k_pressure(const float* __restrict__ px,
+                                                  const float* __restrict__ py,
+                                                  const float* __restrict__ pz,
+                                                  float* __restrict__ vx, float* __restrict__ vy,
+                                                  float* __restrict__ vz,
+                                                  const float* __restrict__ density,
+                                                  const uint32_t* __restrict__ cstart,
+                                                  const uint32_t* __restrict__ sidx, GridDesc g,
+                                                  UnfusedConsts K) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= K.n) return;
+    const float rho_i = density[i];
+    if (rho_i < 1e-6f) return;
+    const float p_i = K.k * (rho_i - K.rho0);
+    float ax = 0.0f, ay = 0.0f, az = 0.0f;
+    unfused_walk(px, py, pz, density, cstart, sidx, g, K, i, px[i], py[i], pz[i],
+                 [&](uint32_t, float djx, float djy, float djz, float r, float rho_j) {
+                     float diff = K.h - r;
+                     float p_j = K.k * (rho_j - K.rho0);
+                     float grad_scale = K.coef * diff * diff / r;
+                     float f_scale = -K.mass * (p_i + p_j) / (2.0f * rho_j) * grad_scale;
+                     ax += f_scale * djx;
+                     ay += f_scale * djy;
+                     az += f_scale * djz;
+                 });
+    vx[i] += (ax / rho_i) * K.dt;
+    vy[i] += (ay / rho_i) * K.dt;
+    vz[i] += (az / rho_i) * K.dt;
+}
+
+// Velocities before the viscosity pass (particle order), read for every neighbour.
+__global__ __launch_bounds__(256) void k_copy_vel(const float* __restrict__ vx,
+                                                  const float* __restrict__ vy,
+                                                  const float* __restrict__ vz, uint32_t n,
+                                                  float4* __restrict__ v0) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) v0[i] = make_float4(vx[i], vy[i], vz[i], 0.0f);
+}
+
+// sph_viscosity.rs:34-105; K.coef = 45 / (pi h^6).
+__global__ __launch_bounds__(256) void k_viscosity(const float* __restrict__ px,
+                                                   const float* __restrict__ py,
+                                                   const float* __restrict__ pz,
+                                                   const float4* __restrict__ v0,
+                                                   float* __restrict__ vx, float* __restrict__ vy,
+                                                   float* __restrict__ vz,
+                                                   const float* __restrict__ density,
+                                                   const uint32_t* __restrict__ cstart,
+                                                   const uint32_t* __restrict__ sidx, GridDesc g,
+                                                   UnfusedConsts K) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= K.n) return;
+    const float rho_i = density[i];
+    if (rho_i < 1e-6f) return;
+    const float4 vi = v0[i];
+    float ax = 0.0f, ay = 0.0f, az = 0.0f;
+    unfused_walk(px, py, pz, density, cstart, sidx, g, K, i, px[i], py[i], pz[i],
+                 [&](uint32_t j, float, float, float, float r, float rho_j) {
+                     float lap = K.coef * (K.h - r);
+                     float scale = K.mu * K.mass / rho_j * lap;
+                     const float4 vj = v0[j];
+                     ax += scale * (vj.x - vi.x);
+                     ay += scale * (vj.y - vi.y);
+                     az += scale * (vj.z - vi.z);
+                 });
+    vx[i] = vi.x + (ax / rho_i) * K.dt;
+    vy[i] = vi.y + (ay / rho_i) * K.dt;
+    vz[i] = vi.z + (az / rho_i) * K.dt;
+}
+
+hipError_t launch_unfused(fh_ctx* c, bool viscosity, const SphArgs& a, const float* px,
+                          const float* py, const float* pz, float* vx, float* vy, float* vz,
+                          const float* density, const uint32_t* cell_start,
+                          const uint32_t* sorted_indices) {
+    if (a.n == 0) return hipSuccess;
+    UnfusedConsts K;
+    K.h = a.h;
+    K.h2 = a.h * a.h;
+    K.mass = a.mass;
+    K.k = a.k;
+    K.rho0 = a.rho0;
+    K.mu = a.mu;
+    const float h6 = K.h2 * K.h2 * K.h2;  // sph_pressure.rs:47-50, sph_viscosity.rs:47-49
+    K.coef = viscosity ? 45.0f / (3.14159265f * h6) : -45.0f / (3.14159265f * h6);
+    K.dt = a.dt;
+    K.n = a.n;
+    const uint32_t blocks = ceil_div(a.n, 256u);
+    if (!viscosity) {
+        k_pressure<<<blocks, 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, density, cell_start,
+                                                  sorted_indices, a.g, K);
+        return hipGetLastError();
+    }
+    k_copy_vel<<<blocks, 256, 0, c->stream>>>(vx, vy, vz, a.n, c->svel);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_viscosity<<<blocks, 256, 0, c->stream>>>(px, py, pz, c->svel, vx, vy, vz, density,
+                                               cell_start, sorted_indices, a.g, K);
+    return hipGetLastError();
+}
+
+// Copy of the grid of the last rebuild (CSR cell_start[C+1], sorted ids) into caller arrays:
+// the FieldSet's u32 fields that the unfused modules read (sph_density.rs:44-74 keeps them).
+__global__ __launch_bounds__(256) void k_copy_grid(const uint32_t* __restrict__ cs_in,
+                                                   uint32_t cells1,
+                                                   const uint32_t* __restrict__ si_in, uint32_t n,
+                                                   uint32_t* __restrict__ cs_out,
+                                                   uint32_t* __restrict__ si_out) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < cells1; t += stride)
+        if (cs_out) cs_out[t] = cs_in[t];
+    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += stride)
+        if (si_out) si_out[t] = si_in[t];
+}
+
+hipError_t launch_copy_grid(fh_ctx* c, uint32_t cells, uint32_t n, uint32_t* cell_start,
+                            uint32_t* sorted_indices) {
+    if (!cell_start && !sorted_indices) return hipSuccess;
+    uint32_t blocks = ceil_div(max(cells + 1u, n), 256u);
+    if (blocks > 2048u) blocks = 2048u;
+    k_copy_grid<<<blocks, 256, 0, c->stream>>>(c->cell_start, cells + 1u, c->sidx, n, cell_start,
+                                               sorted_indices);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
 // gravity.rs:31-34
 __global__ void k_gravity(float* __restrict__ vx, float* __restrict__ vy, float* __restrict__ vz,
                           float gx, float gy, float gz, float dt, uint32_t n) {

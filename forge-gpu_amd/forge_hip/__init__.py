@@ -11,14 +11,16 @@ from ._lib import (FH_EINVAL, FH_ENODEV, FH_EPI_BOX, FH_EPI_GRAVITY, FH_EPI_INTE
                    load)
 from .hashgrid import HashGrid, RadixSorter, find_cell_boundaries
 from .modules import (BoxColliderModule, FieldSet, GravityModule, IntegrateModule, Pipeline,
-                      SimModule, SphDensityModule, SphFusedModule, build_pipeline)
+                      SimModule, SphDensityModule, SphFusedModule, SphPressureModule,
+                      SphViscosityModule, build_pipeline)
 from .runtime import Context, default_context, from_u32, to_u32, u32_empty
 
 __all__ = [
     "FH_OK", "FH_EINVAL", "FH_ERANGE", "FH_ESTATE", "FH_ENODEV", "FH_EPI_GRAVITY",
     "FH_EPI_INTEGRATE", "FH_EPI_BOX", "FH_OPT_SPH_EXACT", "FH_OPT_HEAVY_WORK", "ForgeError", "LibraryNotBuilt", "load", "HashGrid",
     "RadixSorter", "find_cell_boundaries", "FieldSet", "SimModule", "Pipeline",
-    "SphDensityModule", "SphFusedModule", "GravityModule", "IntegrateModule",
+    "SphDensityModule", "SphFusedModule", "SphPressureModule", "SphViscosityModule",
+    "GravityModule", "IntegrateModule",
     "BoxColliderModule", "build_pipeline", "Context", "default_context", "to_u32", "from_u32",
     "u32_empty",
 ]

@@ -90,7 +90,11 @@ SIGNATURES = {
     "fh_neighbor_query": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P, _F32, _P, _P]),
     "fh_query_neighbors": (_I, [_P, _P, _P, _P, _U32, _F32, _F3, _U3, _P, _P,
                                 _P, _P, _P, _U32, _U32, _F32, _P, _P, _P]),
-    "fh_sph_density": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _U32, _P]),
+    "fh_sph_density": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _U32, _P, _P, _P]),
+    "fh_sph_pressure": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _P, _P, _P, _P, _P,
+                             _P, _U32, _F32]),
+    "fh_sph_viscosity": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _P, _P, _P, _P, _P,
+                              _P, _U32, _F32]),
     "fh_sph_fused": (_I, [_P, ctypes.POINTER(FhSphParams), ctypes.POINTER(FhEpilogue),
                           _P, _P, _P, _P, _P, _P, _P, _P, _U32, _F32]),
     "fh_set_option": (_I, [_P, _I, _I]),

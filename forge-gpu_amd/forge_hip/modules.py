@@ -7,13 +7,16 @@ the builtin modules on the SPH path, dispatching to the C ABI.
                            replay of substeps as run_manifest does (manifest_runner.rs:53-77)
   SphFusedModule           builtins/sph_fused.rs:14-22,410-733
   SphDensityModule         builtins/sph_density.rs:16-21,385-501
+  SphPressureModule        builtins/sph_pressure.rs:9-161 (unfused)
+  SphViscosityModule       builtins/sph_viscosity.rs:9-155 (unfused)
   GravityModule            builtins/gravity.rs:5-63
   IntegrateModule          builtins/integrate.rs:5-70
   BoxColliderModule        builtins/box_collider.rs:6-85
   build_pipeline           manifest_runner.rs:322-544 (SPH fusion, parameter defaults, order)
 
 Fields stay in original particle order, as the reference keeps them.  The SPH modules create
-`density` on first use (sph_fused.rs:420-422).  When a pipeline holds [sph_fused, gravity,
+`density` on first use (sph_fused.rs:420-422); SphDensityModule also leaves its grid in the u32
+fields `cell_start` and `sorted_indices`, which the unfused pressure / viscosity modules read.  When a pipeline holds [sph_fused, gravity,
 integrate, box_collider] in that order, Pipeline fuses the three epilogue modules into the SPH
 force pass (one kernel instead of three); the result equals running them separately.
 """
@@ -110,6 +113,15 @@ class SphDensityModule(SimModule):
     def prepare(self, fields: FieldSet) -> None:
         if "density" not in fields.f32_fields:
             fields.add_f32_zeros("density", fields.particle_count)
+        dev = f"cuda:{fields.device}"
+        cells = _cells(self.grid_dims) + 1
+        cs = fields.u32_fields.get("cell_start")
+        if cs is None or cs.numel() != cells:
+            fields.u32_fields["cell_start"] = torch.zeros(cells, dtype=torch.int32, device=dev)
+        si = fields.u32_fields.get("sorted_indices")
+        if si is None or si.numel() != fields.particle_count:
+            fields.u32_fields["sorted_indices"] = torch.zeros(fields.particle_count,
+                                                              dtype=torch.int32, device=dev)
 
     def execute(self, fields: FieldSet, dt: float) -> None:
         n = fields.particle_count
@@ -117,7 +129,69 @@ class SphDensityModule(SimModule):
         ctx = fields.context(_cells(self.grid_dims))
         px, py, pz = fields.pos()
         check(_lib.load().fh_sph_density(ctx.handle, ctypes.byref(_sph_params(self)), ptr(px),
-                                         ptr(py), ptr(pz), n, ptr(fields.f32_fields["density"])))
+                                         ptr(py), ptr(pz), n, ptr(fields.f32_fields["density"]),
+                                         ptr(fields.u32_fields["cell_start"]),
+                                         ptr(fields.u32_fields["sorted_indices"])))
+
+
+class _UnfusedModule(SimModule):
+    """Shared body of the unfused pressure / viscosity modules: they read the grid and density
+    that SphDensityModule left in the field set (sph_pressure.rs:129-137 take them with
+    `.unwrap()`, so a missing field is an error)."""
+
+    _entry = ""
+
+    def execute(self, fields: FieldSet, dt: float) -> None:
+        n = fields.particle_count
+        for nm in ("cell_start", "sorted_indices"):
+            if nm not in fields.u32_fields:
+                raise _lib.ForgeError(_lib.FH_EINVAL, f"missing field {nm} (run sph_density first)")
+        cs = fields.u32_fields["cell_start"]
+        if cs.numel() != _cells(self.grid_dims) + 1:
+            raise _lib.ForgeError(_lib.FH_EINVAL, f"{self.name()}: cell_start has {cs.numel()} "
+                                  f"entries, the grid needs {_cells(self.grid_dims) + 1}")
+        ctx = fields.context(_cells(self.grid_dims))
+        px, py, pz = fields.pos()
+        vx, vy, vz = fields.vel()
+        fn = getattr(_lib.load(), self._entry)
+        check(fn(ctx.handle, ctypes.byref(_sph_params(self)), ptr(px), ptr(py), ptr(pz), ptr(vx),
+                 ptr(vy), ptr(vz), ptr(fields._f("density")), ptr(cs),
+                 ptr(fields.u32_fields["sorted_indices"]), n, float(dt)))
+
+
+class SphPressureModule(_UnfusedModule):
+    """sph_pressure.rs:9-16: v_i += (a_p / rho_i) dt with p = k (rho - rho0)."""
+
+    _entry = "fh_sph_pressure"
+
+    def __init__(self, gas_constant, rest_density, smoothing_radius, cell_size, grid_dims,
+                 particle_mass):
+        self.gas_constant = float(gas_constant)
+        self.rest_density = float(rest_density)
+        self.smoothing_radius = float(smoothing_radius)
+        self.cell_size = float(cell_size)
+        self.grid_dims = [int(d) for d in grid_dims]
+        self.particle_mass = float(particle_mass)
+
+    def name(self) -> str:
+        return "sph_pressure"
+
+
+class SphViscosityModule(_UnfusedModule):
+    """sph_viscosity.rs:9-15: v_i += (a_v / rho_i) dt, neighbours' velocities before the pass."""
+
+    _entry = "fh_sph_viscosity"
+
+    def __init__(self, coefficient, smoothing_radius, cell_size, grid_dims, particle_mass):
+        self.coefficient = float(coefficient)
+        self.viscosity_coefficient = self.coefficient
+        self.smoothing_radius = float(smoothing_radius)
+        self.cell_size = float(cell_size)
+        self.grid_dims = [int(d) for d in grid_dims]
+        self.particle_mass = float(particle_mass)
+
+    def name(self) -> str:
+        return "sph_viscosity"
 
 
 class SphFusedModule(SimModule):
@@ -300,6 +374,12 @@ class Pipeline:
         self._captured_ctx.graph_launch(count)
 
 
+def _grid_dims(spatial: dict | None) -> list[int]:
+    """[spatial].grid_dims with each missing entry 32, or 32^3 (manifest_runner.rs:359-365)."""
+    dims = list(spatial.get("grid_dims", [])) if spatial else []
+    return [int(d) for d in (dims + [32, 32, 32][len(dims):])[:3]]
+
+
 def build_pipeline(forces: list[dict], constraints: list[dict], n: int,
                    spatial: dict | None = None) -> Pipeline:
     """Pipeline construction of manifest_runner.rs:322-544 for the SPH path.
@@ -329,11 +409,22 @@ def build_pipeline(forces: list[dict], constraints: list[dict], n: int,
             pipe.add(GravityModule(v[0], v[1], v[2]))
         elif f["type"] in ("sph_density", "sph_pressure", "sph_viscosity") and fuse:
             continue
-        elif f["type"] == "sph_density":
+        elif f["type"] == "sph_density":  # manifest_runner.rs:419-437
             h = float(f["smoothing_radius"])
             cs = float(spatial["cell_size"]) if spatial else h * 2.0
-            dims = list(spatial.get("grid_dims", [32, 32, 32])) if spatial else [32, 32, 32]
-            pipe.add(SphDensityModule(h, cs, dims, particle_mass(1000.0, n)))
+            pipe.add(SphDensityModule(h, cs, _grid_dims(spatial), particle_mass(1000.0, n)))
+        elif f["type"] in ("sph_pressure", "sph_viscosity"):  # :438-488
+            # cell size 0.05 and h 0.025 unless the manifest sets them (not 2h as for density)
+            cs = float(spatial["cell_size"]) if spatial else 0.05
+            h = next((float(g["smoothing_radius"]) for g in forces if g["type"] == "sph_density"),
+                     0.025)
+            if f["type"] == "sph_pressure":
+                k, rho0 = float(f["gas_constant"]), float(f["rest_density"])
+                pipe.add(SphPressureModule(k, rho0, h, cs, _grid_dims(spatial),
+                                           particle_mass(rho0, n)))
+            else:
+                pipe.add(SphViscosityModule(float(f["coefficient"]), h, cs, _grid_dims(spatial),
+                                            particle_mass(1000.0, n)))
         else:
             raise _lib.ForgeError(_lib.FH_EINVAL, f"force {f['type']} is outside the SPH path")
     pipe.add(IntegrateModule())

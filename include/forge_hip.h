@@ -27,6 +27,8 @@
  *  - forge-runtime/src/radix_sort.rs:229-317   find_cell_boundaries
  *  - forge-manifest/src/modules/builtins/sph_density.rs:16-501   SphDensityModule::execute
  *  - forge-manifest/src/modules/builtins/sph_fused.rs:14-733     SphFusedModule::execute
+ *  - forge-manifest/src/modules/builtins/sph_pressure.rs:9-161   SphPressureModule::execute
+ *  - forge-manifest/src/modules/builtins/sph_viscosity.rs:9-155  SphViscosityModule::execute
  *  - forge-manifest/src/modules/builtins/gravity.rs:23-63        GravityModule::execute
  *  - forge-manifest/src/modules/builtins/integrate.rs:9-70       IntegrateModule::execute
  *  - forge-manifest/src/modules/builtins/box_collider.rs:18-85   BoxColliderModule::execute
@@ -44,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 1
+#define FH_ABI_VERSION 2
 
 /* ---- status codes (negative: argument errors detected on the host) ------------------------- */
 #define FH_OK 0
@@ -162,9 +164,35 @@ int fh_query_neighbors(fh_ctx* ctx, const float* x, const float* y, const float*
 
 /* SphDensityModule::execute (sph_density.rs:388-501): rebuild the grid from pos and write
  * density[i] = sum over j in the 27-cell neighbourhood with r^2 < h^2 (self included) of
- * m * 315/(64*pi*h^9) * (h^2 - r^2)^3, in original particle order. */
+ * m * 315/(64*pi*h^9) * (h^2 - r^2)^3, in original particle order.  The reference module
+ * leaves the rebuilt grid in the FieldSet's u32 fields (sph_density.rs:44-74), where the unfused
+ * pressure / viscosity modules read it: when non-NULL, cell_start (C+1 words, CSR) and
+ * sorted_indices (n words, ascending id within a cell) receive it here. */
 int fh_sph_density(fh_ctx* ctx, const fh_sph_params* prm, const float* px, const float* py,
-                   const float* pz, uint32_t n, float* density);
+                   const float* pz, uint32_t n, float* density, uint32_t* cell_start,
+                   uint32_t* sorted_indices);
+
+/* SphPressureModule::execute (sph_pressure.rs:23-161): for each particle i with
+ * rho_i >= 1e-6, a_p = sum over j != i of the 27-cell neighbourhood of the grid
+ * (cell_start[C+1], sorted_indices[n] as written by fh_sph_density or fh_hashgrid_build with
+ * origin 0) with r^2 < h^2, r^2 > 1e-12 and rho_j >= 1e-6 of
+ * -m (p_i + p_j) / (2 rho_j) * (-45/(pi h^6)) (h - r)^2 / r * (x_i - x_j), p = k (rho - rho0);
+ * then v_i += (a_p / rho_i) * dt in place.  Uses smoothing_radius, cell_size, grid_dims,
+ * particle_mass, gas_constant and rest_density of prm. */
+int fh_sph_pressure(fh_ctx* ctx, const fh_sph_params* prm, const float* px, const float* py,
+                    const float* pz, float* vx, float* vy, float* vz, const float* density,
+                    const uint32_t* cell_start, const uint32_t* sorted_indices, uint32_t n,
+                    float dt);
+
+/* SphViscosityModule::execute (sph_viscosity.rs:22-155): same neighbour set as
+ * fh_sph_pressure; a_v = sum of mu m / rho_j * 45/(pi h^6) (h - r) * (v_j - v_i), every v_j
+ * read from the velocities before this call (the reference kernel updates v in place while
+ * other threads read it); then v_i += (a_v / rho_i) * dt.  Uses smoothing_radius, cell_size,
+ * grid_dims, particle_mass and viscosity_coefficient of prm. */
+int fh_sph_viscosity(fh_ctx* ctx, const fh_sph_params* prm, const float* px, const float* py,
+                     const float* pz, float* vx, float* vy, float* vz, const float* density,
+                     const uint32_t* cell_start, const uint32_t* sorted_indices, uint32_t n,
+                     float dt);
 
 /* SphFusedModule::execute (sph_fused.rs:413-732): rebuild, density, then the fused pressure +
  * viscosity pass: v_i += ((a_p + a_v) / rho_i) * dt, all neighbour velocities read from the

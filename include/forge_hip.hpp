@@ -12,9 +12,10 @@
 //   forge::find_cell_boundaries  forge-runtime/src/radix_sort.rs:229-317
 //   forge::FieldSet, SimModule, Pipeline
 //                                forge-manifest/src/modules/mod.rs:12-117
-//   forge::SphFusedModule, SphDensityModule, GravityModule, IntegrateModule, BoxColliderModule
+//   forge::SphFusedModule, SphDensityModule, SphPressureModule, SphViscosityModule,
+//   GravityModule, IntegrateModule, BoxColliderModule
 //                                forge-manifest/src/modules/builtins/{sph_fused,sph_density,
-//                                gravity,integrate,box_collider}.rs
+//                                sph_pressure,sph_viscosity,gravity,integrate,box_collider}.rs
 // Exceptions stay on this side of the ABI: every C call returns a status that is turned into a
 // forge::Error here.
 #pragma once
@@ -241,9 +242,15 @@ class FieldSet {
         if (it == f32_fields.end()) throw Error(FH_EINVAL, "missing field " + name);
         return it->second;
     }
+    Array<uint32_t>& u(const std::string& name) {
+        auto it = u32_fields.find(name);
+        if (it == u32_fields.end()) throw Error(FH_EINVAL, "missing field " + name);
+        return it->second;
+    }
     Context& ctx;
     size_t particle_count;
     std::map<std::string, Array<float>> f32_fields;
+    std::map<std::string, Array<uint32_t>> u32_fields;
 };
 
 class SimModule {
@@ -288,8 +295,17 @@ struct SphDensityModule : SimModule {
     SphDensityModule(float h, float cs, uint32_t nx, uint32_t ny, uint32_t nz, float m)
         : smoothing_radius(h), cell_size(cs), grid_dims{nx, ny, nz}, particle_mass(m) {}
     const char* name() const override { return "sph_density"; }
+    // Also leaves its grid in the u32 fields cell_start / sorted_indices, which the unfused
+    // pressure and viscosity modules read (sph_density.rs:44-74).
     void prepare(FieldSet& fs) override {
         if (!fs.f32_fields.count("density")) fs.add_f32_zeros("density", fs.particle_count);
+        const size_t cells = (size_t)grid_dims[0] * grid_dims[1] * grid_dims[2] + 1;
+        auto cs = fs.u32_fields.find("cell_start");
+        if (cs == fs.u32_fields.end() || cs->second.len() != cells)
+            fs.u32_fields["cell_start"] = Array<uint32_t>::zeros(cells);
+        auto si = fs.u32_fields.find("sorted_indices");
+        if (si == fs.u32_fields.end() || si->second.len() != fs.particle_count)
+            fs.u32_fields["sorted_indices"] = Array<uint32_t>::zeros(fs.particle_count);
     }
     void execute(FieldSet& fs, float) override {
         prepare(fs);
@@ -297,7 +313,50 @@ struct SphDensityModule : SimModule {
                         particle_mass, 0.0f, 0.0f, 0.0f};
         check(fh_sph_density(fs.ctx.get(), &p, fs.f("pos_x").data(), fs.f("pos_y").data(),
                              fs.f("pos_z").data(), (uint32_t)fs.particle_count,
-                             fs.f("density").data()));
+                             fs.f("density").data(), fs.u("cell_start").data(),
+                             fs.u("sorted_indices").data()));
+    }
+};
+
+// Unfused SphPressureModule (sph_pressure.rs:9-16) and SphViscosityModule
+// (sph_viscosity.rs:9-15): read the density and grid fields SphDensityModule left behind.
+struct SphPressureModule : SimModule {
+    float gas_constant, rest_density, smoothing_radius, cell_size;
+    uint32_t grid_dims[3];
+    float particle_mass;
+    SphPressureModule(float k, float rho0, float h, float cs, uint32_t nx, uint32_t ny,
+                      uint32_t nz, float m)
+        : gas_constant(k), rest_density(rho0), smoothing_radius(h), cell_size(cs),
+          grid_dims{nx, ny, nz}, particle_mass(m) {}
+    const char* name() const override { return "sph_pressure"; }
+    void execute(FieldSet& fs, float dt) override {
+        fh_sph_params p{smoothing_radius, cell_size, {grid_dims[0], grid_dims[1], grid_dims[2]},
+                        particle_mass, gas_constant, rest_density, 0.0f};
+        check(fh_sph_pressure(fs.ctx.get(), &p, fs.f("pos_x").data(), fs.f("pos_y").data(),
+                              fs.f("pos_z").data(), fs.f("vel_x").data(), fs.f("vel_y").data(),
+                              fs.f("vel_z").data(), fs.f("density").data(),
+                              fs.u("cell_start").data(), fs.u("sorted_indices").data(),
+                              (uint32_t)fs.particle_count, dt));
+    }
+};
+
+struct SphViscosityModule : SimModule {
+    float coefficient, smoothing_radius, cell_size;
+    uint32_t grid_dims[3];
+    float particle_mass;
+    SphViscosityModule(float mu, float h, float cs, uint32_t nx, uint32_t ny, uint32_t nz,
+                       float m)
+        : coefficient(mu), smoothing_radius(h), cell_size(cs), grid_dims{nx, ny, nz},
+          particle_mass(m) {}
+    const char* name() const override { return "sph_viscosity"; }
+    void execute(FieldSet& fs, float dt) override {
+        fh_sph_params p{smoothing_radius, cell_size, {grid_dims[0], grid_dims[1], grid_dims[2]},
+                        particle_mass, 0.0f, 0.0f, coefficient};
+        check(fh_sph_viscosity(fs.ctx.get(), &p, fs.f("pos_x").data(), fs.f("pos_y").data(),
+                               fs.f("pos_z").data(), fs.f("vel_x").data(), fs.f("vel_y").data(),
+                               fs.f("vel_z").data(), fs.f("density").data(),
+                               fs.u("cell_start").data(), fs.u("sorted_indices").data(),
+                               (uint32_t)fs.particle_count, dt));
     }
 };
 

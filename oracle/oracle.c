@@ -427,6 +427,160 @@ void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
     }
 }
 
+/* Shared walk of the unfused modules: calls the pair function for every j != i of the
+ * 27-cell neighbourhood with r^2 < h^2 && r^2 > 1e-12 and rho_j >= 1e-6, in the reference's
+ * order (dz, dy, dx, then the cell's range of sorted_indices), sph_pressure.rs:61-99 and
+ * sph_viscosity.rs:58-97 (identical loops). */
+typedef void (*or_pair_fn)(void* st, uint32_t j, float djx, float djy, float djz, float r,
+                           float rho_j);
+
+static void unfused_walk(const or_sph_params* p, const float* px, const float* py,
+                         const float* pz, const float* density, const uint32_t* cell_start,
+                         const uint32_t* sorted_indices, uint32_t i, or_pair_fn fn, void* st) {
+    const float h = p->h, cs = p->cell_size;
+    const int32_t gnx = (int32_t)p->dims[0], gny = (int32_t)p->dims[1], gnz = (int32_t)p->dims[2];
+    float h2 = h * h;
+    float xi = px[i], yi = py[i], zi = pz[i];
+    int32_t cx = sph_cell_coord(xi, cs, p->dims[0]);
+    int32_t cy = sph_cell_coord(yi, cs, p->dims[1]);
+    int32_t cz = sph_cell_coord(zi, cs, p->dims[2]);
+    for (int dz = -1; dz <= 1; dz++) {
+        int32_t nzz = cz + dz;
+        if (nzz < 0 || nzz >= gnz) continue;
+        for (int dy = -1; dy <= 1; dy++) {
+            int32_t nyy = cy + dy;
+            if (nyy < 0 || nyy >= gny) continue;
+            for (int dx = -1; dx <= 1; dx++) {
+                int32_t nxx = cx + dx;
+                if (nxx < 0 || nxx >= gnx) continue;
+                uint32_t cell = (uint32_t)nxx + (uint32_t)nyy * (uint32_t)gnx +
+                                (uint32_t)nzz * (uint32_t)gnx * (uint32_t)gny;
+                uint32_t start = cell_start[cell];
+                uint32_t end = cell_start[cell + 1];
+                for (uint32_t s = start; s < end; s++) {
+                    uint32_t j = sorted_indices[s];
+                    if (j == i) continue;
+                    float djx = xi - px[j];
+                    float djy = yi - py[j];
+                    float djz = zi - pz[j];
+                    float r2 = djx * djx + djy * djy + djz * djz;
+                    if (r2 < h2 && r2 > 1e-12f) {
+                        float r = sqrtf(r2);
+                        float rho_j = density[j];
+                        if (rho_j < 1e-6f) continue;
+                        fn(st, j, djx, djy, djz, r, rho_j);
+                    }
+                }
+            }
+        }
+    }
+}
+
+typedef struct {
+    float h, mass, gas_constant, rest_density, spiky_grad_coeff, p_i;
+    float ax, ay, az;
+} pressure_state;
+
+/* sph_pressure.rs:86-99 */
+static void pressure_pair(void* v, uint32_t j, float djx, float djy, float djz, float r,
+                          float rho_j) {
+    pressure_state* st = (pressure_state*)v;
+    (void)j;
+    float diff = st->h - r;
+    float p_j = st->gas_constant * (rho_j - st->rest_density);
+    float grad_scale = st->spiky_grad_coeff * diff * diff / r;
+    float f_scale = -st->mass * (st->p_i + p_j) / (2.0f * rho_j) * grad_scale;
+    st->ax += f_scale * djx;
+    st->ay += f_scale * djy;
+    st->az += f_scale * djz;
+}
+
+/* sph_pressure.rs:28-112 */
+void or_sph_pressure(const or_sph_params* p, const float* px, const float* py, const float* pz,
+                     const float* vx, const float* vy, const float* vz, const float* density,
+                     uint32_t n, const uint32_t* cell_start, const uint32_t* sorted_indices,
+                     float dt, float* vout) {
+    float h2 = p->h * p->h;
+    float h6 = h2 * h2 * h2;
+    pressure_state st;
+    st.h = p->h;
+    st.mass = p->mass;
+    st.gas_constant = p->gas_constant;
+    st.rest_density = p->rest_density;
+    st.spiky_grad_coeff = -45.0f / (3.14159265f * h6);
+    for (uint32_t i = 0; i < n; i++) {
+        float ox = vx[i], oy = vy[i], oz = vz[i];
+        float rho_i = density[i];
+        if (!(rho_i < 1e-6f)) { /* :42 -- early return leaves v_i untouched */
+            st.p_i = p->gas_constant * (rho_i - p->rest_density);
+            st.ax = st.ay = st.az = 0.0f;
+            unfused_walk(p, px, py, pz, density, cell_start, sorted_indices, i, pressure_pair,
+                         &st);
+            ox += (st.ax / rho_i) * dt; /* :109-111 */
+            oy += (st.ay / rho_i) * dt;
+            oz += (st.az / rho_i) * dt;
+        }
+        vout[i] = ox;
+        vout[(size_t)n + i] = oy;
+        vout[2 * (size_t)n + i] = oz;
+    }
+}
+
+typedef struct {
+    float h, visc_coeff, mass, visc_lap_coeff, vxi, vyi, vzi;
+    const float *vx, *vy, *vz;
+    float ax, ay, az;
+} viscosity_state;
+
+/* sph_viscosity.rs:83-96 */
+static void viscosity_pair(void* v, uint32_t j, float djx, float djy, float djz, float r,
+                           float rho_j) {
+    viscosity_state* st = (viscosity_state*)v;
+    (void)djx;
+    (void)djy;
+    (void)djz;
+    float lap = st->visc_lap_coeff * (st->h - r);
+    float scale = st->visc_coeff * st->mass / rho_j * lap;
+    st->ax += scale * (st->vx[j] - st->vxi);
+    st->ay += scale * (st->vy[j] - st->vyi);
+    st->az += scale * (st->vz[j] - st->vzi);
+}
+
+/* sph_viscosity.rs:27-106 */
+void or_sph_viscosity(const or_sph_params* p, const float* px, const float* py,
+                      const float* pz, const float* vx, const float* vy, const float* vz,
+                      const float* density, uint32_t n, const uint32_t* cell_start,
+                      const uint32_t* sorted_indices, float dt, float* vout) {
+    float h2 = p->h * p->h;
+    float h6 = h2 * h2 * h2;
+    viscosity_state st;
+    st.h = p->h;
+    st.visc_coeff = p->visc;
+    st.mass = p->mass;
+    st.visc_lap_coeff = 45.0f / (3.14159265f * h6);
+    st.vx = vx;
+    st.vy = vy;
+    st.vz = vz;
+    for (uint32_t i = 0; i < n; i++) {
+        float ox = vx[i], oy = vy[i], oz = vz[i];
+        float rho_i = density[i];
+        if (!(rho_i < 1e-6f)) { /* :42 */
+            st.vxi = vx[i];
+            st.vyi = vy[i];
+            st.vzi = vz[i];
+            st.ax = st.ay = st.az = 0.0f;
+            unfused_walk(p, px, py, pz, density, cell_start, sorted_indices, i, viscosity_pair,
+                         &st);
+            ox += (st.ax / rho_i) * dt; /* :101-103 */
+            oy += (st.ay / rho_i) * dt;
+            oz += (st.az / rho_i) * dt;
+        }
+        vout[i] = ox;
+        vout[(size_t)n + i] = oy;
+        vout[2 * (size_t)n + i] = oz;
+    }
+}
+
 /* gravity.rs:31-34 */
 void or_gravity(float* vx, float* vy, float* vz, uint32_t n, float gx, float gy, float gz,
                 float dt) {

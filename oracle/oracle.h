@@ -101,6 +101,25 @@ void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
                       const float* density, uint32_t n, const uint32_t* cell_start,
                       const uint32_t* sorted_indices, double* accel64, double* scale64);
 
+/* Unfused SphPressureModule kernel, sph_pressure.rs:28-112: for each particle i with
+ * rho_i >= 1e-6, a_p over the 27-cell neighbourhood of the grid (cell_start, sorted_indices as
+ * left by the density module), skipping j == i, pairs with r^2 < h^2 && r^2 > 1e-12 and
+ * rho_j >= 1e-6; then v_i += (a_p / rho_i) * dt.  Reads vx..vz and writes vout (3 arrays of n
+ * floats); velocities are not read by the pressure terms. */
+void or_sph_pressure(const or_sph_params* p, const float* px, const float* py, const float* pz,
+                     const float* vx, const float* vy, const float* vz, const float* density,
+                     uint32_t n, const uint32_t* cell_start, const uint32_t* sorted_indices,
+                     float dt, float* vout);
+
+/* Unfused SphViscosityModule kernel, sph_viscosity.rs:27-106: a_v = sum_j mu*m/rho_j *
+ * lap(h - r) * (v_j - v_i) over the same neighbour set as or_sph_pressure, every v_j read from
+ * the input state (the reference kernel updates v in place while neighbours read it; the
+ * intended semantics is the state before the pass); then v_i += (a_v / rho_i) * dt into vout. */
+void or_sph_viscosity(const or_sph_params* p, const float* px, const float* py,
+                      const float* pz, const float* vx, const float* vy, const float* vz,
+                      const float* density, uint32_t n, const uint32_t* cell_start,
+                      const uint32_t* sorted_indices, float dt, float* vout);
+
 /* GravityModule kernel, gravity.rs:31-34. */
 void or_gravity(float* vx, float* vy, float* vz, uint32_t n, float gx, float gy, float gz,
                 float dt);

@@ -38,6 +38,10 @@ _SIG = {
                             _F, _P, _P]),
     "or_sph_force_f64": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
                                 _P, _P, _P]),
+    "or_sph_pressure": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
+                               _P, _F, _P]),
+    "or_sph_viscosity": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
+                                _P, _F, _P]),
     "or_gravity": (None, [_P, _P, _P, _U, _F, _F, _F, _F]),
     "or_integrate": (None, [_P, _P, _P, _P, _P, _P, _U, _F]),
     "or_box_collider": (None, [_P, _P, _P, _P, _P, _P, _U, _P, _P, _F]),
@@ -196,6 +200,27 @@ def sph_force_f64(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted
     lib().or_sph_force_f64(ctypes.byref(p), *[_p(a) for a in arrs], n, _p(cs), _p(si),
                            _p(a64), _p(s64))
     return a64.reshape(3, n), s64.reshape(3, n)
+
+
+def _unfused(fn, p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices, dt):
+    arrs = [_f32(a) for a in (x, y, z, vx, vy, vz, density)]
+    n = arrs[0].size
+    cs, si = _u32(cell_start), _u32(sorted_indices)
+    vout = np.empty(3 * n, np.float32)
+    fn(ctypes.byref(p), *[_p(a) for a in arrs], n, _p(cs), _p(si), float(dt), _p(vout))
+    return vout.reshape(3, n)
+
+
+def sph_pressure(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices, dt):
+    """Unfused SphPressureModule pass; returns the new velocities (3, n)."""
+    return _unfused(lib().or_sph_pressure, p, x, y, z, vx, vy, vz, density, cell_start,
+                    sorted_indices, dt)
+
+
+def sph_viscosity(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices, dt):
+    """Unfused SphViscosityModule pass; returns the new velocities (3, n)."""
+    return _unfused(lib().or_sph_viscosity, p, x, y, z, vx, vy, vz, density, cell_start,
+                    sorted_indices, dt)
 
 
 def gravity(vx, vy, vz, g, dt):

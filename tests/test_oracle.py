@@ -329,3 +329,95 @@ def test_sph_step_is_the_module_sequence(oracle):
     for a, b in zip(out[:6], s):
         assert np.array_equal(a, b)
     assert np.array_equal(out[6], rho) and np.array_equal(out[7], acc)
+
+
+# ---- unfused SphPressureModule / SphViscosityModule (sph_pressure.rs:28-112,
+# sph_viscosity.rs:27-106) --------------------------------------------------------------------
+def pair_parts(xi, xj, vi, vj, rho_i, rho_j):
+    """(pressure, viscosity) accelerations of i due to j, textbook forms in float64 (Mueller
+    2003: spiky gradient for pressure, viscosity Laplacian), each divided by rho_i."""
+    rv = np.asarray(xi, np.float64) - np.asarray(xj, np.float64)
+    r = np.linalg.norm(rv)
+    if not (r < H and r * r > 1e-12):
+        return np.zeros(3), np.zeros(3)
+    grad = -45.0 / (PI * H**6) * (H - r) ** 2 * rv / r
+    a_p = -MASS * (K * (rho_i - RHO0) + K * (rho_j - RHO0)) / (2.0 * rho_j) * grad
+    a_v = MU * MASS * (np.asarray(vj, np.float64) - vi) / rho_j * 45.0 / (PI * H**6) * (H - r)
+    return a_p / rho_i, a_v / rho_i
+
+
+DT = float(np.float32(1e-4))
+
+
+def test_unfused_closed_forms(oracle):
+    p = prm(oracle)
+    # isolated particle: both passes leave the velocity bit-identical
+    x = y = z = np.array([0.5], np.float32)
+    v = (np.array([0.25], np.float32), np.array([-1.5], np.float32), np.array([3.0], np.float32))
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(p, x, y, z, st, si)
+    for fn in (oracle.sph_pressure, oracle.sph_viscosity):
+        out = fn(p, x, y, z, *v, rho, st, si, DT)
+        assert [out[c][0] for c in range(3)] == [v[c][0] for c in range(3)]
+    # two particles: the velocity change over dt is the textbook pair term of each module
+    x = np.array([0.5, 0.512], np.float32)
+    y = np.array([0.4, 0.405], np.float32)
+    z = np.array([0.3, 0.296], np.float32)
+    V = np.array([[0.1, -0.3], [0.0, 0.2], [0.5, 0.5]], np.float32)
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(p, x, y, z, st, si)
+    vp = oracle.sph_pressure(p, x, y, z, *V, rho, st, si, DT)
+    vv = oracle.sph_viscosity(p, x, y, z, *V, rho, st, si, DT)
+    for i, j in ((0, 1), (1, 0)):
+        ep, ev = pair_parts((x[i], y[i], z[i]), (x[j], y[j], z[j]), V[:, i], V[:, j],
+                            float(rho[i]), float(rho[j]))
+        # v + a dt rounds to float32: compare the change against a dt within a few ulp of v
+        tol = 4 * np.spacing(np.abs(V[:, i]).astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs((vp[:, i].astype(np.float64) - V[:, i]) - ep * DT) <= tol + 1e-6 * np.abs(ep * DT))
+        assert np.all(np.abs((vv[:, i].astype(np.float64) - V[:, i]) - ev * DT) <= tol + 1e-6 * np.abs(ev * DT))
+    # equal densities (symmetric pair): pressure changes are opposite, viscosity pulls together
+    assert rho[0] == rho[1]
+    dp = vp.astype(np.float64) - V
+    assert np.allclose(dp[:, 0], -dp[:, 1], rtol=1e-3, atol=1e-12)
+    dv = vv.astype(np.float64) - V
+    assert np.all(dv[:, 0] * (V[:, 1] - V[:, 0]) >= 0)
+    # uniform velocity field: viscosity changes nothing (v_j - v_i = 0 exactly)
+    U = np.ones((3, 2), np.float32) * np.float32(0.7)
+    out = oracle.sph_viscosity(p, x, y, z, *U, rho, st, si, DT)
+    assert np.array_equal(out, U)
+    # a neighbour whose density is below 1e-6 is skipped, and such a particle is left untouched
+    rho0 = rho.copy()
+    rho0[1] = 0.0
+    for fn in (oracle.sph_pressure, oracle.sph_viscosity):
+        out = fn(p, x, y, z, *V, rho0, st, si, DT)
+        assert np.array_equal(out[:, 0], V[:, 0]) and np.array_equal(out[:, 1], V[:, 1])
+
+
+def test_unfused_vs_brute_force_and_fused(oracle):
+    rng = np.random.default_rng(15)
+    n = 2000
+    P = rng.uniform(0.3, 0.44, (n, 3)).astype(np.float32)
+    V = rng.uniform(-1, 1, (n, 3)).astype(np.float32)
+    p = prm(oracle)
+    st, si = grid(oracle, P[:, 0], P[:, 1], P[:, 2])
+    rho = oracle.sph_density(p, P[:, 0], P[:, 1], P[:, 2], st, si)
+    vp = oracle.sph_pressure(p, *P.T, *V.T, rho, st, si, DT)
+    vv = oracle.sph_viscosity(p, *P.T, *V.T, rho, st, si, DT)
+    vf, _ = oracle.sph_force(p, *P.T, *V.T, rho, st, si, DT)
+    a64, s64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
+    # bound of a velocity change: f32 rounding of v + a dt plus 1e-5 of the term magnitudes
+    vt = V.T.astype(np.float64)
+    ulp = 2 * np.spacing(np.abs(V.T)).astype(np.float64)
+    for i in range(0, n, 89):
+        bp, bv = np.zeros(3), np.zeros(3)
+        for j in range(n):
+            if j != i:
+                a, b = pair_parts(P[i], P[j], V[i], V[j], float(rho[i]), float(rho[j]))
+                bp += a
+                bv += b
+        tol = ulp[:, i] + 1e-5 * s64[:, i] * DT
+        assert np.all(np.abs((vp[:, i] - vt[:, i]) - bp * DT) <= tol)
+        assert np.all(np.abs((vv[:, i] - vt[:, i]) - bv * DT) <= tol)
+    # from the same state the two unfused changes add up to the fused pass's change
+    tot = (vp.astype(np.float64) - vt) + (vv.astype(np.float64) - vt)
+    assert np.all(np.abs(tot - (vf.astype(np.float64) - vt)) <= 3 * ulp + 1e-5 * s64 * DT)
