@@ -12,9 +12,15 @@ namespace fh {
 
 // ---- sizes ----------------------------------------------------------------------------------
 constexpr int kWave = 64;              // CDNA wavefront
-constexpr int kSortThreads = 512;      // 8 waves per sort workgroup
+#ifndef FH_SORT_THREADS
+#define FH_SORT_THREADS 512
+#endif
+#ifndef FH_SORT_ITEMS
+#define FH_SORT_ITEMS 16
+#endif
+constexpr int kSortThreads = FH_SORT_THREADS;  // 8 waves per sort workgroup
 constexpr int kSortWaves = kSortThreads / 64;
-constexpr int kSortItems = 16;         // keys per thread per tile
+constexpr int kSortItems = FH_SORT_ITEMS;      // keys per thread per tile
 constexpr int kSortTile = kSortThreads * kSortItems;  // 8192 keys per tile
 constexpr int kMaxPasses = 4;          // 8-bit digits, up to 32-bit keys
 constexpr int kHistThreads = 256;
@@ -67,7 +73,7 @@ struct Line {
 };
 struct Control {
     uint32_t epoch;                     // bumped by k_begin before each sort / scan
-    uint32_t plan;                      // bit p: sort pass p moves keys (not all digits equal)
+    uint32_t plan;                      // bit p: sort pass p runs (k_sort_plan)
     uint32_t pad0[30];
     Line error;                         // nonzero: a look-back spin limit was hit
     Line tile_ctr[kMaxPasses];          // dynamic tile ids of the sort passes
@@ -247,9 +253,10 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
                             uint32_t* keys_out, uint32_t* vals_out);
 // Run a sort whose histograms are ready: reads (k0, v0) (v0 == nullptr: values are the indices
-// 0..n-1), leaves the result in (kfin, vfin).  kfin may equal k0 (in place) and may be null
-// (values only).  Passes whose digit is the same for every key are skipped on the device;
-// the others ping-pong through the context's scratch, and a final kernel copies when needed.
+// 0..n-1), leaves the result in (kfin, vfin).  Either entirely in place ((kfin, vfin) ==
+// (k0, v0)) or entirely out of place (kfin may then be null: values only); anything else
+// returns hipErrorInvalidValue.  Passes whose digit is the same for every key are skipped on
+// the device; the others ping-pong through the context's scratch.
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits);
 // Mark the first index of every run of equal sorted keys in c->run_tag (epoch-tagged).

@@ -8,14 +8,13 @@
 //   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
 //                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
 //   k_hist_reduce  sums the partial rows into the histograms
-//   k_sort_plan    marks which passes move keys (a pass whose digit is equal for every key is
-//                  the identity and is skipped)
+//   k_sort_plan    decides which passes run (a pass whose digit is equal for every key is the
+//                  identity and is skipped)
 //   k_onesweep     one kernel per 8-bit pass: an 8192-key tile per 512-lane workgroup, ranked
 //                  with 64-lane ballot match-any, digit offsets from a decoupled look-back over
 //                  dynamically numbered tiles, then staged in LDS in digit order (keys, then
 //                  values through the same buffer) so the global scatter writes contiguous runs
-//   k_sort_finish  copies the result into place when the number of passes that moved keys
-//                  left it in scratch
+//   k_sort_finish  copies the result of a one-pass sort in place back from scratch
 // Stability: within a tile the rank of a key counts the equal digits before it in input order
 // (earlier items, earlier lanes, earlier waves); across tiles the look-back prefix counts the
 // equal digits of all earlier tiles.  Equal keys therefore keep their input order, which is
@@ -38,7 +37,6 @@ __global__ void k_begin(Control* ctl, uint32_t* __restrict__ lb, uint32_t lb_wor
         if (t == 0) {
             uint32_t e = (ctl->epoch + 1u) & kEpochMask;
             ctl->epoch = e ? e : 1u;
-            ctl->plan = 0u;
             for (int p = 0; p < kMaxPasses; p++) ctl->tile_ctr[p].v = 0u;
             ctl->scan_ctr.v = 0u;
             for (int q = 0; q < kHeavyLists; q++) ctl->heavy_count[q].v = 0u;
@@ -185,29 +183,38 @@ __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict_
     if (s) atomicAdd(&ctl->hist[p][d], s);
 }
 
-// Decide which passes move keys: a pass whose digit is equal for every key is the identity.
-__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t n, Control* ctl) {
-    __shared__ uint32_t s_trivial[kMaxPasses];
+// The passes that run (ctl->plan, one bit per pass).  A pass whose digit is equal for every key
+// (one histogram bin holds all n keys) is the identity and is skipped.  Two adjustments leave
+// the result in (kfin, vfin) without a copy kernel: when no pass moves keys and the sort is out
+// of place, pass 0 runs (a stable copy: its digit is constant); when exactly one pass moves keys
+// in place (it has to write scratch) and the sort has another pass, that pass runs as well
+// (also a copy), so the second of the two writes back in place.  Only one-pass sorts in place
+// keep k_sort_finish.  One workgroup of 256 threads (one bin each).
+__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t n, uint32_t in_place,
+                                                   Control* ctl) {
+    __shared__ uint32_t s_tw[4];
     const uint32_t d = threadIdx.x;
-    if (d < kMaxPasses) s_trivial[d] = 0u;
-    __syncthreads();
+    uint32_t triv = 0;
     for (uint32_t q = 0; q < passes; q++)
-        if (ctl->hist[q][d] == n) s_trivial[q] = 1u;
+        if (__ballot(ctl->hist[q][d] == n) != 0ull) triv |= 1u << q;
+    if ((d & 63u) == 0u) s_tw[d >> 6] = triv;
     __syncthreads();
     if (d == 0) {
-        uint32_t plan = 0;
-        for (uint32_t q = 0; q < passes; q++)
-            if (!s_trivial[q]) plan |= 1u << q;
+        triv = s_tw[0] | s_tw[1] | s_tw[2] | s_tw[3];
+        uint32_t plan = ~triv & ((1u << passes) - 1u);
+        if (plan == 0u && !in_place) {
+            plan = 1u;
+        } else if (__popc(plan) == 1 && in_place && passes >= 2u) {
+            const uint32_t p = (uint32_t)(__ffs(plan) - 1);
+            plan |= 1u << (p > 0u ? p - 1u : 1u);
+        }
         ctl->plan = plan;
     }
 }
 
-hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t passes, uint32_t n) {
+hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t passes) {
     const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
     k_hist_reduce<<<passes * groups, 256, 0, c->stream>>>(c->hist_part, rows, c->ctl);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    k_sort_plan<<<1, 256, 0, c->stream>>>(passes, n, c->ctl);
     return hipGetLastError();
 }
 
@@ -234,7 +241,7 @@ hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_
         default: k_hist_keys<4><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits), n);
+    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits));
     tend(c, KID_HIST);
     return e;
 }
@@ -254,16 +261,17 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && num_bits > 0)
-        e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits), n);
+        e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits));
     tend(c, KID_HASH);
     return e;
 }
 
 // ---------------------------------------------------------------------------------------------
-// Buffers of one sort.  Pass j of the passes that move keys (those in ctl->plan) reads the
-// output of pass j-1 (pass 0: k0 / v0) and writes, alternately, scratch a and b; the last one
-// writes (kfin, vfin) unless it reads kfin itself (a single pass in place), in which case it
-// writes a and k_sort_finish copies back.
+// Buffers of one sort.  A sort is either in place ((kfin, vfin) == (k0, v0)) or entirely out of
+// place (launch_sort_passes checks).  Pass j of the passes that run (the plan) reads the output
+// of pass j-1 (pass 0: k0 / v0) and writes, alternately, scratch a and b; the last one writes
+// (kfin, vfin) unless it is also the first and the sort is in place, in which case it writes a
+// (k_sort_plan avoids that case for sorts of more than one pass).
 struct SortIO {
     const uint32_t* k0;
     const uint32_t* v0;  // null: values are the indices 0..n-1
@@ -282,13 +290,17 @@ struct PassBufs {
     uint32_t* vout;
 };
 
+__device__ __forceinline__ bool sort_in_place(const SortIO& io) {
+    return io.kfin != nullptr && io.kfin == io.k0;
+}
+
 __device__ __forceinline__ PassBufs pass_bufs(SortIO io, uint32_t plan, uint32_t pass) {
     const uint32_t j = (uint32_t)__popc(plan & ((1u << pass) - 1u));
     const bool last = (plan >> (pass + 1u)) == 0u;
     PassBufs b;
     b.kin = j == 0 ? io.k0 : ((j & 1u) ? io.ka : io.kb);
     b.vin = j == 0 ? io.v0 : ((j & 1u) ? io.va : io.vb);
-    if (last && !(j == 0 && io.kfin == io.k0 && io.kfin)) {
+    if (last && !(j == 0 && sort_in_place(io))) {
         b.kout = io.kfin;
         b.vout = io.vfin;
     } else {
@@ -301,15 +313,52 @@ __device__ __forceinline__ PassBufs pass_bufs(SortIO io, uint32_t plan, uint32_t
 // Branch-free 64-lane match of an 8-bit digit: bit l of the result is set iff lane l holds the
 // same digit.  m is 0 or all ones per lane (sign-extended digit bit); ~(ballot ^ m) keeps the
 // lanes that agree with this lane on that bit.
+// Per bit: one signed bit-field extract (m), one compare writing the ballot, and one 3-input
+// bitwise op per half (acc & ~(ballot ^ m), truth table 0x90 over (acc, ballot, m)): 4 VALU
+// per bit.  Left to itself the compiler re-associates the chain into xors and or3s and derives
+// the compare from a separate shift (6 per bit).
 __device__ __forceinline__ void match8(uint32_t d, uint32_t& lo, uint32_t& hi) {
     lo = 0xFFFFFFFFu;
     hi = 0xFFFFFFFFu;
 #pragma unroll
     for (int b = 0; b < 8; b++) {
-        const int32_t m = ((int32_t)(d << (31 - b))) >> 31;
-        const uint64_t bal = __ballot(m != 0);
-        lo &= ~((uint32_t)bal ^ (uint32_t)m);
-        hi &= ~((uint32_t)(bal >> 32) ^ (uint32_t)m);
+        // m is produced by an opaque v_bfe_i32 so the ballot compares it with zero directly
+        // (otherwise the compiler derives the condition with a separate shift).
+        uint32_t m;
+        asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(m) : "v"(d), "n"(b));
+        const uint64_t bal = __ballot(m != 0u);
+        lo = __builtin_amdgcn_bitop3_b32(lo, (uint32_t)bal, m, 0x90);
+        hi = __builtin_amdgcn_bitop3_b32(hi, (uint32_t)(bal >> 32), m, 0x90);
+    }
+}
+
+constexpr int kLbWin = 4;  // look-back words loaded per round trip
+
+// Load of item k of this lane (element wbase + 64k + lane): unchecked in full tiles.
+template <bool Full>
+__device__ __forceinline__ uint32_t item_load(const uint32_t* __restrict__ p, uint32_t idx,
+                                              uint32_t n, uint32_t pad) {
+    return (Full || idx < n) ? p[idx] : pad;
+}
+
+template <bool Full>
+__device__ __forceinline__ void load_items(const uint32_t* __restrict__ p, uint32_t wbase,
+                                           int lane, uint32_t n, uint32_t pad,
+                                           uint32_t (&v)[kSortItems]) {
+#pragma unroll
+    for (int k = 0; k < kSortItems; k++)
+        v[k] = item_load<Full>(p, wbase + (uint32_t)(k * kWave + lane), n, pad);
+}
+
+// Values of the items: loaded, or the element indices when the input values are implicit.
+template <bool Full>
+__device__ __forceinline__ void load_vals(const uint32_t* __restrict__ vin, uint32_t wbase,
+                                          int lane, uint32_t n, uint32_t (&v)[kSortItems]) {
+    if (vin) {
+        load_items<Full>(vin, wbase, lane, n, 0u, v);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kSortItems; k++) v[k] = wbase + (uint32_t)(k * kWave + lane);
     }
 }
 
@@ -325,7 +374,7 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     __shared__ uint32_t s_tile;
 
     const uint32_t plan = ctl->plan;
-    if (!((plan >> pass) & 1u)) return;  // every key has the same digit: identity pass
+    if (!((plan >> pass) & 1u)) return;  // the pass does not run (see k_sort_plan)
     const PassBufs bf = pass_bufs(io, plan, pass);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -336,15 +385,13 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     const uint32_t tile = s_tile;
     const uint32_t tile_base = tile * (uint32_t)kSortTile;
     const uint32_t wbase = tile_base + (uint32_t)wave * (kWave * kSortItems);
+    const bool full = n - tile_base >= (uint32_t)kSortTile;  // workgroup-uniform
 
     // Striped key loads: item k of lane l is element wbase + 64k + l, so (k, l) order = input
     // order.  Slots past n hold digit `mask` and rank after every real key of the tile.
     uint32_t keys[kSortItems], vals[kSortItems], pos[kSortItems];
-#pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
-        const uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
-        keys[k] = idx < n ? bf.kin[idx] : 0xFFFFFFFFu;
-    }
+    if (full) load_items<true>(bf.kin, wbase, lane, n, 0xFFFFFFFFu, keys);
+    else load_items<false>(bf.kin, wbase, lane, n, 0xFFFFFFFFu, keys);
     const uint32_t lt_lo = lane >= 32 ? 0xFFFFFFFFu : ((1u << lane) - 1u);
     const uint32_t lt_hi = lane <= 32 ? 0u : (0xFFFFFFFFu >> (64 - lane));
     const uint32_t gt_lo = lane >= 31 ? 0u : (0xFFFFFFFFu << (lane + 1));
@@ -359,14 +406,13 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
         if (((lo & gt_lo) | (hi & gt_hi)) == 0u)  // highest lane of its digit group
             s_wcnt[wave][d] = before + (uint32_t)(__popc(lo) + __popc(hi));
         // Materialise the rank here: left alone, the compiler defers the popcounts to the
-        // staging loop and keeps every item's 64-bit match mask alive across the look-back
-        // (32 extra VGPRs, one workgroup less per CU).
+        // staging loop and keeps every item's 64-bit match mask alive across the look-back.
         asm volatile("" : "+v"(pos[k]));
     }
     __syncthreads();
 
-    // Per digit (threads 0..255): tile count and aggregate, wave offsets, tile-local digit
-    // start, global digit start, look-back.
+    // Per digit (threads 0..255): tile count, published at once as this tile's aggregate;
+    // wave offsets; tile-local digit start; global digit start.
     const uint32_t d = (uint32_t)tid & 255u;
     uint32_t cnt = 0, wc[kSortWaves];
     if (tid < 256) {
@@ -392,22 +438,56 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     const uint32_t ghist = (tid < 256 && d <= mask) ? ctl->hist[pass][d] : 0u;
     const uint32_t gstart = block_exclusive_scan<kSortWaves>(ghist, s_scan, &total);
 
+    // Stage the keys in tile-local digit order (that needs only this tile's counts; the scan's
+    // barriers published the wave offsets) and issue the value loads, so both overlap the
+    // look-back's wait for earlier tiles.
+#pragma unroll
+    for (int k = 0; k < kSortItems; k++) {
+        pos[k] += s_wcnt[wave][(keys[k] >> shift) & mask];
+        s_buf[pos[k]] = keys[k];
+    }
+    if (full) load_vals<true>(bf.vin, wbase, lane, n, vals);
+    else load_vals<false>(bf.vin, wbase, lane, n, vals);
+    __syncthreads();
+    uint32_t skey[kSortItems];
+#pragma unroll
+    for (int k = 0; k < kSortItems; k++) skey[k] = s_buf[k * kSortThreads + tid];
+
     uint32_t prefix = 0;
     if (tid < 256 && tile > 0) {
-        uint32_t t = tile - 1u, spins = 0;
+        // Windowed look-back: the words of the kLbWin tiles below `t` are loaded together (one
+        // round trip instead of kLbWin), then consumed nearest first: aggregates are summed
+        // until an inclusive prefix ends the walk; a word not yet published stops the window
+        // and is polled again.  Tiles below 0 are never read (tile 0 publishes inclusive).
+        uint32_t t = tile, spins = 0;  // the walk continues at tile t - 1
         for (;;) {
-            const uint32_t w = __hip_atomic_load(lookback + (size_t)t * 256u + d,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t st = w & (3u << 30);
-            if (st != 0u) {
-                prefix += w & 0x3FFFFFFFu;
-                if (st == kLb32Inclusive) break;
-                if (t == 0) {  // tile 0 always publishes inclusive; never walk below it
-                    atomicOr(&ctl->error.v, 2u);
-                    break;
+            uint32_t w[kLbWin];
+#pragma unroll
+            for (int j = 0; j < kLbWin; j++)
+                w[j] = t > (uint32_t)j
+                           ? __hip_atomic_load(lookback + (size_t)(t - 1u - j) * 256u + d,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0u;
+            uint32_t adv = 0;
+            bool done = false, stop = false;
+#pragma unroll
+            for (int j = 0; j < kLbWin; j++) {
+                const uint32_t st = w[j] & (3u << 30);
+                if (!stop && !done && t > (uint32_t)j && st != 0u) {
+                    prefix += w[j] & 0x3FFFFFFFu;
+                    adv++;
+                    done = st == kLb32Inclusive;
+                } else {
+                    stop = true;
                 }
-                t--;
-            } else {
+            }
+            if (done) break;
+            t -= adv;
+            if (t == 0) {  // tile 0 always publishes inclusive; never walk below it
+                atomicOr(&ctl->error.v, 2u);
+                break;
+            }
+            if (adv == 0) {
                 if (++spins >= kSpinLimit) {
                     atomicOr(&ctl->error.v, 1u);
                     break;
@@ -421,60 +501,33 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     if (tid < 256) s_gbase[d] = gstart + prefix - dstart;
     __syncthreads();
 
-    // Stage the keys in digit order, scatter them; then the values through the same buffer.
-#pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
-        pos[k] += s_wcnt[wave][(keys[k] >> shift) & mask];
-        s_buf[pos[k]] = keys[k];
-    }
-    __syncthreads();
-    const uint32_t valid = min(n - tile_base, (uint32_t)kSortTile);
+    // Scatter the keys (contiguous runs per digit), then the values through the same buffer.
+    // dst < n holds whenever the histograms and look-back are consistent; the check keeps a
+    // corrupted state (a spin limit hit) from writing out of bounds.
+    const uint32_t valid = full ? (uint32_t)kSortTile : n - tile_base;
     uint32_t dst[kSortItems];
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) {
         const uint32_t i = (uint32_t)(k * kSortThreads + tid);
-        const uint32_t key = s_buf[i];
-        dst[k] = s_gbase[(key >> shift) & mask] + i;
-        if (i < valid && dst[k] < n && bf.kout) bf.kout[dst[k]] = key;
+        dst[k] = s_gbase[(skey[k] >> shift) & mask] + i;
+        if ((full || i < valid) && dst[k] < n && bf.kout) bf.kout[dst[k]] = skey[k];
     }
-    // Values are loaded only now: holding them through ranking and look-back would cost 16
-    // VGPRs and with them a third workgroup per CU; the other workgroups hide the latency.
-#pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
-        const uint32_t idx = wbase + (uint32_t)(k * kWave + lane);
-        vals[k] = idx < n ? (bf.vin ? bf.vin[idx] : idx) : 0u;
-    }
-    __syncthreads();
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) s_buf[pos[k]] = vals[k];
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kSortItems; k++) {
         const uint32_t i = (uint32_t)(k * kSortThreads + tid);
-        if (i < valid && dst[k] < n) bf.vout[dst[k]] = s_buf[i];
+        if ((full || i < valid) && dst[k] < n) bf.vout[dst[k]] = s_buf[i];
     }
 }
 
-// When no pass moved keys the input is the result; when one pass ran in place it wrote
-// scratch.  Copy into (kfin, vfin) in those cases; otherwise do nothing.
+// A one-pass sort in place whose pass ran wrote scratch a: copy it back.
 __global__ __launch_bounds__(256) void k_sort_finish(SortIO io, const Control* ctl, uint32_t n) {
-    const uint32_t plan = ctl->plan;
-    const uint32_t moved = (uint32_t)__popc(plan);
-    const uint32_t* ks;
-    const uint32_t* vs;
-    if (moved == 0u) {
-        ks = io.k0;
-        vs = io.v0;
-        if (ks == io.kfin && vs == io.vfin && vs) return;
-    } else if (moved == 1u && io.kfin && io.kfin == io.k0) {
-        ks = io.ka;
-        vs = io.va;
-    } else {
-        return;
-    }
+    if (!(ctl->plan & 1u)) return;
     for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
-        if (io.kfin && io.kfin != ks) io.kfin[i] = ks[i];
-        io.vfin[i] = vs ? vs[i] : i;
+        io.kfin[i] = io.ka[i];
+        io.vfin[i] = io.va[i];
     }
 }
 
@@ -482,7 +535,13 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits) {
     const uint32_t passes = passes_for_bits(num_bits);
     const uint32_t tiles = ceil_div(n, (uint32_t)kSortTile);
+    const bool in_place = kfin != nullptr && kfin == k0;
+    if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
+        return hipErrorInvalidValue;  // mixed in place / out of place is not supported
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin};
+    k_sort_plan<<<1, 256, 0, c->stream>>>(passes, n, in_place ? 1u : 0u, c->ctl);
+    hipError_t e0 = hipGetLastError();
+    if (e0 != hipSuccess) return e0;
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t pbits = min(8u, num_bits - 8u * p);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * 256u;
@@ -492,11 +551,14 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    uint32_t blocks = ceil_div(n, 256u * 8u);
-    if (blocks > 1024) blocks = 1024;
-    if (blocks < 1) blocks = 1;
-    k_sort_finish<<<blocks, 256, 0, c->stream>>>(io, c->ctl, n);
-    return hipGetLastError();
+    if (passes == 1u && in_place) {
+        uint32_t blocks = ceil_div(n, 256u * 8u);
+        if (blocks > 1024) blocks = 1024;
+        if (blocks < 1) blocks = 1;
+        k_sort_finish<<<blocks, 256, 0, c->stream>>>(io, c->ctl, n);
+        return hipGetLastError();
+    }
+    return hipSuccess;
 }
 
 }  // namespace fh

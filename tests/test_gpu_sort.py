@@ -76,7 +76,8 @@ def test_sort_heavy_duplicates_is_stable(fh, gpu_ctx):
 
 
 @pytest.mark.parametrize("case", ["all_equal", "one_moving_pass", "trivial_middle_passes",
-                                  "trivial_first_pass", "two_values"])
+                                  "trivial_first_pass", "two_values", "only_last_pass",
+                                  "only_middle_pass"])
 def test_sort_skips_identity_passes(fh, gpu_ctx, oracle, case):
     """Passes whose digit is the same for every key are skipped on the device; the result must
     still be the stable sort, in place, whatever number of passes actually moved keys."""
@@ -87,7 +88,9 @@ def test_sort_skips_identity_passes(fh, gpu_ctx, oracle, case):
             "one_moving_pass": r,                                  # bytes 1..3 are zero
             "trivial_middle_passes": r | (r[::-1] << 24),          # bytes 1, 2 zero
             "trivial_first_pass": (r << 8) | 7,                    # byte 0 constant
-            "two_values": np.where(r < 128, 3, 0x70000).astype(np.uint32)}[case]
+            "two_values": np.where(r < 128, 3, 0x70000).astype(np.uint32),
+            "only_last_pass": (r << 24) | 0x00123456,              # bytes 0..2 constant
+            "only_middle_pass": (r << 16) | 0x9F0000FF & 0xFF00FFFF}[case]
     vals = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
     print(f"sort skip case {case}", flush=True)
     k, v = gpu_sort(fh, gpu_ctx, keys, vals, 32)
