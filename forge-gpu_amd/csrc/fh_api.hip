@@ -93,8 +93,7 @@ hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float
                        const float* py, const float* pz, const float* vx, const float* vy,
                        const float* vz, uint32_t n, bool with_vel) {
     const uint32_t bits = bits_for_cells(cells);
-    hipError_t e = launch_begin(c, n, bits);
-    if (e == hipSuccess) e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr);
+    hipError_t e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr, true);
     if (e == hipSuccess && n > 0)
         e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits);
     if (e == hipSuccess) e = launch_gather(c, px, py, pz, vx, vy, vz, n, with_vel);
@@ -259,7 +258,7 @@ int fh_hash_cells(fh_ctx* c, const float* x, const float* y, const float* z, uin
     uint32_t cells;
     if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hash_cells"))) return rc;
     if (n == 0) return FH_OK;
-    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, 0, keys, vals));
+    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, 0, keys, vals, false));
     return FH_OK;
 }
 
@@ -271,10 +270,8 @@ int fh_sort_pairs(fh_ctx* c, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_
         return fail(FH_EINVAL, "fh_sort_pairs: num_bits=%u outside 1..32", num_bits);
     if ((rc = check_n(c, n, "fh_sort_pairs"))) return rc;
     if (n < 2) return FH_OK;
-    FH_CHECK_HIP(launch_begin(c, n, num_bits));
-    FH_CHECK_HIP(launch_hist_keys(c, keys, n, num_bits));
-    // In place: the last pass that moves keys writes the caller's buffers (a single such pass
-    // writes scratch and the finishing kernel copies back).
+    FH_CHECK_HIP(launch_hist_keys(c, keys, n, num_bits, true));
+    // In place: the last pass that runs writes the caller's buffers (see k_sort_plan).
     FH_CHECK_HIP(launch_sort_passes(c, keys, vals, keys, vals, n, num_bits));
     return FH_OK;
 }
@@ -303,8 +300,7 @@ int fh_hashgrid_build(fh_ctx* c, const float* x, const float* y, const float* z,
     uint32_t cells;
     if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hashgrid_build"))) return rc;
     const uint32_t bits = bits_for_cells(cells);
-    FH_CHECK_HIP(launch_begin(c, n, bits));
-    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr));
+    FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr, true));
     if (n > 0) {
         FH_CHECK_HIP(launch_sort_passes(c, cell_indices, nullptr, c->skeys, sorted_indices, n, bits));
         FH_CHECK_HIP(launch_runs(c, c->skeys, n));
@@ -543,7 +539,7 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
     return FH_OK;
 }
 
-static const char* const kKernelNames[KID_COUNT] = {"begin", "hist", "hash", "scan", "sort",
+static const char* const kKernelNames[KID_COUNT] = {"hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
                                                     "finalize", "runs", "plan",
                                                     "density_heavy", "force_heavy", "group"};

@@ -91,7 +91,7 @@ struct GridDesc {
 };
 
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
-enum KernelId { KID_BEGIN, KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
+enum KernelId { KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
                 KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_DHEAVY, KID_FHEAVY,
                 KID_GROUP, KID_COUNT };
 
@@ -241,17 +241,16 @@ inline void tend(fh_ctx* c, KernelId k, hipStream_t s = nullptr) {
 
 // ---- launchers (host side, enqueue on ctx->stream; return hipError_t) ------------------------
 
-// Bump the epoch, clear histograms and counters, and zero the look-back words of a sort of n
-// keys with num_bits-bit digits (n = 0: no sort follows).
-hipError_t launch_begin(fh_ctx* c, uint32_t n, uint32_t num_bits);
 // Digit histograms of all passes of a num_bits sort of a key array (per-block partials, then
-// the reduce that also decides which passes move keys).
-hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits);
+// the reduce).  begin = true also starts a sort (or rebuild): bumps the epoch, clears the
+// histograms and counters, and zeroes the look-back words of the coming passes.
+hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits,
+                            bool begin);
 // Hash particle positions: keys_out[i] = cell, vals_out[i] = i (if non-null) and, for
-// num_bits > 0, the digit histograms of all passes of a num_bits sort.
+// num_bits > 0, the digit histograms of all passes of a num_bits sort; begin as above.
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
-                            uint32_t* keys_out, uint32_t* vals_out);
+                            uint32_t* keys_out, uint32_t* vals_out, bool begin);
 // Run a sort whose histograms are ready: reads (k0, v0) (v0 == nullptr: values are the indices
 // 0..n-1), leaves the result in (kfin, vfin).  Either entirely in place ((kfin, vfin) ==
 // (k0, v0)) or entirely out of place (kfin may then be null: values only); anything else

@@ -29,8 +29,20 @@
 namespace fh {
 
 // ---------------------------------------------------------------------------------------------
-__global__ void k_begin(Control* ctl, uint32_t* __restrict__ lb, uint32_t lb_words) {
+// Start of a sort (or of a hash-grid rebuild), done by the histogram kernel that every sort
+// begins with: bump the epoch, clear the histograms and counters (workgroup 0), zero the 32-bit
+// look-back words of the coming passes (grid-stride).  Nothing in the histogram kernel reads
+// what it clears; the kernels that do come later on the stream.
+struct Begin {
+    Control* ctl;  // null: no start-of-sort work in this launch
+    uint32_t* lb;
+    uint32_t lb_words;
+};
+
+__device__ __forceinline__ void begin_work(const Begin& b) {
+    if (!b.ctl) return;
     const uint32_t t = threadIdx.x;
+    Control* ctl = b.ctl;
     if (blockIdx.x == 0) {
         for (uint32_t i = t; i < (uint32_t)kMaxPasses * 256u; i += blockDim.x)
             (&ctl->hist[0][0])[i] = 0u;
@@ -44,19 +56,15 @@ __global__ void k_begin(Control* ctl, uint32_t* __restrict__ lb, uint32_t lb_wor
             ctl->big_count.v = 0u;
         }
     }
-    for (uint32_t i = blockIdx.x * blockDim.x + t; i < lb_words; i += gridDim.x * blockDim.x)
-        lb[i] = 0u;
+    for (uint32_t i = blockIdx.x * blockDim.x + t; i < b.lb_words; i += gridDim.x * blockDim.x)
+        b.lb[i] = 0u;
 }
 
-hipError_t launch_begin(fh_ctx* c, uint32_t n, uint32_t num_bits) {
-    const uint32_t words = n ? passes_for_bits(num_bits) * ceil_div(n, (uint32_t)kSortTile) * 256u : 0u;
-    uint32_t blocks = ceil_div(words, 256u * 4u);
-    if (blocks < 1) blocks = 1;
-    if (blocks > 1024) blocks = 1024;
-    tbeg(c, KID_BEGIN);
-    k_begin<<<blocks, 256, 0, c->stream>>>(c->ctl, c->sort_lb, words);
-    tend(c, KID_BEGIN);
-    return hipGetLastError();
+static Begin make_begin(fh_ctx* c, bool begin, uint32_t n, uint32_t num_bits) {
+    if (!begin) return Begin{nullptr, nullptr, 0u};
+    const uint32_t words =
+        n && num_bits ? passes_for_bits(num_bits) * ceil_div(n, (uint32_t)kSortTile) * 256u : 0u;
+    return Begin{c->ctl, c->sort_lb, words};
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -83,6 +91,31 @@ __device__ __forceinline__ void count_key(uint32_t (*sh)[256], uint32_t k, bool 
         hist_add(sh[p], (k >> (8 * p)) & (p == P - 1 ? top : 255u), valid);
 }
 
+// A full chunk of this thread's kHistItems keys.  Per pass, a wave whose 64 x kHistItems keys
+// all share one digit (c1's top byte; c3's top digit in most waves) adds their number with one
+// atomic; otherwise every key adds 1, with no per-key uniformity test.  `tb` = bits of the last
+// pass's digit.
+template <int P>
+__device__ __forceinline__ void count_chunk(uint32_t (*sh)[256], const uint32_t (&k)[kHistItems],
+                                            uint32_t tb) {
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const uint32_t w = p == P - 1 ? tb : 8u;
+        const uint32_t d0 =
+            __builtin_amdgcn_readfirstlane(__builtin_amdgcn_ubfe(k[0], 8u * p, w));
+        uint32_t diff = 0;
+#pragma unroll
+        for (int j = 0; j < kHistItems; j++) diff |= __builtin_amdgcn_ubfe(k[j], 8u * p, w) ^ d0;
+        if (__ballot(diff != 0u) == 0ull) {
+            if ((threadIdx.x & 63u) == 0u) atomicAdd(&sh[p][d0], 64u * kHistItems);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kHistItems; j++)
+                atomicAdd(&sh[p][__builtin_amdgcn_ubfe(k[j], 8u * p, w)], 1u);
+        }
+    }
+}
+
 // Write this workgroup's row of partial histograms (all 256 bins of every pass).
 __device__ __forceinline__ void write_row(uint32_t (*sh)[kMaxPasses][256], uint32_t* part,
                                           uint32_t passes) {
@@ -96,9 +129,11 @@ __device__ __forceinline__ void write_row(uint32_t (*sh)[kMaxPasses][256], uint3
 template <int P>
 __global__ __launch_bounds__(kHistThreads) void k_hist_keys(const uint32_t* __restrict__ keys,
                                                             uint32_t n, uint32_t top,
-                                                            uint32_t* __restrict__ part) {
+                                                            uint32_t* __restrict__ part,
+                                                            Begin bg) {
     __shared__ uint32_t sh[4][kMaxPasses][256];
     const uint32_t wave = threadIdx.x >> 6;
+    begin_work(bg);
     for (uint32_t i = threadIdx.x; i < 4u * kMaxPasses * 256u; i += kHistThreads)
         (&sh[0][0][0])[i] = 0u;
     __syncthreads();
@@ -119,10 +154,14 @@ __global__ __launch_bounds__(kHistThreads) void k_hist_keys(const uint32_t* __re
             const uint32_t i = cn * kHistChunk + j * kHistThreads + threadIdx.x;
             nxt[j] = (cn < chunks && i < n) ? keys[i] : 0u;
         }
+        if ((c + 1u) * kHistChunk <= n) {  // workgroup-uniform
+            count_chunk<P>(sh[wave], cur, (uint32_t)__popc(top));
+        } else {
 #pragma unroll
-        for (int j = 0; j < kHistItems; j++) {
-            const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
-            count_key<P>(sh[wave], cur[j], i < n, top);
+            for (int j = 0; j < kHistItems; j++) {
+                const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
+                count_key<P>(sh[wave], cur[j], i < n, top);
+            }
         }
 #pragma unroll
         for (int j = 0; j < kHistItems; j++) cur[j] = nxt[j];
@@ -134,9 +173,10 @@ template <int P>
 __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ z,
     uint32_t stride, uint32_t n, GridDesc g, uint32_t top, uint32_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, uint32_t* __restrict__ part) {
+    uint32_t* __restrict__ vals_out, uint32_t* __restrict__ part, Begin bg) {
     __shared__ uint32_t sh[4][kMaxPasses][256];
     const uint32_t wave = threadIdx.x >> 6;
+    begin_work(bg);
     if (P > 0) {
         for (uint32_t i = threadIdx.x; i < 4u * kMaxPasses * 256u; i += kHistThreads)
             (&sh[0][0][0])[i] = 0u;
@@ -161,7 +201,17 @@ __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
                 if (keys_out) keys_out[i] = k[j];
                 if (vals_out) vals_out[i] = i;
             }
-            if (P > 0) count_key<P>(sh[wave], k[j], i < n, top);
+        }
+        if (P > 0) {
+            if ((c + 1u) * kHistChunk <= n) {  // workgroup-uniform
+                count_chunk<P>(sh[wave], k, (uint32_t)__popc(top));
+            } else {
+#pragma unroll
+                for (int j = 0; j < kHistItems; j++) {
+                    const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
+                    count_key<P>(sh[wave], k[j], i < n, top);
+                }
+            }
         }
     }
     if (P > 0) write_row(sh, part, P);
@@ -231,14 +281,16 @@ static uint32_t top_mask(uint32_t num_bits) {
     return (1u << b) - 1u;
 }
 
-hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits) {
+hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits,
+                            bool begin) {
     const uint32_t blocks = hist_blocks(n), top = top_mask(num_bits);
+    const Begin bg = make_begin(c, begin, n, num_bits);
     tbeg(c, KID_HIST);
     switch (passes_for_bits(num_bits)) {
-        case 1: k_hist_keys<1><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
-        case 2: k_hist_keys<2><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
-        case 3: k_hist_keys<3><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
-        default: k_hist_keys<4><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part); break;
+        case 1: k_hist_keys<1><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
+        case 2: k_hist_keys<2><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
+        case 3: k_hist_keys<3><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
+        default: k_hist_keys<4><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits));
@@ -248,16 +300,17 @@ hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_
 
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
-                            uint32_t* keys_out, uint32_t* vals_out) {
+                            uint32_t* keys_out, uint32_t* vals_out, bool begin) {
     const uint32_t blocks = hist_blocks(n), top = num_bits ? top_mask(num_bits) : 0u;
+    const Begin bg = make_begin(c, begin, n, num_bits);
     uint32_t* part = c->hist_part;
     tbeg(c, KID_HASH);
     switch (passes_for_bits(num_bits)) {
-        case 0: k_hash_hist<0><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
-        case 1: k_hash_hist<1><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
-        case 2: k_hash_hist<2><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
-        case 3: k_hash_hist<3><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
-        default: k_hash_hist<4><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part); break;
+        case 0: k_hash_hist<0><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+        case 1: k_hash_hist<1><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+        case 2: k_hash_hist<2><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+        case 3: k_hash_hist<3><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+        default: k_hash_hist<4><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && num_bits > 0)

@@ -246,7 +246,7 @@ int fh_graph_launch(fh_ctx* ctx, uint32_t count);
 int fh_event_record(fh_ctx* ctx, uint32_t slot);
 int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
 
-/* Per-kernel timing.  Arm kernel `name` (one of "begin", "hist", "hash", "scan", "sort",
+/* Per-kernel timing.  Arm kernel `name` (one of "hist", "hash", "scan", "sort",
  * "gather", "density", "force", "query", "finalize", "runs", "plan", "density_heavy",
  * "force_heavy", "group") so that its next `max_launches` launches on the
  * context stream are bracketed by HIP events; launches captured into a graph record the events
