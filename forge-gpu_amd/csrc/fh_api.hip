@@ -402,7 +402,7 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
         FH_CHECK_HIP(launch_group(c, n, true));
         FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
-        FH_CHECK_HIP(launch_broadcast(c, n));
+        FH_CHECK_HIP(launch_prep(c, a));
         FH_CHECK_HIP(launch_force_fast(c, a, c->cell_start));
         FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density, accel));
     }

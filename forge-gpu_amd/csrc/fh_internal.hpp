@@ -131,7 +131,7 @@ struct fh_ctx {
     // SPH scratch (sorted order)
     float4* spos;        // [max_n] x, y, z, 0
     float4* svel;        // [max_n] vx, vy, vz, 0
-    float* srho;         // [max_n] density (exact kernels)
+    float* srho;         // [max_n] density (exact kernels; fast force pass via k_prep)
     float* dpart;        // [3][max_n] per-slab density partials (fast kernels)
     float* fpart;        // [3][3][max_n] per-slab acceleration partials (fast kernels)
     uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
@@ -288,8 +288,10 @@ hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const floa
 hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
-// Copy the density partials of each co-located cell's representative to its other particles.
-hipError_t launch_broadcast(fh_ctx* c, uint32_t n);
+// Force records of every sorted particle (positions with pressure, velocity and weight over
+// density; density in srho) from the density partials; written into c->sout, which holds the
+// new state only after the force pass.
+hipError_t launch_prep(fh_ctx* c, const SphArgs& a);
 // Fast passes only: list the cells of >= kCollapseMin particles and move the particles that
 // share the position of the cell's middle particle to the front of the cell when they are at
 // least kCollapseMin (cell_grp).  Reorders spos / svel / sidx inside those cells.

@@ -49,6 +49,14 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
     return v;
 }
 
+// p[i] if ok, else zero: the load always reads a valid element (index 0 when !ok) and the value
+// is selected afterwards (a select between two addresses would compile to a FLAT load).
+template <class T>
+__device__ __forceinline__ T load_or(const T* __restrict__ p, uint32_t i, bool ok, T zero) {
+    const T v = p[ok ? i : 0u];
+    return ok ? v : zero;
+}
+
 // The three row ranges [b, e) of slab dz for one particle (cells clamped like the reference,
 // sph_density.rs:421-437); empty ranges for rows outside the grid.
 __device__ __forceinline__ void slab_ranges(const float4& p, bool live, const GridDesc& g,
@@ -95,6 +103,12 @@ constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a
 #define FH_HGRID 1024
 #endif
 constexpr uint32_t kHeavyGrid = FH_HGRID;  // heavy workgroups (grid-stride over the list)
+#ifndef FH_HU
+#define FH_HU 2
+#endif
+#ifndef FH_HMINW
+#define FH_HMINW 6
+#endif
 
 // Candidate density accumulation of one lane over [jb, je) of a staged chunk, four candidates
 // per iteration with independent accumulators so LDS latency and the FMA chain overlap.
@@ -378,7 +392,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
     const bool live = s < n;
     uint32_t nh = 0;  // heavy items of this wave, kept in s_item[wave * 3 ...]
     if (sub * kSub < n) {  // wave-uniform
-        const float4 pi = live ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 pi = load_or(spos, s, live, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
         bool member = false;
         if (live) {
             const uint32_t c = cell_of(pi.x, pi.y, pi.z, g);
@@ -462,23 +476,6 @@ __device__ __forceinline__ uint32_t heavy_entry(const uint32_t* __restrict__ hea
         q -= c;
     }
     return heavy[(size_t)k * cap + q];
-}
-
-// After the density pass: every particle of a co-located cell takes its representative's
-// density partials (the force pass reads them for candidates and home particles alike).
-__global__ __launch_bounds__(256) void k_broadcast(const uint2* __restrict__ collapsed,
-                                                   uint32_t cap, const Control* __restrict__ ctl,
-                                                   float* __restrict__ dpart, uint32_t stride) {
-    const uint32_t count = min(ctl->collapse_count.v, cap);
-    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {
-        const uint2 fc = collapsed[q];
-        const float d0 = dpart[fc.x], d1 = dpart[stride + fc.x], d2 = dpart[2u * stride + fc.x];
-        for (uint32_t t = fc.x + 1u + threadIdx.x; t < fc.x + fc.y; t += blockDim.x) {
-            dpart[t] = d0;
-            dpart[stride + t] = d1;
-            dpart[2u * stride + t] = d2;
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -609,7 +606,7 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
-    const float4 pi = in ? spos[s] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 pi = load_or(spos, s, in, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
     uint32_t b[3], e[3];
     slab_ranges(pi, in, g, cstart, n, (int)slab - 1, b, e);
     LightStream L;
@@ -795,7 +792,7 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool live = s < n;
-        const float4 pi = live ? spos[s] : z4;
+        const float4 pi = load_or(spos, s, live, z4);
         uint32_t b[3], e[3];
         slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
         const uint32_t hr = home_row(pi, g);
@@ -860,93 +857,105 @@ __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_
     return mc * ((dpart[j] + dpart[stride + j]) + dpart[2u * stride + j]);
 }
 
-// One prefetched candidate of the force pass: position (with its spos.w bits), velocity, the
-// group's summed velocity when it is a representative, and its three density partials;
-// converted at store time to (x, y, z, p_j) and (u/rho_j, w/rho_j) with w the candidate weight
-// (1, M for a representative, 0 for the other members of a group) and u = w * v_j (the group's
-// summed velocity for a representative).  1/rho_j is taken as 0 when rho_j < 1e-6, which removes
-// the pair exactly like the skip of sph_fused.rs:607.
-struct ForceSlot {
-    float4 q, w, g;
-    float d0, d1, d2;
-};
-
-__device__ __forceinline__ ForceSlot force_fetch(const float4* __restrict__ spos,
-                                                 const float4* __restrict__ svel,
-                                                 const float4* __restrict__ vrep,
-                                                 const float* __restrict__ dpart,
-                                                 uint32_t stride, uint32_t j, bool ok) {
-    ForceSlot f;
-    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    f.q = ok ? spos[j] : z4;
-    f.w = ok ? svel[j] : z4;
-    f.g = z4;
-    if (ok && (__float_as_uint(f.q.w) & kRepFlag)) f.g = vrep[j];
-    f.d0 = ok ? dpart[j] : 0.0f;
-    f.d1 = ok ? dpart[stride + j] : 0.0f;
-    f.d2 = ok ? dpart[2u * stride + j] : 0.0f;
-    return f;
-}
-
-__device__ __forceinline__ void force_store(float4* __restrict__ sp, float4* __restrict__ sv,
-                                            uint32_t t, uint32_t j, const ForceSlot& f,
-                                            const FastForce& K) {
-    const float rj = K.mc * ((f.d0 + f.d1) + f.d2);
-    const float inv = rj < 1e-6f ? 0.0f : 1.0f / rj;
-    const uint32_t wb = __float_as_uint(f.q.w);
+// Force records, made once per substep after the density pass (k_prep), one pair per sorted
+// particle j: rec[j] = (x, y, z, p_j) and rec[stride + j] = (u / rho_j, w / rho_j), where w is
+// the candidate weight (1; M for the representative of a co-located group; 0 for the other
+// members, which the representative stands for) and u = w v_j (the group's summed velocity for
+// a representative).  1/rho_j is taken as 0 when rho_j < 1e-6, which removes the pair like the
+// skip of sph_fused.rs:607.  A non-finite position is recorded far away (1e30), so no pair
+// with it passes the distance test and the branch-free pair loop never multiplies by NaN.
+// srho[j] = rho_j; members take their representative's density (they sit at its position).
+// The force kernels then only copy records into LDS.
+__global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
+                                              const float4* __restrict__ svel,
+                                              const float4* __restrict__ vrep,
+                                              const float* __restrict__ dpart, uint32_t n,
+                                              uint32_t stride, float mc, float k, float rho0,
+                                              float* __restrict__ srho,
+                                              float4* __restrict__ rec) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const float4 p = spos[s];
+    const uint32_t wb = __float_as_uint(p.w);
+    uint32_t r = s;
     float wt = 1.0f;
-    float4 u = f.w;
+    float4 u = svel[s];
     if (wb & kRepFlag) {
         wt = (float)(wb & ~kRepFlag);
-        u = f.g;
-    } else if (wb != j) {
+        u = vrep[s];
+    } else if (wb != s) {  // member of a co-located group: wb is its representative
+        r = wb < n ? wb : s;
         wt = 0.0f;
         u = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    sp[t] = make_float4(f.q.x, f.q.y, f.q.z, K.k * (rj - K.rho0));
-    sv[t] = make_float4(u.x * inv, u.y * inv, u.z * inv, wt * inv);
+    const float rho = rho_of(dpart, stride, r, mc);
+    const float inv = rho < 1e-6f ? 0.0f : 1.0f / rho;
+    srho[s] = rho;
+    const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z);
+    rec[s] = fin ? make_float4(p.x, p.y, p.z, k * (rho - rho0))
+                 : make_float4(1e30f, 1e30f, 1e30f, 0.0f);
+    rec[stride + s] = make_float4(u.x * inv, u.y * inv, u.z * inv, wt * inv);
 }
 
-// Pressure + viscosity pair terms of one lane over [jb, je) of a staged chunk: per candidate
-// w/rho_j * [fp (p_i + p_j) (h - r)^2 / r (x_i - x_j)] + fv (h - r) (u/rho_j - w/rho_j v_i).
+// Pressure + viscosity pair terms of one lane over [jb, je) of staged records:
+// per candidate  fp (p_i + p_j) (w/rho_j) (h - r)^2 / r (x_i - x_j) + fv (h - r) (u/rho_j),
+// and wv += fv (h - r) (w/rho_j), the weight of -v_i in the viscosity sum (applied once by the
+// caller).  Branch-free: the pair test selects the two scale factors, so the loads of the next
+// candidates issue ahead of the arithmetic; staged positions are finite (k_prep), so a zero
+// scale never meets a NaN.
+__device__ __forceinline__ void force_pair(const float4& q, const float4& w, const float4& pi,
+                                           float p_i, const FastForce& K, float& ax, float& ay,
+                                           float& az, float& wv) {
+    const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
+    const float r2 = fmaf(dz, dz, fmaf(dy, dy, dx * dx));
+    const bool ok = r2 < K.h2 && r2 > 1e-12f;
+    const float rinv = __builtin_amdgcn_rsqf(r2);
+    const float diff = fmaf(-r2, rinv, K.h);
+    const float fs = ok ? K.fp * (p_i + q.w) * w.w * (diff * diff) * rinv : 0.0f;
+    const float vs = ok ? K.fv * diff : 0.0f;
+    wv = fmaf(vs, w.w, wv);
+    ax = fmaf(vs, w.x, fmaf(fs, dx, ax));
+    ay = fmaf(vs, w.y, fmaf(fs, dy, ay));
+    az = fmaf(vs, w.z, fmaf(fs, dz, az));
+}
+
+// U candidates per iteration (their loads issued together).
+template <int U>
 __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
                                           const float4* __restrict__ sv, uint32_t c0,
-                                          uint32_t jb, uint32_t je, float4 pi, float4 vi,
-                                          float p_i, const FastForce& K, float& ax, float& ay,
-                                          float& az, float& wv) {
-#pragma unroll 2
-    for (uint32_t j = jb; j < je; j++) {
-        const float4 q = sp[j - c0];
-        const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
-        const float r2 = fmaf(dz, dz, fmaf(dy, dy, dx * dx));
-        if (r2 < K.h2 && r2 > 1e-12f) {
-            const float4 w = sv[j - c0];
-            const float rinv = __builtin_amdgcn_rsqf(r2);
-            const float diff = K.h - r2 * rinv;
-            const float fs = K.fp * (p_i + q.w) * w.w * (diff * diff) * rinv;
-            const float vs = K.fv * diff;
-            wv = fmaf(vs, w.w, wv);  // a_i depends on v_i only through -wv * v_i
-            ax = fmaf(vs, fmaf(-w.w, vi.x, w.x), fmaf(fs, dx, ax));
-            ay = fmaf(vs, fmaf(-w.w, vi.y, w.y), fmaf(fs, dy, ay));
-            az = fmaf(vs, fmaf(-w.w, vi.z, w.z), fmaf(fs, dz, az));
+                                          uint32_t jb, uint32_t je, float4 pi, float p_i,
+                                          const FastForce& K, float& ax, float& ay, float& az,
+                                          float& wv) {
+    uint32_t j = jb;
+    if (U > 1) {
+        for (; j + U <= je; j += U) {
+            float4 q[U], w[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                q[u] = sp[j + u - c0];
+                w[u] = sv[j + u - c0];
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) force_pair(q[u], w[u], pi, p_i, K, ax, ay, az, wv);
         }
     }
+    for (; j < je; j++) force_pair(sp[j - c0], sv[j - c0], pi, p_i, K, ax, ay, az, wv);
 }
 
 // Acceleration partials: fpart[slab][c][s] = sum over the slab's neighbours j of the pressure
 // and viscosity pair terms (sph_fused.rs:604-623), not yet divided by rho_i.  Same windowed
-// stream as k_density_wave; light items hold no co-located group, so every candidate has weight
-// 1 and is staged as (x, y, z, p_j), (v_j / rho_j, 1 / rho_j).
+// stream as k_density_wave; the window is staged by copying force records (k_prep).
 __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict__ spos,
                                                        const float4* __restrict__ svel,
-                                                       const float* __restrict__ dpart,
+                                                       const float* __restrict__ srho,
+                                                       const float4* __restrict__ rec,
                                                        uint32_t n, GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
                                                        FastForce K, float* __restrict__ fpart,
                                                        uint32_t stride, uint32_t items,
                                                        const uint8_t* __restrict__ flag) {
     __shared__ float4 s_p[kTileP / kWave][kWin];  // x, y, z, p_j
-    __shared__ float4 s_v[kTileP / kWave][kWin];  // vx, vy, vz, 1/rho_j
+    __shared__ float4 s_v[kTileP / kWave][kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
     if (item >= items || flag[item]) return;  // whole wave; heavy items: k_force_heavy
@@ -954,9 +963,9 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const float4 pi = in ? spos[s] : z4;
-    const float4 vi = in ? svel[s] : z4;
-    const float rho_i = in ? rho_of(dpart, stride, s, K.mc) : 0.0f;
+    const float4 pi = load_or(spos, s, in, z4);
+    const float4 vi = load_or(svel, s, in, z4);
+    const float rho_i = load_or(srho, s, in, 0.0f);
     const bool live = in && !(rho_i < 1e-6f);  // sph_fused.rs:550
     const float p_i = K.k * (rho_i - K.rho0);
     uint32_t b[3], e[3];
@@ -970,22 +979,16 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         uint32_t j[kWinLoads];
         window_indices(L, w0, lane, j);
         float4 q[kWinLoads], w[kWinLoads];
-        float d0[kWinLoads], d1[kWinLoads], d2[kWinLoads];
 #pragma unroll
         for (int k = 0; k < kWinLoads; k++) {
-            q[k] = spos[j[k]];
-            w[k] = svel[j[k]];
-            d0[k] = dpart[j[k]];
-            d1[k] = dpart[stride + j[k]];
-            d2[k] = dpart[2u * stride + j[k]];
+            q[k] = rec[j[k]];
+            w[k] = rec[stride + j[k]];
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int k = 0; k < kWinLoads; k++) {
-            const float rj = K.mc * ((d0[k] + d1[k]) + d2[k]);
-            const float inv = rj < 1e-6f ? 0.0f : 1.0f / rj;
-            bp[k * kWave + lane] = make_float4(q[k].x, q[k].y, q[k].z, K.k * (rj - K.rho0));
-            bv[k * kWave + lane] = make_float4(w[k].x * inv, w[k].y * inv, w[k].z * inv, inv);
+            bp[k * kWave + lane] = q[k];
+            bv[k * kWave + lane] = w[k];
         }
         __builtin_amdgcn_wave_barrier();
         if (live) {
@@ -993,22 +996,22 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
             for (int r = 0; r < 3; r++) {
                 const uint32_t jb = max(L.S[r], w0);
                 const uint32_t je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin);
-                if (jb < je) force_run(bp, bv, w0, jb, je, pi, vi, p_i, K, ax, ay, az, wv);
+                if (jb < je) force_run<2>(bp, bv, w0, jb, je, pi, p_i, K, ax, ay, az, wv);
             }
         }
     }
     if (in) {
         float* o = fpart + (size_t)slab * 3u * stride;
-        o[s] = ax;
-        o[stride + s] = ay;
-        o[2u * (size_t)stride + s] = az;
+        o[s] = fmaf(-wv, vi.x, ax);
+        o[stride + s] = fmaf(-wv, vi.y, ay);
+        o[2u * (size_t)stride + s] = fmaf(-wv, vi.z, az);
     }
 }
 
 template <int HW>
-__global__ __launch_bounds__(HW * kWave) void k_force_heavy(
+__global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
-    const float4* __restrict__ vrep, const float* __restrict__ dpart, uint32_t n, GridDesc g,
+    const float* __restrict__ srho, const float4* __restrict__ rec, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
     float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
     const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const Control* __restrict__ ctl) {
@@ -1027,9 +1030,8 @@ __global__ __launch_bounds__(HW * kWave) void k_force_heavy(
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool in = s < n;
-        const float4 pi = in ? spos[s] : z4;
-        const float4 vi = in ? svel[s] : z4;
-        const float rho_i = in ? rho_of(dpart, stride, s, K.mc) : 0.0f;
+        const float4 pi = load_or(spos, s, in, z4);
+        const float rho_i = load_or(srho, s, in, 0.0f);
         const bool live = in && !(rho_i < 1e-6f);
         const float p_i = K.k * (rho_i - K.rho0);
         uint32_t b[3], e[3];
@@ -1051,30 +1053,37 @@ __global__ __launch_bounds__(HW * kWave) void k_force_heavy(
             int r;
             uint32_t c0, m;
             seg_chunk(R, t, r, c0, m);
-            ForceSlot f = force_fetch(spos, svel, vrep, dpart, stride, c0 + lane,
-                                      r < 3 && (uint32_t)lane < m);
+            // records of chunk t (lanes past the chunk load a valid index; their slots are
+            // never read), the next chunk's fetched before the current one is evaluated
+            float4 q = load_or(rec, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
+            float4 w = load_or(rec + stride, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
             while (r < 3) {  // uniform within the wave
                 int nr;
                 uint32_t nc0, nm;
                 seg_chunk(R, t + HW, nr, nc0, nm);
-                const ForceSlot nf = force_fetch(spos, svel, vrep, dpart, stride, nc0 + lane,
-                                                 nr < 3 && (uint32_t)lane < nm);
+                const float4 nq = load_or(rec, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
+                const float4 nw =
+                    load_or(rec + stride, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
                 __builtin_amdgcn_wave_barrier();
-                force_store(bp, bv, lane, c0 + lane, f, K);  // members of a group: weight 0
+                bp[lane] = q;
+                bv[lane] = w;
                 __builtin_amdgcn_wave_barrier();
                 if (mine)
-                    force_run(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m), pi, vi,
-                              p_i, K, ax, ay, az, wv);
+                    force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m),
+                                     pi, p_i, K, ax, ay, az, wv);
                 t += HW;
                 r = nr;
                 c0 = nc0;
                 m = nm;
-                f = nf;
+                q = nq;
+                w = nw;
             }
         }
-        s_acc[0][wave][lane] = ax;
-        s_acc[1][wave][lane] = ay;
-        s_acc[2][wave][lane] = az;
+        // the -wv v_i part of the viscosity sum (wave partials add linearly)
+        const float4 vi = load_or(svel, s, in, z4);
+        s_acc[0][wave][lane] = fmaf(-wv, vi.x, ax);
+        s_acc[1][wave][lane] = fmaf(-wv, vi.y, ay);
+        s_acc[2][wave][lane] = fmaf(-wv, vi.z, az);
         s_acc[3][wave][lane] = wv;
         __syncthreads();
         if (wave < 3) {  // wave c reduces component c in wave order
@@ -1286,10 +1295,11 @@ hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
     return e;
 }
 
-hipError_t launch_broadcast(fh_ctx* c, uint32_t n) {
-    if (n == 0) return hipSuccess;
-    k_broadcast<<<64, 256, 0, c->stream>>>(c->collapsed, ceil_div(c->max_n, 64u) + 1u, c->ctl,
-                                           c->dpart, c->max_n);
+hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
+    if (a.n == 0) return hipSuccess;
+    k_prep<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
+                                                       c->max_n, poly6_mc(a.h, a.mass), a.k,
+                                                       a.rho0, c->srho, c->sout);
     return hipGetLastError();
 }
 
@@ -1312,13 +1322,14 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     if (e != hipSuccess) return e;
     tbeg(c, KID_FHEAVY, c->side);
     k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
-        c->spos, c->svel, c->vrep, c->dpart, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
+        c->spos, c->svel, c->srho, c->sout, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
         c->wpart, c->max_n, c->heavy, c->heavy_cap, c->ctl);
     tend(c, KID_FHEAVY, c->side);
     e = hipGetLastError();
     tbeg(c, KID_FORCE);
-    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->dpart, a.n, a.g, cell_start,
-                                                 K, c->fpart, c->max_n, items, c->heavy_flag);
+    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, a.n, a.g,
+                                                 cell_start, K, c->fpart, c->max_n, items,
+                                                 c->heavy_flag);
     tend(c, KID_FORCE);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c);
