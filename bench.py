@@ -17,6 +17,9 @@ One JSON line on stdout:
                sample, timed on this host
   extra.sort_c1  the standalone 16,777,216-pair 32-bit sort: Gkeys/s and the
                onesweep pass against the HBM roofline
+  extra.query_c2 HashGrid build + neighbour query of configs[2] (4,194,304 points)
+  extra.sph_c4   one grid build + density + force pass of configs[4] (8,388,608 particles,
+               skewed occupancy): time, candidate tests per second, occupancy max / p99
 """
 from __future__ import annotations
 
@@ -243,6 +246,135 @@ def bench_sort(args, fh, torch, log):
     return out
 
 
+def sort_bytes(n: int, bits: int) -> int:
+    """B_sort(N, bits) = N (4 + 16 ceil(bits / 8)): one key read for the all-digit histogram,
+    then a read and write of (key, value) per 8-bit pass."""
+    return n * (4 + 16 * ((bits + 7) // 8))
+
+
+def bench_query_c2(args, fh, torch, log):
+    """HashGrid build + 3x3x3 neighbour query (counts and poly6 weight sums) of
+    4,194,304 uniform points, r = cell = 0.0122, 82^3 cells.  Each leg is timed with HIP
+    events around `reps` back-to-back calls on the context stream."""
+    from forge_hip import _lib, workloads
+    from forge_hip._lib import check, f3, u3
+    from forge_hip.runtime import ptr, u32_empty
+
+    c = workloads.config2()
+    n = c["n"]
+    C = c["dims"][0] * c["dims"][1] * c["dims"][2]
+    ctx = fh.Context(max_n=n, max_cells=C)
+    grid = fh.HashGrid(c["cell_size"], c["dims"], c["origin"], n, ctx=ctx)
+    P = tuple(torch.from_numpy(c[a]).cuda() for a in "xyz")
+    counts = u32_empty(n, P[0].device)
+    wsum = torch.empty(n, dtype=torch.float32, device=P[0].device)
+    torch.cuda.synchronize()
+    lib = _lib.load()
+    bargs = (ctx.handle, ptr(P[0]), ptr(P[1]), ptr(P[2]), 1, n, grid.cell_size, f3(grid.origin),
+             u3(grid.dims), ptr(grid.cell_start), ptr(grid.sorted_indices),
+             ptr(grid.cell_indices))
+    qargs = (ctx.handle, ptr(P[0]), ptr(P[1]), ptr(P[2]), 1, n, grid.cell_size, f3(grid.origin),
+             u3(grid.dims), ptr(grid.cell_start), ptr(grid.sorted_indices), float(c["radius"]),
+             ptr(counts), ptr(wsum))
+    reps = max(args.sort_reps, 1)
+    check(lib.fh_hashgrid_build(*bargs))
+    check(lib.fh_neighbor_query(*qargs))
+    ctx.sync()
+    ctx.event_record(4)
+    for _ in range(reps):
+        check(lib.fh_hashgrid_build(*bargs))
+    ctx.event_record(5)
+    for _ in range(reps):
+        check(lib.fh_neighbor_query(*qargs))
+    ctx.event_record(6)
+    ctx.sync()
+    build_ms = ctx.event_elapsed_ms(4, 5) / reps
+    query_ms = ctx.event_elapsed_ms(5, 6) / reps
+    mean_count = float(counts.double().mean().item())
+    ctx.close()
+    bits = max(1, (C - 1).bit_length())
+    b_build = 20 * n + sort_bytes(n, bits) + 4 * n + 8 * C
+    b_query = 28 * n + 8 * C
+    out = {
+        "workload": "c2: HashGrid build + 3x3x3 neighbour query, 4,194,304 uniform points, "
+                    "r = cell = 0.0122, 82^3 cells",
+        "build_ms": build_ms, "query_ms": query_ms,
+        "points_per_s": n / ((build_ms + query_ms) * 1e-3),
+        "mean_neighbours": mean_count,
+        "build_alg_bytes": b_build, "build_alg_GBs": b_build / (build_ms * 1e-3) / 1e9,
+        "query_alg_bytes": b_query, "query_alg_GBs": b_query / (query_ms * 1e-3) / 1e9,
+        "query_frac_of_hbm_peak": b_query / (query_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "reps": reps,
+    }
+    log(f"c2: build {build_ms:.3f} ms, query {query_ms:.3f} ms")
+    return out
+
+
+def candidate_tests(x, y, z, cs, dims):
+    """Pair candidates of one neighbour pass: sum over particles of the occupancy of their
+    clamped 3x3x3 cell neighbourhood."""
+    import numpy as np
+
+    nx, ny, nz = dims
+    c = [np.clip(np.floor(a / np.float32(cs)).astype(np.int64), 0, d - 1)
+         for a, d in ((x, nx), (y, ny), (z, nz))]
+    occ = np.bincount(c[0] + nx * (c[1] + ny * c[2]), minlength=nx * ny * nz)
+    o3 = occ.reshape(nz, ny, nx)
+    p = np.pad(o3, 1)
+    s = np.zeros_like(o3)
+    for a in range(3):
+        for b in range(3):
+            for d in range(3):
+                s += p[a:a + nz, b:b + ny, d:d + nx]
+    return int((o3 * s).sum()), occ
+
+
+def bench_sph_c4(args, fh, torch, log):
+    """one HashGrid build + SPH density + pressure/viscosity pass over 8,388,608
+    particles of 64 Gaussian clumps + 10 % uniform background (load-imbalance stress); the
+    fused module alone (rebuild, density, force), timed with HIP events over `reps` calls."""
+    import numpy as np
+    from forge_hip import workloads
+
+    cfg = workloads.config4()
+    f = build_fields(fh, cfg, torch)
+    p = fh.Pipeline()
+    p.add(fh.SphFusedModule(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity))
+    ctx = f.context(cfg.num_cells)
+    torch.cuda.synchronize()
+    p.step(f, cfg.dt)  # warm-up (positions do not move: every call is the same workload)
+    reps = 3
+    ctx.event_record(7)
+    for _ in range(reps):
+        p.step_async(f, cfg.dt)
+    ctx.event_record(8)
+    ctx.sync()
+    ms = ctx.event_elapsed_ms(7, 8) / reps
+    ks = ["density", "density_heavy", "force", "force_heavy"]
+    for k in ks:
+        ctx.time_kernel(k, 1)
+    p.step_async(f, cfg.dt)
+    ctx.sync()
+    kt = {k: 1e3 * sum(ctx.kernel_times_ms(k)) for k in ks}
+    for k in ks:
+        ctx.time_kernel(k, 0)
+    cand, occ = candidate_tests(cfg.x, cfg.y, cfg.z, cfg.cell_size, cfg.dims)
+    nz = occ[occ > 0]
+    out = {
+        "workload": "c4: 8,388,608 particles (64 Gaussian clumps + 10 % uniform), h = cell = "
+                    "0.01, 100^3 cells: one grid build + density + fused force pass",
+        "ms": ms, "particles_per_s": cfg.n / (ms * 1e-3),
+        "candidate_tests_per_pass": cand,
+        "candidate_tests_per_s": 2 * cand / (ms * 1e-3),
+        "occupancy_max": int(occ.max()), "occupancy_p99_nonempty": float(np.percentile(nz, 99)),
+        "kernels_us": {k: round(v, 1) for k, v in kt.items()},
+        "reps": reps, "input_sha256": cfg.digest(),
+    }
+    log(f"c4: {ms:.2f} ms per build + density + force, max occupancy {occ.max()}")
+    return out
+
+
 def cpu_baseline(args, log):
     import numpy as np
 
@@ -281,6 +413,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sort", action="store_true", help="skip the c1 sort line")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip the c2 (grid build + query) and c4 (skewed SPH pass) lines")
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--sort-only", action="store_true",
                     help="only the c1 sort line (for a profile of the sort alone)")
@@ -315,6 +449,8 @@ def main(argv=None) -> int:
         return 0
     s = bench_sph(args, fh, torch, log)
     sort = None if args.no_sort else bench_sort(args, fh, torch, log)
+    q2 = None if args.no_extra_configs else bench_query_c2(args, fh, torch, log)
+    s4 = None if args.no_extra_configs else bench_sph_c4(args, fh, torch, log)
     cpu = None if args.no_cpu else cpu_baseline(args, log)
 
     cfg, K = s["cfg"], s["K"]
@@ -362,6 +498,8 @@ def main(argv=None) -> int:
             "passes": {p: {q: (round(v, 3) if isinstance(v, float) else v) for q, v in d.items()}
                        for p, d in s["pas"].items()},
             "sort_c1": sort,
+            "query_c2": q2,
+            "sph_c4": s4,
         },
     }
     print(json.dumps(line), flush=True)

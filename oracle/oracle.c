@@ -238,48 +238,62 @@ static int32_t sph_cell_coord(float p, float cell_size, uint32_t dim) {
 }
 
 /* sph_density.rs:409-460 */
-void or_sph_density(const or_sph_params* p, const float* px, const float* py, const float* pz,
-                    uint32_t n, const uint32_t* cell_start, const uint32_t* sorted_indices,
-                    float* density) {
+/* Density of particle i, the body of the per-particle loop of sph_density.rs:401-461. */
+static float density_one(const or_sph_params* p, const float* px, const float* py,
+                         const float* pz, const uint32_t* cell_start,
+                         const uint32_t* sorted_indices, uint32_t i) {
     const float h = p->h, mass = p->mass, cs = p->cell_size;
     const int32_t gnx = (int32_t)p->dims[0], gny = (int32_t)p->dims[1], gnz = (int32_t)p->dims[2];
     float h2 = h * h;
     float h9 = h2 * h2 * h2 * h2 * h;
     float poly6_coeff = 315.0f / (64.0f * 3.14159265f * h9);
-    for (uint32_t i = 0; i < n; i++) {
-        float xi = px[i], yi = py[i], zi = pz[i];
-        float rho = 0.0f;
-        int32_t cx = sph_cell_coord(xi, cs, p->dims[0]);
-        int32_t cy = sph_cell_coord(yi, cs, p->dims[1]);
-        int32_t cz = sph_cell_coord(zi, cs, p->dims[2]);
-        for (int dz = -1; dz <= 1; dz++) {
-            int32_t nz = cz + dz;
-            if (nz < 0 || nz >= gnz) continue;
-            for (int dy = -1; dy <= 1; dy++) {
-                int32_t ny = cy + dy;
-                if (ny < 0 || ny >= gny) continue;
-                for (int dx = -1; dx <= 1; dx++) {
-                    int32_t nx = cx + dx;
-                    if (nx < 0 || nx >= gnx) continue;
-                    uint32_t cell = (uint32_t)nx + (uint32_t)ny * (uint32_t)gnx +
-                                    (uint32_t)nz * (uint32_t)gnx * (uint32_t)gny;
-                    uint32_t start = cell_start[cell], end = cell_start[cell + 1];
-                    for (uint32_t s = start; s < end; s++) {
-                        uint32_t j = sorted_indices[s];
-                        float dx2 = xi - px[j];
-                        float dy2 = yi - py[j];
-                        float dz2 = zi - pz[j];
-                        float r2 = dx2 * dx2 + dy2 * dy2 + dz2 * dz2;
-                        if (r2 < h2) {
-                            float diff = h2 - r2;
-                            rho += mass * poly6_coeff * diff * diff * diff;
-                        }
+    float xi = px[i], yi = py[i], zi = pz[i];
+    float rho = 0.0f;
+    int32_t cx = sph_cell_coord(xi, cs, p->dims[0]);
+    int32_t cy = sph_cell_coord(yi, cs, p->dims[1]);
+    int32_t cz = sph_cell_coord(zi, cs, p->dims[2]);
+    for (int dz = -1; dz <= 1; dz++) {
+        int32_t nz = cz + dz;
+        if (nz < 0 || nz >= gnz) continue;
+        for (int dy = -1; dy <= 1; dy++) {
+            int32_t ny = cy + dy;
+            if (ny < 0 || ny >= gny) continue;
+            for (int dx = -1; dx <= 1; dx++) {
+                int32_t nx = cx + dx;
+                if (nx < 0 || nx >= gnx) continue;
+                uint32_t cell = (uint32_t)nx + (uint32_t)ny * (uint32_t)gnx +
+                                (uint32_t)nz * (uint32_t)gnx * (uint32_t)gny;
+                uint32_t start = cell_start[cell], end = cell_start[cell + 1];
+                for (uint32_t s = start; s < end; s++) {
+                    uint32_t j = sorted_indices[s];
+                    float dx2 = xi - px[j];
+                    float dy2 = yi - py[j];
+                    float dz2 = zi - pz[j];
+                    float r2 = dx2 * dx2 + dy2 * dy2 + dz2 * dz2;
+                    if (r2 < h2) {
+                        float diff = h2 - r2;
+                        rho += mass * poly6_coeff * diff * diff * diff;
                     }
                 }
             }
         }
-        density[i] = rho;
     }
+    return rho;
+}
+
+void or_sph_density(const or_sph_params* p, const float* px, const float* py, const float* pz,
+                    uint32_t n, const uint32_t* cell_start, const uint32_t* sorted_indices,
+                    float* density) {
+    for (uint32_t i = 0; i < n; i++)
+        density[i] = density_one(p, px, py, pz, cell_start, sorted_indices, i);
+}
+
+void or_sph_density_at(const or_sph_params* p, const float* px, const float* py,
+                       const float* pz, const uint32_t* cell_start,
+                       const uint32_t* sorted_indices, const uint32_t* which, uint32_t m,
+                       float* density) {
+    for (uint32_t k = 0; k < m; k++)
+        density[k] = density_one(p, px, py, pz, cell_start, sorted_indices, which[k]);
 }
 
 /* Per-pair maths of sph_fused.rs:542-638 (identical to sph_pressure.rs / sph_viscosity.rs
@@ -364,10 +378,11 @@ void or_sph_force(const or_sph_params* p, const float* px, const float* py, cons
     }
 }
 
-void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
-                      const float* pz, const float* vx, const float* vy, const float* vz,
-                      const float* density, uint32_t n, const uint32_t* cell_start,
-                      const uint32_t* sorted_indices, double* accel64, double* scale64) {
+/* fp64 acceleration and error scale of particle i (body of or_sph_force_f64's loop). */
+static void force64_one(const or_sph_params* p, const float* px, const float* py,
+                        const float* pz, const float* vx, const float* vy, const float* vz,
+                        const float* density, const uint32_t* cell_start,
+                        const uint32_t* sorted_indices, uint32_t i, double a[3], double s[3]) {
     const double h = p->h, mass = p->mass;
     const double k = p->gas_constant, rho0 = p->rest_density, mu = p->visc;
     const int32_t gnx = (int32_t)p->dims[0], gny = (int32_t)p->dims[1], gnz = (int32_t)p->dims[2];
@@ -375,54 +390,75 @@ void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
     const double PI = 3.14159265358979323846;
     double h6 = h * h * h * h * h * h;
     double gcoef = -45.0 / (PI * h6), lcoef = 45.0 / (PI * h6);
-    for (uint32_t i = 0; i < n; i++) {
-        double a[3] = {0, 0, 0}, s[3] = {0, 0, 0};
-        float rho_if = density[i];
-        if (!(rho_if < 1e-6f)) {
-            double rho_i = rho_if, p_i = k * (rho_i - rho0);
-            int32_t cx = sph_cell_coord(px[i], p->cell_size, p->dims[0]);
-            int32_t cy = sph_cell_coord(py[i], p->cell_size, p->dims[1]);
-            int32_t cz = sph_cell_coord(pz[i], p->cell_size, p->dims[2]);
-            for (int dz = -1; dz <= 1; dz++)
-                for (int dy = -1; dy <= 1; dy++)
-                    for (int dx = -1; dx <= 1; dx++) {
-                        int32_t ncx = cx + dx, ncy = cy + dy, ncz = cz + dz;
-                        if (ncx < 0 || ncx >= gnx || ncy < 0 || ncy >= gny || ncz < 0 ||
-                            ncz >= gnz)
-                            continue;
-                        uint32_t cell = (uint32_t)ncx + (uint32_t)ncy * (uint32_t)gnx +
-                                        (uint32_t)ncz * (uint32_t)gnx * (uint32_t)gny;
-                        for (uint32_t q = cell_start[cell]; q < cell_start[cell + 1]; q++) {
-                            uint32_t j = sorted_indices[q];
-                            float fx = px[i] - px[j], fy = py[i] - py[j], fz = pz[i] - pz[j];
-                            float r2f = fx * fx + fy * fy + fz * fz;
-                            if (!(r2f < h2f && r2f > 1e-12f)) continue;
-                            if (density[j] < 1e-6f) continue;
-                            double d[3] = {(double)px[i] - px[j], (double)py[i] - py[j],
-                                           (double)pz[i] - pz[j]};
-                            double r = sqrt(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
-                            double rho_j = density[j], p_j = k * (rho_j - rho0);
-                            double diff = h - r;
-                            double fsc = -mass * (p_i + p_j) / (2.0 * rho_j) *
-                                         (gcoef * diff * diff / r);
-                            double vsc = mu * mass / rho_j * (lcoef * diff);
-                            double dv[3] = {(double)vx[j] - vx[i], (double)vy[j] - vy[i],
-                                            (double)vz[j] - vz[i]};
-                            for (int c = 0; c < 3; c++) {
-                                double tp = fsc * d[c], tv = vsc * dv[c];
-                                a[c] += tp + tv;
-                                s[c] += fabs(tp) + fabs(tv);
-                            }
-                        }
+    for (int c = 0; c < 3; c++) a[c] = s[c] = 0.0;
+    float rho_if = density[i];
+    if (rho_if < 1e-6f) return;
+    double rho_i = rho_if, p_i = k * (rho_i - rho0);
+    int32_t cx = sph_cell_coord(px[i], p->cell_size, p->dims[0]);
+    int32_t cy = sph_cell_coord(py[i], p->cell_size, p->dims[1]);
+    int32_t cz = sph_cell_coord(pz[i], p->cell_size, p->dims[2]);
+    for (int dz = -1; dz <= 1; dz++)
+        for (int dy = -1; dy <= 1; dy++)
+            for (int dx = -1; dx <= 1; dx++) {
+                int32_t ncx = cx + dx, ncy = cy + dy, ncz = cz + dz;
+                if (ncx < 0 || ncx >= gnx || ncy < 0 || ncy >= gny || ncz < 0 || ncz >= gnz)
+                    continue;
+                uint32_t cell = (uint32_t)ncx + (uint32_t)ncy * (uint32_t)gnx +
+                                (uint32_t)ncz * (uint32_t)gnx * (uint32_t)gny;
+                for (uint32_t q = cell_start[cell]; q < cell_start[cell + 1]; q++) {
+                    uint32_t j = sorted_indices[q];
+                    float fx = px[i] - px[j], fy = py[i] - py[j], fz = pz[i] - pz[j];
+                    float r2f = fx * fx + fy * fy + fz * fz;
+                    if (!(r2f < h2f && r2f > 1e-12f)) continue;
+                    if (density[j] < 1e-6f) continue;
+                    double d[3] = {(double)px[i] - px[j], (double)py[i] - py[j],
+                                   (double)pz[i] - pz[j]};
+                    double r = sqrt(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+                    double rho_j = density[j], p_j = k * (rho_j - rho0);
+                    double diff = h - r;
+                    double fsc = -mass * (p_i + p_j) / (2.0 * rho_j) * (gcoef * diff * diff / r);
+                    double vsc = mu * mass / rho_j * (lcoef * diff);
+                    double dv[3] = {(double)vx[j] - vx[i], (double)vy[j] - vy[i],
+                                    (double)vz[j] - vz[i]};
+                    for (int c = 0; c < 3; c++) {
+                        double tp = fsc * d[c], tv = vsc * dv[c];
+                        a[c] += tp + tv;
+                        s[c] += fabs(tp) + fabs(tv);
                     }
-            for (int c = 0; c < 3; c++) {
-                a[c] /= rho_i;
-                s[c] /= rho_i;
+                }
             }
-        }
+    for (int c = 0; c < 3; c++) {
+        a[c] /= rho_i;
+        s[c] /= rho_i;
+    }
+}
+
+void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
+                      const float* pz, const float* vx, const float* vy, const float* vz,
+                      const float* density, uint32_t n, const uint32_t* cell_start,
+                      const uint32_t* sorted_indices, double* accel64, double* scale64) {
+    for (uint32_t i = 0; i < n; i++) {
+        double a[3], s[3];
+        force64_one(p, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices, i, a, s);
         for (int c = 0; c < 3; c++) {
             accel64[(size_t)c * n + i] = a[c];
             scale64[(size_t)c * n + i] = s[c];
+        }
+    }
+}
+
+void or_sph_force_f64_at(const or_sph_params* p, const float* px, const float* py,
+                         const float* pz, const float* vx, const float* vy, const float* vz,
+                         const float* density, const uint32_t* cell_start,
+                         const uint32_t* sorted_indices, const uint32_t* which, uint32_t m,
+                         double* accel64, double* scale64) {
+    for (uint32_t q = 0; q < m; q++) {
+        double a[3], s[3];
+        force64_one(p, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices, which[q], a,
+                    s);
+        for (int c = 0; c < 3; c++) {
+            accel64[(size_t)c * m + q] = a[c];
+            scale64[(size_t)c * m + q] = s[c];
         }
     }
 }

@@ -84,6 +84,13 @@ void or_sph_density(const or_sph_params* p, const float* px, const float* py, co
                     uint32_t n, const uint32_t* cell_start, const uint32_t* sorted_indices,
                     float* density);
 
+/* or_sph_density for the particles which[0..m) only: density[k] of particle which[k], the
+ * same per-particle sum in the same order (for workloads too large for the full pass). */
+void or_sph_density_at(const or_sph_params* p, const float* px, const float* py,
+                       const float* pz, const uint32_t* cell_start,
+                       const uint32_t* sorted_indices, const uint32_t* which, uint32_t m,
+                       float* density);
+
 /* Fused pressure + viscosity pass, per-pair maths of sph_fused.rs:542-638 over the true
  * 27-cell neighbourhood, every neighbour velocity read from the input state (vx..vz are not
  * modified).  Writes vout = v + a*dt (if non-NULL) and accel a = (a_p + a_v)/rho_i (if non-NULL),
@@ -100,6 +107,14 @@ void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
                       const float* pz, const float* vx, const float* vy, const float* vz,
                       const float* density, uint32_t n, const uint32_t* cell_start,
                       const uint32_t* sorted_indices, double* accel64, double* scale64);
+
+/* or_sph_force_f64 for the particles which[0..m) only: accel64 / scale64 as 3 arrays of m
+ * doubles, entry k for particle which[k]. */
+void or_sph_force_f64_at(const or_sph_params* p, const float* px, const float* py,
+                         const float* pz, const float* vx, const float* vy, const float* vz,
+                         const float* density, const uint32_t* cell_start,
+                         const uint32_t* sorted_indices, const uint32_t* which, uint32_t m,
+                         double* accel64, double* scale64);
 
 /* Unfused SphPressureModule kernel, sph_pressure.rs:28-112: for each particle i with
  * rho_i >= 1e-6, a_p over the 27-cell neighbourhood of the grid (cell_start, sorted_indices as

@@ -34,6 +34,9 @@ _SIG = {
     "or_query_neighbors": (_U, [_F, _F, _F, _F, _P, _P, _P, _U, _F, _P, _P, _P, _P, _P, _U]),
     "or_neighbor_counts": (None, [_P, _P, _P, _U, _U, _F, _P, _P, _P, _P, _F, _P, _P]),
     "or_sph_density": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _U, _P, _P, _P]),
+    "or_sph_density_at": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _U, _P]),
+    "or_sph_force_f64_at": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _P, _P, _U, _P, _P]),
     "or_sph_force": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P, _P,
                             _F, _P, _P]),
     "or_sph_force_f64": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
@@ -178,6 +181,29 @@ def sph_density(p: SphParams, x, y, z, cell_start, sorted_indices):
     rho = np.empty(x.size, np.float32)
     lib().or_sph_density(ctypes.byref(p), _p(x), _p(y), _p(z), x.size, _p(cs), _p(si), _p(rho))
     return rho
+
+
+def sph_density_at(p: SphParams, x, y, z, cell_start, sorted_indices, which):
+    """Densities of the particles `which` only (same sums as sph_density)."""
+    x, y, z = _f32(x), _f32(y), _f32(z)
+    cs, si, w = _u32(cell_start), _u32(sorted_indices), _u32(which)
+    rho = np.empty(w.size, np.float32)
+    lib().or_sph_density_at(ctypes.byref(p), _p(x), _p(y), _p(z), _p(cs), _p(si), _p(w), w.size,
+                            _p(rho))
+    return rho
+
+
+def sph_force_f64_at(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices,
+                     which):
+    """sph_force_f64 of the particles `which` only: (3, m) accelerations and error scales."""
+    arrs = [_f32(a) for a in (x, y, z, vx, vy, vz, density)]
+    cs, si, w = _u32(cell_start), _u32(sorted_indices), _u32(which)
+    m = w.size
+    a64 = np.empty(3 * m, np.float64)
+    s64 = np.empty(3 * m, np.float64)
+    lib().or_sph_force_f64_at(ctypes.byref(p), *[_p(a) for a in arrs], _p(cs), _p(si), _p(w), m,
+                              _p(a64), _p(s64))
+    return a64.reshape(3, m), s64.reshape(3, m)
 
 
 def sph_force(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices, dt):

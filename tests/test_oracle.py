@@ -293,6 +293,23 @@ def test_force_vs_brute_force_and_f64(oracle):
         assert np.all(np.abs(acc[:, i] - a64[:, i]) <= 1e-5 * s64[:, i] + 1e-12)
 
 
+def test_subset_passes_equal_the_full_passes(oracle):
+    """sph_density_at / sph_force_f64_at (used where the full pass is too slow, c4) give the
+    full passes' values for the listed particles, bit for bit, in any order, repeats included."""
+    rng = np.random.default_rng(15)
+    n = 3000
+    P = rng.uniform(0.3, 0.45, (n, 3)).astype(np.float32)
+    V = rng.uniform(-1, 1, (n, 3)).astype(np.float32)
+    p = prm(oracle)
+    st, si = grid(oracle, P[:, 0], P[:, 1], P[:, 2])
+    rho = oracle.sph_density(p, *P.T, st, si)
+    a64, s64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
+    which = np.concatenate([rng.permutation(n)[:400], [0, n - 1, 7, 7]]).astype(np.uint32)
+    assert np.array_equal(oracle.sph_density_at(p, *P.T, st, si, which), rho[which])
+    b64, t64 = oracle.sph_force_f64_at(p, *P.T, *V.T, rho, st, si, which)
+    assert np.array_equal(b64, a64[:, which]) and np.array_equal(t64, s64[:, which])
+
+
 def test_epilogue_closed_forms(oracle):
     vx, vy, vz = (np.array([1.0, np.nan, -2.0], np.float32), np.array([0.0, 1.0, np.inf], np.float32),
                   np.array([3.0, -1.0, 0.5], np.float32))
