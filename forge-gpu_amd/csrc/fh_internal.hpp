@@ -18,15 +18,24 @@ constexpr int kWave = 64;              // CDNA wavefront
 #ifndef FH_SORT_ITEMS
 #define FH_SORT_ITEMS 16
 #endif
+#ifndef FH_SORT_MINB
+#define FH_SORT_MINB 4  // sort workgroups per CU the register budget is sized for
+#endif
 constexpr int kSortThreads = FH_SORT_THREADS;  // 8 waves per sort workgroup
 constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kSortItems = FH_SORT_ITEMS;      // keys per thread per tile
 constexpr int kSortTile = kSortThreads * kSortItems;  // 8192 keys per tile
+constexpr int kSortItemsLarge = 24;                  // keys per thread from kSortLargeN keys on
+constexpr int kSortTileLarge = kSortThreads * kSortItemsLarge;
+constexpr uint32_t kSortLargeN = 1u << 22;
 constexpr int kMaxPasses = 4;          // 8-bit digits, up to 32-bit keys
 constexpr int kHistThreads = 256;
 constexpr int kHistItems = 16;
 constexpr int kHistChunk = kHistThreads * kHistItems;  // keys per histogram chunk
-constexpr int kHistBlocks = 1024;      // rows of per-block partial histograms
+#ifndef FH_HIST_BLOCKS
+#define FH_HIST_BLOCKS 1024
+#endif
+constexpr int kHistBlocks = FH_HIST_BLOCKS;  // rows of per-block partial histograms
 constexpr int kHistRowsPerReduce = 8;  // partial rows summed by one reduce workgroup
 constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
 // Co-located particles: when at least kCollapseMin particles of a cell sit at one position (the

@@ -145,14 +145,14 @@ __global__ __launch_bounds__(kHistThreads) void k_hist_keys(const uint32_t* __re
 #pragma unroll
     for (int j = 0; j < kHistItems; j++) {
         const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
-        cur[j] = (c < chunks && i < n) ? keys[i] : 0u;
+        cur[j] = keys[min(i, n - 1u)];  // n >= 2; loads past n are never counted
     }
     for (; c < chunks; c += gridDim.x) {
         const uint32_t cn = c + gridDim.x;
 #pragma unroll
         for (int j = 0; j < kHistItems; j++) {
             const uint32_t i = cn * kHistChunk + j * kHistThreads + threadIdx.x;
-            nxt[j] = (cn < chunks && i < n) ? keys[i] : 0u;
+            nxt[j] = keys[min(i, n - 1u)];
         }
         if ((c + 1u) * kHistChunk <= n) {  // workgroup-uniform
             count_chunk<P>(sh[wave], cur, (uint32_t)__popc(top));
@@ -394,33 +394,36 @@ __device__ __forceinline__ uint32_t item_load(const uint32_t* __restrict__ p, ui
     return (Full || idx < n) ? p[idx] : pad;
 }
 
-template <bool Full>
+template <bool Full, int Items>
 __device__ __forceinline__ void load_items(const uint32_t* __restrict__ p, uint32_t wbase,
                                            int lane, uint32_t n, uint32_t pad,
-                                           uint32_t (&v)[kSortItems]) {
+                                           uint32_t (&v)[Items]) {
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++)
+    for (int k = 0; k < Items; k++)
         v[k] = item_load<Full>(p, wbase + (uint32_t)(k * kWave + lane), n, pad);
 }
 
 // Values of the items: loaded, or the element indices when the input values are implicit.
-template <bool Full>
+template <bool Full, int Items>
 __device__ __forceinline__ void load_vals(const uint32_t* __restrict__ vin, uint32_t wbase,
-                                          int lane, uint32_t n, uint32_t (&v)[kSortItems]) {
+                                          int lane, uint32_t n, uint32_t (&v)[Items]) {
     if (vin) {
-        load_items<Full>(vin, wbase, lane, n, 0u, v);
+        load_items<Full, Items>(vin, wbase, lane, n, 0u, v);
     } else {
 #pragma unroll
-        for (int k = 0; k < kSortItems; k++) v[k] = wbase + (uint32_t)(k * kWave + lane);
+        for (int k = 0; k < Items; k++) v[k] = wbase + (uint32_t)(k * kWave + lane);
     }
 }
 
-__global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control* ctl,
-                                                              uint32_t pass,
-                                                              uint32_t* __restrict__ lookback,
-                                                              uint32_t n, uint32_t shift,
-                                                              uint32_t pbits) {
-    __shared__ uint32_t s_buf[kSortTile];
+// Items = keys per thread: a tile holds Items * kSortThreads keys (kSortItems for small sorts,
+// kSortItemsLarge from kSortLargeN keys on: longer per-digit runs in the scatter and half as
+// many look-back words per key, at two workgroups per CU).
+template <int Items>
+__global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB) void k_onesweep(
+    SortIO io, Control* ctl, uint32_t pass, uint32_t* __restrict__ lookback, uint32_t n,
+    uint32_t shift, uint32_t pbits) {
+    constexpr uint32_t kTile = (uint32_t)(Items * kSortThreads);
+    __shared__ uint32_t s_buf[kTile];
     __shared__ uint32_t s_wcnt[kSortWaves][256];  // per-wave digit counts, then wave offsets
     __shared__ uint32_t s_gbase[256];             // global index of tile slot 0 of digit d
     __shared__ uint32_t s_scan[kSortWaves];
@@ -436,21 +439,21 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_wcnt[0][0])[i] = 0u;
     __syncthreads();
     const uint32_t tile = s_tile;
-    const uint32_t tile_base = tile * (uint32_t)kSortTile;
-    const uint32_t wbase = tile_base + (uint32_t)wave * (kWave * kSortItems);
-    const bool full = n - tile_base >= (uint32_t)kSortTile;  // workgroup-uniform
+    const uint32_t tile_base = tile * kTile;
+    const uint32_t wbase = tile_base + (uint32_t)wave * (kWave * Items);
+    const bool full = n - tile_base >= kTile;  // workgroup-uniform
 
     // Striped key loads: item k of lane l is element wbase + 64k + l, so (k, l) order = input
     // order.  Slots past n hold digit `mask` and rank after every real key of the tile.
-    uint32_t keys[kSortItems], vals[kSortItems], pos[kSortItems];
-    if (full) load_items<true>(bf.kin, wbase, lane, n, 0xFFFFFFFFu, keys);
-    else load_items<false>(bf.kin, wbase, lane, n, 0xFFFFFFFFu, keys);
+    uint32_t keys[Items], vals[Items], pos[Items];
+    if (full) load_items<true, Items>(bf.kin, wbase, lane, n, 0xFFFFFFFFu, keys);
+    else load_items<false, Items>(bf.kin, wbase, lane, n, 0xFFFFFFFFu, keys);
     const uint32_t lt_lo = lane >= 32 ? 0xFFFFFFFFu : ((1u << lane) - 1u);
     const uint32_t lt_hi = lane <= 32 ? 0u : (0xFFFFFFFFu >> (64 - lane));
     const uint32_t gt_lo = lane >= 31 ? 0u : (0xFFFFFFFFu << (lane + 1));
     const uint32_t gt_hi = lane < 31 ? 0xFFFFFFFFu : (lane == 63 ? 0u : (0xFFFFFFFFu << (lane - 31)));
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
+    for (int k = 0; k < Items; k++) {
         const uint32_t d = (keys[k] >> shift) & mask;
         uint32_t lo, hi;
         match8(d, lo, hi);
@@ -495,16 +498,16 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     // barriers published the wave offsets) and issue the value loads, so both overlap the
     // look-back's wait for earlier tiles.
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
+    for (int k = 0; k < Items; k++) {
         pos[k] += s_wcnt[wave][(keys[k] >> shift) & mask];
         s_buf[pos[k]] = keys[k];
     }
-    if (full) load_vals<true>(bf.vin, wbase, lane, n, vals);
-    else load_vals<false>(bf.vin, wbase, lane, n, vals);
+    if (full) load_vals<true, Items>(bf.vin, wbase, lane, n, vals);
+    else load_vals<false, Items>(bf.vin, wbase, lane, n, vals);
     __syncthreads();
-    uint32_t skey[kSortItems];
+    uint32_t skey[Items];
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++) skey[k] = s_buf[k * kSortThreads + tid];
+    for (int k = 0; k < Items; k++) skey[k] = s_buf[k * kSortThreads + tid];
 
     uint32_t prefix = 0;
     if (tid < 256 && tile > 0) {
@@ -557,19 +560,19 @@ __global__ __launch_bounds__(kSortThreads, 4) void k_onesweep(SortIO io, Control
     // Scatter the keys (contiguous runs per digit), then the values through the same buffer.
     // dst < n holds whenever the histograms and look-back are consistent; the check keeps a
     // corrupted state (a spin limit hit) from writing out of bounds.
-    const uint32_t valid = full ? (uint32_t)kSortTile : n - tile_base;
-    uint32_t dst[kSortItems];
+    const uint32_t valid = full ? kTile : n - tile_base;
+    uint32_t dst[Items];
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
+    for (int k = 0; k < Items; k++) {
         const uint32_t i = (uint32_t)(k * kSortThreads + tid);
         dst[k] = s_gbase[(skey[k] >> shift) & mask] + i;
         if ((full || i < valid) && dst[k] < n && bf.kout) bf.kout[dst[k]] = skey[k];
     }
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++) s_buf[pos[k]] = vals[k];
+    for (int k = 0; k < Items; k++) s_buf[pos[k]] = vals[k];
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kSortItems; k++) {
+    for (int k = 0; k < Items; k++) {
         const uint32_t i = (uint32_t)(k * kSortThreads + tid);
         if ((full || i < valid) && dst[k] < n) bf.vout[dst[k]] = s_buf[i];
     }
@@ -587,7 +590,8 @@ __global__ __launch_bounds__(256) void k_sort_finish(SortIO io, const Control* c
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits) {
     const uint32_t passes = passes_for_bits(num_bits);
-    const uint32_t tiles = ceil_div(n, (uint32_t)kSortTile);
+    const bool large = n >= kSortLargeN;
+    const uint32_t tiles = ceil_div(n, (uint32_t)(large ? kSortTileLarge : kSortTile));
     const bool in_place = kfin != nullptr && kfin == k0;
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
@@ -599,7 +603,12 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
         const uint32_t pbits = min(8u, num_bits - 8u * p);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * 256u;
         tbeg(c, KID_SORT);
-        k_onesweep<<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb, n, 8u * p, pbits);
+        if (large)
+            k_onesweep<kSortItemsLarge><<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb,
+                                                                               n, 8u * p, pbits);
+        else
+            k_onesweep<kSortItems><<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb, n,
+                                                                          8u * p, pbits);
         tend(c, KID_SORT);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

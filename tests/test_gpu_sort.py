@@ -52,7 +52,8 @@ def test_radix_sort_xorshift_streams(fh, gpu_ctx, oracle, name):
 
 @pytest.mark.parametrize("n,bits", [(0, 8), (1, 32), (2, 1), (3, 5), (4095, 12), (4096, 16),
                                     (4097, 20), (65537, 8), (100_000, 7), (100_000, 32),
-                                    (1 << 20, 20), (1_000_003, 24), (2_500_000, 31)])
+                                    (1 << 20, 20), (1_000_003, 24), (2_500_000, 31),
+                                    (1 << 22, 32), (5_000_011, 19)])
 def test_sort_matches_oracle(fh, gpu_ctx, oracle, n, bits):
     rng = np.random.default_rng(n * 131 + bits)
     keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)  # high bits beyond num_bits too
@@ -101,7 +102,8 @@ def test_sort_skips_identity_passes(fh, gpu_ctx, oracle, case):
 def test_sort_back_to_back_sizes(fh, gpu_ctx, oracle):
     """Consecutive sorts of different sizes on one context (look-back words are re-zeroed)."""
     rng = np.random.default_rng(5)
-    for n, bits in [(1_000_000, 24), (10_000, 32), (300_000, 16), (8193, 9), (1_000_000, 24)]:
+    for n, bits in [(1_000_000, 24), (10_000, 32), (4_200_000, 32), (300_000, 16), (8193, 9),
+                    (4_194_304, 17), (1_000_000, 24)]:
         keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
         vals = np.arange(n, dtype=np.uint32)
         k, v = gpu_sort(fh, gpu_ctx, keys, vals, bits)
