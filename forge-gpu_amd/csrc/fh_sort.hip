@@ -385,7 +385,10 @@ __device__ __forceinline__ void match8(uint32_t d, uint32_t& lo, uint32_t& hi) {
     }
 }
 
-constexpr int kLbWin = 4;  // look-back words loaded per round trip
+#ifndef FH_LB_WIN
+#define FH_LB_WIN 4
+#endif
+constexpr int kLbWin = FH_LB_WIN;  // look-back words loaded per round trip
 
 // Load of item k of this lane (element wbase + 64k + lane): unchecked in full tiles.
 template <bool Full>

@@ -120,22 +120,22 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
     for (; j + 4 <= je; j += 4) {
         const float4 q0 = sp[j - c0], q1 = sp[j + 1 - c0], q2 = sp[j + 2 - c0], q3 = sp[j + 3 - c0];
         float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
-        float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a0 = fmaf(d * d, d, a0);
         dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
-        d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a1 = fmaf(d * d, d, a1);
         dx = pi.x - q2.x; dy = pi.y - q2.y; dz = pi.z - q2.z;
-        d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a2 = fmaf(d * d, d, a2);
         dx = pi.x - q3.x; dy = pi.y - q3.y; dz = pi.z - q3.z;
-        d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a3 = fmaf(d * d, d, a3);
     }
     for (; j < je; j++) {
         const float4 q = sp[j - c0];
         const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
-        const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        const float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a0 = fmaf(d * d, d, a0);
     }
     return acc + ((a0 + a1) + (a2 + a3));
@@ -352,16 +352,16 @@ __device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, ui
     for (; j + 2 <= je; j += 2) {
         const float4 q0 = sp[j - c0], q1 = sp[j + 1 - c0];
         float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
-        float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a0 = fmaf(q0.w * d, d * d, a0);
         dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
-        d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a1 = fmaf(q1.w * d, d * d, a1);
     }
     if (j < je) {
         const float4 q = sp[j - c0];
         const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
-        const float d = fmaxf(h2 - fmaf(dz, dz, fmaf(dy, dy, dx * dx)), 0.0f);
+        const float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a0 = fmaf(q.w * d, d * d, a0);
     }
     return acc + (a0 + a1);
@@ -850,6 +850,7 @@ struct FastForce {
     float h, h2, mc, k, rho0;
     float fp;  // -mass * gcoef / 2: pressure pair term = fp*(p_i+p_j)/rho_j*(h-r)^2/r * (x_i-x_j)
     float fv;  // mu * mass * lcoef: viscosity pair term = fv/rho_j*(h-r) * (v_j-v_i)
+    float fr;  // fv / fp (0 when fp = 0, i.e. mass = 0, where fv = 0 as well)
 };
 
 __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_t stride,
@@ -858,11 +859,13 @@ __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_
 }
 
 // Force records, made once per substep after the density pass (k_prep), one pair per sorted
-// particle j: rec[j] = (x, y, z, p_j) and rec[stride + j] = (u / rho_j, w / rho_j), where w is
-// the candidate weight (1; M for the representative of a co-located group; 0 for the other
-// members, which the representative stands for) and u = w v_j (the group's summed velocity for
-// a representative).  1/rho_j is taken as 0 when rho_j < 1e-6, which removes the pair like the
-// skip of sph_fused.rs:607.  A non-finite position is recorded far away (1e30), so no pair
+// particle j: rec[j] = (x, y, z, A_j p_j) and rec[stride + j] = (fv u / rho_j, A_j) with
+// A_j = fp w / rho_j, where w is the candidate weight (1; M for the representative of a
+// co-located group; 0 for the other members, which the representative stands for) and u = w v_j
+// (the group's summed velocity for a representative).  The pressure factor of a pair is then
+// one fused multiply-add, p_i A_j + A_j p_j = fp (p_i + p_j) w / rho_j, and the constants fp and
+// fv are folded in once per particle instead of once per pair.  1/rho_j is taken as 0 when
+// rho_j < 1e-6, which removes the pair like the skip of sph_fused.rs:607.  A non-finite position is recorded far away (1e30), so no pair
 // with it passes the distance test and the branch-free pair loop never multiplies by NaN.
 // srho[j] = rho_j; members take their representative's density (they sit at its position).
 // The force kernels then only copy records into LDS.
@@ -871,7 +874,7 @@ __global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
                                               const float4* __restrict__ vrep,
                                               const float* __restrict__ dpart, uint32_t n,
                                               uint32_t stride, float mc, float k, float rho0,
-                                              float* __restrict__ srho,
+                                              float fp, float fv, float* __restrict__ srho,
                                               float4* __restrict__ rec) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
@@ -892,28 +895,29 @@ __global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
     const float inv = rho < 1e-6f ? 0.0f : 1.0f / rho;
     srho[s] = rho;
     const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z);
-    rec[s] = fin ? make_float4(p.x, p.y, p.z, k * (rho - rho0))
+    const float A = fp * (wt * inv), vi = fv * inv;
+    rec[s] = fin ? make_float4(p.x, p.y, p.z, A * (k * (rho - rho0)))
                  : make_float4(1e30f, 1e30f, 1e30f, 0.0f);
-    rec[stride + s] = make_float4(u.x * inv, u.y * inv, u.z * inv, wt * inv);
+    rec[stride + s] = make_float4(u.x * vi, u.y * vi, u.z * vi, A);
 }
 
-// Pressure + viscosity pair terms of one lane over [jb, je) of staged records:
-// per candidate  fp (p_i + p_j) (w/rho_j) (h - r)^2 / r (x_i - x_j) + fv (h - r) (u/rho_j),
-// and wv += fv (h - r) (w/rho_j), the weight of -v_i in the viscosity sum (applied once by the
-// caller).  Branch-free: the pair test selects the two scale factors, so the loads of the next
-// candidates issue ahead of the arithmetic; staged positions are finite (k_prep), so a zero
-// scale never meets a NaN.
+// Pressure + viscosity pair terms of one lane over [jb, je) of staged records (k_prep):
+// per candidate  (p_i A_j + A_j p_j) (h - r)^2 / r (x_i - x_j) + (h - r) (fv u_j / rho_j), and
+// wa += (h - r) A_j; the weight of -v_i in the viscosity sum is fr * wa (applied once by the
+// caller).  Branch-free: the pair test selects the scale factors, so the loads of the next
+// candidates issue ahead of the arithmetic; staged positions are finite (k_prep) and the
+// pressure factor is selected after its product, so a non-pair (r = 0 included) adds exact zeros.
 __device__ __forceinline__ void force_pair(const float4& q, const float4& w, const float4& pi,
                                            float p_i, const FastForce& K, float& ax, float& ay,
-                                           float& az, float& wv) {
+                                           float& az, float& wa) {
     const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
     const float r2 = fmaf(dz, dz, fmaf(dy, dy, dx * dx));
     const bool ok = r2 < K.h2 && r2 > 1e-12f;
     const float rinv = __builtin_amdgcn_rsqf(r2);
     const float diff = fmaf(-r2, rinv, K.h);
-    const float fs = ok ? K.fp * (p_i + q.w) * w.w * (diff * diff) * rinv : 0.0f;
-    const float vs = ok ? K.fv * diff : 0.0f;
-    wv = fmaf(vs, w.w, wv);
+    const float fs = ok ? (fmaf(p_i, w.w, q.w) * diff) * (diff * rinv) : 0.0f;
+    const float vs = ok ? diff : 0.0f;
+    wa = fmaf(vs, w.w, wa);
     ax = fmaf(vs, w.x, fmaf(fs, dx, ax));
     ay = fmaf(vs, w.y, fmaf(fs, dy, ay));
     az = fmaf(vs, w.z, fmaf(fs, dz, az));
@@ -1001,6 +1005,7 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         }
     }
     if (in) {
+        wv *= K.fr;
         float* o = fpart + (size_t)slab * 3u * stride;
         o[s] = fmaf(-wv, vi.x, ax);
         o[stride + s] = fmaf(-wv, vi.y, ay);
@@ -1080,6 +1085,7 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
             }
         }
         // the -wv v_i part of the viscosity sum (wave partials add linearly)
+        wv *= K.fr;
         const float4 vi = load_or(svel, s, in, z4);
         s_acc[0][wave][lane] = fmaf(-wv, vi.x, ax);
         s_acc[1][wave][lane] = fmaf(-wv, vi.y, ay);
@@ -1295,16 +1301,7 @@ hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
     return e;
 }
 
-hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
-    if (a.n == 0) return hipSuccess;
-    k_prep<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
-                                                       c->max_n, poly6_mc(a.h, a.mass), a.k,
-                                                       a.rho0, c->srho, c->sout);
-    return hipGetLastError();
-}
-
-hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
-    if (a.n == 0) return hipSuccess;
+static FastForce fast_force(const SphArgs& a) {
     FastForce K;
     K.h = a.h;
     K.h2 = a.h * a.h;
@@ -1316,6 +1313,22 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     const float lcoef = 45.0f / (3.14159265f * h6);   // sph_fused.rs:555
     K.fp = -a.mass * gcoef * 0.5f;
     K.fv = a.mu * a.mass * lcoef;
+    K.fr = K.fp != 0.0f ? K.fv / K.fp : 0.0f;
+    return K;
+}
+
+hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
+    if (a.n == 0) return hipSuccess;
+    const FastForce K = fast_force(a);
+    k_prep<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
+                                                       c->max_n, K.mc, a.k, a.rho0, K.fp, K.fv,
+                                                       c->srho, c->sout);
+    return hipGetLastError();
+}
+
+hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
+    if (a.n == 0) return hipSuccess;
+    const FastForce K = fast_force(a);
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
     hipError_t e = fork_side(c);
