@@ -131,6 +131,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     c->device = device;
     c->max_n = max_n;
     c->max_cells = max_cells;
+    c->direct_mode = 1u;
     c->max_sort_tiles = ceil_div(max_n, (uint32_t)kSortTile);
     c->max_scan_tiles = ceil_div(max_cells, (uint32_t)kScanTile);
     size_t tot = 0;
@@ -456,6 +457,11 @@ int fh_set_option(fh_ctx* c, int option, int value) {
         case FH_OPT_HEAVY_WORK:
             if (value < 0) return fail(FH_EINVAL, "fh_set_option: heavy work %d < 0", value);
             c->heavy_work = (uint32_t)value;
+            return FH_OK;
+        case FH_OPT_DIRECT_ITEMS:
+            if (value < 0 || value > 2)
+                return fail(FH_EINVAL, "fh_set_option: direct items mode %d outside 0..2", value);
+            c->direct_mode = (uint32_t)value;
             return FH_OK;
         default:
             return fail(FH_EINVAL, "fh_set_option: unknown option %d", option);

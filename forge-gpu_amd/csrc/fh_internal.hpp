@@ -156,6 +156,7 @@ struct fh_ctx {
                          // order: pairs (x, y, z, rho), (vx, vy, vz, .), then (ax, ay, az, .)
     bool sph_exact;      // FH_OPT_SPH_EXACT
     uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
+    uint32_t direct_mode; // FH_OPT_DIRECT_ITEMS: 0 never, 1 automatic (default), 2 always
     uint32_t* h_error;   // pinned host word for the device error flag
     size_t scratch_bytes;
     hipGraph_t graph;

@@ -99,6 +99,18 @@ constexpr int kHeavyWaves = FH_HW;      // waves per heavy workgroup (one item a
 constexpr int kHeavyThreads = kHeavyWaves * kWave;
 constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
 constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
+constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transposed
+// Item flags (k_plan): light (one wavefront), heavy (heavy list), every particle co-located
+// (skipped by both passes).
+constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
+// Transposed heavy items: the particles' candidate ranges overlap little (sparse particles
+// spread along a row beside a dense one), so the union of a segment's ranges -- what the shared
+// walk stages and every lane steps through -- is many times longer than any one particle's
+// range.  The item is walked the other way round: one particle at a time, its candidates spread
+// over the 64 lanes (coalesced loads), a wave reduction per particle.  Chosen when the stream
+// is longer than kTransRatio times the largest particle's candidate count plus kTransOffset
+// (below that the per-particle reductions cost more than the idle lanes).
+constexpr uint32_t kTransRatio = 2, kTransOffset = 512;
 #ifndef FH_HGRID
 #define FH_HGRID 1024
 #endif
@@ -367,6 +379,107 @@ __device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, ui
     return acc + (a0 + a1);
 }
 
+__device__ __forceinline__ uint32_t pick3(const uint32_t v[3], int r) {
+    return r == 0 ? v[0] : (r == 1 ? v[1] : v[2]);
+}
+
+// Home-row segments.  A wave owns 64 consecutive sorted particles (a sub-tile); the particles of
+// one home row (cy, cz) are consecutive lanes, and for each of the slab's 3 rows the union of
+// their neighbour ranges is one contiguous range (x-adjacent cells of that row only): from the
+// first lane's begin to the last lane's end.
+__device__ __forceinline__ uint32_t home_row(const float4& p, const GridDesc& g) {
+    return cell_coord(p.y, 0.0f, g.cs, g.ny) + cell_coord(p.z, 0.0f, g.cs, g.nz) * g.ny;
+}
+
+// Length of the wave's candidate stream for one slab (the sum over home-row segments of the
+// unions of their rows, as laid out by light_stream).
+__device__ __forceinline__ uint32_t stream_total(const uint32_t b[3], const uint32_t e[3],
+                                                 uint32_t hr, bool in, int lane) {
+    const uint32_t hnext = (uint32_t)__shfl_down((int)hr, 1u, kWave);
+    const bool innext = __shfl_down((int)in, 1u, kWave) != 0 && lane < 63;
+    const uint32_t hprev = (uint32_t)__shfl_up((int)hr, 1u, kWave);
+    const uint64_t starts = __ballot(in && (lane == 0 || hprev != hr));
+    const bool last = in && !(innext && hnext == hr);
+    // the leader's begins, read by the segment's last lane
+    const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+    const uint64_t before = starts & upto;
+    const int leader = before ? 63 - __clzll((long long)before) : 0;
+    uint32_t len = 0;
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const uint32_t lo = (uint32_t)__shfl((int)b[r], leader, kWave);
+        len += last ? e[r] - lo : 0u;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) len += (uint32_t)__shfl_xor((int)len, off, kWave);
+    return len;
+}
+
+// A member of a co-located group other than its representative (spos.w bits of sorted slot j).
+__device__ __forceinline__ bool is_member(uint32_t bits, uint32_t j) {
+    return !(bits & kRepFlag) && bits != j;
+}
+
+// Lanes w, w + HW, w + 2 HW, ... of a wave (the particles wave w takes in a transposed walk).
+__device__ __forceinline__ uint64_t trans_lanes(int wave, int hw) {
+    uint64_t m = 0;
+    for (int l = wave; l < kWave; l += hw) m |= 1ull << l;
+    return m;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Next chunk start of a transposed walk: j0 + 64, or past a co-located group whose
+// representative (spos.w = kRepFlag | M) is in this chunk and whose members run beyond it.
+__device__ __forceinline__ uint32_t trans_next(uint32_t j0, uint32_t j, bool ok, uint32_t wb) {
+    const bool rep = ok && (wb & kRepFlag);
+    uint32_t nx = j0 + (uint32_t)kWave;
+    if (__ballot(rep) != 0ull) nx = max(nx, wave_max(rep ? j + (wb & ~kRepFlag) : 0u));
+    return nx;
+}
+
+// Transposed density walk of the item's particles taken by this wave: returns, in the lane of
+// each such particle, its density partial (sum of w (h^2 - r^2)^3; weights from spos.w).
+__device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
+                                               const uint32_t b[3], const uint32_t e[3],
+                                               const float4& pi, bool mine, float h2,
+                                               uint64_t lanes, int lane) {
+    float out = 0.0f;
+    uint64_t todo = __ballot(mine) & lanes;
+    while (todo) {  // uniform
+        const int l = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1ull;
+        const float px = __shfl(pi.x, l, kWave), py = __shfl(pi.y, l, kWave),
+                    pz = __shfl(pi.z, l, kWave);
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const uint32_t bb = (uint32_t)__shfl((int)b[r], l, kWave);
+            const uint32_t ee = (uint32_t)__shfl((int)e[r], l, kWave);
+            for (uint32_t j0 = bb; j0 < ee;) {  // uniform
+                const uint32_t j = j0 + (uint32_t)lane;
+                const bool ok = j < ee;
+                const float4 q = spos[ok ? j : j0];
+                const uint32_t wb = __float_as_uint(q.w);
+                const float c = ok ? ((wb & kRepFlag) ? (float)(wb & ~kRepFlag)
+                                                      : (wb == j ? 1.0f : 0.0f))
+                                   : 0.0f;
+                const float dx = px - q.x, dy = py - q.y, dz = pz - q.z;
+                const float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+                acc = fmaf(c * d, d * d, acc);
+                j0 = trans_next(j0, j, ok, wb);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == l) out = acc;
+    }
+    return out;
+}
+
 // Plan.  First the co-located groups (k_group): particles f+1 .. f+M-1 of a grouped cell are
 // tagged in spos[s].w with their representative f (which gets kRepFlag and appends the group
 // to the collapsed list).  A sub-tile made only of such non-representative particles is
@@ -382,7 +495,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
                                                        uint32_t* __restrict__ heavy,
                                                        uint32_t heavy_cap,
                                                        uint2* __restrict__ collapsed, uint32_t cap,
-                                                       uint32_t heavy_work, Control* ctl) {
+                                                       uint32_t heavy_work, uint32_t direct_mode,
+                                                       Control* ctl) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
     __shared__ uint32_t s_count[kWaves];
@@ -412,7 +526,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
         }
         if (__ballot(live && !member) == 0ull) {  // every particle of the sub-tile is co-located
             if (lane == 0)
-                for (int slab = 0; slab < 3; slab++) flag[sub * 3u + (uint32_t)slab] = 2;
+                for (int slab = 0; slab < 3; slab++) flag[sub * 3u + (uint32_t)slab] = kItemSkip;
         } else {
             const uint32_t epoch = ctl->epoch;
             for (int slab = 0; slab < 3; slab++) {
@@ -426,11 +540,19 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
                 }
                 const uint32_t w = wave_max(cand);
                 const bool touches = __ballot(excess > 0u) != 0ull;
-                const bool hv = w > heavy_work || touches;  // light items hold no group
+                bool hv = w > heavy_work || touches;  // light items hold no group
+                bool trans = direct_mode == 2u;
+                if (direct_mode == 1u && hv) {
+                    const uint32_t T = stream_total(b, e, home_row(pi, g), live, lane);
+                    trans = T > kTransRatio * w + kTransOffset;
+                }
+                hv = hv || trans;
                 if (lane == 0) {
                     const uint32_t item = sub * 3u + (uint32_t)slab;
-                    flag[item] = hv ? 1 : 0;
-                    if (hv) s_item[wave * 3 + (int)nh] = item | (touches ? kCutFlag : 0u);
+                    flag[item] = hv ? kItemHeavy : kItemLight;
+                    if (hv)
+                        s_item[wave * 3 + (int)nh] =
+                            item | (touches ? kCutFlag : 0u) | (trans ? kTransFlag : 0u);
                 }
                 nh += hv ? 1u : 0u;
             }
@@ -489,23 +611,11 @@ __device__ __forceinline__ float4 chunk_load(const float4* __restrict__ spos, ui
     return (uint32_t)lane < m ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-__device__ __forceinline__ uint32_t pick3(const uint32_t v[3], int r) {
-    return r == 0 ? v[0] : (r == 1 ? v[1] : v[2]);
-}
-
 // Next non-empty row after r (3 if none) of a segment whose row r spans [lo[r], hi[r]).
 __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[3], int r) {
     for (r = r + 1; r < 3; r++)
         if (pick3(lo, r) < pick3(hi, r)) break;
     return r;
-}
-
-// Home-row segments.  A wave owns 64 consecutive sorted particles (a sub-tile); the particles of
-// one home row (cy, cz) are consecutive lanes, and for each of the slab's 3 rows the union of
-// their neighbour ranges is one contiguous range (x-adjacent cells of that row only): from the
-// first lane's begin to the last lane's end.
-__device__ __forceinline__ uint32_t home_row(const float4& p, const GridDesc& g) {
-    return cell_coord(p.y, 0.0f, g.cs, g.ny) + cell_coord(p.z, 0.0f, g.cs, g.nz) * g.ny;
 }
 
 // Light items.  The candidates of a wave are laid out as one stream: for each home-row segment
@@ -602,7 +712,7 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     __shared__ float4 s_p[kTileP / kWave][kWin];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
-    if (item >= items || flag[item]) return;  // whole wave
+    if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
@@ -788,7 +898,8 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
         const uint32_t entry = heavy_entry(heavy, ctl, heavy_cap, it);
         const bool cut = (entry & kCutFlag) != 0u;  // the item touches a co-located group
-        const uint32_t item = entry & ~kCutFlag;
+        const bool trans = (entry & kTransFlag) != 0u;
+        const uint32_t item = entry & ~(kCutFlag | kTransFlag);
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool live = s < n;
@@ -797,7 +908,10 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
         slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
         const uint32_t hr = home_row(pi, g);
         float acc = 0.0f;
-        uint64_t pending = __ballot(live);
+        if (trans)  // members take their representative's density
+            acc = density_trans(spos, b, e, pi, live && !is_member(__float_as_uint(pi.w), s),
+                                h2, trans_lanes(wave, HW), lane);
+        uint64_t pending = trans ? 0ull : __ballot(live);
         while (pending) {  // uniform, identical in every wave
             const int leader = __ffsll((unsigned long long)pending) - 1;
             const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
@@ -946,6 +1060,53 @@ __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
     for (; j < je; j++) force_pair(sp[j - c0], sv[j - c0], pi, p_i, K, ax, ay, az, wv);
 }
 
+// Transposed force walk of the item's particles taken by this wave: in the lane of each such
+// particle, its acceleration partial (a_x, a_y, a_z) and viscosity weight sum wa (force_pair).
+__device__ __forceinline__ void force_trans(const float4* __restrict__ rec,
+                                            const float4* __restrict__ spos, uint32_t stride,
+                                            const uint32_t b[3], const uint32_t e[3],
+                                            const float4& pi, float p_i, bool mine,
+                                            const FastForce& K, uint64_t lanes, int lane,
+                                            float& oax, float& oay, float& oaz, float& owa) {
+    uint64_t todo = __ballot(mine) & lanes;
+    while (todo) {  // uniform
+        const int l = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1ull;
+        const float4 pl = make_float4(__shfl(pi.x, l, kWave), __shfl(pi.y, l, kWave),
+                                      __shfl(pi.z, l, kWave), 0.0f);
+        const float pp = __shfl(p_i, l, kWave);
+        float ax = 0.0f, ay = 0.0f, az = 0.0f, wa = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const uint32_t bb = (uint32_t)__shfl((int)b[r], l, kWave);
+            const uint32_t ee = (uint32_t)__shfl((int)e[r], l, kWave);
+            for (uint32_t j0 = bb; j0 < ee;) {  // uniform
+                const uint32_t j = j0 + (uint32_t)lane;
+                const bool ok = j < ee;
+                const uint32_t jj = ok ? j : j0;
+                float4 q = rec[jj], w = rec[stride + jj];
+                const uint32_t wb = __float_as_uint(spos[jj].w);
+                if (!ok) {  // adds zeros
+                    q.w = 0.0f;
+                    w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+                force_pair(q, w, pl, pp, K, ax, ay, az, wa);
+                j0 = trans_next(j0, j, ok, wb);
+            }
+        }
+        ax = wave_sum(ax);
+        ay = wave_sum(ay);
+        az = wave_sum(az);
+        wa = wave_sum(wa);
+        if (lane == l) {
+            oax = ax;
+            oay = ay;
+            oaz = az;
+            owa = wa;
+        }
+    }
+}
+
 // Acceleration partials: fpart[slab][c][s] = sum over the slab's neighbours j of the pressure
 // and viscosity pair terms (sph_fused.rs:604-623), not yet divided by rho_i.  Same windowed
 // stream as k_density_wave; the window is staged by copying force records (k_prep).
@@ -962,7 +1123,7 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     __shared__ float4 s_v[kTileP / kWave][kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
-    if (item >= items || flag[item]) return;  // whole wave; heavy items: k_force_heavy
+    if (item >= items || flag[item] != kItemLight) return;  // whole wave; heavy: k_force_heavy
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
@@ -1031,7 +1192,8 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
     for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
         const uint32_t entry = heavy_entry(heavy, ctl, heavy_cap, it);
         const bool cut = (entry & kCutFlag) != 0u;
-        const uint32_t item = entry & ~kCutFlag;
+        const bool trans = (entry & kTransFlag) != 0u;
+        const uint32_t item = entry & ~(kCutFlag | kTransFlag);
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool in = s < n;
@@ -1043,7 +1205,11 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
         slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
         const uint32_t hr = home_row(pi, g);
         float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
-        uint64_t pending = __ballot(live);
+        if (trans)  // members are finished from their representative
+            force_trans(rec, spos, stride, b, e, pi, p_i,
+                        live && !is_member(__float_as_uint(pi.w), s), K, trans_lanes(wave, HW),
+                        lane, ax, ay, az, wv);
+        uint64_t pending = trans ? 0ull : __ballot(live);
         while (pending) {  // uniform, identical in every wave
             const int leader = __ffsll((unsigned long long)pending) - 1;
             const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
@@ -1246,6 +1412,7 @@ hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) 
     k_plan<<<ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0, c->stream>>>(
         c->spos, a.n, a.g, cell_start, c->cell_grp, c->heavy_flag, c->heavy, c->heavy_cap,
         c->collapsed, ceil_div(c->max_n, 64u) + 1u, c->heavy_work ? c->heavy_work : kHeavyWork,
+        c->direct_mode,
         c->ctl);
     tend(c, KID_PLAN);
     return hipGetLastError();

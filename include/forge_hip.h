@@ -215,6 +215,12 @@ int fh_sph_fused(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, 
  * by a 1024-lane workgroup instead of one wavefront; value 0 restores the default (384).
  * Results differ only by rounding. */
 #define FH_OPT_HEAVY_WORK 2
+/* FH_OPT_DIRECT_ITEMS = 3: items whose particles' candidate ranges barely overlap (sparse
+ * particles along a row, or beside a dense one) are walked by each lane on its own, reading
+ * candidates straight from memory, instead of through a shared LDS-staged stream.  0: never,
+ * 1: chosen per item from the stream and per-particle lengths (default), 2: every item.
+ * Results differ only by rounding. */
+#define FH_OPT_DIRECT_ITEMS 3
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
 /* GravityModule (gravity.rs:31-34): v += g * dt. */

@@ -50,10 +50,12 @@ def rel_err(a, b):
 
 def set_mode(fh, f, cfg, mode):
     """fast: default work split; heavy: every (sub-tile, slab) item through the 1024-lane
-    kernels; light: none of them (one wavefront per item); exact: the bit-exact passes."""
+    kernels; light: none of them (one wavefront per item, shared stream); direct: every item
+    walked lane by lane; exact: the bit-exact passes."""
     ctx = f.context(cfg.num_cells)
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, {"heavy": 1, "light": 1 << 30}.get(mode, 0))
+    ctx.set_option(fh.FH_OPT_DIRECT_ITEMS, {"heavy": 0, "light": 0, "direct": 2}.get(mode, 1))
 
 
 def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast"):
@@ -110,7 +112,7 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "light", "direct"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
     from forge_hip import workloads
@@ -130,7 +132,7 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "light"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "light", "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
@@ -178,7 +180,7 @@ def colocated_cfg(n=40_000, seed=33):
     return cfg, vel
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "light"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "light", "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
