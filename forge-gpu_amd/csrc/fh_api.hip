@@ -87,17 +87,18 @@ hipError_t alloc(T** p, size_t count, size_t* total) {
 }
 
 // Rebuild of the SPH grid from the positions: hash + digit histograms, the stable sort giving
-// skeys / sidx (ascending id within a cell), the gather into sorted float4 order (which also
-// tags the key runs), and the CSR cell_start scan.
+// skeys / sidx (ascending id within a cell) and rank (its inverse), the gather into sorted
+// float4 order, and the CSR cell_start from the sorted keys (with the candidate co-located
+// groups of the fast passes).
 hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
                        const float* py, const float* pz, const float* vx, const float* vy,
                        const float* vz, uint32_t n, bool with_vel) {
     const uint32_t bits = bits_for_cells(cells);
     hipError_t e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr, true);
     if (e == hipSuccess && n > 0)
-        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits);
-    if (e == hipSuccess) e = launch_gather(c, px, py, pz, vx, vy, vz, n, with_vel);
-    if (e == hipSuccess) e = launch_scan_starts(c, cells, n, c->cell_start);
+        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits, c->rank);
+    if (e == hipSuccess)
+        e = launch_gather(c, g, cells, px, py, pz, vx, vy, vz, n, with_vel, !c->sph_exact);
     return e;
 }
 
@@ -272,7 +273,7 @@ int fh_sort_pairs(fh_ctx* c, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_
     if ((rc = check_n(c, n, "fh_sort_pairs"))) return rc;
     if (n < 2) return FH_OK;
     FH_CHECK_HIP(launch_hist_keys(c, keys, n, num_bits, true));
-    // In place: the last pass that runs writes the caller's buffers (see k_sort_plan).
+    // In place: the last pass that runs writes the caller's buffers (see sort_plan).
     FH_CHECK_HIP(launch_sort_passes(c, keys, vals, keys, vals, n, num_bits));
     return FH_OK;
 }

@@ -82,7 +82,7 @@ struct Line {
 };
 struct Control {
     uint32_t epoch;                     // bumped by k_begin before each sort / scan
-    uint32_t plan;                      // bit p: sort pass p runs (k_sort_plan)
+    uint32_t plan;                      // bit p: sort pass p runs (written by pass 0)
     uint32_t pad0[30];
     Line error;                         // nonzero: a look-back spin limit was hit
     Line tile_ctr[kMaxPasses];          // dynamic tile ids of the sort passes
@@ -267,7 +267,8 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
 // returns hipErrorInvalidValue.  Passes whose digit is the same for every key are skipped on
 // the device; the others ping-pong through the context's scratch.
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
-                              uint32_t* vfin, uint32_t n, uint32_t num_bits);
+                              uint32_t* vfin, uint32_t n, uint32_t num_bits,
+                              uint32_t* rank = nullptr);
 // Mark the first index of every run of equal sorted keys in c->run_tag (epoch-tagged).
 hipError_t launch_runs(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n);
 // CSR cell_start[0..C] from the run tags: cell_start[c] = first sorted index with key >= c
@@ -292,9 +293,9 @@ struct SphArgs {
     uint32_t n;
 };
 // Gather positions (and velocities) into sorted float4 order and mark the key runs.
-hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const float* pz,
-                         const float* vx, const float* vy, const float* vz, uint32_t n,
-                         bool with_vel);
+hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
+                         const float* py, const float* pz, const float* vx, const float* vy,
+                         const float* vz, uint32_t n, bool with_vel, bool list_big);
 hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);

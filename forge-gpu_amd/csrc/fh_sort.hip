@@ -8,8 +8,8 @@
 //   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
 //                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
 //   k_hist_reduce  sums the partial rows into the histograms
-//   k_sort_plan    decides which passes run (a pass whose digit is equal for every key is the
-//                  identity and is skipped)
+//   sort_plan      (in every pass) decides which passes run (a pass whose digit is equal for
+//                  every key is the identity and is skipped)
 //   k_onesweep     one kernel per 8-bit pass: an 8192-key tile per 512-lane workgroup, ranked
 //                  with 64-lane ballot match-any, digit offsets from a decoupled look-back over
 //                  dynamically numbered tiles, then staged in LDS in digit order (keys, then
@@ -233,33 +233,30 @@ __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict_
     if (s) atomicAdd(&ctl->hist[p][d], s);
 }
 
-// The passes that run (ctl->plan, one bit per pass).  A pass whose digit is equal for every key
-// (one histogram bin holds all n keys) is the identity and is skipped.  Two adjustments leave
-// the result in (kfin, vfin) without a copy kernel: when no pass moves keys and the sort is out
-// of place, pass 0 runs (a stable copy: its digit is constant); when exactly one pass moves keys
-// in place (it has to write scratch) and the sort has another pass, that pass runs as well
-// (also a copy), so the second of the two writes back in place.  Only one-pass sorts in place
-// keep k_sort_finish.  One workgroup of 256 threads (one bin each).
-__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t n, uint32_t in_place,
-                                                   Control* ctl) {
-    __shared__ uint32_t s_tw[4];
+// The passes that run (one bit per pass), derived from the digit histograms by every workgroup
+// of every pass (the same function of the same data, so all agree).  A pass whose digit is
+// equal for every key (one histogram bin holds all n keys) is the identity and is skipped.  Two
+// adjustments leave the result in (kfin, vfin) without a copy kernel: when no pass moves keys
+// and the sort is out of place, pass 0 runs (a stable copy: its digit is constant); when exactly
+// one pass moves keys in place (it has to write scratch) and the sort has another pass, that
+// pass runs as well (also a copy), so the second of the two writes back in place.  Only
+// one-pass sorts in place keep k_sort_finish (which reads ctl->plan, written by pass 0).
+// Threads 0..255 (one bin each) test the bins; s_triv collects the trivial passes.
+__device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, uint32_t passes,
+                                              uint32_t n, bool in_place, uint32_t* s_triv) {
     const uint32_t d = threadIdx.x;
-    uint32_t triv = 0;
-    for (uint32_t q = 0; q < passes; q++)
-        if (__ballot(ctl->hist[q][d] == n) != 0ull) triv |= 1u << q;
-    if ((d & 63u) == 0u) s_tw[d >> 6] = triv;
+    if (d < 256u)
+        for (uint32_t q = 0; q < passes; q++)
+            if (ctl->hist[q][d] == n) atomicOr(s_triv, 1u << q);
     __syncthreads();
-    if (d == 0) {
-        triv = s_tw[0] | s_tw[1] | s_tw[2] | s_tw[3];
-        uint32_t plan = ~triv & ((1u << passes) - 1u);
-        if (plan == 0u && !in_place) {
-            plan = 1u;
-        } else if (__popc(plan) == 1 && in_place && passes >= 2u) {
-            const uint32_t p = (uint32_t)(__ffs(plan) - 1);
-            plan |= 1u << (p > 0u ? p - 1u : 1u);
-        }
-        ctl->plan = plan;
+    uint32_t plan = ~*s_triv & ((1u << passes) - 1u);
+    if (plan == 0u && !in_place) {
+        plan = 1u;
+    } else if (__popc(plan) == 1 && in_place && passes >= 2u) {
+        const uint32_t p = (uint32_t)(__ffs(plan) - 1);
+        plan |= 1u << (p > 0u ? p - 1u : 1u);
     }
+    return plan;
 }
 
 hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t passes) {
@@ -324,7 +321,7 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
 // place (launch_sort_passes checks).  Pass j of the passes that run (the plan) reads the output
 // of pass j-1 (pass 0: k0 / v0) and writes, alternately, scratch a and b; the last one writes
 // (kfin, vfin) unless it is also the first and the sort is in place, in which case it writes a
-// (k_sort_plan avoids that case for sorts of more than one pass).
+// (sort_plan avoids that case for sorts of more than one pass).
 struct SortIO {
     const uint32_t* k0;
     const uint32_t* v0;  // null: values are the indices 0..n-1
@@ -334,6 +331,9 @@ struct SortIO {
     uint32_t* vb;
     uint32_t* kfin;      // null: keys are not needed in the output
     uint32_t* vfin;
+    uint32_t* rank;      // non-null: the last pass also writes rank[value] = output index
+    uint32_t passes;     // passes of the sort (the plan is derived in every pass's workgroups)
+    uint32_t in_place;
 };
 
 struct PassBufs {
@@ -431,12 +431,17 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     __shared__ uint32_t s_gbase[256];             // global index of tile slot 0 of digit d
     __shared__ uint32_t s_scan[kSortWaves];
     __shared__ uint32_t s_tile;
-
-    const uint32_t plan = ctl->plan;
-    if (!((plan >> pass) & 1u)) return;  // the pass does not run (see k_sort_plan)
-    const PassBufs bf = pass_bufs(io, plan, pass);
+    __shared__ uint32_t s_triv;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_triv = 0u;
+    __syncthreads();
+    const uint32_t plan = sort_plan(ctl, io.passes, n, io.in_place != 0u, &s_triv);
+    if (pass == 0u && blockIdx.x == 0u && tid == 0) ctl->plan = plan;  // for k_sort_finish
+    if (!((plan >> pass) & 1u)) return;  // the pass does not run (workgroup-uniform)
+    const PassBufs bf = pass_bufs(io, plan, pass);
+    const bool last = (plan >> (pass + 1u)) == 0u;
+
     const uint32_t mask = (1u << pbits) - 1u;
     if (tid == 0) s_tile = atomicAdd(&ctl->tile_ctr[pass].v, 1u);
     for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_wcnt[0][0])[i] = 0u;
@@ -577,7 +582,11 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
 #pragma unroll
     for (int k = 0; k < Items; k++) {
         const uint32_t i = (uint32_t)(k * kSortThreads + tid);
-        if ((full || i < valid) && dst[k] < n) bf.vout[dst[k]] = s_buf[i];
+        if ((full || i < valid) && dst[k] < n) {
+            const uint32_t v = s_buf[i];
+            bf.vout[dst[k]] = v;
+            if (last && io.rank && v < n) io.rank[v] = dst[k];  // inverse permutation
+        }
     }
 }
 
@@ -591,17 +600,14 @@ __global__ __launch_bounds__(256) void k_sort_finish(SortIO io, const Control* c
 }
 
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
-                              uint32_t* vfin, uint32_t n, uint32_t num_bits) {
+                              uint32_t* vfin, uint32_t n, uint32_t num_bits, uint32_t* rank) {
     const uint32_t passes = passes_for_bits(num_bits);
     const bool large = n >= kSortLargeN;
     const uint32_t tiles = ceil_div(n, (uint32_t)(large ? kSortTileLarge : kSortTile));
     const bool in_place = kfin != nullptr && kfin == k0;
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
-    SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin};
-    k_sort_plan<<<1, 256, 0, c->stream>>>(passes, n, in_place ? 1u : 0u, c->ctl);
-    hipError_t e0 = hipGetLastError();
-    if (e0 != hipSuccess) return e0;
+    SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u};
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t pbits = min(8u, num_bits - 8u * p);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * 256u;

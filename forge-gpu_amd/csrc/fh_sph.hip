@@ -17,24 +17,10 @@
 
 namespace fh {
 
-// Sorted-order copies of the state, in two passes.  k_rank (sorted order): the run tags of the
-// sorted keys (first index of each cell's run, see k_runs) and rank[sidx[s]] = s.  k_gather
-// (particle order): spos[rank[i]] = (pos[i], bits of rank[i]), svel[rank[i]] = vel[i] -- the
-// caller's arrays are read in order and each particle costs two 16-byte stores, instead of six
-// 4-byte reads from scattered lines.
-__global__ __launch_bounds__(256) void k_rank(const uint32_t* __restrict__ sidx,
-                                              const uint32_t* __restrict__ skeys, uint32_t n,
-                                              uint32_t* __restrict__ rank,
-                                              uint64_t* __restrict__ run_tag,
-                                              const Control* __restrict__ ctl) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= n) return;
-    const uint32_t k = skeys[s];
-    if (s == 0 || skeys[s - 1] != k) run_tag[k] = ((uint64_t)ctl->epoch << 32) | s;
-    const uint32_t i = sidx[s];
-    if (i < n) rank[i] = s;
-}
-
+// Sorted-order copies of the state.  The sort's last pass wrote rank[i] = sorted slot of
+// particle i; k_gather (particle order) writes spos[rank[i]] = (pos[i], bits of rank[i]) and
+// svel[rank[i]] = vel[i] -- the caller's arrays are read in order and each particle costs two
+// 16-byte stores, instead of six 4-byte reads from scattered lines.
 __global__ __launch_bounds__(256) void k_gather(
     const float* __restrict__ px, const float* __restrict__ py, const float* __restrict__ pz,
     const float* __restrict__ vx, const float* __restrict__ vy, const float* __restrict__ vz,
@@ -48,21 +34,94 @@ __global__ __launch_bounds__(256) void k_gather(
     if (svel) svel[r] = make_float4(vx[i], vy[i], vz[i], 0.0f);
 }
 
-hipError_t launch_gather(fh_ctx* c, const float* px, const float* py, const float* pz,
-                         const float* vx, const float* vy, const float* vz, uint32_t n,
-                         bool with_vel) {
-    if (n == 0) return hipSuccess;
-    tbeg(c, KID_GATHER);
-    k_rank<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->sidx, c->skeys, n, c->rank, c->run_tag,
-                                                     c->ctl);
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess) {
-        k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->rank, n,
-                                                           c->spos, with_vel ? c->svel : nullptr);
-        e = hipGetLastError();
+// CSR cell ranges straight from the sorted keys, no scan: the key in slot s starts its run when
+// the key before it, pk, differs; slot s then writes cell_start[c] = s for the cells
+// pk < c <= k (the empty cells before its own take its index: the first sorted index with key
+// >= c), and the last slot also writes n for the cells after its key up to and including C.
+// These ranges partition 0..C, so every entry is written once; together they are the prefix
+// sum of the per-cell counts of hashgrid.rs:102-106.  Short ranges are written by their lane,
+// long ones by the whole wave.
+__device__ __forceinline__ void fill_cells(uint32_t* __restrict__ cell_start, uint32_t lo,
+                                           uint32_t hi, uint32_t val, int lane) {
+    const bool mine = hi - lo <= 8u;
+    if (mine)
+        for (uint32_t c = lo; c < hi; c++) cell_start[c] = val;
+    uint64_t wide = __ballot(!mine);
+    while (wide) {  // uniform
+        const int l = __ffsll((unsigned long long)wide) - 1;
+        wide &= wide - 1ull;
+        const uint32_t wlo = (uint32_t)__shfl((int)lo, l, kWave);
+        const uint32_t whi = (uint32_t)__shfl((int)hi, l, kWave);
+        const uint32_t wv = (uint32_t)__shfl((int)val, l, kWave);
+        for (uint32_t c = wlo + (uint32_t)lane; c < whi; c += kWave) cell_start[c] = wv;
     }
+}
+
+// Cell ranges, and (big != null) the candidate co-located groups: runs of at least
+// kCollapseMin keys in which at least kGroupHits of kGroupSamples evenly spaced particles (over
+// the first L of the run, L its length rounded down to a power of two) sit at the position of
+// the middle one.  Listed as (first slot, 0); k_group counts the run and its members exactly.
+__global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict__ skeys,
+                                                     uint32_t n, uint32_t C,
+                                                     uint32_t* __restrict__ cell_start,
+                                                     const float4* __restrict__ spos,
+                                                     uint2* __restrict__ big, uint32_t cap,
+                                                     Control* ctl) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    uint32_t lo = 0, hi = 0, lo2 = 0, hi2 = 0;
+    bool cand = false;
+    uint32_t k = 0;
+    if (s < n) {
+        k = skeys[s];
+        const uint32_t pk = s > 0u ? skeys[s - 1u] : 0xFFFFFFFFu;  // "-1" before slot 0
+        if (pk != k) {
+            lo = pk + 1u;
+            hi = min(k, C - 1u) + 1u;
+            cand = big && s + kCollapseMin - 1u < n && skeys[s + kCollapseMin - 1u] == k;
+        }
+        if (s == n - 1u) {
+            lo2 = min(k, C - 1u) + 1u;
+            hi2 = C + 1u;
+        }
+    }
+    fill_cells(cell_start, lo, hi, s, lane);
+    fill_cells(cell_start, lo2, hi2, n, lane);
+    if (cand) {  // rare: a run of at least kCollapseMin
+        uint32_t L = kCollapseMin;
+        while (L < (1u << 30) && s + 2u * L - 1u < n && skeys[s + 2u * L - 1u] == k) L *= 2u;
+        const float4 P = spos[s + L / 2u];
+        uint32_t hits = 0;
+        for (uint32_t q = 0; q < kGroupSamples; q++) {
+            const float4 v = spos[s + (q * L) / kGroupSamples];
+            hits += (__float_as_uint(v.x) == __float_as_uint(P.x) &&
+                     __float_as_uint(v.y) == __float_as_uint(P.y) &&
+                     __float_as_uint(v.z) == __float_as_uint(P.z)) ? 1u : 0u;
+        }
+        if (hits >= kGroupHits) {
+            const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
+            if (slot < cap) big[slot] = make_uint2(s, 0u);
+        }
+    }
+}
+
+hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
+                         const float* py, const float* pz, const float* vx, const float* vy,
+                         const float* vz, uint32_t n, bool with_vel, bool list_big) {
+    (void)g;
+    if (n == 0) return launch_fill_u32(c, c->cell_start, 0u, cells + 1u);
+    tbeg(c, KID_GATHER);
+    k_gather<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, c->rank, n,
+                                                       c->spos, with_vel ? c->svel : nullptr);
+    hipError_t e = hipGetLastError();
     tend(c, KID_GATHER);
-    return e;
+    if (e != hipSuccess) return e;
+    tbeg(c, KID_SCAN);
+    k_cell_starts<<<ceil_div(n, 256u), 256, 0, c->stream>>>(
+        c->skeys, n, cells, c->cell_start, c->spos, list_big ? c->big : nullptr,
+        ceil_div(c->max_n, 64u) + 1u, c->ctl);
+    tend(c, KID_SCAN);
+    return hipGetLastError();
 }
 
 // Clamped cell of a particle in the SPH kernels (sph_density.rs:421-426): grid origin 0.

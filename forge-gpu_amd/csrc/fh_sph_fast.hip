@@ -110,7 +110,13 @@ constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
 // over the 64 lanes (coalesced loads), a wave reduction per particle.  Chosen when the stream
 // is longer than kTransRatio times the largest particle's candidate count plus kTransOffset
 // (below that the per-particle reductions cost more than the idle lanes).
-constexpr uint32_t kTransRatio = 2, kTransOffset = 512;
+#ifndef FH_TRANS_RATIO
+#define FH_TRANS_RATIO 4
+#endif
+#ifndef FH_TRANS_OFFSET
+#define FH_TRANS_OFFSET 512
+#endif
+constexpr uint32_t kTransRatio = FH_TRANS_RATIO, kTransOffset = FH_TRANS_OFFSET;
 #ifndef FH_HGRID
 #define FH_HGRID 1024
 #endif
@@ -153,9 +159,10 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
     return acc + ((a0 + a1) + (a2 + a3));
 }
 
-// Co-located groups.  k_big lists the cells of >= kCollapseMin particles in which at least
-// kGroupHits of kGroupSamples evenly spaced particles sit at the position P of the middle
-// particle.  k_group, one workgroup per listed cell, counts the particles at exactly P (M) and,
+// Co-located groups.  k_cell_starts lists the cells of >= kCollapseMin particles in which at
+// least kGroupHits of kGroupSamples evenly spaced particles sit at the position of a middle
+// one.  k_group, one workgroup per listed cell, takes the position P of the cell's middle
+// particle, counts the particles at exactly P (M) and,
 // when M >= kCollapseMin, moves them to the front of the cell: the misplaced particles on both
 // sides are ranked and swapped pairwise, in place.  The order inside such a cell then differs
 // from ascending particle id (sums only change by rounding).
@@ -163,30 +170,6 @@ __device__ __forceinline__ bool same_pos(const float4& a, const float4& b) {
     return __float_as_uint(a.x) == __float_as_uint(b.x) &&
            __float_as_uint(a.y) == __float_as_uint(b.y) &&
            __float_as_uint(a.z) == __float_as_uint(b.z);
-}
-
-__global__ __launch_bounds__(256) void k_big(const uint32_t* __restrict__ skeys,
-                                             const uint32_t* __restrict__ cstart,
-                                             const float4* __restrict__ spos, uint32_t n,
-                                             uint2* __restrict__ big, uint32_t cap,
-                                             Control* ctl) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= n) return;
-    const uint32_t c = skeys[s];
-    if (cstart[c] != s) return;  // not the first particle of its cell
-    const uint32_t cnt = min(cstart[c + 1u], n) - s;
-    if (cnt < kCollapseMin) return;
-    const float4 P = spos[s + cnt / 2u];
-    float4 v[kGroupSamples];
-#pragma unroll
-    for (uint32_t k = 0; k < kGroupSamples; k++)
-        v[k] = spos[s + (uint32_t)(((uint64_t)k * cnt) / kGroupSamples)];
-    uint32_t hits = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < kGroupSamples; k++) hits += same_pos(v[k], P) ? 1u : 0u;
-    if (hits < kGroupHits) return;
-    const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
-    if (slot < cap) big[slot] = make_uint2(s, cnt);
 }
 
 __device__ __forceinline__ void swap4(float4* p, uint32_t a, uint32_t b) {
@@ -227,8 +210,9 @@ __device__ __forceinline__ uint32_t match_bits(const float4* __restrict__ spos, 
 
 // Blocked layout: thread t owns particles [f + t L, f + (t + 1) L) of the cell, L = ceil(cnt / 1024).
 __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict__ big,
-                                                         uint32_t cap,
+                                                         uint32_t cap, uint32_t n,
                                                          const uint32_t* __restrict__ skeys,
+                                                         const uint32_t* __restrict__ cstart,
                                                          float4* __restrict__ spos,
                                                          float4* __restrict__ svel,
                                                          uint32_t* __restrict__ sidx,
@@ -243,7 +227,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict
     const uint32_t count = min(ctl->big_count.v, cap);
     const uint32_t epoch = ctl->epoch;
     for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform
-        const uint32_t f = big[q].x, cnt = big[q].y, end = f + cnt;
+        const uint32_t f = big[q].x, cnt = min(cstart[skeys[f] + 1u], n) - f, end = f + cnt;
         const float4 P = spos[f + cnt / 2u];
         const uint32_t L = ceil_div(cnt, (uint32_t)kGroupThreads);
         const uint32_t t0 = min(f + tid * L, end), t1 = min(t0 + L, end);
@@ -1453,19 +1437,13 @@ hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
     if (n == 0) return hipSuccess;
     const uint32_t cap = ceil_div(c->max_n, 64u) + 1u;
     tbeg(c, KID_GROUP);
-    k_big<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->skeys, c->cell_start, c->spos, n, c->big,
-                                                    cap, c->ctl);
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess) {
-        // scratch: the sort's key buffer, free after the sort (disjoint ranges per cell)
-        k_group<<<256, kGroupThreads, 0, c->stream>>>(c->big, cap, c->skeys, c->spos,
-                                                      with_vel ? c->svel : nullptr, c->sidx,
-                                                      c->rank, c->ka, c->cell_grp, c->vrep,
-                                                      c->ctl);
-        e = hipGetLastError();
-    }
+    // the candidate cells were listed with the cell ranges (k_cell_starts); scratch: the sort's
+    // key buffer, free after the sort (disjoint ranges per cell)
+    k_group<<<256, kGroupThreads, 0, c->stream>>>(c->big, cap, n, c->skeys, c->cell_start,
+                                                  c->spos, with_vel ? c->svel : nullptr, c->sidx,
+                                                  c->rank, c->ka, c->cell_grp, c->vrep, c->ctl);
     tend(c, KID_GROUP);
-    return e;
+    return hipGetLastError();
 }
 
 static FastForce fast_force(const SphArgs& a) {
