@@ -8,8 +8,9 @@
 //   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
 //                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
 //   k_hist_reduce  sums the partial rows into the histograms
-//   sort_plan      (in every pass) decides which passes run (a pass whose digit is equal for
-//                  every key is the identity and is skipped)
+//   sort_plan      decides which passes run (a pass whose digit is equal for every key is the
+//                  identity and is skipped): k_sort_plan for large sorts, in every workgroup
+//                  of every pass for small ones
 //   k_onesweep     one kernel per 8-bit pass: an 8192-key tile per 512-lane workgroup, ranked
 //                  with 64-lane ballot match-any, digit offsets from a decoupled look-back over
 //                  dynamically numbered tiles, then staged in LDS in digit order (keys, then
@@ -233,8 +234,8 @@ __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict_
     if (s) atomicAdd(&ctl->hist[p][d], s);
 }
 
-// The passes that run (one bit per pass), derived from the digit histograms by every workgroup
-// of every pass (the same function of the same data, so all agree).  A pass whose digit is
+// The passes that run (one bit per pass), derived from the digit histograms (for small sorts
+// by every workgroup of every pass: the same function of the same data, so all agree).  A pass whose digit is
 // equal for every key (one histogram bin holds all n keys) is the identity and is skipped.  Two
 // adjustments leave the result in (kfin, vfin) without a copy kernel: when no pass moves keys
 // and the sort is out of place, pass 0 runs (a stable copy: its digit is constant); when exactly
@@ -257,6 +258,17 @@ __device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, u
         plan |= 1u << (p > 0u ? p - 1u : 1u);
     }
     return plan;
+}
+
+// The same plan as one kernel (256 threads) before the passes: for large sorts, where a load
+// of the histograms and a barrier in each of thousands of workgroups cost more than a launch.
+__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t n, uint32_t in_place,
+                                                   Control* ctl) {
+    __shared__ uint32_t s_triv;
+    if (threadIdx.x == 0) s_triv = 0u;
+    __syncthreads();
+    const uint32_t plan = sort_plan(ctl, passes, n, in_place != 0u, &s_triv);
+    if (threadIdx.x == 0) ctl->plan = plan;
 }
 
 hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t passes) {
@@ -332,8 +344,9 @@ struct SortIO {
     uint32_t* kfin;      // null: keys are not needed in the output
     uint32_t* vfin;
     uint32_t* rank;      // non-null: the last pass also writes rank[value] = output index
-    uint32_t passes;     // passes of the sort (the plan is derived in every pass's workgroups)
+    uint32_t passes;     // passes of the sort
     uint32_t in_place;
+    uint32_t plan_in_wg; // 1: every workgroup derives the plan; 0: k_sort_plan wrote ctl->plan
 };
 
 struct PassBufs {
@@ -434,10 +447,15 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     __shared__ uint32_t s_triv;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_triv = 0u;
-    __syncthreads();
-    const uint32_t plan = sort_plan(ctl, io.passes, n, io.in_place != 0u, &s_triv);
-    if (pass == 0u && blockIdx.x == 0u && tid == 0) ctl->plan = plan;  // for k_sort_finish
+    uint32_t plan;
+    if (io.plan_in_wg) {  // uniform
+        if (tid == 0) s_triv = 0u;
+        __syncthreads();
+        plan = sort_plan(ctl, io.passes, n, io.in_place != 0u, &s_triv);
+        if (pass == 0u && blockIdx.x == 0u && tid == 0) ctl->plan = plan;  // for k_sort_finish
+    } else {
+        plan = ctl->plan;
+    }
     if (!((plan >> pass) & 1u)) return;  // the pass does not run (workgroup-uniform)
     const PassBufs bf = pass_bufs(io, plan, pass);
     const bool last = (plan >> (pass + 1u)) == 0u;
@@ -607,7 +625,13 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     const bool in_place = kfin != nullptr && kfin == k0;
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
-    SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u};
+    SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
+              large ? 0u : 1u};
+    if (large) {
+        k_sort_plan<<<1, 256, 0, c->stream>>>(passes, n, in_place ? 1u : 0u, c->ctl);
+        const hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return e0;
+    }
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t pbits = min(8u, num_bits - 8u * p);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * 256u;
