@@ -39,13 +39,17 @@ for _p in (REPO, REPO / "forge-gpu_amd"):
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 METRIC = "SPH particle-steps/s @1M; radix sort Gkeys/s; achieved HBM GB/s vs peak"
 KERNELS = ["hash", "sort", "gather", "scan", "group", "plan", "density", "density_heavy",
-           "force", "force_heavy", "finalize"]
+           "prep", "force", "force_heavy", "finalize"]
 # A "pass" groups the kernels of one stage of the substep; its duration per substep is the sum
-# of its kernels' launch durations (the heavy kernels of a pass process the items its light
-# kernel skips, so the pair moves the pass's bytes together).
+# of its kernels' launch durations, or its wall time for the two passes whose kernels overlap
+# (the heavy kernels of a pass process the items its light kernel skips, so the pair moves the
+# pass's bytes together).
 PASSES = {"hash": ["hash"], "sort": ["sort"], "gather": ["gather"], "scan": ["scan"],
           "plan": ["group", "plan"], "density": ["density", "density_heavy"],
-          "force": ["force", "force_heavy"], "finalize": ["finalize"]}
+          "force": ["prep", "force", "force_heavy"], "finalize": ["finalize"]}
+# The density and force passes run their light and heavy kernels concurrently on two streams:
+# their duration is the pass's wall time (first launch to the join), from these timers.
+PASS_TIMERS = {"density": "density_pass", "force": "force_pass"}
 
 
 def algorithmic_bytes(n: int, cells: int, passes: int) -> dict:
@@ -86,6 +90,22 @@ def read_traffic(kernel_pass: str):
                 return int(float(kv["fetch_bytes"]) + float(kv["write_bytes"]))
             except (KeyError, ValueError):
                 return None
+    return None
+
+
+VALU_PEAK_INSTS = 256 * 2.4e9  # MI355X: one non-packed VALU wave instruction per cycle per CU
+
+
+def read_valu(kernel_pass: str):
+    """VALU wave instructions per substep of a pass, from the committed rocprofv3 PMC summary
+    (profiles/valu_c3.txt, lines `<pass> valu_insts=<N>`), or None."""
+    f = REPO / "profiles" / "valu_c3.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == kernel_pass and parts[1].startswith("valu_insts="):
+            return int(parts[1].split("=", 1)[1])
     return None
 
 
@@ -163,13 +183,13 @@ def bench_sph(args, fh, torch, log):
 
     # Per-kernel durations: G more substeps launched eagerly on the same stream with every
     # kernel bracketed by HIP events (events recorded by graph nodes cannot be timed on HIP).
-    for k in KERNELS:
+    for k in KERNELS + list(PASS_TIMERS.values()):
         ctx.time_kernel(k, (passes if k == "sort" else 1) * G)
     for _ in range(G):
         pipe.step_async(fields, cfg.dt)
     ctx.sync()
     kern = {}
-    for k in KERNELS:
+    for k in KERNELS + list(PASS_TIMERS.values()):
         t = ctx.kernel_times_ms(k)
         kern[k] = {"launches": len(t), "mean_us": 1e3 * sum(t) / max(len(t), 1),
                    "per_substep_us": 1e3 * sum(t) / G}
@@ -177,8 +197,12 @@ def bench_sph(args, fh, torch, log):
     byts = algorithmic_bytes(cfg.n, C, passes)
     pas = {}
     for p, ks in PASSES.items():
-        us = sum(kern[k]["per_substep_us"] for k in ks)
-        pas[p] = {"kernels": ks, "per_substep_us": us, "alg_bytes": byts[p],
+        # a pass whose kernels overlap on two streams is timed as a whole (wall time)
+        us = kern[PASS_TIMERS[p]]["per_substep_us"] if p in PASS_TIMERS else \
+            sum(kern[k]["per_substep_us"] for k in ks)
+        pas[p] = {"kernels": ks, "per_substep_us": us,
+                  "kernel_sum_us": sum(kern[k]["per_substep_us"] for k in ks),
+                  "alg_bytes": byts[p],
                   "alg_GBs": byts[p] / (us * 1e-6) / 1e9 if us > 0 else None}
     dom = max(pas, key=lambda p: pas[p]["per_substep_us"])
     achieved = pas[dom]["alg_GBs"]
@@ -403,6 +427,14 @@ def cpu_baseline(args, log):
             "seconds": el, "cpu": cpu_info(), "host_cpus": os.cpu_count()}
 
 
+def valu_block(insts, us):
+    if not insts or not us:
+        return None
+    return {"insts_per_launch": insts, "peak_insts_per_s": VALU_PEAK_INSTS,
+            "achieved_insts_per_s": insts / (us * 1e-6),
+            "frac": insts / (us * 1e-6) / VALU_PEAK_INSTS, "source": "profiles/valu_c3.txt"}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -484,6 +516,10 @@ def main(argv=None) -> int:
             "frac": s["achieved"] / HBM_PEAK_GBS, "traffic": read_traffic(dom),
             "alg_bytes_per_launch": s["pas"][dom]["alg_bytes"],
             "mean_launch_us": s["pas"][dom]["per_substep_us"],
+            # the SPH passes are limited by vector ALU issue, not HBM: VALU wave instructions of
+            # the pass (PMC, profiles/valu_c3.txt) over the time measured here, against the
+            # issue rate of 256 CUs at 2.4 GHz
+            "valu": valu_block(read_valu(dom), s["pas"][dom]["per_substep_us"]),
         },
         "cpu_baseline": cpu,
         "extra": {

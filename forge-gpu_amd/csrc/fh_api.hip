@@ -403,9 +403,14 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
     } else {
         FH_CHECK_HIP(launch_group(c, n, true));
         FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
+        // pass timers: first launch to the join of the side stream (wall time of the pass)
+        tbeg(c, KID_DPASS);
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
+        tend(c, KID_DPASS);
+        tbeg(c, KID_FPASS);
         FH_CHECK_HIP(launch_prep(c, a));
         FH_CHECK_HIP(launch_force_fast(c, a, c->cell_start));
+        tend(c, KID_FPASS);
         FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density, accel));
     }
     return FH_OK;
@@ -549,7 +554,8 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
 static const char* const kKernelNames[KID_COUNT] = {"hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
                                                     "finalize", "runs", "plan",
-                                                    "density_heavy", "force_heavy", "group"};
+                                                    "density_heavy", "force_heavy", "group",
+                                                    "prep", "density_pass", "force_pass"};
 
 static int kernel_id(const char* name) {
     if (!name) return -1;

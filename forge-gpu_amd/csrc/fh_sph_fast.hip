@@ -1465,9 +1465,11 @@ static FastForce fast_force(const SphArgs& a) {
 hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
     if (a.n == 0) return hipSuccess;
     const FastForce K = fast_force(a);
+    tbeg(c, KID_PREP);
     k_prep<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
                                                        c->max_n, K.mc, a.k, a.rho0, K.fp, K.fv,
                                                        c->srho, c->sout);
+    tend(c, KID_PREP);
     return hipGetLastError();
 }
 

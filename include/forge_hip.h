@@ -254,7 +254,9 @@ int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, flo
 
 /* Per-kernel timing.  Arm kernel `name` (one of "hist", "hash", "scan", "sort",
  * "gather", "density", "force", "query", "finalize", "runs", "plan", "density_heavy",
- * "force_heavy", "group") so that its next `max_launches` launches on the
+ * "force_heavy", "group", "prep"; or a whole fast pass of fh_sph_fused, "density_pass" or
+ * "force_pass", from its first launch to the join of its side stream) so that its next
+ * `max_launches` launches on the
  * context stream are bracketed by HIP events; launches captured into a graph record the events
  * on every replay.  max_launches = 0 disarms.  Arming allocates events: call outside capture.
  * fh_kernel_times waits for the last armed launch and writes the durations (ms) of the armed
