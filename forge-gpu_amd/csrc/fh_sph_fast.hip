@@ -613,65 +613,83 @@ constexpr int kWinLoads = kWin / kWave;
 struct LightStream {
     uint32_t S[3], cnt[3];  // the lane's own intervals
     uint32_t T;             // stream length (wave-uniform)
-    int nin;                // lanes holding a particle (a prefix of the wave)
-    // the lane's segment: first stream position, row unions [lo[r], lo[r] + L[r])
-    uint32_t base, lo0, lo1, lo2, L0, L1;
+    int nseg;               // home-row segments (wave-uniform)
+    // segment table: lane q < nseg holds segment q's first stream position and row unions
+    // [lo[r], lo[r] + L[r])
+    uint32_t cb, clo0, clo1, clo2, cL0, cL1;
 };
 
 __device__ __forceinline__ void light_stream(LightStream& L, const uint32_t b[3],
                                              const uint32_t e[3], uint32_t hr, bool in, int lane) {
-    L.nin = __popcll(__ballot(in));
+    const int nin = __popcll(__ballot(in));
     const uint32_t hprev = (uint32_t)__shfl_up((int)hr, 1u, kWave);
-    const uint64_t starts = __ballot(in && (lane == 0 || hprev != hr));
+    const bool lead = in && (lane == 0 || hprev != hr);
+    const uint64_t starts = __ballot(lead);
     const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
     const uint64_t before = starts & upto, after = starts & ~upto;
     const int leader = before ? 63 - __clzll((long long)before) : 0;
-    const int last = after ? __ffsll((unsigned long long)after) - 2 : L.nin - 1;
+    const int last = after ? __ffsll((unsigned long long)after) - 2 : nin - 1;
     const uint32_t lo0 = (uint32_t)__shfl((int)b[0], leader, kWave);
     const uint32_t lo1 = (uint32_t)__shfl((int)b[1], leader, kWave);
     const uint32_t lo2 = (uint32_t)__shfl((int)b[2], leader, kWave);
     const uint32_t hi0 = (uint32_t)__shfl((int)e[0], last < 0 ? 0 : last, kWave);
     const uint32_t hi1 = (uint32_t)__shfl((int)e[1], last < 0 ? 0 : last, kWave);
     const uint32_t hi2 = (uint32_t)__shfl((int)e[2], last < 0 ? 0 : last, kWave);
-    L.lo0 = lo0;
-    L.lo1 = lo1;
-    L.lo2 = lo2;
-    L.L0 = hi0 - lo0;
-    L.L1 = hi1 - lo1;
-    const uint32_t len = L.L0 + L.L1 + (hi2 - lo2);
+    const uint32_t L0 = hi0 - lo0, L1 = hi1 - lo1;
+    const uint32_t len = L0 + L1 + (hi2 - lo2);
     // inclusive scan of the segment lengths, counted at their leaders
-    uint32_t x = (in && lane == leader) ? len : 0u;
+    uint32_t x = lead ? len : 0u;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
         const uint32_t y = (uint32_t)__shfl_up((int)x, (unsigned)d, kWave);
         if (lane >= d) x += y;
     }
     L.T = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-    const uint32_t excl = x - ((in && lane == leader) ? len : 0u);
-    L.base = (uint32_t)__shfl((int)excl, leader, kWave);
-    L.S[0] = L.base + (b[0] - lo0);
-    L.S[1] = L.base + L.L0 + (b[1] - lo1);
-    L.S[2] = L.base + L.L0 + L.L1 + (b[2] - lo2);
+    const uint32_t excl = x - (lead ? len : 0u);
+    const uint32_t base = (uint32_t)__shfl((int)excl, leader, kWave);
+    L.S[0] = base + (b[0] - lo0);
+    L.S[1] = base + L0 + (b[1] - lo1);
+    L.S[2] = base + L0 + L1 + (b[2] - lo2);
 #pragma unroll
     for (int r = 0; r < 3; r++) L.cnt[r] = in ? e[r] - b[r] : 0u;
+    // segment table: each leader sends its segment to lane (its rank among the leaders); the
+    // other lanes send to lane 63, which is a table entry only when all 64 lanes lead
+    L.nseg = __popcll(starts);
+    const int rk = lead ? (int)__popcll(starts & (upto >> 1)) : 63;
+    const int to = rk << 2;
+    L.cb = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)base);
+    L.clo0 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)lo0);
+    L.clo1 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)lo1);
+    L.clo2 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)lo2);
+    L.cL0 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)L0);
+    L.cL1 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)L1);
 }
 
-// Sorted index of stream position t (< T): the last lane whose segment starts at or before t
-// (segment bases are non-decreasing over the lanes) gives the segment, then the row.
+// Sorted index of stream position t (< T): the last segment that starts at or before t (a
+// binary search over the nseg table entries; none for one segment), then the row.
 __device__ __forceinline__ uint32_t stream_index(const LightStream& L, uint32_t t) {
-    int pos = 0;
-#pragma unroll
-    for (int step = 32; step >= 1; step >>= 1) {
-        const int c = pos + step;
-        const uint32_t sb = (uint32_t)__shfl((int)L.base, c < 64 ? c : 63, kWave);
-        if (c < L.nin && sb <= t) pos = c;
+    uint32_t base, lo0, lo1, lo2, L0, L1;
+    if (L.nseg == 1) {  // wave-uniform: the one segment's values from lane 0
+        base = (uint32_t)__builtin_amdgcn_readlane((int)L.cb, 0);
+        lo0 = (uint32_t)__builtin_amdgcn_readlane((int)L.clo0, 0);
+        lo1 = (uint32_t)__builtin_amdgcn_readlane((int)L.clo1, 0);
+        lo2 = (uint32_t)__builtin_amdgcn_readlane((int)L.clo2, 0);
+        L0 = (uint32_t)__builtin_amdgcn_readlane((int)L.cL0, 0);
+        L1 = (uint32_t)__builtin_amdgcn_readlane((int)L.cL1, 0);
+    } else {
+        int pos = 0;
+        for (int step = 1 << (31 - __clz(L.nseg - 1)); step >= 1; step >>= 1) {  // uniform
+            const int c = pos + step;
+            const uint32_t sb = (uint32_t)__shfl((int)L.cb, c < L.nseg ? c : 0, kWave);
+            if (c < L.nseg && sb <= t) pos = c;
+        }
+        base = (uint32_t)__shfl((int)L.cb, pos, kWave);
+        lo0 = (uint32_t)__shfl((int)L.clo0, pos, kWave);
+        lo1 = (uint32_t)__shfl((int)L.clo1, pos, kWave);
+        lo2 = (uint32_t)__shfl((int)L.clo2, pos, kWave);
+        L0 = (uint32_t)__shfl((int)L.cL0, pos, kWave);
+        L1 = (uint32_t)__shfl((int)L.cL1, pos, kWave);
     }
-    const uint32_t base = (uint32_t)__shfl((int)L.base, pos, kWave);
-    const uint32_t lo0 = (uint32_t)__shfl((int)L.lo0, pos, kWave);
-    const uint32_t lo1 = (uint32_t)__shfl((int)L.lo1, pos, kWave);
-    const uint32_t lo2 = (uint32_t)__shfl((int)L.lo2, pos, kWave);
-    const uint32_t L0 = (uint32_t)__shfl((int)L.L0, pos, kWave);
-    const uint32_t L1 = (uint32_t)__shfl((int)L.L1, pos, kWave);
     const uint32_t u = t - base;
     return u < L0 ? lo0 + u : (u < L0 + L1 ? lo1 + (u - L0) : lo2 + (u - L0 - L1));
 }
