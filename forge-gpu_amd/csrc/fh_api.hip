@@ -161,7 +161,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess) e = alloc(&c->cell_grp, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->big, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
-    if (e == hipSuccess) e = alloc(&c->collapsed, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
+    if (e == hipSuccess) e = alloc(&c->skip_tag, (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess) e = alloc(&c->wpart, 3 * (size_t)max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->vrep, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->rank, max_n, &tot);
@@ -185,6 +185,8 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->run_tag, 0, (size_t)max_cells * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->cell_grp, 0, (size_t)max_cells * 8u, c->stream);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(c->skip_tag, 0, (size_t)ceil_div(max_n, 64u) * 4u, c->stream);
     for (int q = 0; q < kEvents && e == hipSuccess; q++) e = hipEventCreate(&c->ev[q]);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     c->scratch_bytes = tot;
@@ -217,7 +219,7 @@ int fh_destroy(fh_ctx* c) {
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
                     c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hist_part,
-                    c->cell_grp, c->big, c->collapsed, c->wpart, c->vrep, c->rank, c->sout};
+                    c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);
@@ -371,8 +373,7 @@ int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const f
     if (c->sph_exact) {
         FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
     } else {
-        FH_CHECK_HIP(launch_group(c, n, false));
-        FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_group_plan(c, a, false));
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
         FH_CHECK_HIP(launch_finalize(c, a, nullptr, true, nullptr, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, density, nullptr));
@@ -401,8 +402,7 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
         FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
         FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
     } else {
-        FH_CHECK_HIP(launch_group(c, n, true));
-        FH_CHECK_HIP(launch_plan(c, a, c->cell_start));
+        FH_CHECK_HIP(launch_group_plan(c, a, true));
         // pass timers: first launch to the join of the side stream (wall time of the pass)
         tbeg(c, KID_DPASS);
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));

@@ -148,7 +148,7 @@ struct fh_ctx {
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
     uint64_t* cell_grp;  // [max_cells] epoch << 32 | number of co-located leading particles
     uint2* big;          // [ceil(max_n / 64) + 1] (first, count) of cells of >= kCollapseMin
-    uint2* collapsed;    // [ceil(max_n / 64) + 1] (representative, count) of co-located groups
+    uint32_t* skip_tag;  // [ceil(max_n / 64)] epoch of the rebuild whose sub-tile holds only group members
     float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
     float4* vrep;        // [max_n] summed velocity of the group, at representative indices
     uint32_t* rank;      // [max_n] sorted position of each particle (inverse of sidx)
@@ -296,7 +296,6 @@ struct SphArgs {
 hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
                          const float* py, const float* pz, const float* vx, const float* vy,
                          const float* vz, uint32_t n, bool with_vel, bool list_big);
-hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 // Force records of every sorted particle (positions with pressure, velocity and weight over
@@ -306,7 +305,8 @@ hipError_t launch_prep(fh_ctx* c, const SphArgs& a);
 // Fast passes only: list the cells of >= kCollapseMin particles and move the particles that
 // share the position of the cell's middle particle to the front of the cell when they are at
 // least kCollapseMin (cell_grp).  Reorders spos / svel / sidx inside those cells.
-hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel);
+// Co-located groups (k_group, side stream) beside the work plan of the fast passes (k_plan).
+hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel);
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
                            bool density_only, float* px, float* py, float* pz, float* vx,
                            float* vy, float* vz, float* density, float* accel);

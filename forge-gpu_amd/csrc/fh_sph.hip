@@ -60,12 +60,14 @@ __device__ __forceinline__ void fill_cells(uint32_t* __restrict__ cell_start, ui
 // Cell ranges, and (big != null) the candidate co-located groups: runs of at least
 // kCollapseMin keys in which at least kGroupHits of kGroupSamples evenly spaced particles (over
 // the first L of the run, L its length rounded down to a power of two) sit at the position of
-// the middle one.  Listed as (first slot, 0); k_group counts the run and its members exactly.
+// the middle one.  Listed as (first slot, 0) -- k_group counts the run and its members exactly
+// -- and tagged with the epoch in cand_tag[cell] for k_plan, which runs beside k_group.
 __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict__ skeys,
                                                      uint32_t n, uint32_t C,
                                                      uint32_t* __restrict__ cell_start,
                                                      const float4* __restrict__ spos,
                                                      uint2* __restrict__ big, uint32_t cap,
+                                                     uint64_t* __restrict__ cand_tag,
                                                      Control* ctl) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     const int lane = threadIdx.x & 63;
@@ -101,6 +103,7 @@ __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict_
         if (hits >= kGroupHits) {
             const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
             if (slot < cap) big[slot] = make_uint2(s, 0u);
+            cand_tag[k] = (uint64_t)ctl->epoch << 32;  // k_plan: this cell may hold a group
         }
     }
 }
@@ -119,7 +122,7 @@ hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const flo
     tbeg(c, KID_SCAN);
     k_cell_starts<<<ceil_div(n, 256u), 256, 0, c->stream>>>(
         c->skeys, n, cells, c->cell_start, c->spos, list_big ? c->big : nullptr,
-        ceil_div(c->max_n, 64u) + 1u, c->ctl);
+        ceil_div(c->max_n, 64u) + 1u, c->run_tag, c->ctl);
     tend(c, KID_SCAN);
     return hipGetLastError();
 }

@@ -113,6 +113,9 @@ constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
 #ifndef FH_TRANS_RATIO
 #define FH_TRANS_RATIO 4
 #endif
+#ifndef FH_TRANS_TOUCH
+#define FH_TRANS_TOUCH 1
+#endif
 #ifndef FH_TRANS_OFFSET
 #define FH_TRANS_OFFSET 512
 #endif
@@ -220,6 +223,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict
                                                          uint32_t* __restrict__ scratch,
                                                          uint64_t* __restrict__ cell_grp,
                                                          float4* __restrict__ vrep,
+                                                         uint32_t* __restrict__ skip_tag,
                                                          const Control* __restrict__ ctl) {
     __shared__ uint32_t s_scan[kGroupWaves];
     __shared__ float s_w[kGroupWaves];
@@ -304,15 +308,25 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict
             vz = group_sum(vz, s_w);
             if (tid == 0) vrep[f] = make_float4(vx, vy, vz, 0.0f);
         }
+        // tags in spos.w: the representative f carries kRepFlag | M, the other members f (the
+        // positions moved above; the .w slot index bits stay with the slot)
+        for (uint32_t t = f + tid; t < f + M; t += kGroupThreads)
+            reinterpret_cast<float*>(spos + t)[3] = __uint_as_float(t == f ? (M | kRepFlag) : f);
+        // sub-tiles made only of members are skipped by both passes (finished from f)
+        for (uint32_t q = ceil_div(f + 1u, (uint32_t)kSub) + tid; (q + 1u) * kSub <= f + M;
+             q += kGroupThreads)
+            skip_tag[q] = epoch;
         if (tid == 0) cell_grp[skeys[f]] = ((uint64_t)epoch << 32) | M;
         __syncthreads();
     }
 }
 
-// Candidates of the grouped cells among the 9 cells of a slab, as a count to subtract: a group
-// of M particles is one candidate.
+// Candidates of the possibly grouped cells among the 9 cells of a slab (tagged by
+// k_cell_starts; k_group, which runs beside the plan, decides), as a count to subtract: such a
+// cell of k particles is counted as one (a group of M counts as one candidate, M <= k).
 __device__ __forceinline__ uint32_t grouped_excess(const float4& p, const GridDesc& g,
-                                                   const uint64_t* __restrict__ cell_grp,
+                                                   const uint64_t* __restrict__ cand_tag,
+                                                   const uint32_t* __restrict__ cstart,
                                                    uint32_t epoch, int dz) {
     const int cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
     const int cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny);
@@ -323,8 +337,8 @@ __device__ __forceinline__ uint32_t grouped_excess(const float4& p, const GridDe
         if (y < 0 || y >= (int)g.ny) continue;
         for (int x = cx - 1; x <= cx + 1; x++) {
             if (x < 0 || x >= (int)g.nx) continue;
-            const uint64_t grp = cell_grp[(uint32_t)x + (uint32_t)y * g.nx + (uint32_t)cz * g.nx * g.ny];
-            if ((uint32_t)(grp >> 32) == epoch) ex += (uint32_t)grp - 1u;
+            const uint32_t c = (uint32_t)x + (uint32_t)y * g.nx + (uint32_t)cz * g.nx * g.ny;
+            if ((uint32_t)(cand_tag[c] >> 32) == epoch) ex += cstart[c + 1u] - cstart[c] - 1u;
         }
     }
     return ex;
@@ -464,23 +478,22 @@ __device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
     return out;
 }
 
-// Plan.  First the co-located groups (k_group): particles f+1 .. f+M-1 of a grouped cell are
-// tagged in spos[s].w with their representative f (which gets kRepFlag and appends the group
-// to the collapsed list).  A sub-tile made only of such non-representative particles is
-// skipped by both passes (flag 2): its particles take the representative's density, and its
-// acceleration up to the viscosity term that depends on the particle's own velocity
-// (k_finalize).  Then a (sub-tile, slab) item is heavy when its largest per-particle candidate
-// count (a group counting once) exceeds heavy_work or when it touches a co-located group.
-__global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos, uint32_t n,
-                                                       GridDesc g,
+// Plan, beside the co-located groups (k_group, which tags particles f+1 .. f+M-1 of a grouped
+// cell in spos[s].w with their representative f, f itself with kRepFlag | M, and marks the
+// sub-tiles made only of such non-representative particles in skip_tag: both passes skip them,
+// their particles take the representative's density, and its acceleration up to the viscosity
+// term that depends on the particle's own velocity, in k_finalize).  A (sub-tile, slab) item is
+// heavy when its largest per-particle candidate count (a cell that may hold a group counting
+// once) exceeds heavy_work or when it touches such a cell, and transposed (heavy) when its
+// stream is much longer than that count.
+__global__ __launch_bounds__(kPlanThreads) void k_plan(const float4* __restrict__ spos,
+                                                       uint32_t n, GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
-                                                       const uint64_t* __restrict__ cell_grp,
+                                                       const uint64_t* __restrict__ cand_tag,
                                                        uint8_t* __restrict__ flag,
                                                        uint32_t* __restrict__ heavy,
-                                                       uint32_t heavy_cap,
-                                                       uint2* __restrict__ collapsed, uint32_t cap,
-                                                       uint32_t heavy_work, uint32_t direct_mode,
-                                                       Control* ctl) {
+                                                       uint32_t heavy_cap, uint32_t heavy_work,
+                                                       uint32_t direct_mode, Control* ctl) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
     __shared__ uint32_t s_count[kWaves];
@@ -491,27 +504,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
     uint32_t nh = 0;  // heavy items of this wave, kept in s_item[wave * 3 ...]
     if (sub * kSub < n) {  // wave-uniform
         const float4 pi = load_or(spos, s, live, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
-        bool member = false;
-        if (live) {
-            const uint32_t c = cell_of(pi.x, pi.y, pi.z, g);
-            const uint64_t grp = cell_grp[c];
-            if ((uint32_t)(grp >> 32) == ctl->epoch) {
-                const uint32_t f = cstart[c], M = (uint32_t)grp;
-                float* w = reinterpret_cast<float*>(spos + s) + 3;
-                if (s == f) {
-                    *w = __uint_as_float(M | kRepFlag);
-                    const uint32_t slot = atomicAdd(&ctl->collapse_count.v, 1u);
-                    if (slot < cap) collapsed[slot] = make_uint2(f, M);
-                } else if (s < f + M) {
-                    *w = __uint_as_float(f);
-                    member = true;
-                }
-            }
-        }
-        if (__ballot(live && !member) == 0ull) {  // every particle of the sub-tile is co-located
-            if (lane == 0)
-                for (int slab = 0; slab < 3; slab++) flag[sub * 3u + (uint32_t)slab] = kItemSkip;
-        } else {
+        {
             const uint32_t epoch = ctl->epoch;
             for (int slab = 0; slab < 3; slab++) {
                 uint32_t b[3], e[3];
@@ -519,7 +512,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
                 uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
                 uint32_t excess = 0;
                 if (cand >= kCollapseMin) {  // a grouped cell holds at least kCollapseMin
-                    excess = grouped_excess(pi, g, cell_grp, epoch, slab - 1);
+                    excess = grouped_excess(pi, g, cand_tag, cstart, epoch, slab - 1);
                     cand -= excess;
                 }
                 const uint32_t w = wave_max(cand);
@@ -528,7 +521,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(float4* __restrict__ spos
                 bool trans = direct_mode == 2u;
                 if (direct_mode == 1u && hv) {
                     const uint32_t T = stream_total(b, e, home_row(pi, g), live, lane);
-                    trans = T > kTransRatio * w + kTransOffset;
+                    trans = T > kTransRatio * w + kTransOffset && (FH_TRANS_TOUCH || !touches);
                 }
                 hv = hv || trans;
                 if (lane == 0) {
@@ -710,12 +703,15 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
                                                          const uint32_t* __restrict__ cstart,
                                                          float h2, float* __restrict__ dpart,
                                                          uint32_t stride, uint32_t items,
-                                                         const uint8_t* __restrict__ flag) {
+                                                         const uint8_t* __restrict__ flag,
+                                                         const uint32_t* __restrict__ skip_tag,
+                                                         const Control* __restrict__ ctl) {
     __shared__ float4 s_p[kTileP / kWave][kWin];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
     if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
+    if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
     const float4 pi = load_or(spos, s, in, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
@@ -890,7 +886,8 @@ template <int HW>
 __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
     const float4* __restrict__ spos, uint32_t n, GridDesc g, const uint32_t* __restrict__ cstart,
     const uint64_t* __restrict__ cell_grp, float h2, float* __restrict__ dpart, uint32_t stride,
-    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const Control* __restrict__ ctl) {
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const uint32_t* __restrict__ skip_tag,
+    const Control* __restrict__ ctl) {
     __shared__ float4 s_p[HW][kWave];
     __shared__ float s_acc[HW][kSub];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -903,6 +900,7 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
         const bool trans = (entry & kTransFlag) != 0u;
         const uint32_t item = entry & ~(kCutFlag | kTransFlag);
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
+        if (skip_tag[sub] == epoch) continue;  // uniform: only group members
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool live = s < n;
         const float4 pi = load_or(spos, s, live, z4);
@@ -1120,13 +1118,16 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
                                                        const uint32_t* __restrict__ cstart,
                                                        FastForce K, float* __restrict__ fpart,
                                                        uint32_t stride, uint32_t items,
-                                                       const uint8_t* __restrict__ flag) {
+                                                       const uint8_t* __restrict__ flag,
+                                                       const uint32_t* __restrict__ skip_tag,
+                                                       const Control* __restrict__ ctl) {
     __shared__ float4 s_p[kTileP / kWave][kWin];  // x, y, z, p_j
     __shared__ float4 s_v[kTileP / kWave][kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
     if (item >= items || flag[item] != kItemLight) return;  // whole wave; heavy: k_force_heavy
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
+    if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -1182,7 +1183,8 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
     const float* __restrict__ srho, const float4* __restrict__ rec, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
     float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
-    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const Control* __restrict__ ctl) {
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const uint32_t* __restrict__ skip_tag,
+    const Control* __restrict__ ctl) {
     __shared__ float4 s_p[HW][kWave];
     __shared__ float4 s_v[HW][kWave];
     __shared__ float s_acc[4][HW][kSub];
@@ -1197,6 +1199,7 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
         const bool trans = (entry & kTransFlag) != 0u;
         const uint32_t item = entry & ~(kCutFlag | kTransFlag);
         const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
+        if (skip_tag[sub] == epoch) continue;  // uniform: only group members
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool in = s < n;
         const float4 pi = load_or(spos, s, in, z4);
@@ -1408,17 +1411,7 @@ static float poly6_mc(float h, float mass) {
     return mass * poly6;
 }
 
-hipError_t launch_plan(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
-    if (a.n == 0) return hipSuccess;
-    tbeg(c, KID_PLAN);
-    k_plan<<<ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0, c->stream>>>(
-        c->spos, a.n, a.g, cell_start, c->cell_grp, c->heavy_flag, c->heavy, c->heavy_cap,
-        c->collapsed, ceil_div(c->max_n, 64u) + 1u, c->heavy_work ? c->heavy_work : kHeavyWork,
-        c->direct_mode,
-        c->ctl);
-    tend(c, KID_PLAN);
-    return hipGetLastError();
-}
+
 
 // Fork the side stream off the main one (heavy kernels go there), and join it back.
 static hipError_t fork_side(fh_ctx* c) {
@@ -1430,6 +1423,32 @@ static hipError_t join_side(fh_ctx* c) {
     return e == hipSuccess ? hipStreamWaitEvent(c->stream, c->join_ev, 0) : e;
 }
 
+// k_group on the side stream beside k_plan: the plan needs only the cells that may hold a group
+// (tagged by k_cell_starts), not their outcome, and every particle of a cell gives the cell's
+// neighbour ranges whether or not k_group has moved it yet.
+hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
+    if (a.n == 0) return hipSuccess;
+    hipError_t e = fork_side(c);
+    if (e != hipSuccess) return e;
+    // the candidate cells were listed with the cell ranges (k_cell_starts); scratch: the sort's
+    // key buffer, free after the sort (disjoint ranges per cell)
+    tbeg(c, KID_GROUP, c->side);
+    k_group<<<256, kGroupThreads, 0, c->side>>>(c->big, ceil_div(c->max_n, 64u) + 1u, a.n,
+                                                c->skeys, c->cell_start, c->spos,
+                                                with_vel ? c->svel : nullptr, c->sidx, c->rank,
+                                                c->ka, c->cell_grp, c->vrep, c->skip_tag, c->ctl);
+    tend(c, KID_GROUP, c->side);
+    e = hipGetLastError();
+    tbeg(c, KID_PLAN);
+    k_plan<<<ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0, c->stream>>>(
+        c->spos, a.n, a.g, c->cell_start, c->run_tag, c->heavy_flag, c->heavy, c->heavy_cap,
+        c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode, c->ctl);
+    tend(c, KID_PLAN);
+    if (e == hipSuccess) e = hipGetLastError();
+    const hipError_t j = join_side(c);  // joined even after a failed launch
+    return e != hipSuccess ? e : j;
+}
+
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
     if (a.n == 0) return hipSuccess;
     uint32_t items;
@@ -1439,30 +1458,19 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     tbeg(c, KID_DHEAVY, c->side);
     k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
         c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
-        c->heavy_cap, c->ctl);
+        c->heavy_cap, c->skip_tag, c->ctl);
     tend(c, KID_DHEAVY, c->side);
     e = hipGetLastError();
     tbeg(c, KID_DENSITY);
     k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, a.n, a.g, cell_start, a.h * a.h,
-                                                   c->dpart, c->max_n, items, c->heavy_flag);
+                                                   c->dpart, c->max_n, items, c->heavy_flag,
+                                                   c->skip_tag, c->ctl);
     tend(c, KID_DENSITY);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c);  // joined even after a failed launch
     return e != hipSuccess ? e : j;
 }
 
-hipError_t launch_group(fh_ctx* c, uint32_t n, bool with_vel) {
-    if (n == 0) return hipSuccess;
-    const uint32_t cap = ceil_div(c->max_n, 64u) + 1u;
-    tbeg(c, KID_GROUP);
-    // the candidate cells were listed with the cell ranges (k_cell_starts); scratch: the sort's
-    // key buffer, free after the sort (disjoint ranges per cell)
-    k_group<<<256, kGroupThreads, 0, c->stream>>>(c->big, cap, n, c->skeys, c->cell_start,
-                                                  c->spos, with_vel ? c->svel : nullptr, c->sidx,
-                                                  c->rank, c->ka, c->cell_grp, c->vrep, c->ctl);
-    tend(c, KID_GROUP);
-    return hipGetLastError();
-}
 
 static FastForce fast_force(const SphArgs& a) {
     FastForce K;
@@ -1501,13 +1509,13 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     tbeg(c, KID_FHEAVY, c->side);
     k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
         c->spos, c->svel, c->srho, c->sout, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
-        c->wpart, c->max_n, c->heavy, c->heavy_cap, c->ctl);
+        c->wpart, c->max_n, c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
     tend(c, KID_FHEAVY, c->side);
     e = hipGetLastError();
     tbeg(c, KID_FORCE);
     k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, a.n, a.g,
                                                  cell_start, K, c->fpart, c->max_n, items,
-                                                 c->heavy_flag);
+                                                 c->heavy_flag, c->skip_tag, c->ctl);
     tend(c, KID_FORCE);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c);
