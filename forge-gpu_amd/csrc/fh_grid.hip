@@ -12,6 +12,7 @@
 //                  sorted order, so the 27-cell walk is 9 contiguous ranges visited in the
 //                  reference's dz, dy, dx order.
 #include "fh_internal.hpp"
+#include "fh_stream.hpp"
 
 namespace fh {
 
@@ -250,6 +251,115 @@ __global__ __launch_bounds__(256) void k_nbr_query(const float4* __restrict__ sp
     if (wsum) wsum[i] = w;
 }
 
+// The same query, with the neighbour candidates of 64 consecutive sorted points staged through
+// LDS (the wave candidate stream of fh_stream.hpp, one z-slab at a time): each lane still visits
+// its own candidates in the reference's order (dz, dy, then ascending sorted index) with the
+// reference's expressions, so counts and weight sums stay bit-identical; the staging turns the
+// per-lane scattered reads into shared, coalesced ones.  Points whose query cell lies outside
+// the grid (the reference does not clamp it) take the per-lane walk of k_nbr_query afterwards.
+__global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__ spos,
+                                                      const uint32_t* __restrict__ sidx,
+                                                      uint32_t n, GridDesc g,
+                                                      const uint32_t* __restrict__ cell_start,
+                                                      float radius_sq, float coeff,
+                                                      uint32_t* __restrict__ counts,
+                                                      float* __restrict__ wsum) {
+    __shared__ float4 s_p[kWin];
+    const int lane = threadIdx.x;
+    const uint32_t s = blockIdx.x * kWave + (uint32_t)lane;
+    const bool in = s < n;
+    const float4 q = spos[in ? s : 0u];
+    // the sort's (clamped) cell, and the reference's unclamped query cell
+    const uint32_t cxc = cell_coord(q.x, g.ox, g.cs, g.nx);
+    const uint32_t cyc = cell_coord(q.y, g.oy, g.cs, g.ny);
+    const uint32_t czc = cell_coord(q.z, g.oz, g.cs, g.nz);
+    const int64_t cxu = rust_as_i32(floorf((q.x - g.ox) / g.cs));
+    const int64_t cyu = rust_as_i32(floorf((q.y - g.oy) / g.cs));
+    const int64_t czu = rust_as_i32(floorf((q.z - g.oz) / g.cs));
+    const bool inside = cxu == (int64_t)cxc && cyu == (int64_t)cyc && czu == (int64_t)czc;
+    const uint32_t hr = cyc + czc * g.ny;  // home row of the sorted order
+    const uint32_t x0 = cxc > 0u ? cxc - 1u : 0u;
+    const uint32_t x1 = cxc + 1u < g.nx ? cxc + 1u : g.nx - 1u;
+    uint32_t cnt = 0;
+    float w = 0.0f;
+    for (int dz = -1; dz <= 1; dz++) {  // uniform
+        uint32_t b[3], e[3];
+        const int nz = (int)czc + dz;
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const int ny = (int)cyc + r - 1;
+            b[r] = e[r] = 0u;
+            if (in && nz >= 0 && nz < (int)g.nz && ny >= 0 && ny < (int)g.ny) {
+                const uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
+                b[r] = cell_start[row + x0];
+                // outside points: an empty range at their place in the row (walked later)
+                e[r] = inside ? min(cell_start[row + x1 + 1u], n) : b[r];
+            }
+        }
+        LightStream L;
+        light_stream(L, b, e, hr, in, lane);
+        for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // uniform
+            uint32_t j[kWinLoads];
+            window_indices(L, w0, lane, j);
+            float4 v[kWinLoads];
+#pragma unroll
+            for (int k = 0; k < kWinLoads; k++) v[k] = spos[j[k]];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int k = 0; k < kWinLoads; k++) s_p[k * kWave + lane] = v[k];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                const uint32_t jb = max(L.S[r], w0);
+                const uint32_t je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin);
+                for (uint32_t t = jb; t < je; t++) {
+                    const float4 p = s_p[t - w0];
+                    const float dx = p.x - q.x, dy2 = p.y - q.y, dz2 = p.z - q.z;
+                    const float dist_sq = dx * dx + dy2 * dy2 + dz2 * dz2;
+                    if (dist_sq <= radius_sq) {
+                        const float diff = radius_sq - dist_sq;
+                        cnt++;
+                        w += coeff * diff * diff * diff;
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    if (in && !inside) {  // rare: the reference's walk around an unclamped query cell
+        cnt = 0;
+        w = 0.0f;
+        const int64_t lx0 = cxu - 1 < 0 ? 0 : cxu - 1;
+        const int64_t lx1 = cxu + 1 > (int64_t)g.nx - 1 ? (int64_t)g.nx - 1 : cxu + 1;
+        for (int dz = -1; dz <= 1; dz++) {
+            const int64_t nz = czu + dz;
+            if (nz < 0 || nz >= (int64_t)g.nz) continue;
+            for (int dy = -1; dy <= 1; dy++) {
+                const int64_t ny = cyu + dy;
+                if (ny < 0 || ny >= (int64_t)g.ny || lx0 > lx1) continue;
+                const uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
+                const uint32_t jb = cell_start[row + (uint32_t)lx0];
+                const uint32_t je = min(cell_start[row + (uint32_t)lx1 + 1u], n);
+                for (uint32_t j = jb; j < je; j++) {
+                    const float4 p = spos[j];
+                    const float dx = p.x - q.x, dy2 = p.y - q.y, dz2 = p.z - q.z;
+                    const float dist_sq = dx * dx + dy2 * dy2 + dz2 * dz2;
+                    if (dist_sq <= radius_sq) {
+                        const float diff = radius_sq - dist_sq;
+                        cnt++;
+                        w += coeff * diff * diff * diff;
+                    }
+                }
+            }
+        }
+    }
+    if (!in) return;
+    const uint32_t i = sidx[s];
+    if (i >= n) return;
+    counts[i] = cnt;
+    if (wsum) wsum[i] = w;
+}
+
 // Batched HashGrid::query_neighbors: one thread per query, neighbour positions read through
 // sorted_indices from the caller's arrays exactly like hashgrid.rs:176-186.
 __global__ __launch_bounds__(256) void k_query(const float* __restrict__ x,
@@ -328,9 +438,8 @@ hipError_t launch_neighbor_query(fh_ctx* c, const float* x, const float* y, cons
     float h9 = h2 * h2 * h2 * h2 * h;
     float coeff = 315.0f / (64.0f * 3.14159265f * h9);
     tbeg(c, KID_NBR);
-    k_nbr_query<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->spos, sorted_indices, n, g,
-                                                          cell_start, radius * radius, coeff,
-                                                          counts, wsum);
+    k_nbr_stream<<<ceil_div(n, (uint32_t)kWave), kWave, 0, c->stream>>>(
+        c->spos, sorted_indices, n, g, cell_start, radius * radius, coeff, counts, wsum);
     tend(c, KID_NBR);
     return hipGetLastError();
 }

@@ -24,6 +24,7 @@
 // as (slab -1 + slab 0) + slab +1.  Differences to the CPU restatement are rounding only
 // (checked against rel 1e-4 on density and 1e-4 * sum|pair terms| on accelerations).
 #include "fh_internal.hpp"
+#include "fh_stream.hpp"
 
 namespace fh {
 
@@ -37,17 +38,6 @@ constexpr int kLightWaves = FH_LW;
 constexpr int kTileP = kLightWaves * 64;  // home particles per light workgroup
 constexpr int kStage = 512;   // neighbour particles staged per chunk
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
-
-__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, off, kWave));
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, kWave));
-    return v;
-}
 
 // p[i] if ok, else zero: the load always reads a valid element (index 0 when !ok) and the value
 // is selected afterwards (a select between two addresses would compile to a FLAT load).
@@ -593,107 +583,6 @@ __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[
     for (r = r + 1; r < 3; r++)
         if (pick3(lo, r) < pick3(hi, r)) break;
     return r;
-}
-
-// Light items.  The candidates of a wave are laid out as one stream: for each home-row segment
-// in lane order, the unions of its rows 0, 1, 2.  Every lane's own range of row r is then one
-// contiguous interval [S[r], S[r] + cnt[r]) of the stream.  The stream is staged through the
-// wave's LDS slice kWin candidates at a time, and all lanes (of every segment at once) evaluate
-// their own intervals clipped to the window: segments no longer take turns.
-constexpr int kWin = 256;  // candidates staged per window
-constexpr int kWinLoads = kWin / kWave;
-
-struct LightStream {
-    uint32_t S[3], cnt[3];  // the lane's own intervals
-    uint32_t T;             // stream length (wave-uniform)
-    int nseg;               // home-row segments (wave-uniform)
-    // segment table: lane q < nseg holds segment q's first stream position and row unions
-    // [lo[r], lo[r] + L[r])
-    uint32_t cb, clo0, clo1, clo2, cL0, cL1;
-};
-
-__device__ __forceinline__ void light_stream(LightStream& L, const uint32_t b[3],
-                                             const uint32_t e[3], uint32_t hr, bool in, int lane) {
-    const int nin = __popcll(__ballot(in));
-    const uint32_t hprev = (uint32_t)__shfl_up((int)hr, 1u, kWave);
-    const bool lead = in && (lane == 0 || hprev != hr);
-    const uint64_t starts = __ballot(lead);
-    const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
-    const uint64_t before = starts & upto, after = starts & ~upto;
-    const int leader = before ? 63 - __clzll((long long)before) : 0;
-    const int last = after ? __ffsll((unsigned long long)after) - 2 : nin - 1;
-    const uint32_t lo0 = (uint32_t)__shfl((int)b[0], leader, kWave);
-    const uint32_t lo1 = (uint32_t)__shfl((int)b[1], leader, kWave);
-    const uint32_t lo2 = (uint32_t)__shfl((int)b[2], leader, kWave);
-    const uint32_t hi0 = (uint32_t)__shfl((int)e[0], last < 0 ? 0 : last, kWave);
-    const uint32_t hi1 = (uint32_t)__shfl((int)e[1], last < 0 ? 0 : last, kWave);
-    const uint32_t hi2 = (uint32_t)__shfl((int)e[2], last < 0 ? 0 : last, kWave);
-    const uint32_t L0 = hi0 - lo0, L1 = hi1 - lo1;
-    const uint32_t len = L0 + L1 + (hi2 - lo2);
-    // inclusive scan of the segment lengths, counted at their leaders
-    uint32_t x = lead ? len : 0u;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const uint32_t y = (uint32_t)__shfl_up((int)x, (unsigned)d, kWave);
-        if (lane >= d) x += y;
-    }
-    L.T = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-    const uint32_t excl = x - (lead ? len : 0u);
-    const uint32_t base = (uint32_t)__shfl((int)excl, leader, kWave);
-    L.S[0] = base + (b[0] - lo0);
-    L.S[1] = base + L0 + (b[1] - lo1);
-    L.S[2] = base + L0 + L1 + (b[2] - lo2);
-#pragma unroll
-    for (int r = 0; r < 3; r++) L.cnt[r] = in ? e[r] - b[r] : 0u;
-    // segment table: each leader sends its segment to lane (its rank among the leaders); the
-    // other lanes send to lane 63, which is a table entry only when all 64 lanes lead
-    L.nseg = __popcll(starts);
-    const int rk = lead ? (int)__popcll(starts & (upto >> 1)) : 63;
-    const int to = rk << 2;
-    L.cb = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)base);
-    L.clo0 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)lo0);
-    L.clo1 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)lo1);
-    L.clo2 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)lo2);
-    L.cL0 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)L0);
-    L.cL1 = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)L1);
-}
-
-// Sorted index of stream position t (< T): the last segment that starts at or before t (a
-// binary search over the nseg table entries; none for one segment), then the row.
-__device__ __forceinline__ uint32_t stream_index(const LightStream& L, uint32_t t) {
-    uint32_t base, lo0, lo1, lo2, L0, L1;
-    if (L.nseg == 1) {  // wave-uniform: the one segment's values from lane 0
-        base = (uint32_t)__builtin_amdgcn_readlane((int)L.cb, 0);
-        lo0 = (uint32_t)__builtin_amdgcn_readlane((int)L.clo0, 0);
-        lo1 = (uint32_t)__builtin_amdgcn_readlane((int)L.clo1, 0);
-        lo2 = (uint32_t)__builtin_amdgcn_readlane((int)L.clo2, 0);
-        L0 = (uint32_t)__builtin_amdgcn_readlane((int)L.cL0, 0);
-        L1 = (uint32_t)__builtin_amdgcn_readlane((int)L.cL1, 0);
-    } else {
-        int pos = 0;
-        for (int step = 1 << (31 - __clz(L.nseg - 1)); step >= 1; step >>= 1) {  // uniform
-            const int c = pos + step;
-            const uint32_t sb = (uint32_t)__shfl((int)L.cb, c < L.nseg ? c : 0, kWave);
-            if (c < L.nseg && sb <= t) pos = c;
-        }
-        base = (uint32_t)__shfl((int)L.cb, pos, kWave);
-        lo0 = (uint32_t)__shfl((int)L.clo0, pos, kWave);
-        lo1 = (uint32_t)__shfl((int)L.clo1, pos, kWave);
-        lo2 = (uint32_t)__shfl((int)L.clo2, pos, kWave);
-        L0 = (uint32_t)__shfl((int)L.cL0, pos, kWave);
-        L1 = (uint32_t)__shfl((int)L.cL1, pos, kWave);
-    }
-    const uint32_t u = t - base;
-    return u < L0 ? lo0 + u : (u < L0 + L1 ? lo1 + (u - L0) : lo2 + (u - L0 - L1));
-}
-
-// Sorted indices of the window's staging slots: slot k * 64 + lane holds stream position
-// w0 + k * 64 + lane; positions past the stream repeat its last element.
-__device__ __forceinline__ void window_indices(const LightStream& L, uint32_t w0, int lane,
-                                               uint32_t j[kWinLoads]) {
-#pragma unroll
-    for (int k = 0; k < kWinLoads; k++)
-        j[k] = stream_index(L, min(w0 + (uint32_t)(k * kWave + lane), L.T - 1u));
 }
 
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
@@ -1414,11 +1303,23 @@ static float poly6_mc(float h, float mass) {
 
 
 // Fork the side stream off the main one (heavy kernels go there), and join it back.
-static hipError_t fork_side(fh_ctx* c) {
+#ifndef FH_SIDE_MODE
+#define FH_SIDE_MODE 7
+#endif
+// Which concurrent pairs use the side stream (bit 0: k_group beside k_plan, bit 1: the heavy
+// density kernel beside the light one, bit 2: the same for the force pass); otherwise the pair
+// runs one after the other on the context stream.
+constexpr uint32_t kSideGroup = 1u, kSideDensity = 2u, kSideForce = 4u;
+static hipStream_t side_of(fh_ctx* c, uint32_t use) {
+    return (FH_SIDE_MODE & use) ? c->side : c->stream;
+}
+static hipError_t fork_side(fh_ctx* c, uint32_t use) {
+    if (!(FH_SIDE_MODE & use)) return hipSuccess;
     hipError_t e = hipEventRecord(c->fork_ev, c->stream);
     return e == hipSuccess ? hipStreamWaitEvent(c->side, c->fork_ev, 0) : e;
 }
-static hipError_t join_side(fh_ctx* c) {
+static hipError_t join_side(fh_ctx* c, uint32_t use) {
+    if (!(FH_SIDE_MODE & use)) return hipSuccess;
     hipError_t e = hipEventRecord(c->join_ev, c->side);
     return e == hipSuccess ? hipStreamWaitEvent(c->stream, c->join_ev, 0) : e;
 }
@@ -1428,16 +1329,16 @@ static hipError_t join_side(fh_ctx* c) {
 // neighbour ranges whether or not k_group has moved it yet.
 hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
     if (a.n == 0) return hipSuccess;
-    hipError_t e = fork_side(c);
+    hipError_t e = fork_side(c, kSideGroup);
     if (e != hipSuccess) return e;
     // the candidate cells were listed with the cell ranges (k_cell_starts); scratch: the sort's
     // key buffer, free after the sort (disjoint ranges per cell)
-    tbeg(c, KID_GROUP, c->side);
-    k_group<<<256, kGroupThreads, 0, c->side>>>(c->big, ceil_div(c->max_n, 64u) + 1u, a.n,
+    tbeg(c, KID_GROUP, side_of(c, kSideGroup));
+    k_group<<<256, kGroupThreads, 0, side_of(c, kSideGroup)>>>(c->big, ceil_div(c->max_n, 64u) + 1u, a.n,
                                                 c->skeys, c->cell_start, c->spos,
                                                 with_vel ? c->svel : nullptr, c->sidx, c->rank,
                                                 c->ka, c->cell_grp, c->vrep, c->skip_tag, c->ctl);
-    tend(c, KID_GROUP, c->side);
+    tend(c, KID_GROUP, side_of(c, kSideGroup));
     e = hipGetLastError();
     tbeg(c, KID_PLAN);
     k_plan<<<ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0, c->stream>>>(
@@ -1445,7 +1346,7 @@ hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
         c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode, c->ctl);
     tend(c, KID_PLAN);
     if (e == hipSuccess) e = hipGetLastError();
-    const hipError_t j = join_side(c);  // joined even after a failed launch
+    const hipError_t j = join_side(c, kSideGroup);  // joined even after a failed launch
     return e != hipSuccess ? e : j;
 }
 
@@ -1453,13 +1354,13 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     if (a.n == 0) return hipSuccess;
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
-    hipError_t e = fork_side(c);
+    hipError_t e = fork_side(c, kSideDensity);
     if (e != hipSuccess) return e;
-    tbeg(c, KID_DHEAVY, c->side);
-    k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
+    tbeg(c, KID_DHEAVY, side_of(c, kSideDensity));
+    k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, side_of(c, kSideDensity)>>>(
         c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
         c->heavy_cap, c->skip_tag, c->ctl);
-    tend(c, KID_DHEAVY, c->side);
+    tend(c, KID_DHEAVY, side_of(c, kSideDensity));
     e = hipGetLastError();
     tbeg(c, KID_DENSITY);
     k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, a.n, a.g, cell_start, a.h * a.h,
@@ -1467,7 +1368,7 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
                                                    c->skip_tag, c->ctl);
     tend(c, KID_DENSITY);
     if (e == hipSuccess) e = hipGetLastError();
-    const hipError_t j = join_side(c);  // joined even after a failed launch
+    const hipError_t j = join_side(c, kSideDensity);  // joined even after a failed launch
     return e != hipSuccess ? e : j;
 }
 
@@ -1504,13 +1405,13 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     const FastForce K = fast_force(a);
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
-    hipError_t e = fork_side(c);
+    hipError_t e = fork_side(c, kSideForce);
     if (e != hipSuccess) return e;
-    tbeg(c, KID_FHEAVY, c->side);
-    k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, c->side>>>(
+    tbeg(c, KID_FHEAVY, side_of(c, kSideForce));
+    k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, side_of(c, kSideForce)>>>(
         c->spos, c->svel, c->srho, c->sout, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
         c->wpart, c->max_n, c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
-    tend(c, KID_FHEAVY, c->side);
+    tend(c, KID_FHEAVY, side_of(c, kSideForce));
     e = hipGetLastError();
     tbeg(c, KID_FORCE);
     k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, a.n, a.g,
@@ -1518,7 +1419,7 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
                                                  c->heavy_flag, c->skip_tag, c->ctl);
     tend(c, KID_FORCE);
     if (e == hipSuccess) e = hipGetLastError();
-    const hipError_t j = join_side(c);
+    const hipError_t j = join_side(c, kSideForce);
     return e != hipSuccess ? e : j;
 }
 
