@@ -30,7 +30,10 @@ constexpr int kSortTileLarge = kSortThreads * kSortItemsLarge;
 constexpr uint32_t kSortLargeN = 1u << 22;
 constexpr int kMaxPasses = 4;          // 8-bit digits, up to 32-bit keys
 constexpr int kHistThreads = 256;
-constexpr int kHistItems = 16;
+#ifndef FH_HIST_ITEMS
+#define FH_HIST_ITEMS 16
+#endif
+constexpr int kHistItems = FH_HIST_ITEMS;
 constexpr int kHistChunk = kHistThreads * kHistItems;  // keys per histogram chunk
 #ifndef FH_HIST_BLOCKS
 #define FH_HIST_BLOCKS 1024

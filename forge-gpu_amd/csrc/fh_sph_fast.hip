@@ -202,25 +202,24 @@ __device__ __forceinline__ uint32_t match_bits(const float4* __restrict__ spos, 
 }
 
 // Blocked layout: thread t owns particles [f + t L, f + (t + 1) L) of the cell, L = ceil(cnt / 1024).
-__global__ __launch_bounds__(kGroupThreads) void k_group(const uint2* __restrict__ big,
-                                                         uint32_t cap, uint32_t n,
-                                                         const uint32_t* __restrict__ skeys,
-                                                         const uint32_t* __restrict__ cstart,
-                                                         float4* __restrict__ spos,
-                                                         float4* __restrict__ svel,
-                                                         uint32_t* __restrict__ sidx,
-                                                         uint32_t* __restrict__ rank,
-                                                         uint32_t* __restrict__ scratch,
-                                                         uint64_t* __restrict__ cell_grp,
-                                                         float4* __restrict__ vrep,
-                                                         uint32_t* __restrict__ skip_tag,
-                                                         const Control* __restrict__ ctl) {
+__device__ __forceinline__ void group_work(uint32_t bid, uint32_t nb, const uint2* __restrict__ big,
+                                           uint32_t cap, uint32_t n,
+                                           const uint32_t* __restrict__ skeys,
+                                           const uint32_t* __restrict__ cstart,
+                                           float4* __restrict__ spos, float4* __restrict__ svel,
+                                           uint32_t* __restrict__ sidx,
+                                           uint32_t* __restrict__ rank,
+                                           uint32_t* __restrict__ scratch,
+                                           uint64_t* __restrict__ cell_grp,
+                                           float4* __restrict__ vrep,
+                                           uint32_t* __restrict__ skip_tag,
+                                           const Control* __restrict__ ctl) {
     __shared__ uint32_t s_scan[kGroupWaves];
     __shared__ float s_w[kGroupWaves];
     const uint32_t tid = threadIdx.x;
     const uint32_t count = min(ctl->big_count.v, cap);
     const uint32_t epoch = ctl->epoch;
-    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform
+    for (uint32_t q = bid; q < count; q += nb) {  // uniform
         const uint32_t f = big[q].x, cnt = min(cstart[skeys[f] + 1u], n) - f, end = f + cnt;
         const float4 P = spos[f + cnt / 2u];
         const uint32_t L = ceil_div(cnt, (uint32_t)kGroupThreads);
@@ -476,18 +475,18 @@ __device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
 // heavy when its largest per-particle candidate count (a cell that may hold a group counting
 // once) exceeds heavy_work or when it touches such a cell, and transposed (heavy) when its
 // stream is much longer than that count.
-__global__ __launch_bounds__(kPlanThreads) void k_plan(const float4* __restrict__ spos,
-                                                       uint32_t n, GridDesc g,
-                                                       const uint32_t* __restrict__ cstart,
-                                                       const uint64_t* __restrict__ cand_tag,
-                                                       uint8_t* __restrict__ flag,
-                                                       uint32_t* __restrict__ heavy,
-                                                       uint32_t heavy_cap, uint32_t heavy_work,
-                                                       uint32_t direct_mode, Control* ctl) {
+__device__ __forceinline__ void plan_work(uint32_t bid, const float4* __restrict__ spos,
+                                          uint32_t n, GridDesc g,
+                                          const uint32_t* __restrict__ cstart,
+                                          const uint64_t* __restrict__ cand_tag,
+                                          uint8_t* __restrict__ flag,
+                                          uint32_t* __restrict__ heavy, uint32_t heavy_cap,
+                                          uint32_t heavy_work, uint32_t direct_mode,
+                                          Control* ctl) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
     __shared__ uint32_t s_count[kWaves];
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t s = bid * blockDim.x + threadIdx.x;
     const uint32_t sub = s / kSub;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const bool live = s < n;
@@ -532,7 +531,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(const float4* __restrict_
     if (threadIdx.x == 0) {
         uint32_t tot = 0;
         for (int w = 0; w < kWaves; w++) tot += s_count[w];
-        s_base = tot ? atomicAdd(&ctl->heavy_count[blockIdx.x % kHeavyLists].v, tot) : 0u;
+        s_base = tot ? atomicAdd(&ctl->heavy_count[bid % kHeavyLists].v, tot) : 0u;
     }
     __syncthreads();
     if (threadIdx.x < kWaves * 3) {
@@ -542,9 +541,30 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(const float4* __restrict_
         if ((uint32_t)k < s_count[w]) {
             const uint32_t pos = s_base + off + (uint32_t)k;
             if (pos < heavy_cap)
-                heavy[(size_t)(blockIdx.x % kHeavyLists) * heavy_cap + pos] = s_item[w * 3 + k];
+                heavy[(size_t)(bid % kHeavyLists) * heavy_cap + pos] = s_item[w * 3 + k];
         }
     }
+}
+
+// Co-located groups and the work plan in one launch: the first kGroupBlocks workgroups walk the
+// candidate group cells (k_cell_starts' list), the others plan the items.  The plan needs only
+// the cells that may hold a group (tagged by k_cell_starts), not their outcome, and every
+// particle of a cell gives the cell's neighbour ranges whether or not it has been moved yet.
+constexpr uint32_t kGroupBlocks = 64;
+__global__ __launch_bounds__(kPlanThreads) void k_group_plan(
+    const uint2* __restrict__ big, uint32_t cap, uint32_t n, const uint32_t* __restrict__ skeys,
+    const uint32_t* __restrict__ cstart, float4* __restrict__ spos, float4* __restrict__ svel,
+    uint32_t* __restrict__ sidx, uint32_t* __restrict__ rank, uint32_t* __restrict__ scratch,
+    uint64_t* __restrict__ cell_grp, float4* __restrict__ vrep, uint32_t* __restrict__ skip_tag,
+    GridDesc g, const uint64_t* __restrict__ cand_tag, uint8_t* __restrict__ flag,
+    uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t heavy_work, uint32_t direct_mode,
+    Control* ctl) {
+    if (blockIdx.x < kGroupBlocks)
+        group_work(blockIdx.x, kGroupBlocks, big, cap, n, skeys, cstart, spos, svel, sidx, rank,
+                   scratch, cell_grp, vrep, skip_tag, ctl);
+    else
+        plan_work(blockIdx.x - kGroupBlocks, spos, n, g, cstart, cand_tag, flag, heavy,
+                  heavy_cap, heavy_work, direct_mode, ctl);
 }
 
 // The heavy work lists of this substep as one sequence: entry q of the concatenation of the
@@ -1324,30 +1344,19 @@ static hipError_t join_side(fh_ctx* c, uint32_t use) {
     return e == hipSuccess ? hipStreamWaitEvent(c->stream, c->join_ev, 0) : e;
 }
 
-// k_group on the side stream beside k_plan: the plan needs only the cells that may hold a group
-// (tagged by k_cell_starts), not their outcome, and every particle of a cell gives the cell's
-// neighbour ranges whether or not k_group has moved it yet.
 hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
     if (a.n == 0) return hipSuccess;
-    hipError_t e = fork_side(c, kSideGroup);
-    if (e != hipSuccess) return e;
-    // the candidate cells were listed with the cell ranges (k_cell_starts); scratch: the sort's
-    // key buffer, free after the sort (disjoint ranges per cell)
-    tbeg(c, KID_GROUP, side_of(c, kSideGroup));
-    k_group<<<256, kGroupThreads, 0, side_of(c, kSideGroup)>>>(c->big, ceil_div(c->max_n, 64u) + 1u, a.n,
-                                                c->skeys, c->cell_start, c->spos,
-                                                with_vel ? c->svel : nullptr, c->sidx, c->rank,
-                                                c->ka, c->cell_grp, c->vrep, c->skip_tag, c->ctl);
-    tend(c, KID_GROUP, side_of(c, kSideGroup));
-    e = hipGetLastError();
+    // scratch of k_group: the sort's key buffer, free after the sort (disjoint ranges per cell)
     tbeg(c, KID_PLAN);
-    k_plan<<<ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0, c->stream>>>(
-        c->spos, a.n, a.g, c->cell_start, c->run_tag, c->heavy_flag, c->heavy, c->heavy_cap,
-        c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode, c->ctl);
+    k_group_plan<<<kGroupBlocks + ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0,
+                   c->stream>>>(c->big, ceil_div(c->max_n, 64u) + 1u, a.n, c->skeys, c->cell_start,
+                                c->spos, with_vel ? c->svel : nullptr, c->sidx, c->rank, c->ka,
+                                c->cell_grp, c->vrep, c->skip_tag, a.g, c->run_tag,
+                                c->heavy_flag, c->heavy, c->heavy_cap,
+                                c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode,
+                                c->ctl);
     tend(c, KID_PLAN);
-    if (e == hipSuccess) e = hipGetLastError();
-    const hipError_t j = join_side(c, kSideGroup);  // joined even after a failed launch
-    return e != hipSuccess ? e : j;
+    return hipGetLastError();
 }
 
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start) {
