@@ -111,7 +111,7 @@ constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
 #endif
 constexpr uint32_t kTransRatio = FH_TRANS_RATIO, kTransOffset = FH_TRANS_OFFSET;
 #ifndef FH_HGRID
-#define FH_HGRID 1024
+#define FH_HGRID 4096
 #endif
 constexpr uint32_t kHeavyGrid = FH_HGRID;  // heavy workgroups (grid-stride over the list)
 #ifndef FH_HU
