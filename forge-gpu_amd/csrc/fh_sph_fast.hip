@@ -97,19 +97,22 @@ constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
 // spread along a row beside a dense one), so the union of a segment's ranges -- what the shared
 // walk stages and every lane steps through -- is many times longer than any one particle's
 // range.  The item is walked the other way round: one particle at a time, its candidates spread
-// over the 64 lanes (coalesced loads), a wave reduction per particle.  Chosen when the stream
-// is longer than kTransRatio times the largest particle's candidate count plus kTransOffset
-// (below that the per-particle reductions cost more than the idle lanes).
+// over the 64 lanes (coalesced loads), a wave reduction per particle.  Chosen for a heavy item
+// when the stream is longer than kTransRatio times the largest particle's candidate count plus
+// kTransOffset (below that the per-particle reductions cost more than the idle lanes), and for
+// a light item only when it is pathologically longer (kTransLightRatio, kTransLightOffset): a
+// light wave would then step through window after window serving one lane at a time.
 #ifndef FH_TRANS_RATIO
 #define FH_TRANS_RATIO 4
 #endif
-#ifndef FH_TRANS_TOUCH
-#define FH_TRANS_TOUCH 1
+#ifndef FH_TRANS_LIGHT_RATIO
+#define FH_TRANS_LIGHT_RATIO 16
 #endif
 #ifndef FH_TRANS_OFFSET
 #define FH_TRANS_OFFSET 512
 #endif
 constexpr uint32_t kTransRatio = FH_TRANS_RATIO, kTransOffset = FH_TRANS_OFFSET;
+constexpr uint32_t kTransLightRatio = FH_TRANS_LIGHT_RATIO, kTransLightOffset = 2048;
 #ifndef FH_HGRID
 #define FH_HGRID 4096
 #endif
@@ -508,9 +511,12 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const float4* __restrict
                 const bool touches = __ballot(excess > 0u) != 0ull;
                 bool hv = w > heavy_work || touches;  // light items hold no group
                 bool trans = direct_mode == 2u;
-                if (direct_mode == 1u && hv) {
+                if (direct_mode == 1u) {
+                    // a light item only when its stream is far longer (pathologically
+                    // disjoint ranges: one window would serve one lane at a time)
                     const uint32_t T = stream_total(b, e, home_row(pi, g), live, lane);
-                    trans = T > kTransRatio * w + kTransOffset && (FH_TRANS_TOUCH || !touches);
+                    trans = hv ? T > kTransRatio * w + kTransOffset
+                               : T > kTransLightRatio * w + kTransLightOffset;
                 }
                 hv = hv || trans;
                 if (lane == 0) {
