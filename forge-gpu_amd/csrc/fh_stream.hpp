@@ -32,7 +32,10 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
 // contiguous interval [S[r], S[r] + cnt[r]) of the stream.  The stream is staged through the
 // wave's LDS slice kWin candidates at a time, and all lanes (of every segment at once) evaluate
 // their own intervals clipped to the window: segments no longer take turns.
-constexpr int kWin = 256;  // candidates staged per window
+#ifndef FH_WIN
+#define FH_WIN 192
+#endif
+constexpr int kWin = FH_WIN;  // candidates staged per window
 constexpr int kWinLoads = kWin / kWave;
 
 struct LightStream {
