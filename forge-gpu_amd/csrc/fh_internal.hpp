@@ -50,8 +50,8 @@ constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
 constexpr uint32_t kCollapseMin = 64;
 constexpr uint32_t kRepFlag = 0x80000000u;
 // A cell of >= kCollapseMin particles is examined in full only when at least kGroupHits of
-// kGroupSamples evenly spaced particles sit at the position of its middle particle (groups that
-// are a small minority of their cell are not collapsed; results are the same either way).
+// kGroupSamples evenly spaced particles sit at the position of one of them (groups that are a
+// small minority of their cell are not collapsed; results are the same either way).
 constexpr uint32_t kGroupSamples = 16;
 constexpr uint32_t kGroupHits = 4;
 // The heavy SPH work list is split into kHeavyLists sub-lists with counters on separate lines,
@@ -150,7 +150,7 @@ struct fh_ctx {
     uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
     uint64_t* cell_grp;  // [max_cells] epoch << 32 | number of co-located leading particles
-    uint2* big;          // [ceil(max_n / 64) + 1] (first, count) of cells of >= kCollapseMin
+    uint2* big;          // [ceil(max_n / 64) + 1] (first slot, sample offset) of group cells
     uint32_t* skip_tag;  // [ceil(max_n / 64)] epoch of the rebuild whose sub-tile holds only group members
     float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
     float4* vrep;        // [max_n] summed velocity of the group, at representative indices

@@ -60,8 +60,9 @@ __device__ __forceinline__ void fill_cells(uint32_t* __restrict__ cell_start, ui
 // Cell ranges, and (big != null) the candidate co-located groups: runs of at least
 // kCollapseMin keys in which at least kGroupHits of kGroupSamples evenly spaced particles (over
 // the first L of the run, L its length rounded down to a power of two) sit at the position of
-// the middle one.  Listed as (first slot, 0) -- k_group counts the run and its members exactly
-// -- and tagged with the epoch in cand_tag[cell] for k_plan, which runs beside k_group.
+// one of them.  Listed as (first slot, offset of that sample) -- the group pass counts the run
+// and the members at that sample's position exactly -- and tagged with the epoch in
+// cand_tag[cell] for the plan, which runs beside the group pass.
 __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict__ skeys,
                                                      uint32_t n, uint32_t C,
                                                      uint32_t* __restrict__ cell_start,
@@ -92,17 +93,32 @@ __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict_
     if (cand) {  // rare: a run of at least kCollapseMin
         uint32_t L = kCollapseMin;
         while (L < (1u << 30) && s + 2u * L - 1u < n && skeys[s + 2u * L - 1u] == k) L *= 2u;
-        const float4 P = spos[s + L / 2u];
-        uint32_t hits = 0;
+        // The samples are loaded once; the middle one is tried first as the group's position,
+        // then each other in turn (a corner group can fill all but the middle of a run).
+        uint32_t sx[kGroupSamples], sy[kGroupSamples], sz[kGroupSamples];
+#pragma unroll
         for (uint32_t q = 0; q < kGroupSamples; q++) {
             const float4 v = spos[s + (q * L) / kGroupSamples];
-            hits += (__float_as_uint(v.x) == __float_as_uint(P.x) &&
-                     __float_as_uint(v.y) == __float_as_uint(P.y) &&
-                     __float_as_uint(v.z) == __float_as_uint(P.z)) ? 1u : 0u;
+            sx[q] = __float_as_uint(v.x);
+            sy[q] = __float_as_uint(v.y);
+            sz[q] = __float_as_uint(v.z);
+        }
+        uint32_t off = 0, hits = 0;
+#pragma unroll
+        for (uint32_t a = 0; a < kGroupSamples; a++) {
+            const uint32_t qa = a == 0u ? kGroupSamples / 2u : (a <= kGroupSamples / 2u ? a - 1u : a);
+            uint32_t hq = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < kGroupSamples; q++)
+                hq += (sx[q] == sx[qa] && sy[q] == sy[qa] && sz[q] == sz[qa]) ? 1u : 0u;
+            if (hits < kGroupHits) {
+                hits = hq;
+                off = (qa * L) / kGroupSamples;
+            }
         }
         if (hits >= kGroupHits) {
             const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
-            if (slot < cap) big[slot] = make_uint2(s, 0u);
+            if (slot < cap) big[slot] = make_uint2(s, off);
             cand_tag[k] = (uint64_t)ctl->epoch << 32;  // k_plan: this cell may hold a group
         }
     }

@@ -224,7 +224,7 @@ __device__ __forceinline__ void group_work(uint32_t bid, uint32_t nb, const uint
     const uint32_t epoch = ctl->epoch;
     for (uint32_t q = bid; q < count; q += nb) {  // uniform
         const uint32_t f = big[q].x, cnt = min(cstart[skeys[f] + 1u], n) - f, end = f + cnt;
-        const float4 P = spos[f + cnt / 2u];
+        const float4 P = spos[f + big[q].y];  // the sample that k_cell_starts matched
         const uint32_t L = ceil_div(cnt, (uint32_t)kGroupThreads);
         const uint32_t t0 = min(f + tid * L, end), t1 = min(t0 + L, end);
         // Membership bits of the thread's particles (L <= 32 kept in a register word; larger

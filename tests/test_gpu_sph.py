@@ -176,7 +176,19 @@ def colocated_cfg(n=40_000, seed=33):
     perm = rng.permutation(cfg.n)
     for a in ("x", "y", "z"):
         setattr(cfg, a, np.ascontiguousarray(getattr(cfg, a)[perm]))
-    vel = [rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
+    # A cell of 1000 (in an empty part of the box) whose sorted run holds one point at both
+    # ends and 271 distinct points in the middle (run slots 250..520): the middle sample and
+    # the middle slot are not in the group, which is found from another sample.  The run
+    # order is the particle order (stable sort), so the 1000 are taken in index order from
+    # former lattice particles.
+    idx = np.nonzero(perm >= at)[0][:1000]
+    mid = np.zeros(1000, bool)
+    mid[250:521] = True
+    cfg.x[idx] = np.float32(0.905)
+    cfg.y[idx] = np.float32(0.505)
+    cfg.z[idx] = np.float32(0.305)
+    cfg.x[idx[mid]] = np.float32(0.905) + np.arange(1, 272, dtype=np.float32) * np.float32(1e-5)
+    vel =[rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
     return cfg, vel
 
 
