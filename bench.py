@@ -38,14 +38,14 @@ for _p in (REPO, REPO / "forge-gpu_amd"):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 METRIC = "SPH particle-steps/s @1M; radix sort Gkeys/s; achieved HBM GB/s vs peak"
-KERNELS = ["hash", "sort", "gather", "scan", "group", "plan", "density", "density_heavy",
+KERNELS = ["hash", "sort", "gather", "scan", "plan", "density", "density_heavy",
            "prep", "force", "force_heavy", "finalize"]
 # A "pass" groups the kernels of one stage of the substep; its duration per substep is the sum
 # of its kernels' launch durations, or its wall time for the two passes whose kernels overlap
 # (the heavy kernels of a pass process the items its light kernel skips, so the pair moves the
 # pass's bytes together).
 PASSES = {"hash": ["hash"], "sort": ["sort"], "gather": ["gather"], "scan": ["scan"],
-          "plan": ["group", "plan"], "density": ["density", "density_heavy"],
+          "plan": ["plan"], "density": ["density", "density_heavy"],
           "force": ["prep", "force", "force_heavy"], "finalize": ["finalize"]}
 # The density and force passes run their light and heavy kernels concurrently on two streams:
 # their duration is the pass's wall time (first launch to the join), from these timers.

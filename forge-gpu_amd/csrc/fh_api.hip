@@ -554,7 +554,7 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
 static const char* const kKernelNames[KID_COUNT] = {"hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
                                                     "finalize", "runs", "plan",
-                                                    "density_heavy", "force_heavy", "group",
+                                                    "density_heavy", "force_heavy",
                                                     "prep", "density_pass", "force_pass"};
 
 static int kernel_id(const char* name) {

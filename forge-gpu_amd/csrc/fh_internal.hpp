@@ -105,7 +105,7 @@ struct GridDesc {
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
 enum KernelId { KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
                 KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_DHEAVY, KID_FHEAVY,
-                KID_GROUP, KID_PREP, KID_DPASS, KID_FPASS, KID_COUNT };
+                KID_PREP, KID_DPASS, KID_FPASS, KID_COUNT };
 
 // Event pairs bracketing the first `max` launches of one kernel after it was armed; when the
 // launches are captured, every replay of the graph re-records the same events.
