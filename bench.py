@@ -181,12 +181,12 @@ def bench_sph(args, fh, torch, log):
     ev_ms = ctx.event_elapsed_ms(0, 1)
     log(f"timed {K} substeps: wall {wall * 1e3:.2f} ms, events {ev_ms:.2f} ms")
 
-    # Per-kernel durations: G more substeps launched eagerly on the same stream with every
-    # kernel bracketed by HIP events (events recorded by graph nodes cannot be timed on HIP).
+    # Per-kernel durations: the G substeps of the graph once more, launched eagerly on the same
+    # stream with every kernel bracketed by HIP events (events recorded by graph nodes cannot be
+    # timed on HIP).
     for k in KERNELS + list(PASS_TIMERS.values()):
         ctx.time_kernel(k, (passes if k == "sort" else 1) * G)
-    for _ in range(G):
-        pipe.step_async(fields, cfg.dt)
+    pipe.run_async(fields, cfg.dt, G)
     ctx.sync()
     kern = {}
     for k in KERNELS + list(PASS_TIMERS.values()):

@@ -102,6 +102,18 @@ hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float
     return e;
 }
 
+// The same from the previous substep's new state in sorted order (c->sout: (x, y, z, rho),
+// (vx, vy, vz, .) per slot), whose slots take the place of particle ids as sort values.
+hipError_t sph_rebuild_resident(fh_ctx* c, const GridDesc& g, uint32_t cells, uint32_t n) {
+    const uint32_t bits = bits_for_cells(cells);
+    const float* so = reinterpret_cast<const float*>(c->sout);
+    hipError_t e = launch_hash_hist(c, so, so + 1, so + 2, 8, n, g, bits, c->kb, nullptr, true);
+    if (e == hipSuccess && n > 0)
+        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx2, n, bits);
+    if (e == hipSuccess) e = launch_gather_resident(c, cells, n);
+    return e;
+}
+
 }  // namespace
 
 extern "C" {
@@ -166,6 +178,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->vrep, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->rank, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sout, 3 * (size_t)max_n, &tot);
+    if (e == hipSuccess) e = alloc(&c->sidx2, max_n, &tot);
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_error, sizeof(uint32_t), hipHostMallocDefault);
     if (e == hipSuccess) {
         if (stream) {
@@ -219,7 +232,8 @@ int fh_destroy(fh_ctx* c) {
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
                     c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hist_part,
-                    c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout};
+                    c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout,
+                    c->sidx2};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);
@@ -381,27 +395,39 @@ int fh_sph_density(fh_ctx* c, const fh_sph_params* prm, const float* px, const f
     return FH_OK;
 }
 
-int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
-                 float* py, float* pz, float* vx, float* vy, float* vz, float* density,
-                 float* accel, uint32_t n, float dt) {
+// `steps` substeps of the fused SPH step.  The first rebuilds from the caller's arrays; in the
+// fast mode the later ones start from the previous substep's new state, kept in sorted order
+// (resident), and only the last moves its state to the caller's arrays.
+static int sph_fused_steps(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi,
+                           float* px, float* py, float* pz, float* vx, float* vy, float* vz,
+                           float* density, float* accel, uint32_t n, float dt, uint32_t steps,
+                           const char* what) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (n && (!px || !py || !pz || !vx || !vy || !vz || !density))
-        return fail(FH_EINVAL, "fh_sph_fused: null pointer");
-    if ((rc = check_n(c, n, "fh_sph_fused"))) return rc;
+        return fail(FH_EINVAL, "%s: null pointer", what);
+    if (steps == 0) return fail(FH_EINVAL, "%s: steps must be >= 1", what);
+    if ((rc = check_n(c, n, what))) return rc;
     if (epi && (epi->flags & ~(FH_EPI_GRAVITY | FH_EPI_INTEGRATE | FH_EPI_BOX)))
-        return fail(FH_EINVAL, "fh_sph_fused: unknown epilogue flags 0x%x", epi->flags);
+        return fail(FH_EINVAL, "%s: unknown epilogue flags 0x%x", what, epi->flags);
     GridDesc g;
     uint32_t cells;
-    if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_fused"))) return rc;
-    FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, vx, vy, vz, n, true));
-    if (n == 0) return FH_OK;
+    if ((rc = check_sph(c, prm, &g, &cells, what))) return rc;
     SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
               prm->rest_density, prm->viscosity_coefficient, dt, n};
-    if (c->sph_exact) {
-        FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
-        FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
-    } else {
+    for (uint32_t k = 0; k < steps; k++) {
+        const bool resident = k > 0 && !c->sph_exact && n > 0;
+        const bool last = k + 1 == steps || c->sph_exact;
+        if (resident)
+            FH_CHECK_HIP(sph_rebuild_resident(c, g, cells, n));
+        else
+            FH_CHECK_HIP(sph_rebuild(c, g, cells, px, py, pz, vx, vy, vz, n, true));
+        if (n == 0) continue;
+        if (c->sph_exact) {
+            FH_CHECK_HIP(launch_density(c, a, c->cell_start, density));
+            FH_CHECK_HIP(launch_force(c, a, epi, c->cell_start, px, py, pz, vx, vy, vz, accel));
+            continue;
+        }
         FH_CHECK_HIP(launch_group_plan(c, a, true));
         // pass timers: first launch to the join of the side stream (wall time of the pass)
         tbeg(c, KID_DPASS);
@@ -411,9 +437,24 @@ int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, fl
         FH_CHECK_HIP(launch_prep(c, a));
         FH_CHECK_HIP(launch_force_fast(c, a, c->cell_start));
         tend(c, KID_FPASS);
-        FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density, accel));
+        FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density,
+                                     last ? accel : nullptr, last, last && steps > 1));
     }
     return FH_OK;
+}
+
+int fh_sph_fused(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
+                 float* py, float* pz, float* vx, float* vy, float* vz, float* density,
+                 float* accel, uint32_t n, float dt) {
+    return sph_fused_steps(c, prm, epi, px, py, pz, vx, vy, vz, density, accel, n, dt, 1u,
+                           "fh_sph_fused");
+}
+
+int fh_sph_fused_steps(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
+                       float* py, float* pz, float* vx, float* vy, float* vz, float* density,
+                       float* accel, uint32_t n, float dt, uint32_t steps) {
+    return sph_fused_steps(c, prm, epi, px, py, pz, vx, vy, vz, density, accel, n, dt, steps,
+                           "fh_sph_fused_steps");
 }
 
 static int unfused(fh_ctx* c, bool viscosity, const fh_sph_params* prm, const float* px,

@@ -155,8 +155,10 @@ struct fh_ctx {
     float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
     float4* vrep;        // [max_n] summed velocity of the group, at representative indices
     uint32_t* rank;      // [max_n] sorted position of each particle (inverse of sidx)
+    uint32_t* sidx2;     // [max_n] resident substeps: previous slot of each new slot
     float4* sout;        // [3 * max_n] new state in sorted order before it is moved to particle
-                         // order: pairs (x, y, z, rho), (vx, vy, vz, .), then (ax, ay, az, .)
+                         // order: pairs (x, y, z, rho), (vx, vy, vz, particle id), then
+                         // (ax, ay, az, .); the next substep's input in resident substeps
     bool sph_exact;      // FH_OPT_SPH_EXACT
     uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
     uint32_t direct_mode; // FH_OPT_DIRECT_ITEMS: 0 never, 1 automatic (default), 2 always
@@ -299,20 +301,28 @@ struct SphArgs {
 hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
                          const float* py, const float* pz, const float* vx, const float* vy,
                          const float* vz, uint32_t n, bool with_vel, bool list_big);
+// Resident substeps: the same from the previous substep's sorted state (c->sout), whose slots
+// the sort of its keys took as values (sorted: c->sidx2, the previous slot of each new slot).
+// The particle ids travel in svel[.].w; c->sidx and c->rank are not maintained (launch_finalize
+// rebuilds c->rank from the ids before the final move to particle order).
+hipError_t launch_gather_resident(fh_ctx* c, uint32_t cells, uint32_t n);
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 // Force records of every sorted particle (positions with pressure, velocity and weight over
 // density; density in srho) from the density partials; written into c->sout, which holds the
 // new state only after the force pass.
 hipError_t launch_prep(fh_ctx* c, const SphArgs& a);
-// Fast passes only: list the cells of >= kCollapseMin particles and move the particles that
-// share the position of the cell's middle particle to the front of the cell when they are at
-// least kCollapseMin (cell_grp).  Reorders spos / svel / sidx inside those cells.
-// Co-located groups (k_group, side stream) beside the work plan of the fast passes (k_plan).
+// Fast passes only, one launch: in the cells listed by k_cell_starts, move the particles that
+// share the matched sample's position to the front of the cell when they are at least
+// kCollapseMin (cell_grp; reorders spos / svel / sidx / rank inside those cells), beside the
+// work plan of the fast passes.
 hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel);
+// New state in sorted order (c->sout); with `to_particles`, also moved to the caller's arrays
+// (`rebuild_rank`: first recompute c->rank from c->sidx, after resident substeps).
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
                            bool density_only, float* px, float* py, float* pz, float* vx,
-                           float* vy, float* vz, float* density, float* accel);
+                           float* vy, float* vz, float* density, float* accel,
+                           bool to_particles = true, bool rebuild_rank = false);
 hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start,
                           float* density_out);
 hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,

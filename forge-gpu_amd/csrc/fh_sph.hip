@@ -19,8 +19,10 @@ namespace fh {
 
 // Sorted-order copies of the state.  The sort's last pass wrote rank[i] = sorted slot of
 // particle i; k_gather (particle order) writes spos[rank[i]] = (pos[i], bits of rank[i]) and
-// svel[rank[i]] = vel[i] -- the caller's arrays are read in order and each particle costs two
-// 16-byte stores, instead of six 4-byte reads from scattered lines.
+// svel[rank[i]] = (vel[i], bits of i) -- the caller's arrays are read in order and each
+// particle costs two 16-byte stores, instead of six 4-byte reads from scattered lines.  The
+// particle id in svel[.].w travels with the particle through later reorderings (co-located
+// groups, resident substeps) and into the new state (k_finalize).
 __global__ __launch_bounds__(256) void k_gather(
     const float* __restrict__ px, const float* __restrict__ py, const float* __restrict__ pz,
     const float* __restrict__ vx, const float* __restrict__ vy, const float* __restrict__ vz,
@@ -31,7 +33,7 @@ __global__ __launch_bounds__(256) void k_gather(
     const uint32_t r = rank[i];
     if (r >= n) return;  // never taken when the sort is consistent
     spos[r] = make_float4(px[i], py[i], pz[i], __uint_as_float(r));
-    if (svel) svel[r] = make_float4(vx[i], vy[i], vz[i], 0.0f);
+    if (svel) svel[r] = make_float4(vx[i], vy[i], vz[i], __uint_as_float(i));
 }
 
 // CSR cell ranges straight from the sorted keys, no scan: the key in slot s starts its run when
@@ -124,6 +126,15 @@ __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict_
     }
 }
 
+static hipError_t launch_cell_starts(fh_ctx* c, uint32_t cells, uint32_t n, bool list_big) {
+    tbeg(c, KID_SCAN);
+    k_cell_starts<<<ceil_div(n, 256u), 256, 0, c->stream>>>(
+        c->skeys, n, cells, c->cell_start, c->spos, list_big ? c->big : nullptr,
+        ceil_div(c->max_n, 64u) + 1u, c->run_tag, c->ctl);
+    tend(c, KID_SCAN);
+    return hipGetLastError();
+}
+
 hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
                          const float* py, const float* pz, const float* vx, const float* vy,
                          const float* vz, uint32_t n, bool with_vel, bool list_big) {
@@ -135,12 +146,33 @@ hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const flo
     hipError_t e = hipGetLastError();
     tend(c, KID_GATHER);
     if (e != hipSuccess) return e;
-    tbeg(c, KID_SCAN);
-    k_cell_starts<<<ceil_div(n, 256u), 256, 0, c->stream>>>(
-        c->skeys, n, cells, c->cell_start, c->spos, list_big ? c->big : nullptr,
-        ceil_div(c->max_n, 64u) + 1u, c->run_tag, c->ctl);
-    tend(c, KID_SCAN);
-    return hipGetLastError();
+    return launch_cell_starts(c, cells, n, list_big);
+}
+
+// Resident substeps: new slot r takes the state of previous slot prev[r] from c->sout (one
+// 32-byte read: (x, y, z, rho), (vx, vy, vz, particle id)) and writes spos / svel in order.
+__global__ __launch_bounds__(256) void k_gather_resident(const float4* __restrict__ sout,
+                                                         const uint32_t* __restrict__ prev,
+                                                         uint32_t n, float4* __restrict__ spos,
+                                                         float4* __restrict__ svel) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const uint32_t q = prev[r];
+    if (q >= n) return;  // never taken when the sort is consistent
+    const float4 p = sout[2u * q], v = sout[2u * q + 1u];
+    spos[r] = make_float4(p.x, p.y, p.z, __uint_as_float(r));
+    svel[r] = v;
+}
+
+hipError_t launch_gather_resident(fh_ctx* c, uint32_t cells, uint32_t n) {
+    if (n == 0) return launch_fill_u32(c, c->cell_start, 0u, cells + 1u);
+    tbeg(c, KID_GATHER);
+    k_gather_resident<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->sout, c->sidx2, n, c->spos,
+                                                                c->svel);
+    hipError_t e = hipGetLastError();
+    tend(c, KID_GATHER);
+    if (e != hipSuccess) return e;
+    return launch_cell_starts(c, cells, n, true);
 }
 
 // Clamped cell of a particle in the SPH kernels (sph_density.rs:421-426): grid origin 0.

@@ -78,7 +78,7 @@ __device__ __forceinline__ void slab_ranges(const float4& p, bool live, const Gr
 // ---------------------------------------------------------------------------------------------
 // Load balance.  A (64-particle sub-tile, slab) item whose particles each face more than
 // kHeavyWork candidates -- the box corners of c3 collect thousands of particles at one point --
-// is moved to a heavy list and processed by a 1024-lane workgroup in which 16 waves split the
+// is moved to a heavy list and processed by a 512-lane workgroup in which 8 waves split the
 // candidates of the same 64 particles and reduce their partial sums in wave order.  The light
 // kernels skip those items.  The plan is made once per substep and serves both passes.
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
@@ -1202,7 +1202,8 @@ constexpr uint32_t kDensityOnly = 1u << 31;
 
 // Sum the slab partials, apply v += a dt and the fused epilogue (gravity.rs:33,
 // integrate.rs:23-29, box_collider.rs:37-46), in sorted order: the new state of particle s goes
-// to sout[2 s] = (x, y, z, rho) and sout[2 s + 1] = (vx, vy, vz, 0) (32 contiguous bytes) and,
+// to sout[2 s] = (x, y, z, rho) and sout[2 s + 1] = (vx, vy, vz, bits of the particle id) (32
+// contiguous bytes) and,
 // when accelerations are asked for, to sout[2 stride + s] = (ax, ay, az, 0).  k_scatter then
 // moves it to particle order.
 __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spos,
@@ -1272,7 +1273,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
         if (npz > F.mx[2]) { npz = F.mx[2]; nvz = -fabsf(nvz) * F.e; }
     }
     sout[2u * s] = make_float4(npx, npy, npz, rho);
-    sout[2u * s + 1u] = make_float4(nvx, nvy, nvz, 0.0f);
+    sout[2u * s + 1u] = make_float4(nvx, nvy, nvz, v.w);  // .w: the particle id
     if (want_accel) sout[2 * (size_t)stride + s] = make_float4(ax, ay, az, 0.0f);
 }
 
@@ -1438,9 +1439,19 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     return e != hipSuccess ? e : j;
 }
 
+// rank[id] = s for the particle id carried in the new state of slot s (sout[2 s + 1].w): the
+// particle -> slot map after resident substeps.
+__global__ __launch_bounds__(256) void k_rank_of(const float4* __restrict__ sout, uint32_t n,
+                                                 uint32_t* __restrict__ rank) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const uint32_t i = __float_as_uint(sout[2u * s + 1u].w);
+    if (i < n) rank[i] = s;
+}
+
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, bool density_only,
                            float* px, float* py, float* pz, float* vx, float* vy, float* vz,
-                           float* density, float* accel) {
+                           float* density, float* accel, bool to_particles, bool rebuild_rank) {
     if (a.n == 0) return hipSuccess;
     Finish F;
     F.mc = poly6_mc(a.h, a.mass);
@@ -1459,7 +1470,11 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
                                                            c->wpart, a.n, c->max_n, F,
                                                            accel != nullptr, c->sout);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) {
+    if (e == hipSuccess && to_particles && rebuild_rank) {
+        k_rank_of<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->sout, a.n, c->rank);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess && to_particles) {
         k_scatter<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->sout, c->rank, a.n, c->max_n,
                                                               F.flags, px, py, pz, vx, vy, vz,
                                                               density, accel);

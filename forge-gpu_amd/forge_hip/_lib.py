@@ -98,6 +98,8 @@ SIGNATURES = {
                               _P, _U32, _F32]),
     "fh_sph_fused": (_I, [_P, ctypes.POINTER(FhSphParams), ctypes.POINTER(FhEpilogue),
                           _P, _P, _P, _P, _P, _P, _P, _P, _U32, _F32]),
+    "fh_sph_fused_steps": (_I, [_P, ctypes.POINTER(FhSphParams), ctypes.POINTER(FhEpilogue),
+                                _P, _P, _P, _P, _P, _P, _P, _P, _U32, _F32, _U32]),
     "fh_set_option": (_I, [_P, _I, _I]),
     "fh_gravity": (_I, [_P, _P, _P, _P, _U32, _F32, _F32, _F32, _F32]),
     "fh_integrate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _F32]),

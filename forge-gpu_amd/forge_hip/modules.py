@@ -215,16 +215,27 @@ class SphFusedModule(SimModule):
             fields.add_f32_zeros("density", fields.particle_count)
 
     def execute(self, fields: FieldSet, dt: float) -> None:
+        self._call(fields, dt, None)
+
+    def execute_steps(self, fields: FieldSet, dt: float, steps: int) -> None:
+        """`steps` substeps in one call (fh_sph_fused_steps): the state stays in sorted order on
+        the device between them and the fields are written once, after the last."""
+        self._call(fields, dt, int(steps))
+
+    def _call(self, fields: FieldSet, dt: float, steps: int | None) -> None:
         n = fields.particle_count
         self.prepare(fields)
         ctx = fields.context(_cells(self.grid_dims))
         px, py, pz = fields.pos()
         vx, vy, vz = fields.vel()
         epi = ctypes.byref(self.epilogue) if self.epilogue is not None else None
-        check(_lib.load().fh_sph_fused(ctx.handle, ctypes.byref(_sph_params(self)), epi,
-                                       ptr(px), ptr(py), ptr(pz), ptr(vx), ptr(vy), ptr(vz),
-                                       ptr(fields.f32_fields["density"]), ptr(self.accel), n,
-                                       float(dt)))
+        args = (ctx.handle, ctypes.byref(_sph_params(self)), epi, ptr(px), ptr(py), ptr(pz),
+                ptr(vx), ptr(vy), ptr(vz), ptr(fields.f32_fields["density"]), ptr(self.accel),
+                n, float(dt))
+        if steps is None:
+            check(_lib.load().fh_sph_fused(*args))
+        else:
+            check(_lib.load().fh_sph_fused_steps(*args, steps))
 
 
 class GravityModule(SimModule):
@@ -277,9 +288,10 @@ class BoxColliderModule(SimModule):
 
 
 class Pipeline:
-    def __init__(self, fuse_epilogue: bool = True):
+    def __init__(self, fuse_epilogue: bool = True, resident: bool = True):
         self.modules: list[SimModule] = []
         self.fuse_epilogue = fuse_epilogue
+        self.resident = resident  # run / capture: sorted state kept on the device between substeps
         self._plan: list[SimModule] | None = None
         self._captured_ctx: Context | None = None
 
@@ -345,9 +357,26 @@ class Pipeline:
         self.step_async(fields, dt)
         fields.context().sync()
 
+    def run_async(self, fields: FieldSet, dt: float, steps: int) -> None:
+        """`steps` substeps queued on the field set's stream.  When the (fused) plan is a single
+        sph_fused module and `resident` is set, they are one fh_sph_fused_steps call: the state
+        stays in sorted order on the device and the fields are written after the last substep
+        only (nothing else reads them in between)."""
+        plan = self._fused_plan()
+        steps = int(steps)
+        if self.resident and steps > 1 and len(plan) == 1 and isinstance(plan[0], SphFusedModule):
+            ctx = fields.context(_cells(plan[0].grid_dims))
+            if not getattr(ctx, "capturing", False):
+                ctx.torch_stream().wait_stream(torch.cuda.current_stream())
+            plan[0].execute_steps(fields, dt, steps)
+            return
+        for _ in range(steps):
+            self.step_async(fields, dt)
+
     def run(self, fields: FieldSet, dt: float, steps: int) -> None:
-        for _ in range(int(steps)):
-            self.step(fields, dt)
+        """`steps` substeps, then wait for the stream (modules/mod.rs:106-112)."""
+        self.run_async(fields, dt, steps)
+        fields.context().sync()
 
     def capture(self, fields: FieldSet, dt: float, substeps: int) -> None:
         """Record `substeps` step_async calls into one HIP graph (manifest_runner.rs:57-69)."""
@@ -360,8 +389,7 @@ class Pipeline:
         ctx.graph_begin()
         ctx.capturing = True
         try:
-            for _ in range(int(substeps)):
-                self.step_async(fields, dt)
+            self.run_async(fields, dt, substeps)
         finally:
             ctx.capturing = False
             ctx.graph_end()

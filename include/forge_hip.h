@@ -203,6 +203,18 @@ int fh_sph_viscosity(fh_ctx* ctx, const fh_sph_params* prm, const float* px, con
 int fh_sph_fused(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
                  float* py, float* pz, float* vx, float* vy, float* vz, float* density,
                  float* accel, uint32_t n, float dt);
+/* `steps` (>= 1) consecutive fh_sph_fused substeps in one call, for a module that runs alone
+ * in a pipeline's substep loop (Pipeline.run / capture, manifest_runner.rs:53-77, with
+ * sph_fused.rs:413-732 each substep).  In the fast mode the state stays in HBM in cell-sorted
+ * order between the substeps of the call: each later substep hashes and sorts the previous
+ * substep's sorted state, and only the last one writes the caller's arrays (positions,
+ * velocities, density, accel), so the arrays are not updated in between.  Particles of one cell
+ * are then visited in the previous substep's order instead of ascending id, which changes sums
+ * only by rounding.  With FH_OPT_SPH_EXACT, `steps` separate fh_sph_fused calls.
+ * steps == 1 is fh_sph_fused. */
+int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
+                       float* py, float* pz, float* vx, float* vy, float* vz, float* density,
+                       float* accel, uint32_t n, float dt, uint32_t steps);
 
 /* Context options.  FH_OPT_SPH_EXACT = 1 makes fh_sph_density / fh_sph_fused evaluate the
  * reference's float expressions term by term in the reference's neighbour order (one thread per
