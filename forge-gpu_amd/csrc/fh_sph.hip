@@ -65,14 +65,12 @@ __device__ __forceinline__ void fill_cells(uint32_t* __restrict__ cell_start, ui
 // one of them.  Listed as (first slot, offset of that sample) -- the group pass counts the run
 // and the members at that sample's position exactly -- and tagged with the epoch in
 // cand_tag[cell] for the plan, which runs beside the group pass.
-__global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict__ skeys,
-                                                     uint32_t n, uint32_t C,
-                                                     uint32_t* __restrict__ cell_start,
-                                                     const float4* __restrict__ spos,
-                                                     uint2* __restrict__ big, uint32_t cap,
-                                                     uint64_t* __restrict__ cand_tag,
-                                                     Control* ctl) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+template <class Pos>
+__device__ __forceinline__ void cell_starts_slot(uint32_t s, const uint32_t* __restrict__ skeys,
+                                                 uint32_t n, uint32_t C,
+                                                 uint32_t* __restrict__ cell_start, Pos pos,
+                                                 uint2* __restrict__ big, uint32_t cap,
+                                                 uint64_t* __restrict__ cand_tag, Control* ctl) {
     const int lane = threadIdx.x & 63;
     uint32_t lo = 0, hi = 0, lo2 = 0, hi2 = 0;
     bool cand = false;
@@ -100,7 +98,7 @@ __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict_
         uint32_t sx[kGroupSamples], sy[kGroupSamples], sz[kGroupSamples];
 #pragma unroll
         for (uint32_t q = 0; q < kGroupSamples; q++) {
-            const float4 v = spos[s + (q * L) / kGroupSamples];
+            const float4 v = pos(s + (q * L) / kGroupSamples);
             sx[q] = __float_as_uint(v.x);
             sy[q] = __float_as_uint(v.y);
             sz[q] = __float_as_uint(v.z);
@@ -124,6 +122,31 @@ __global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict_
             cand_tag[k] = (uint64_t)ctl->epoch << 32;  // k_plan: this cell may hold a group
         }
     }
+}
+
+// Position of sorted slot x for the samples of cell_starts_slot: from the sorted copy, or, in
+// resident substeps (which build that copy in the same kernel), from the previous substep's
+// state through the slot map.
+struct SortedPos {
+    const float4* __restrict__ spos;
+    __device__ float4 operator()(uint32_t x) const { return spos[x]; }
+};
+struct ResidentPos {
+    const float4* __restrict__ sout;
+    const uint32_t* __restrict__ prev;
+    uint32_t n;
+    __device__ float4 operator()(uint32_t x) const { return sout[2u * min(prev[x], n - 1u)]; }
+};
+
+__global__ __launch_bounds__(256) void k_cell_starts(const uint32_t* __restrict__ skeys,
+                                                     uint32_t n, uint32_t C,
+                                                     uint32_t* __restrict__ cell_start,
+                                                     const float4* __restrict__ spos,
+                                                     uint2* __restrict__ big, uint32_t cap,
+                                                     uint64_t* __restrict__ cand_tag,
+                                                     Control* ctl) {
+    cell_starts_slot(blockIdx.x * blockDim.x + threadIdx.x, skeys, n, C, cell_start,
+                     SortedPos{spos}, big, cap, cand_tag, ctl);
 }
 
 static hipError_t launch_cell_starts(fh_ctx* c, uint32_t cells, uint32_t n, bool list_big) {
@@ -150,29 +173,34 @@ hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const flo
 }
 
 // Resident substeps: new slot r takes the state of previous slot prev[r] from c->sout (one
-// 32-byte read: (x, y, z, rho), (vx, vy, vz, particle id)) and writes spos / svel in order.
-__global__ __launch_bounds__(256) void k_gather_resident(const float4* __restrict__ sout,
-                                                         const uint32_t* __restrict__ prev,
-                                                         uint32_t n, float4* __restrict__ spos,
-                                                         float4* __restrict__ svel) {
+// 32-byte read: (x, y, z, rho), (vx, vy, vz, particle id)) and writes spos / svel in order;
+// the same thread then does k_cell_starts' work for slot r.
+__global__ __launch_bounds__(256) void k_gather_resident(
+    const float4* __restrict__ sout, const uint32_t* __restrict__ prev, uint32_t n,
+    float4* __restrict__ spos, float4* __restrict__ svel, const uint32_t* __restrict__ skeys,
+    uint32_t C, uint32_t* __restrict__ cell_start, uint2* __restrict__ big, uint32_t cap,
+    uint64_t* __restrict__ cand_tag, Control* ctl) {
     const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= n) return;
-    const uint32_t q = prev[r];
-    if (q >= n) return;  // never taken when the sort is consistent
-    const float4 p = sout[2u * q], v = sout[2u * q + 1u];
-    spos[r] = make_float4(p.x, p.y, p.z, __uint_as_float(r));
-    svel[r] = v;
+    if (r < n) {
+        const uint32_t q = prev[r];
+        if (q < n) {  // always, when the sort is consistent
+            const float4 p = sout[2u * q], v = sout[2u * q + 1u];
+            spos[r] = make_float4(p.x, p.y, p.z, __uint_as_float(r));
+            svel[r] = v;
+        }
+    }
+    cell_starts_slot(r, skeys, n, C, cell_start, ResidentPos{sout, prev, n}, big, cap, cand_tag,
+                     ctl);
 }
 
 hipError_t launch_gather_resident(fh_ctx* c, uint32_t cells, uint32_t n) {
     if (n == 0) return launch_fill_u32(c, c->cell_start, 0u, cells + 1u);
     tbeg(c, KID_GATHER);
-    k_gather_resident<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->sout, c->sidx2, n, c->spos,
-                                                                c->svel);
-    hipError_t e = hipGetLastError();
+    k_gather_resident<<<ceil_div(n, 256u), 256, 0, c->stream>>>(
+        c->sout, c->sidx2, n, c->spos, c->svel, c->skeys, cells, c->cell_start, c->big,
+        ceil_div(c->max_n, 64u) + 1u, c->run_tag, c->ctl);
     tend(c, KID_GATHER);
-    if (e != hipSuccess) return e;
-    return launch_cell_starts(c, cells, n, true);
+    return hipGetLastError();
 }
 
 // Clamped cell of a particle in the SPH kernels (sph_density.rs:421-426): grid origin 0.
