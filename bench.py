@@ -38,13 +38,13 @@ for _p in (REPO, REPO / "forge-gpu_amd"):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 METRIC = "SPH particle-steps/s @1M; radix sort Gkeys/s; achieved HBM GB/s vs peak"
-KERNELS = ["hash", "sort", "gather", "scan", "plan", "density", "density_heavy",
+KERNELS = ["hash", "hist", "sort", "gather", "scan", "plan", "density", "density_heavy",
            "prep", "force", "force_heavy", "finalize"]
 # A "pass" groups the kernels of one stage of the substep; its duration per substep is the sum
 # of its kernels' launch durations, or its wall time for the two passes whose kernels overlap
 # (the heavy kernels of a pass process the items its light kernel skips, so the pair moves the
 # pass's bytes together).
-PASSES = {"hash": ["hash"], "sort": ["sort"], "gather": ["gather"], "scan": ["scan"],
+PASSES = {"hash": ["hash", "hist"], "sort": ["sort"], "gather": ["gather"], "scan": ["scan"],
           "plan": ["plan"], "density": ["density", "density_heavy"],
           "force": ["prep", "force", "force_heavy"], "finalize": ["finalize"]}
 # The density and force passes run their light and heavy kernels concurrently on two streams:
@@ -52,21 +52,37 @@ PASSES = {"hash": ["hash"], "sort": ["sort"], "gather": ["gather"], "scan": ["sc
 PASS_TIMERS = {"density": "density_pass", "force": "force_pass"}
 
 
-def algorithmic_bytes(n: int, cells: int, passes: int) -> dict:
-    """Bytes each pass of one substep must move at minimum (neighbour re-reads counted once:
-    they are served from L2/LDS).  See DESIGN.md for the derivation."""
-    return {
+def algorithmic_bytes(n: int, cells: int, passes: int, substeps: int = 1) -> dict:
+    """Bytes each pass must move at minimum per substep (neighbour re-reads counted once: they
+    are served from L2/LDS), averaged over one call of `substeps` substeps: the first rebuilds
+    from the caller's arrays, the later ones (resident) from the previous substep's sorted
+    state, and only the last moves the state back to particle order."""
+    G = max(1, int(substeps))
+    C4 = 4 * (cells + 1)
+    entry = {
         "hash": 12 * n + 4 * n,                      # positions in, cell keys out
         # pass 0 reads keys (values are the indices), middle passes read + write (key, value),
-        # the last pass writes (key, value)
-        "sort": 12 * n + 16 * n * max(passes - 2, 0) + 16 * n,
-        "gather": 8 * n + 24 * n + 32 * n,           # sorted (key, id), pos/vel in, float4 out
-        "scan": 8 * cells + 4 * (cells + 1),         # run tags in, cell_start out
-        "plan": 16 * n,                              # sorted positions
-        "density": 16 * n + 12 * n + 4 * (cells + 1),           # positions in, 3 slab partials
-        "force": 32 * n + 12 * n + 36 * n + 4 * (cells + 1),    # pos/vel/density in, 9 partials
-        "finalize": 32 * n + 12 * n + 36 * n + 4 * n + 28 * n,  # + ids; pos, vel, density out
+        # the last pass writes (key, value) and the rank of each particle
+        "sort": 12 * n + 16 * n * max(passes - 2, 0) + 16 * n + 4 * n,
+        "gather": 4 * n + 24 * n + 32 * n,           # rank, pos / vel in, float4 pairs out
+        "scan": 4 * n + C4,                          # sorted keys in, cell_start out
     }
+    resident = {
+        "hash": 4 * n,                               # keys (written by k_finalize) in
+        "sort": 12 * n + 16 * n * max(passes - 2, 0) + 16 * n,
+        "gather": 4 * n + 32 * n + 32 * n + 4 * n + C4,  # slot map, state in and out, + cells
+        "scan": 0,                                   # done by the gather kernel
+    }
+    per = {k: (entry[k] + (G - 1) * resident[k]) / G for k in entry}
+    per.update({
+        "plan": 16 * n,                              # sorted positions
+        "density": 16 * n + 12 * n + C4,             # positions in, 3 slab partials out
+        "force": 32 * n + 12 * n + 36 * n + C4,      # pos / vel / density in, 9 partials out
+        # pos, vel, partials in, new state (32 B) out; + next keys (all but the last substep);
+        # the last substep also moves the state to particle order (rank, 32 B in, 28 B out)
+        "finalize": 80 * n + 32 * n + ((G - 1) * 4 * n + 64 * n) / G,
+    })
+    return {k: int(v) for k, v in per.items()}
 
 
 def survey_step_bytes(n: int, cells: int, passes: int) -> int:
@@ -194,7 +210,7 @@ def bench_sph(args, fh, torch, log):
         kern[k] = {"launches": len(t), "mean_us": 1e3 * sum(t) / max(len(t), 1),
                    "per_substep_us": 1e3 * sum(t) / G}
         ctx.time_kernel(k, 0)
-    byts = algorithmic_bytes(cfg.n, C, passes)
+    byts = algorithmic_bytes(cfg.n, C, passes, G)
     pas = {}
     for p, ks in PASSES.items():
         # a pass whose kernels overlap on two streams is timed as a whole (wall time)

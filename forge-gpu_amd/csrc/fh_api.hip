@@ -102,12 +102,13 @@ hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float
     return e;
 }
 
-// The same from the previous substep's new state in sorted order (c->sout: (x, y, z, rho),
-// (vx, vy, vz, .) per slot), whose slots take the place of particle ids as sort values.
+// The same from the previous substep's new state in sorted order (c->sout), whose slots take
+// the place of particle ids as sort values; its cells were written to c->kb by the previous
+// substep's k_finalize, so only their histograms remain to be counted.
 hipError_t sph_rebuild_resident(fh_ctx* c, const GridDesc& g, uint32_t cells, uint32_t n) {
+    (void)g;
     const uint32_t bits = bits_for_cells(cells);
-    const float* so = reinterpret_cast<const float*>(c->sout);
-    hipError_t e = launch_hash_hist(c, so, so + 1, so + 2, 8, n, g, bits, c->kb, nullptr, true);
+    hipError_t e = n ? launch_hist_keys(c, c->kb, n, bits, true) : hipSuccess;
     if (e == hipSuccess && n > 0)
         e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx2, n, bits);
     if (e == hipSuccess) e = launch_gather_resident(c, cells, n);
@@ -438,7 +439,8 @@ static int sph_fused_steps(fh_ctx* c, const fh_sph_params* prm, const fh_epilogu
         FH_CHECK_HIP(launch_force_fast(c, a, c->cell_start));
         tend(c, KID_FPASS);
         FH_CHECK_HIP(launch_finalize(c, a, epi, false, px, py, pz, vx, vy, vz, density,
-                                     last ? accel : nullptr, last, last && steps > 1));
+                                     last ? accel : nullptr, last, last && steps > 1,
+                                     last ? nullptr : c->kb));
     }
     return FH_OK;
 }

@@ -318,11 +318,14 @@ hipError_t launch_prep(fh_ctx* c, const SphArgs& a);
 // work plan of the fast passes.
 hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel);
 // New state in sorted order (c->sout); with `to_particles`, also moved to the caller's arrays
-// (`rebuild_rank`: first recompute c->rank from c->sidx, after resident substeps).
+// (`rebuild_rank`: first recompute c->rank from the particle ids, after resident substeps).
+// `next_keys` (may be null) receives the cell of each new position, the keys of the next
+// resident substep.
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,
                            bool density_only, float* px, float* py, float* pz, float* vx,
                            float* vy, float* vz, float* density, float* accel,
-                           bool to_particles = true, bool rebuild_rank = false);
+                           bool to_particles = true, bool rebuild_rank = false,
+                           uint32_t* next_keys = nullptr);
 hipError_t launch_density(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start,
                           float* density_out);
 hipError_t launch_force(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi,

@@ -1212,7 +1212,8 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
                                                   const float* __restrict__ fpart,
                                                   const float* __restrict__ wpart, uint32_t n,
                                                   uint32_t stride, Finish F, bool want_accel,
-                                                  float4* __restrict__ sout) {
+                                                  float4* __restrict__ sout, GridDesc g,
+                                                  uint32_t* __restrict__ keys_out) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const float4 p = spos[s];
@@ -1274,6 +1275,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     }
     sout[2u * s] = make_float4(npx, npy, npz, rho);
     sout[2u * s + 1u] = make_float4(nvx, nvy, nvz, v.w);  // .w: the particle id
+    if (keys_out) keys_out[s] = cell_of(npx, npy, npz, g);  // the next resident substep's keys
     if (want_accel) sout[2 * (size_t)stride + s] = make_float4(ax, ay, az, 0.0f);
 }
 
@@ -1451,7 +1453,8 @@ __global__ __launch_bounds__(256) void k_rank_of(const float4* __restrict__ sout
 
 hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, bool density_only,
                            float* px, float* py, float* pz, float* vx, float* vy, float* vz,
-                           float* density, float* accel, bool to_particles, bool rebuild_rank) {
+                           float* density, float* accel, bool to_particles, bool rebuild_rank,
+                           uint32_t* next_keys) {
     if (a.n == 0) return hipSuccess;
     Finish F;
     F.mc = poly6_mc(a.h, a.mass);
@@ -1468,7 +1471,8 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     tbeg(c, KID_FINAL);
     k_finalize<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
                                                            c->wpart, a.n, c->max_n, F,
-                                                           accel != nullptr, c->sout);
+                                                           accel != nullptr, c->sout, a.g,
+                                                           density_only ? nullptr : next_keys);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && to_particles && rebuild_rank) {
         k_rank_of<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->sout, a.n, c->rank);
