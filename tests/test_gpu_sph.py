@@ -403,3 +403,40 @@ def test_resident_substeps_match_separate_substeps(fh, gpu_ctx, case):
     f1.context().sync()
     for k in f1.f32_fields:
         assert torch.equal(f1.f32_fields[k], f2.f32_fields[k]), k
+
+
+def test_fused_steps_edge_cases(fh, gpu_ctx):
+    """fh_sph_fused_steps: steps = 0 is an error; n = 0 is a no-op; with FH_OPT_SPH_EXACT the
+    call is `steps` separate exact substeps, bit for bit."""
+    import ctypes
+    from forge_hip import _lib, workloads
+    from forge_hip.modules import _sph_params
+    from forge_hip.runtime import ptr
+    cfg = workloads.small_sph(n=6000, cols=16)
+    m = sph_pipeline(fh, cfg)._fused_plan()[0]
+    f = fields_from(fh, cfg)
+    m.prepare(f)
+    ctx = f.context(cfg.num_cells)
+    lib = _lib.load()
+    px, py, pz = f.pos()
+    vx, vy, vz = f.vel()
+    args = [ctx.handle, ctypes.byref(_sph_params(m)), ctypes.byref(m.epilogue)] + \
+        [ptr(t) for t in (px, py, pz, vx, vy, vz, f.f32_fields["density"])] + [None]
+    assert lib.fh_sph_fused_steps(*args, cfg.n, cfg.dt, 0) == fh.FH_EINVAL
+    assert lib.fh_sph_fused_steps(*args, 0, cfg.dt, 3) == fh.FH_OK
+    ctx.sync()
+    # exact mode: one call of 3 substeps == 3 calls
+    f1, f2 = fields_from(fh, cfg), fields_from(fh, cfg)
+    for ff in (f1, f2):
+        m.prepare(ff)
+        ff.context(cfg.num_cells).set_option(fh.FH_OPT_SPH_EXACT, 1)
+    torch.cuda.synchronize()
+    m.execute_steps(f1, cfg.dt, 3)
+    for _ in range(3):
+        m.execute(f2, cfg.dt)
+    f1.context().sync()
+    f2.context().sync()
+    for k in f1.f32_fields:
+        assert torch.equal(f1.f32_fields[k], f2.f32_fields[k]), k
+    for ff in (f1, f2):
+        ff.context(cfg.num_cells).set_option(fh.FH_OPT_SPH_EXACT, 0)
