@@ -57,7 +57,11 @@ constexpr uint32_t kGroupHits = 4;
 // The heavy SPH work list is split into kHeavyLists sub-lists with counters on separate lines,
 // so that appends from different workgroups do not serialise on one address.
 constexpr int kHeavyLists = 8;
-constexpr int kPlanThreads = 1024;  // k_plan workgroup: 16 sub-tiles, 48 (sub-tile, slab) items
+#ifndef FH_PLAN_THREADS
+#define FH_PLAN_THREADS 512
+#endif
+// k_group_plan workgroup: a co-located group, or 8 sub-tiles = 24 (sub-tile, slab) items
+constexpr int kPlanThreads = FH_PLAN_THREADS;
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;  // 4096 cells per scan tile

@@ -174,7 +174,7 @@ __device__ __forceinline__ void swap4(float4* p, uint32_t a, uint32_t b) {
     p[b] = t;
 }
 
-constexpr int kGroupThreads = 1024;
+constexpr int kGroupThreads = kPlanThreads;  // one launch: the same workgroup size
 constexpr int kGroupWaves = kGroupThreads / kWave;
 constexpr uint32_t kGroupUnroll = 8;  // particles loaded per thread before they are examined
 
