@@ -247,6 +247,12 @@ def bench_sort(args, fh, torch, log):
         k.copy_(k0)
         v.copy_(v0)
         ctx.torch_stream().wait_stream(torch.cuda.current_stream())
+        # A ~100 us device-side delay ahead of the timed region, so that all the sort's launches
+        # are queued before the device reaches it: the events time device execution, not the
+        # host's launch rate (an eager call's 7 launches otherwise leave the device idle for
+        # 10-30 us while the host catches up).
+        with torch.cuda.stream(ctx.torch_stream()):
+            torch.cuda._sleep(200_000)
         ctx.event_record(2)
         sorter.sort(k, v, n, 32, sync=False)
         ctx.event_record(3)
