@@ -528,7 +528,8 @@ def main(argv=None) -> int:
         "config": {
             "workload": "configs[3]: SPH dam-break substep, 1,048,576 particles, h = cell = 0.01, "
                         "100^3 cells, re-hash + sort every substep, hipGraph of "
-                        f"{s['G']} substeps",
+                        f"{s['G']} substeps (one fh_sph_fused_steps call: state resident in "
+                        "sorted order between them, fields written after the last)",
             "particles": cfg.n, "cells": s["C"], "sort_passes": s["passes"],
             "graph_substeps": s["G"], "input_sha256": s["digest"], "parallelism": "single GPU",
         },
