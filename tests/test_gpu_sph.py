@@ -231,14 +231,17 @@ def test_fused_epilogue_equals_separate_modules(fh, gpu_ctx):
         assert np.array_equal(outs[0][k], outs[1][k]), k
 
 
-@pytest.mark.parametrize("resident", [True, False])
-def test_graph_replay_matches_eager(fh, gpu_ctx, resident):
+@pytest.mark.parametrize("resident,case", [(True, "small"), (False, "small"), (True, "c3")])
+def test_graph_replay_matches_eager(fh, gpu_ctx, resident, case):
     """10 captured substeps replayed twice == the same 10 substeps run eagerly twice, bit for
     bit; each replay is checked after eager work and synchronisation in between (graph nodes
     must not go stale).  resident: one fh_sph_fused_steps call of 10 substeps; otherwise 10
-    fh_sph_fused calls."""
+    fh_sph_fused calls.  c3: the full 1M-particle dam break (co-located corner groups, heavy
+    and transposed items, both streams), whose heavy-list order varies from run to run while
+    every item's sums must not."""
     from forge_hip import workloads
-    cfg = workloads.small_sph(n=16384, cols=32)
+    cfg = workloads.small_sph(n=16384, cols=32) if case == "small" else workloads.config3()
+    print(f"graph replay {case} resident={resident}", flush=True)
     f_e = fields_from(fh, cfg)
     f_g = fields_from(fh, cfg)
     p_e = sph_pipeline(fh, cfg)
