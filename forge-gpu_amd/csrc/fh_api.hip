@@ -167,7 +167,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->srho, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->dpart, 3 * (size_t)max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->fpart, 9 * (size_t)max_n, &tot);
-    // k_plan workgroup b appends to sub-list b % kHeavyLists, at most 3 * 16 items per workgroup
+    // plan workgroup b appends to sub-list b % kHeavyLists, at most 3 * kPlanThreads / 64 items
     c->heavy_cap = 3u * (kPlanThreads / 64u) *
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);

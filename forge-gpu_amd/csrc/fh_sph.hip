@@ -119,7 +119,7 @@ __device__ __forceinline__ void cell_starts_slot(uint32_t s, const uint32_t* __r
         if (hits >= kGroupHits) {
             const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
             if (slot < cap) big[slot] = make_uint2(s, off);
-            cand_tag[k] = (uint64_t)ctl->epoch << 32;  // k_plan: this cell may hold a group
+            cand_tag[k] = (uint64_t)ctl->epoch << 32;  // the plan: this cell may hold a group
         }
     }
 }

@@ -90,7 +90,7 @@ constexpr int kHeavyThreads = kHeavyWaves * kWave;
 constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
 constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
 constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transposed
-// Item flags (k_plan): light (one wavefront), heavy (heavy list), every particle co-located
+// Item flags (the plan): light (one wavefront), heavy (heavy list), every particle co-located
 // (skipped by both passes).
 constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
 // Transposed heavy items: the particles' candidate ranges overlap little (sparse particles
@@ -156,9 +156,9 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
 }
 
 // Co-located groups.  k_cell_starts lists the cells of >= kCollapseMin particles in which at
-// least kGroupHits of kGroupSamples evenly spaced particles sit at the position of a middle
-// one.  k_group, one workgroup per listed cell, takes the position P of the cell's middle
-// particle, counts the particles at exactly P (M) and,
+// least kGroupHits of kGroupSamples evenly spaced particles sit at the position of one of them.
+// The group part of k_group_plan, one workgroup per listed cell, takes that sample's position
+// P, counts the particles at exactly P (M) and,
 // when M >= kCollapseMin, moves them to the front of the cell: the misplaced particles on both
 // sides are ranked and swapped pairwise, in place.  The order inside such a cell then differs
 // from ascending particle id (sums only change by rounding).
@@ -314,7 +314,7 @@ __device__ __forceinline__ void group_work(uint32_t bid, uint32_t nb, const uint
 }
 
 // Candidates of the possibly grouped cells among the 9 cells of a slab (tagged by
-// k_cell_starts; k_group, which runs beside the plan, decides), as a count to subtract: such a
+// k_cell_starts; the group part, which runs beside the plan, decides), as a count to subtract: such a
 // cell of k particles is counted as one (a group of M counts as one candidate, M <= k).
 __device__ __forceinline__ uint32_t grouped_excess(const float4& p, const GridDesc& g,
                                                    const uint64_t* __restrict__ cand_tag,
@@ -470,7 +470,7 @@ __device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
     return out;
 }
 
-// Plan, beside the co-located groups (k_group, which tags particles f+1 .. f+M-1 of a grouped
+// Plan, beside the co-located groups (the group part, which tags particles f+1 .. f+M-1 of a grouped
 // cell in spos[s].w with their representative f, f itself with kRepFlag | M, and marks the
 // sub-tiles made only of such non-representative particles in skip_tag: both passes skip them,
 // their particles take the representative's density, and its acceleration up to the viscosity
@@ -612,7 +612,7 @@ __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[
 }
 
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
-// Light items hold no co-located group (k_plan sends those to the heavy list).
+// Light items hold no co-located group (the plan sends those to the heavy list).
 __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restrict__ spos,
                                                          uint32_t n, GridDesc g,
                                                          const uint32_t* __restrict__ cstart,
@@ -655,9 +655,9 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     if (in) dpart[(size_t)slab * stride + s] = acc;
 }
 
-// Heavy items: the 16 waves of a workgroup hold the same 64 particles of one (sub-tile, slab)
+// Heavy items: the 8 waves of a workgroup hold the same 64 particles of one (sub-tile, slab)
 // and walk the same home-row segments as k_density_wave, but split each segment row's chunks
-// round-robin (wave w takes chunks w, w + 16, ...), each through its own LDS slice (no
+// round-robin (wave w takes chunks w, w + 8, ...), each through its own LDS slice (no
 // workgroup barrier until the final reduction in wave order).  The members of co-located groups
 // in a segment row are cut out of its candidate range (the representative stays, with weight M).
 constexpr int kMaxCut = 4;  // groups cut out per segment row (further ones are staged, weight 0)
@@ -1335,7 +1335,8 @@ static float poly6_mc(float h, float mass) {
 #ifndef FH_SIDE_MODE
 #define FH_SIDE_MODE 7
 #endif
-// Which concurrent pairs use the side stream (bit 0: k_group beside k_plan, bit 1: the heavy
+// Which concurrent pairs use the side stream (bit 0: unused since groups and plan share one
+// launch, bit 1: the heavy
 // density kernel beside the light one, bit 2: the same for the force pass); otherwise the pair
 // runs one after the other on the context stream.
 constexpr uint32_t kSideGroup = 1u, kSideDensity = 2u, kSideForce = 4u;
@@ -1355,7 +1356,7 @@ static hipError_t join_side(fh_ctx* c, uint32_t use) {
 
 hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
     if (a.n == 0) return hipSuccess;
-    // scratch of k_group: the sort's key buffer, free after the sort (disjoint ranges per cell)
+    // scratch of the group part: the sort's key buffer, free after the sort (disjoint ranges per cell)
     tbeg(c, KID_PLAN);
     k_group_plan<<<kGroupBlocks + ceil_div(a.n, (uint32_t)kPlanThreads), kPlanThreads, 0,
                    c->stream>>>(c->big, ceil_div(c->max_n, 64u) + 1u, a.n, c->skeys, c->cell_start,
