@@ -306,6 +306,18 @@ int fh_find_cell_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
     return FH_OK;
 }
 
+int fh_cell_start_csr(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n, uint32_t num_cells,
+                      uint32_t* cell_start) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((n && !sorted_keys) || !cell_start)
+        return fail(FH_EINVAL, "fh_cell_start_csr: null pointer");
+    if (num_cells == 0 || num_cells == 0xFFFFFFFFu)
+        return fail(FH_EINVAL, "fh_cell_start_csr: num_cells must be in 1..2^32-2");
+    FH_CHECK_HIP(launch_csr_from_sorted(c, sorted_keys, n, num_cells, cell_start));
+    return FH_OK;
+}
+
 int fh_hashgrid_build(fh_ctx* c, const float* x, const float* y, const float* z,
                       uint32_t stride, uint32_t n, float cell_size, const float origin[3],
                       const uint32_t dims[3], uint32_t* cell_start, uint32_t* sorted_indices,
@@ -457,6 +469,40 @@ int fh_sph_fused_steps(fh_ctx* c, const fh_sph_params* prm, const fh_epilogue* e
                        float* accel, uint32_t n, float dt, uint32_t steps) {
     return sph_fused_steps(c, prm, epi, px, py, pz, vx, vy, vz, density, accel, n, dt, steps,
                            "fh_sph_fused_steps");
+}
+
+int fh_sph_force(fh_ctx* c, const fh_sph_params* prm, const float* px, const float* py,
+                 const float* pz, float* vx, float* vy, float* vz, const float* density,
+                 const uint32_t* cell_start, const uint32_t* sorted_indices, float* accel,
+                 uint32_t n, float dt) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!cell_start || (n && (!px || !py || !pz || !vx || !vy || !vz || !density || !sorted_indices)))
+        return fail(FH_EINVAL, "fh_sph_force: null pointer");
+    if ((rc = check_n(c, n, "fh_sph_force"))) return rc;
+    GridDesc g;
+    uint32_t cells;
+    if ((rc = check_sph(c, prm, &g, &cells, "fh_sph_force"))) return rc;
+    if (n == 0) return FH_OK;
+    SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
+              prm->rest_density, prm->viscosity_coefficient, dt, n};
+    // the caller's state in the caller's grid order, then the exact fused pass (velocities
+    // written back through sorted_indices; positions untouched without an epilogue)
+    FH_CHECK_HIP(launch_gather_grid(c, px, py, pz, vx, vy, vz, density, sorted_indices, n));
+    FH_CHECK_HIP(launch_force(c, a, nullptr, cell_start, nullptr, nullptr, nullptr, vx, vy, vz,
+                              accel));
+    return FH_OK;
+}
+
+int fh_pack_frame(fh_ctx* c, const float* px, const float* py, const float* pz, uint32_t n,
+                  uint32_t frame, uint32_t* frame_counter, void* out) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!out || (n && (!px || !py || !pz))) return fail(FH_EINVAL, "fh_pack_frame: null pointer");
+    if (n > (0xFFFFFFFFu - 2u) / 3u)
+        return fail(FH_ERANGE, "fh_pack_frame: n=%u does not fit a frame", n);
+    FH_CHECK_HIP(launch_pack_frame(c, px, py, pz, n, frame, frame_counter, out));
+    return FH_OK;
 }
 
 static int unfused(fh_ctx* c, bool viscosity, const fh_sph_params* prm, const float* px,

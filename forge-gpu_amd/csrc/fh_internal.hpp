@@ -310,6 +310,13 @@ hipError_t launch_gather(fh_ctx* c, const GridDesc& g, uint32_t cells, const flo
 // The particle ids travel in svel[.].w; c->sidx and c->rank are not maintained (launch_finalize
 // rebuilds c->rank from the ids before the final move to particle order).
 hipError_t launch_gather_resident(fh_ctx* c, uint32_t cells, uint32_t n);
+hipError_t launch_gather_grid(fh_ctx* c, const float* px, const float* py, const float* pz,
+                              const float* vx, const float* vy, const float* vz,
+                              const float* density, const uint32_t* sorted_indices, uint32_t n);
+hipError_t launch_csr_from_sorted(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t cells,
+                                  uint32_t* cell_start);
+hipError_t launch_pack_frame(fh_ctx* c, const float* px, const float* py, const float* pz,
+                             uint32_t n, uint32_t frame, uint32_t* counter, void* out);
 hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_start);
 // Force records of every sorted particle (positions with pressure, velocity and weight over

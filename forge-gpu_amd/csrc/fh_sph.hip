@@ -203,6 +203,110 @@ hipError_t launch_gather_resident(fh_ctx* c, uint32_t cells, uint32_t n) {
     return hipGetLastError();
 }
 
+// CSR cell_start from keys the caller already sorted (hashgrid.rs:102-106 computes the same
+// array as the prefix sum of per-cell counts): cell_start[c] = number of keys < c for
+// c = 0..C, so keys >= C count in no cell.  Each slot fills the cells between the previous
+// slot's key and its own (both clamped to C), the last slot the cells after its key; the
+// filled ranges partition 0..C.
+__global__ __launch_bounds__(256) void k_csr_from_sorted(const uint32_t* __restrict__ keys,
+                                                         uint32_t n, uint32_t C,
+                                                         uint32_t* __restrict__ cell_start) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    uint32_t lo = 0, hi = 0, lo2 = 0, hi2 = 0;
+    if (s < n) {
+        const uint32_t k = min(keys[s], C);
+        const uint32_t lo_k = s > 0u ? min(keys[s - 1u], C) + 1u : 0u;  // "-1" before slot 0
+        lo = lo_k;
+        hi = lo_k <= k ? k + 1u : lo_k;
+        if (s == n - 1u) {
+            lo2 = k + 1u;
+            hi2 = C + 1u;
+        }
+    }
+    fill_cells(cell_start, lo, hi, s, lane);
+    fill_cells(cell_start, lo2, hi2, n, lane);
+}
+
+hipError_t launch_csr_from_sorted(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t cells,
+                                  uint32_t* cell_start) {
+    if (n == 0) return launch_fill_u32(c, cell_start, 0u, cells + 1u);
+    k_csr_from_sorted<<<ceil_div(n, 256u), 256, 0, c->stream>>>(keys, n, cells, cell_start);
+    return hipGetLastError();
+}
+
+// Sorted-order state for the exact force pass over a caller's grid (sorted_indices[s] = the
+// particle in slot s): the same layout k_gather writes, plus the densities.
+__global__ __launch_bounds__(256) void k_gather_grid(
+    const float* __restrict__ px, const float* __restrict__ py, const float* __restrict__ pz,
+    const float* __restrict__ vx, const float* __restrict__ vy, const float* __restrict__ vz,
+    const float* __restrict__ density, const uint32_t* __restrict__ sorted_indices, uint32_t n,
+    float4* __restrict__ spos, float4* __restrict__ svel, float* __restrict__ srho,
+    uint32_t* __restrict__ sidx) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const uint32_t i = sorted_indices[s];
+    const bool ok = i < n;  // a malformed id reads particle 0 and is never written back
+    const uint32_t q = ok ? i : 0u;
+    spos[s] = make_float4(px[q], py[q], pz[q], __uint_as_float(s));
+    svel[s] = make_float4(vx[q], vy[q], vz[q], __uint_as_float(q));
+    srho[s] = density[q];
+    sidx[s] = ok ? i : 0xFFFFFFFFu;
+}
+
+hipError_t launch_gather_grid(fh_ctx* c, const float* px, const float* py, const float* pz,
+                              const float* vx, const float* vy, const float* vz,
+                              const float* density, const uint32_t* sorted_indices, uint32_t n) {
+    if (n == 0) return hipSuccess;
+    tbeg(c, KID_GATHER);
+    k_gather_grid<<<ceil_div(n, 256u), 256, 0, c->stream>>>(px, py, pz, vx, vy, vz, density,
+                                                            sorted_indices, n, c->spos, c->svel,
+                                                            c->srho, c->sidx);
+    tend(c, KID_GATHER);
+    return hipGetLastError();
+}
+
+// Binary position frame of the streaming runner (manifest_runner.rs:150-167 interleaves
+// pos_x/y/z per particle; serve.rs:43-62 packs u32 frame, u32 count, then the f32 values,
+// all little-endian -- the device's byte order).  Word w of the output is written by thread
+// w (coalesced stores): words 0 and 1 are the header, word 2 + 3 i + a is component a of
+// particle i.  The frame number is `frame`, or, when `counter` is non-NULL, *counter, which the
+// kernel then increments (so a captured graph emits consecutive frame numbers).
+__global__ __launch_bounds__(256) void k_pack_frame(const float* __restrict__ px,
+                                                    const float* __restrict__ py,
+                                                    const float* __restrict__ pz, uint32_t n,
+                                                    uint32_t frame, uint32_t* counter,
+                                                    uint32_t* __restrict__ out) {
+    const uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t words = 2ull + 3ull * n;
+    if (w >= words) return;
+    if (w < 2u) {
+        if (w == 0u) {
+            uint32_t f = frame;
+            if (counter) {
+                f = *counter;
+                *counter = f + 1u;  // one thread of one workgroup: no other access in the launch
+            }
+            out[0] = f;
+        } else {
+            out[1] = n;
+        }
+        return;
+    }
+    const uint64_t t = w - 2u;
+    const uint32_t i = (uint32_t)(t / 3u), a = (uint32_t)(t - 3u * (t / 3u));
+    const float* src = a == 0u ? px : (a == 1u ? py : pz);
+    out[w] = __float_as_uint(src[i]);
+}
+
+hipError_t launch_pack_frame(fh_ctx* c, const float* px, const float* py, const float* pz,
+                             uint32_t n, uint32_t frame, uint32_t* counter, void* out) {
+    const uint64_t words = 2ull + 3ull * n;
+    k_pack_frame<<<(uint32_t)((words + 255u) / 256u), 256, 0, c->stream>>>(
+        px, py, pz, n, frame, counter, (uint32_t*)out);
+    return hipGetLastError();
+}
+
 // Clamped cell of a particle in the SPH kernels (sph_density.rs:421-426): grid origin 0.
 struct Cell3 {
     int cx, cy, cz;

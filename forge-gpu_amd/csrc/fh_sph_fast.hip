@@ -1032,6 +1032,7 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
                                                        uint32_t n, GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
                                                        FastForce K, float* __restrict__ fpart,
+                                                       float* __restrict__ wpart,
                                                        uint32_t stride, uint32_t items,
                                                        const uint8_t* __restrict__ flag,
                                                        const uint32_t* __restrict__ skip_tag,
@@ -1089,6 +1090,9 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         o[s] = fmaf(-wv, vi.x, ax);
         o[stride + s] = fmaf(-wv, vi.y, ay);
         o[2u * (size_t)stride + s] = fmaf(-wv, vi.z, az);
+        // a group representative's viscosity weight for this slab (k_finalize finishes its
+        // members with it); every slab of a representative is written by one of the two kernels
+        if (__float_as_uint(pi.w) & kRepFlag) wpart[(size_t)slab * stride + s] = wv;
     }
 }
 
@@ -1434,7 +1438,7 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     e = hipGetLastError();
     tbeg(c, KID_FORCE);
     k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, a.n, a.g,
-                                                 cell_start, K, c->fpart, c->max_n, items,
+                                                 cell_start, K, c->fpart, c->wpart, c->max_n, items,
                                                  c->heavy_flag, c->skip_tag, c->ctl);
     tend(c, KID_FORCE);
     if (e == hipSuccess) e = hipGetLastError();

@@ -87,6 +87,7 @@ SIGNATURES = {
     "fh_hash_cells": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P]),
     "fh_sort_pairs": (_I, [_P, _P, _P, _U32, _U32]),
     "fh_find_cell_boundaries": (_I, [_P, _P, _U32, _U32, _P, _P]),
+    "fh_cell_start_csr": (_I, [_P, _P, _U32, _U32, _P]),
     "fh_hashgrid_build": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P, _P]),
     "fh_neighbor_query": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P, _F32, _P, _P]),
     "fh_query_neighbors": (_I, [_P, _P, _P, _P, _U32, _F32, _F3, _U3, _P, _P,
@@ -96,6 +97,8 @@ SIGNATURES = {
                              _P, _U32, _F32]),
     "fh_sph_viscosity": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _P, _P, _P, _P, _P,
                               _P, _U32, _F32]),
+    "fh_sph_force": (_I, [_P, ctypes.POINTER(FhSphParams), _P, _P, _P, _P, _P, _P, _P, _P,
+                          _P, _P, _U32, _F32]),
     "fh_sph_fused": (_I, [_P, ctypes.POINTER(FhSphParams), ctypes.POINTER(FhEpilogue),
                           _P, _P, _P, _P, _P, _P, _P, _P, _U32, _F32]),
     "fh_sph_fused_steps": (_I, [_P, ctypes.POINTER(FhSphParams), ctypes.POINTER(FhEpilogue),
@@ -104,6 +107,7 @@ SIGNATURES = {
     "fh_gravity": (_I, [_P, _P, _P, _P, _U32, _F32, _F32, _F32, _F32]),
     "fh_integrate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _F32]),
     "fh_box_collider": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _F3, _F3, _F32]),
+    "fh_pack_frame": (_I, [_P, _P, _P, _P, _U32, _U32, _P, _P]),
     "fh_graph_begin": (_I, [_P]),
     "fh_graph_end": (_I, [_P]),
     "fh_graph_launch": (_I, [_P, _U32]),

@@ -9,6 +9,8 @@ Same names, argument meaning and outputs as the reference:
   HashGrid.query_neighbors(pos, radius, positions)            hashgrid.rs:145-193
   RadixSorter(max_n).sort(keys, values, n, num_bits)          radix_sort.rs:55-220
   find_cell_boundaries(sorted, start, end, n, num_cells)      radix_sort.rs:229-317
+  cell_start_csr(sorted, n, num_cells)                        hashgrid.rs:102-106 (CSR from
+                                                              already-sorted keys)
 Differences: errors raise ForgeError instead of panicking (n > max_n, bad num_bits), and
 num_bits may be any of 1..32 (the reference required a multiple of 4).
 """
@@ -167,3 +169,17 @@ def find_cell_boundaries(sorted_cell_ids: torch.Tensor, cell_start: torch.Tensor
                                               int(n), int(num_cells), ptr(cell_start, U32),
                                               ptr(cell_end, U32)))
     ctx.sync()
+
+
+def cell_start_csr(sorted_cell_ids: torch.Tensor, n: int, num_cells: int,
+                   cell_start: torch.Tensor | None = None, ctx: Context | None = None):
+    """CSR cell_start[0..num_cells] of keys sorted ascending: cell_start[c] = number of keys < c
+    (the prefix sum of per-cell counts of hashgrid.rs:102-106).  Returns cell_start."""
+    ctx = ctx or default_context(max(int(n), 1), int(num_cells))
+    if cell_start is None:
+        cell_start = u32_empty(int(num_cells) + 1, sorted_cell_ids.device)
+    _pre(ctx)
+    check(_lib.load().fh_cell_start_csr(ctx.handle, ptr(sorted_cell_ids, U32), int(n),
+                                        int(num_cells), ptr(cell_start, U32)))
+    ctx.sync()
+    return cell_start

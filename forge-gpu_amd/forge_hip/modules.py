@@ -13,6 +13,9 @@ the builtin modules on the SPH path, dispatching to the C ABI.
   IntegrateModule          builtins/integrate.rs:5-70
   BoxColliderModule        builtins/box_collider.rs:6-85
   build_pipeline           manifest_runner.rs:322-544 (SPH fusion, parameter defaults, order)
+  init_fields              manifest_runner.rs:192-319 (field definitions -> SoA f32 fields)
+  run_streaming            manifest_runner.rs:106-181 (substeps, then a binary position frame
+                           every frame_interval steps; frame format of serve.rs:7-10,43-62)
 
 Fields stay in original particle order, as the reference keeps them.  The SPH modules create
 `density` on first use (sph_fused.rs:420-422); SphDensityModule also leaves its grid in the u32
@@ -216,6 +219,27 @@ class SphFusedModule(SimModule):
 
     def execute(self, fields: FieldSet, dt: float) -> None:
         self._call(fields, dt, None)
+
+    def execute_force(self, fields: FieldSet, dt: float) -> None:
+        """The fused force pass alone (sph_fused.rs:519-639) over the grid and densities already
+        in the field set (u32 cell_start / sorted_indices and f32 density, as SphDensityModule
+        leaves them): v += a dt in place; a_i into self.accel when set."""
+        n = fields.particle_count
+        for nm in ("cell_start", "sorted_indices"):
+            if nm not in fields.u32_fields:
+                raise _lib.ForgeError(_lib.FH_EINVAL, f"missing field {nm} (run sph_density first)")
+        cs = fields.u32_fields["cell_start"]
+        if cs.numel() != _cells(self.grid_dims) + 1:
+            raise _lib.ForgeError(_lib.FH_EINVAL, f"sph_fused: cell_start has {cs.numel()} "
+                                  f"entries, the grid needs {_cells(self.grid_dims) + 1}")
+        ctx = fields.context(_cells(self.grid_dims))
+        px, py, pz = fields.pos()
+        vx, vy, vz = fields.vel()
+        check(_lib.load().fh_sph_force(ctx.handle, ctypes.byref(_sph_params(self)), ptr(px),
+                                       ptr(py), ptr(pz), ptr(vx), ptr(vy), ptr(vz),
+                                       ptr(fields._f("density")), ptr(cs),
+                                       ptr(fields.u32_fields["sorted_indices"]), ptr(self.accel),
+                                       n, float(dt)))
 
     def execute_steps(self, fields: FieldSet, dt: float, steps: int) -> None:
         """`steps` substeps in one call (fh_sph_fused_steps): the state stays in sorted order on
@@ -459,7 +483,147 @@ def build_pipeline(forces: list[dict], constraints: list[dict], n: int,
     for c in constraints:
         if c["type"] != "box":
             raise _lib.ForgeError(_lib.FH_EINVAL, f"constraint {c['type']} is outside the SPH path")
-        mn, mx = c.get("min", [0, 0, 0]), c.get("max", [1, 1, 1])
+        # each missing element defaults on its own: min 0.0, max 1.0 (manifest_runner.rs:528-537);
+        # restitution 0.5 when absent (schema.rs:151-159)
+        mn = _elems(c.get("min", []), 3, 0.0)
+        mx = _elems(c.get("max", []), 3, 1.0)
         pipe.add(BoxColliderModule(mn[0], mn[1], mn[2], mx[0], mx[1], mx[2],
                                    float(c.get("restitution", 0.5))))
     return pipe
+
+
+# ---- fields from the manifest's field definitions (manifest_runner.rs:192-319) --------------
+
+_BASE_NAMES = {"position": "pos", "pos": "pos", "velocity": "vel", "vel": "vel"}
+
+
+def _elems(v, count: int, default: float) -> list[float]:
+    """`v.first()/get(1)/get(2).unwrap_or(default)`: each missing element defaults alone."""
+    v = list(v or [])
+    return [float(v[a]) if a < len(v) else default for a in range(count)]
+
+
+def _init_vec3(n: int, init: dict | None, seed: int, stream: int) -> list[np.ndarray]:
+    """init_vec3 (manifest_runner.rs:255-300) in float32.  `random` draws from the seeded
+    generator of workloads (the reference's thread_rng is unseeded, so no draw is reproducible
+    there); every other kind is deterministic and equals the reference's values bit for bit."""
+    from .workloads import uniform_f32
+
+    f32 = np.float32
+    kind = (init or {}).get("type", "zero")
+    if kind == "random":
+        mn = _elems(init.get("min", [-1.0, -1.0, -1.0]), 3, -1.0)  # schema.rs:83 defaults
+        mx = _elems(init.get("max", [1.0, 1.0, 1.0]), 3, 1.0)
+        out = []
+        for a in range(3):
+            u = uniform_f32(seed, 100 + 3 * stream + a, n)  # [0, 1)
+            lo, hi = f32(mn[a]), f32(mx[a])
+            v = (u * (hi - lo) + lo).astype(f32)
+            out.append(np.minimum(v, np.nextafter(hi, lo)) if hi > lo else v)  # half-open range
+        return out
+    if kind == "constant":
+        val = _elems(init.get("value", []), 3, 0.0)
+        return [np.full(n, f32(val[a]), f32) for a in range(3)]
+    if kind == "grid":
+        # side = ceil(sqrt(n as f32)); particle i at (ox + ix sp, oy, oz + iz sp), ix = i % side
+        sp = f32(init.get("spacing", 0.1))
+        o = _elems(init.get("origin", [0.0, 0.0, 0.0]), 3, 0.0)
+        side = int(np.ceil(np.sqrt(f32(n), dtype=f32)))
+        i = np.arange(n, dtype=np.int64)
+        ix, iz = (i % side).astype(f32), (i // side).astype(f32)
+        return [(f32(o[0]) + ix * sp).astype(f32), np.full(n, f32(o[1]), f32),
+                (f32(o[2]) + iz * sp).astype(f32)]
+    return [np.zeros(n, f32) for _ in range(3)]  # zero, absent or unknown
+
+
+def init_field_arrays(field_defs: list[dict], n: int, seed: int | None = None) -> dict:
+    """Host arrays of init_fields: a vec3f field `name` becomes `<base>_x/_y/_z` (base "pos" for
+    position / pos, "vel" for velocity / vel, else the name), an f32 field keeps its name
+    (constant value[0] or zeros); vel_* and pos_* default to zeros when no field made them."""
+    from .workloads import DEFAULT_SEED
+
+    seed = DEFAULT_SEED if seed is None else int(seed)
+    out: dict[str, np.ndarray] = {}
+    for k, fd in enumerate(field_defs):
+        name, kind = fd["name"], fd.get("type", "vec3f")
+        if kind == "vec3f":
+            base = _BASE_NAMES.get(name, name)
+            for a, arr in zip("xyz", _init_vec3(n, fd.get("init"), seed, k)):
+                out[f"{base}_{a}"] = arr
+        elif kind == "f32":
+            init = fd.get("init") or {}
+            v = _elems(init.get("value", []), 1, 0.0)[0] if init.get("type") == "constant" else 0.0
+            out[name] = np.full(n, np.float32(v), np.float32)
+    for base in ("vel", "pos"):
+        if f"{base}_x" not in out:
+            for a in "xyz":
+                out[f"{base}_{a}"] = np.zeros(n, np.float32)
+    return out
+
+
+def init_fields(fields: FieldSet, field_defs: list[dict], seed: int | None = None) -> None:
+    """init_fields (manifest_runner.rs:192-233): the field definitions' arrays, uploaded."""
+    for nm, arr in init_field_arrays(field_defs, fields.particle_count, seed).items():
+        fields.add_f32(nm, arr)
+
+
+# ---- frames (run_manifest_streaming, manifest_runner.rs:106-181; serve.rs:7-10,43-62) -------
+
+def frame_bytes(n: int) -> int:
+    """Size of one binary frame: u32 frame, u32 count, f32 x 3n."""
+    return 8 + 12 * int(n)
+
+
+def pack_frame(fields: FieldSet, frame: int, out: torch.Tensor | None = None,
+               counter: torch.Tensor | None = None) -> torch.Tensor:
+    """The binary frame of the current positions, packed on the device into `out` (uint8,
+    frame_bytes(n)); with `counter` (a device int32 of one element) the frame number is taken
+    from it and incremented there instead (for captured graphs)."""
+    n = fields.particle_count
+    ctx = fields.context()
+    if out is None:
+        out = torch.empty(frame_bytes(n), dtype=torch.uint8, device=f"cuda:{fields.device}")
+    if out.numel() < frame_bytes(n) or out.dtype != torch.uint8:
+        raise _lib.ForgeError(_lib.FH_EINVAL, f"frame buffer needs {frame_bytes(n)} uint8 bytes")
+    px, py, pz = fields.pos()
+    check(_lib.load().fh_pack_frame(ctx.handle, ptr(px), ptr(py), ptr(pz), n, int(frame),
+                                    ptr(counter), ptr(out)))
+    return out
+
+
+def run_streaming(pipeline: Pipeline, fields: FieldSet, dt: float, total_steps: int,
+                  substeps: int, frame_interval: int, on_frame) -> dict:
+    """run_manifest_streaming's loop (manifest_runner.rs:145-181): each step runs `substeps`
+    substeps; after step s with s % frame_interval == 0 (interval at least 1) the frame
+    (u32 frame number, u32 count, interleaved f32 positions) is packed on the device, copied
+    into pinned host memory and passed to on_frame(frame_number, frame) as a uint8 array (the
+    positions are frame[8:].view(float32)).  Returns the final positions (interleaved), count,
+    substeps run and elapsed seconds, as SimResult does."""
+    import time
+
+    n = fields.particle_count
+    interval = max(int(frame_interval), 1)
+    ctx = fields.context(max((_cells(m.grid_dims) for m in pipeline.modules
+                              if hasattr(m, "grid_dims")), default=1))
+    dev = torch.empty(frame_bytes(n), dtype=torch.uint8, device=f"cuda:{fields.device}")
+    host = torch.empty(frame_bytes(n), dtype=torch.uint8, pin_memory=True)
+    start = time.perf_counter()
+    count = frame_num = 0
+    for step in range(int(total_steps)):
+        pipeline.run_async(fields, dt, int(substeps))
+        count += int(substeps)
+        if step % interval == 0:
+            pack_frame(fields, frame_num, dev)
+            with torch.cuda.stream(ctx.torch_stream()):
+                host.copy_(dev, non_blocking=True)
+            ctx.sync()
+            on_frame(frame_num, host.numpy())
+            frame_num += 1
+    ctx.sync()
+    elapsed = time.perf_counter() - start
+    pack_frame(fields, 0, dev)
+    with torch.cuda.stream(ctx.torch_stream()):
+        host.copy_(dev, non_blocking=True)
+    ctx.sync()
+    return dict(positions=host.numpy()[8:].view(np.float32).copy(), count=n, steps=count,
+                elapsed_secs=elapsed)

@@ -124,6 +124,13 @@ int fh_sort_pairs(fh_ctx* ctx, uint32_t* keys, uint32_t* vals, uint32_t n, uint3
 int fh_find_cell_boundaries(fh_ctx* ctx, const uint32_t* sorted_keys, uint32_t n,
                             uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end);
 
+/* From keys sorted ascending: the CSR cell_start[0..C] with cell_start[c] = number of keys < c
+ * (the exclusive prefix sum of the per-cell counts that HashGrid::build writes,
+ * hashgrid.rs:102-106; cell_start[C] = n when every key is < C, keys >= C count in no cell).
+ * C = num_cells (1..2^32-2); cell_start has C+1 words. */
+int fh_cell_start_csr(fh_ctx* ctx, const uint32_t* sorted_keys, uint32_t n, uint32_t num_cells,
+                      uint32_t* cell_start);
+
 /* ---- hash grid ------------------------------------------------------------------------------ */
 
 /* HashGrid::build on the GPU (hashgrid.rs:82-125): cell_indices[i] = cell of particle i,
@@ -203,6 +210,17 @@ int fh_sph_viscosity(fh_ctx* ctx, const fh_sph_params* prm, const float* px, con
 int fh_sph_fused(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue* epi, float* px,
                  float* py, float* pz, float* vx, float* vy, float* vz, float* density,
                  float* accel, uint32_t n, float dt);
+/* The fused pressure + viscosity pass alone (the sph_fused_force kernel, sph_fused.rs:519-639,
+ * as SphFusedModule::execute launches it after its rebuild and density pass, :700-726) over a
+ * caller's grid and densities: cell_start[C+1] and sorted_indices[n] as fh_hashgrid_build or
+ * fh_sph_density write them for these positions (origin 0), density[n] in particle order.
+ * v_i += ((a_p + a_v) / rho_i) * dt in place, every neighbour velocity read from the state
+ * before the call; accel (may be NULL) receives a_i as 3 SoA arrays of n floats.  Reference
+ * expressions in the reference's neighbour order: bit-identical to the CPU restatement. */
+int fh_sph_force(fh_ctx* ctx, const fh_sph_params* prm, const float* px, const float* py,
+                 const float* pz, float* vx, float* vy, float* vz, const float* density,
+                 const uint32_t* cell_start, const uint32_t* sorted_indices, float* accel,
+                 uint32_t n, float dt);
 /* `steps` (>= 1) consecutive fh_sph_fused substeps in one call, for a module that runs alone
  * in a pipeline's substep loop (Pipeline.run / capture, manifest_runner.rs:53-77, with
  * sph_fused.rs:413-732 each substep).  In the fast mode the state stays in HBM in cell-sorted
@@ -248,6 +266,17 @@ int fh_integrate(fh_ctx* ctx, float* px, float* py, float* pz, float* vx, float*
 int fh_box_collider(fh_ctx* ctx, float* px, float* py, float* pz, float* vx, float* vy,
                     float* vz, uint32_t n, const float box_min[3], const float box_max[3],
                     float restitution);
+
+/* ---- frames (run_manifest_streaming, manifest_runner.rs:145-167; serve.rs:7-10,43-62) ------- */
+
+/* Pack the binary position frame of the streaming runner into the device buffer `out`
+ * (8 + 12 n bytes, 4-byte aligned): u32 frame number, u32 particle count n, then
+ * x0 y0 z0 x1 y1 z1 ... as f32, all little-endian.  The frame number is `frame`, or, when
+ * frame_counter (a device u32) is non-NULL, the counter's value, which the call then
+ * increments on the device -- so a captured graph that packs a frame emits consecutive
+ * numbers on its replays.  Copying `out` to the host is the caller's (one contiguous D2H). */
+int fh_pack_frame(fh_ctx* ctx, const float* px, const float* py, const float* pz, uint32_t n,
+                  uint32_t frame, uint32_t* frame_counter, void* out);
 
 /* ---- graphs (run_manifest capture/replay, manifest_runner.rs:53-77) ------------------------- */
 

@@ -378,11 +378,20 @@ void or_sph_force(const or_sph_params* p, const float* px, const float* py, cons
     }
 }
 
-/* fp64 acceleration and error scale of particle i (body of or_sph_force_f64's loop). */
+/* Relative size of a pair distance's float32 rounding in the sensitivity scale: r^2 from
+ * rounded differences, squares and sums (about 4 units of roundoff), then a square root or a
+ * reciprocal square root (1-2 more), with a margin: 8 units of 2^-24. */
+#define OR_DR_REL (8.0 / 16777216.0)
+
+/* fp64 acceleration, error scale and distance-rounding sensitivity of particle i (body of
+ * or_sph_force_f64's loop).  s = sum over pairs of |pressure term| + |viscosity term|;
+ * e = sum over pairs of |d term / d r| * OR_DR_REL * r: (h - r) cancels for r near h, so a
+ * float32 rounding of r changes such a term by far more than its own relative rounding. */
 static void force64_one(const or_sph_params* p, const float* px, const float* py,
                         const float* pz, const float* vx, const float* vy, const float* vz,
                         const float* density, const uint32_t* cell_start,
-                        const uint32_t* sorted_indices, uint32_t i, double a[3], double s[3]) {
+                        const uint32_t* sorted_indices, uint32_t i, double a[3], double s[3],
+                        double e[3]) {
     const double h = p->h, mass = p->mass;
     const double k = p->gas_constant, rho0 = p->rest_density, mu = p->visc;
     const int32_t gnx = (int32_t)p->dims[0], gny = (int32_t)p->dims[1], gnz = (int32_t)p->dims[2];
@@ -390,7 +399,7 @@ static void force64_one(const or_sph_params* p, const float* px, const float* py
     const double PI = 3.14159265358979323846;
     double h6 = h * h * h * h * h * h;
     double gcoef = -45.0 / (PI * h6), lcoef = 45.0 / (PI * h6);
-    for (int c = 0; c < 3; c++) a[c] = s[c] = 0.0;
+    for (int c = 0; c < 3; c++) a[c] = s[c] = e[c] = 0.0;
     float rho_if = density[i];
     if (rho_if < 1e-6f) return;
     double rho_i = rho_if, p_i = k * (rho_i - rho0);
@@ -420,29 +429,37 @@ static void force64_one(const or_sph_params* p, const float* px, const float* py
                     double vsc = mu * mass / rho_j * (lcoef * diff);
                     double dv[3] = {(double)vx[j] - vx[i], (double)vy[j] - vy[i],
                                     (double)vz[j] - vz[i]};
+                    /* d/dr of the pair factors (the direction d / r is well conditioned) */
+                    double dfsc = -mass * (p_i + p_j) / (2.0 * rho_j) * (gcoef * 2.0 * diff / r);
+                    double dvsc = mu * mass / rho_j * lcoef;
+                    double dr = OR_DR_REL * r;
                     for (int c = 0; c < 3; c++) {
                         double tp = fsc * d[c], tv = vsc * dv[c];
                         a[c] += tp + tv;
                         s[c] += fabs(tp) + fabs(tv);
+                        e[c] += (fabs(dfsc * d[c]) + fabs(dvsc * dv[c])) * dr;
                     }
                 }
             }
     for (int c = 0; c < 3; c++) {
         a[c] /= rho_i;
         s[c] /= rho_i;
+        e[c] /= rho_i;
     }
 }
 
 void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
                       const float* pz, const float* vx, const float* vy, const float* vz,
                       const float* density, uint32_t n, const uint32_t* cell_start,
-                      const uint32_t* sorted_indices, double* accel64, double* scale64) {
+                      const uint32_t* sorted_indices, double* accel64, double* scale64,
+                      double* sens64) {
     for (uint32_t i = 0; i < n; i++) {
-        double a[3], s[3];
-        force64_one(p, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices, i, a, s);
+        double a[3], s[3], e[3];
+        force64_one(p, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices, i, a, s, e);
         for (int c = 0; c < 3; c++) {
             accel64[(size_t)c * n + i] = a[c];
             scale64[(size_t)c * n + i] = s[c];
+            if (sens64) sens64[(size_t)c * n + i] = e[c];
         }
     }
 }
@@ -451,14 +468,15 @@ void or_sph_force_f64_at(const or_sph_params* p, const float* px, const float* p
                          const float* pz, const float* vx, const float* vy, const float* vz,
                          const float* density, const uint32_t* cell_start,
                          const uint32_t* sorted_indices, const uint32_t* which, uint32_t m,
-                         double* accel64, double* scale64) {
+                         double* accel64, double* scale64, double* sens64) {
     for (uint32_t q = 0; q < m; q++) {
-        double a[3], s[3];
+        double a[3], s[3], e[3];
         force64_one(p, px, py, pz, vx, vy, vz, density, cell_start, sorted_indices, which[q], a,
-                    s);
+                    s, e);
         for (int c = 0; c < 3; c++) {
             accel64[(size_t)c * m + q] = a[c];
             scale64[(size_t)c * m + q] = s[c];
+            if (sens64) sens64[(size_t)c * m + q] = e[c];
         }
     }
 }

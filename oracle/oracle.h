@@ -102,19 +102,23 @@ void or_sph_force(const or_sph_params* p, const float* px, const float* py, cons
 
 /* fp64 restatement of or_sph_force (same neighbour set, selected with the fp32 r^2 tests):
  * accel64 = a_i in double, scale64 = sum_j (|pressure term| + |viscosity term|) / rho_i per
- * component -- the error scale of the force tolerance. */
+ * component -- the error scale of the force tolerance -- and, if sens64 is non-NULL,
+ * sens64 = sum_j |d(pressure term + viscosity term)/dr| * 8 * 2^-24 * r / rho_i (per term, the
+ * change an 8-unit float32 rounding of the pair distance makes: the factor h - r cancels near
+ * r = h, so such a rounding moves the term by far more than 2^-24 of itself). */
 void or_sph_force_f64(const or_sph_params* p, const float* px, const float* py,
                       const float* pz, const float* vx, const float* vy, const float* vz,
                       const float* density, uint32_t n, const uint32_t* cell_start,
-                      const uint32_t* sorted_indices, double* accel64, double* scale64);
+                      const uint32_t* sorted_indices, double* accel64, double* scale64,
+                      double* sens64);
 
-/* or_sph_force_f64 for the particles which[0..m) only: accel64 / scale64 as 3 arrays of m
- * doubles, entry k for particle which[k]. */
+/* or_sph_force_f64 for the particles which[0..m) only: accel64 / scale64 / sens64 as 3 arrays
+ * of m doubles, entry k for particle which[k]. */
 void or_sph_force_f64_at(const or_sph_params* p, const float* px, const float* py,
                          const float* pz, const float* vx, const float* vy, const float* vz,
                          const float* density, const uint32_t* cell_start,
                          const uint32_t* sorted_indices, const uint32_t* which, uint32_t m,
-                         double* accel64, double* scale64);
+                         double* accel64, double* scale64, double* sens64);
 
 /* Unfused SphPressureModule kernel, sph_pressure.rs:28-112: for each particle i with
  * rho_i >= 1e-6, a_p over the 27-cell neighbourhood of the grid (cell_start, sorted_indices as

@@ -36,11 +36,11 @@ _SIG = {
     "or_sph_density": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _U, _P, _P, _P]),
     "or_sph_density_at": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _U, _P]),
     "or_sph_force_f64_at": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _P,
-                                   _P, _P, _U, _P, _P]),
+                                   _P, _P, _U, _P, _P, _P]),
     "or_sph_force": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P, _P,
                             _F, _P, _P]),
     "or_sph_force_f64": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
-                                _P, _P, _P]),
+                                _P, _P, _P, _P]),
     "or_sph_pressure": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
                                _P, _F, _P]),
     "or_sph_viscosity": (None, [ctypes.POINTER(SphParams), _P, _P, _P, _P, _P, _P, _P, _U, _P,
@@ -195,15 +195,17 @@ def sph_density_at(p: SphParams, x, y, z, cell_start, sorted_indices, which):
 
 def sph_force_f64_at(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices,
                      which):
-    """sph_force_f64 of the particles `which` only: (3, m) accelerations and error scales."""
+    """sph_force_f64 of the particles `which` only: (3, m) accelerations, error scales and
+    distance-rounding sensitivities."""
     arrs = [_f32(a) for a in (x, y, z, vx, vy, vz, density)]
     cs, si, w = _u32(cell_start), _u32(sorted_indices), _u32(which)
     m = w.size
     a64 = np.empty(3 * m, np.float64)
     s64 = np.empty(3 * m, np.float64)
+    e64 = np.empty(3 * m, np.float64)
     lib().or_sph_force_f64_at(ctypes.byref(p), *[_p(a) for a in arrs], _p(cs), _p(si), _p(w), m,
-                              _p(a64), _p(s64))
-    return a64.reshape(3, m), s64.reshape(3, m)
+                              _p(a64), _p(s64), _p(e64))
+    return a64.reshape(3, m), s64.reshape(3, m), e64.reshape(3, m)
 
 
 def sph_force(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices, dt):
@@ -223,9 +225,10 @@ def sph_force_f64(p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted
     cs, si = _u32(cell_start), _u32(sorted_indices)
     a64 = np.empty(3 * n, np.float64)
     s64 = np.empty(3 * n, np.float64)
+    e64 = np.empty(3 * n, np.float64)
     lib().or_sph_force_f64(ctypes.byref(p), *[_p(a) for a in arrs], n, _p(cs), _p(si),
-                           _p(a64), _p(s64))
-    return a64.reshape(3, n), s64.reshape(3, n)
+                           _p(a64), _p(s64), _p(e64))
+    return a64.reshape(3, n), s64.reshape(3, n), e64.reshape(3, n)
 
 
 def _unfused(fn, p: SphParams, x, y, z, vx, vy, vz, density, cell_start, sorted_indices, dt):

@@ -1,8 +1,9 @@
 """GPU parity of the SPH modules (C ABI fh_sph_fused, fh_sph_density, fh_gravity,
 fh_integrate, fh_box_collider) against the oracle, one Pipeline::step from identical inputs.
 Bar: densities and positions within rel 1e-4; accelerations
-("forces") within 1e-4 * sum_j |pair terms| per component, with the reference acceleration and
-that scale computed in fp64 (or_sph_force_f64)."""
+("forces") within 1e-4 * sum_j |pair terms| per component plus the terms' sensitivity to a
+float32 rounding of the pair distances, with the reference acceleration and both scales
+computed in fp64 (or_sph_force_f64)."""
 import numpy as np
 import pytest
 import torch
@@ -36,14 +37,6 @@ def sph_pipeline(fh, cfg, fuse=True, accel=None):
     return p
 
 
-def oracle_step(oracle, cfg, vel=None, flags=7):
-    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
-                            cfg.rest_density, cfg.viscosity)
-    v = vel if vel is not None else [np.zeros(cfg.n, np.float32)] * 3
-    return prm, oracle.sph_step(prm, flags, cfg.gravity, cfg.box_min, cfg.box_max,
-                                cfg.restitution, cfg.x, cfg.y, cfg.z, v[0], v[1], v[2], cfg.dt)
-
-
 def rel_err(a, b):
     return np.abs(a - b) / np.maximum(np.abs(b), 1e-30)
 
@@ -58,7 +51,10 @@ def set_mode(fh, f, cfg, mode):
     ctx.set_option(fh.FH_OPT_DIRECT_ITEMS, {"heavy": 0, "light": 0, "direct": 2}.get(mode, 1))
 
 
-def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast"):
+def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast", visible=None):
+    """One step through the pipeline against the oracle.  visible: particle indices whose
+    acceleration must be resolvable by the bound (median |a64| >= 100 x 1e-4 sum|terms|, over
+    all particles and over these), so that the term under test cannot hide in the tolerance."""
     accel = torch.zeros((3, cfg.n), dtype=torch.float32, device="cuda")
     f = fields_from(fh, cfg, vel)
     set_mode(fh, f, cfg, mode)
@@ -67,40 +63,64 @@ def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast"):
     p.step(f, cfg.dt)
     set_mode(fh, f, cfg, "fast")
     got = {k: f.f32_fields[k].cpu().numpy() for k in f.f32_fields}
-    prm, (ox, oy, oz, ovx, ovy, ovz, orho, oacc) = oracle_step(oracle, cfg, vel)
-    # density: rel 1e-4
+    return assert_oracle_step(oracle, cfg, (cfg.x, cfg.y, cfg.z), vel, got,
+                              accel.cpu().numpy(), exact=mode == "exact", visible=visible)
+
+
+def assert_oracle_step(oracle, cfg, pos, vel, got, gacc, exact=False, visible=None):
+    """`got` (fields after one substep) and `gacc` (its accelerations) against one oracle step
+    (or_sph_step) from positions `pos` and velocities `vel`, particle by particle:
+      density            |d - d_ref| <= 1e-4 |d_ref|
+      acceleration       |a - a64| <= 1e-4 sum_j |pair terms| + sens  (fp64 reference)
+      velocity           |v - v_ref| <= 1e-4 |v_ref| + dt * (the acceleration bound)
+      position           |x - x_ref| <= 1e-4 |x_ref| + dt^2 * (the acceleration bound)
+    sens (or_sph_force_f64) is the change of the pair terms under a float32 rounding of the pair
+    distances: a pair near r = h has a factor h - r that cancels, so any float32 evaluation of
+    it (the float32 oracle's included) is off by more than 1e-4 of the term, and a particle
+    whose only neighbours sit there has nothing else in its sum.
+    v = v0 + a dt + g dt and x = x0 + v dt, hence the dt and dt^2 terms.  A particle whose
+    unclamped position lies within that bound of a box wall has an ill-conditioned clamp
+    decision (reflected or not) and is left out of the field checks (the count is returned).
+    exact: every output bit-identical to the oracle."""
+    x, y, z = (np.ascontiguousarray(a, dtype=np.float32) for a in pos)
+    v0 = [np.ascontiguousarray(a, dtype=np.float32) for a in vel] if vel is not None \
+        else [np.zeros(cfg.n, np.float32)] * 3
+    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity)
+    args = (cfg.gravity, cfg.box_min, cfg.box_max, cfg.restitution, x, y, z, *v0, cfg.dt)
+    ox, oy, oz, ovx, ovy, ovz, orho, oacc = oracle.sph_step(prm, 7, *args)
     assert rel_err(got["density"], orho).max() <= REL
-    # accelerations: |a - a64| <= 1e-4 * sum|terms| (fp64 reference and scale)
-    v0 = vel if vel is not None else [np.zeros(cfg.n, np.float32)] * 3
-    ocs, osi, _ = oracle.hashgrid_build(cfg.x, cfg.y, cfg.z, cfg.cell_size, (0, 0, 0), cfg.dims)
-    a64, s64 = oracle.sph_force_f64(prm, cfg.x, cfg.y, cfg.z, *v0, orho, ocs, osi)
-    ga = accel.cpu().numpy().astype(np.float64)
-    assert np.all(np.abs(ga - a64) <= REL * s64 + 1e-30)
-    # Positions and velocities after gravity / integrate / box.  v = v0 + a dt + g dt and
-    # x = x0 + v dt, so the admissible error is rel 1e-4 of the value plus dt (resp. dt^2) times
-    # the force tolerance.  A particle whose unclamped position lies within that error of a box
-    # wall has an ill-conditioned clamp decision (reflected or not) and is left out.
-    _, pre = oracle_step(oracle, cfg, vel, flags=3)  # same step without the box
+    ocs, osi, _ = oracle.hashgrid_build(x, y, z, cfg.cell_size, (0, 0, 0), cfg.dims)
+    a64, s64, e64 = oracle.sph_force_f64(prm, x, y, z, *v0, orho, ocs, osi)
+    ga = gacc.astype(np.float64)
+    atol = REL * s64 + e64 + 1e-30
+    bad = np.abs(ga - a64) > atol
+    assert not bad.any(), (int(bad.any(0).sum()), float((np.abs(ga - a64) / atol).max()))
+    if visible is not None:
+        ratio = np.abs(a64) / atol
+        assert np.median(ratio) >= 100 and np.median(ratio[:, visible]) >= 100, \
+            (np.median(ratio), np.median(ratio[:, visible]))
+    pre = oracle.sph_step(prm, 3, *args)  # the same step without the box
     amb = np.zeros(cfg.n, bool)
     for a, o in enumerate(pre[:3]):
-        ptol = REL * np.abs(o) + cfg.dt * cfg.dt * REL * s64[a]
+        ptol = REL * np.abs(o) + cfg.dt * cfg.dt * atol[a]
         amb |= (np.abs(o - cfg.box_min[a]) <= ptol) | (np.abs(o - cfg.box_max[a]) <= ptol)
     ok = ~amb
     for a, (k, o) in enumerate((("pos_x", ox), ("pos_y", oy), ("pos_z", oz))):
-        tol = REL * np.abs(o) + cfg.dt * cfg.dt * REL * s64[a] + 1e-30
+        tol = REL * np.abs(o) + cfg.dt * cfg.dt * atol[a]
         assert np.all((np.abs(got[k] - o) <= tol)[ok]), k
     for a, (k, o) in enumerate((("vel_x", ovx), ("vel_y", ovy), ("vel_z", ovz))):
-        tol = REL * np.abs(o) + cfg.dt * REL * s64[a] + 1e-30
+        tol = REL * np.abs(o) + cfg.dt * atol[a]
         assert np.all((np.abs(got[k] - o) <= tol)[ok]), k
-    exact = {k: float(np.mean(got[k] == o)) for k, o in
-             (("density", orho), ("pos_x", ox), ("pos_y", oy), ("pos_z", oz), ("vel_x", ovx),
-              ("vel_y", ovy), ("vel_z", ovz))}
-    exact["accel"] = float(np.mean(accel.cpu().numpy() == oacc))
-    exact["ambiguous_clamps"] = int(amb.sum())
-    if mode == "exact":
+    fr = {k: float(np.mean(got[k] == o)) for k, o in
+          (("density", orho), ("pos_x", ox), ("pos_y", oy), ("pos_z", oz), ("vel_x", ovx),
+           ("vel_y", ovy), ("vel_z", ovz))}
+    fr["accel"] = float(np.mean(gacc == oacc))
+    fr["ambiguous_clamps"] = int(amb.sum())
+    if exact:
         # reference float expressions in the reference order: bit-identical to the oracle
-        assert all(exact[k] == 1.0 for k in exact if k != "ambiguous_clamps"), exact
-    return exact
+        assert all(fr[k] == 1.0 for k in fr if k != "ambiguous_clamps"), fr
+    return fr
 
 
 @pytest.mark.parametrize("mode", ["fast", "exact"])
@@ -197,6 +217,59 @@ def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
     exact = check_step(fh, oracle, cfg, vel, mode=mode)
+    print("bit-exact fractions", exact)
+
+
+def interior_groups_cfg(seed=36):
+    """Co-located groups inside the lattice block (x, y in [0, 0.3), z in [0, 0.87)): every
+    group's 27 cells hold lattice particles, the z +-1 slabs included, and every member has a
+    velocity of its own.  Returns the config, the velocities and the members' indices."""
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=40_000, cols=24)
+    rng = np.random.default_rng(seed)
+    spots = [((0.1, 0.15, 0.3), 400), ((0.2, 0.08, 0.55), 120), ((0.13, 0.22, 0.7), 64)]
+    at = cfg.n
+    members = []
+    for (x, y, z), k in spots:  # taken from the top layers, so the block below stays whole
+        cfg.x[at - k:at], cfg.y[at - k:at], cfg.z[at - k:at] = x, y, z
+        members.append(np.arange(at - k, at))
+        at -= k
+    perm = rng.permutation(cfg.n)
+    for a in ("x", "y", "z"):
+        setattr(cfg, a, np.ascontiguousarray(getattr(cfg, a)[perm]))
+    members = np.argsort(perm)[np.concatenate(members)]
+    vel = [rng.uniform(-1, 1, cfg.n).astype(np.float32) for _ in range(3)]
+    return cfg, vel, members
+
+
+def viscosity_cfg(case):
+    """gas_constant = 0: the pressure term vanishes and the acceleration is the viscosity term
+    alone (with the reference's constants the pressure term is ~10^4 times larger, so the
+    viscosity term is invisible within the force bound)."""
+    from forge_hip import workloads
+    if case == "lattice":
+        cfg = workloads.small_sph(n=20_000, cols=24)
+        rng = np.random.default_rng(5)
+        vel = [rng.uniform(-0.5, 0.5, cfg.n).astype(np.float32) for _ in range(3)]
+        visible = np.arange(cfg.n)
+    elif case == "groups":
+        cfg, vel, visible = interior_groups_cfg()
+    else:  # the corner and stand-alone groups, members with distinct velocities
+        cfg, vel = colocated_cfg(seed=37)
+        visible = np.arange(cfg.n)
+    cfg.gas_constant = 0.0
+    return cfg, vel, visible
+
+
+@pytest.mark.parametrize("case", ["lattice", "groups", "colocated"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "light", "direct"])
+def test_viscosity_without_pressure_matches_oracle(fh, gpu_ctx, oracle, case, mode):
+    """The fused force's viscosity half (sph_fused.rs:617-623) on its own, in every work split:
+    plain lattice particles, and members of co-located groups, which are finished from their
+    representative with the viscosity weight of all three z-slabs."""
+    cfg, vel, visible = viscosity_cfg(case)
+    print(f"viscosity without pressure: {case} ({mode})", flush=True)
+    exact = check_step(fh, oracle, cfg, vel, mode=mode, visible=visible)
     print("bit-exact fractions", exact)
 
 
@@ -341,63 +414,23 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle):
                             cfg.rest_density, cfg.viscosity)
     orho = oracle.sph_density_at(prm, cfg.x, cfg.y, cfg.z, ocs, osi, which)
     assert rel_err(rho[which], orho).max() <= REL
-    a64, s64 = oracle.sph_force_f64_at(prm, cfg.x, cfg.y, cfg.z, *vel, rho, ocs, osi, which)
-    assert np.all(np.abs(acc[:, which] - a64) <= REL * s64 + 1e-30)
+    a64, s64, e64 = oracle.sph_force_f64_at(prm, cfg.x, cfg.y, cfg.z, *vel, rho, ocs, osi,
+                                            which)
+    assert np.all(np.abs(acc[:, which] - a64) <= REL * s64 + e64 + 1e-30)
     print(f"c4: {which.size} particles checked, density max rel "
           f"{rel_err(rho[which], orho).max():.3g}")
 
 
-def close(a, b, rel=REL):
-    """|a - b| <= rel (|b| + max|b|): two fast-mode results that differ only by summation order."""
-    return np.abs(a - b) <= rel * (np.abs(b) + np.abs(b).max())
-
-
-@pytest.mark.parametrize("case", ["small", "colocated", "c0"])
-def test_resident_substeps_match_separate_substeps(fh, gpu_ctx, case):
-    """fh_sph_fused_steps (state kept in sorted order between substeps) against the same number
-    of fh_sph_fused calls: equal up to rounding (particles of a cell are visited in the previous
-    substep's order), on the fields after the last substep and the accelerations of the last
-    substep; steps = 1 is fh_sph_fused bit for bit."""
+@pytest.mark.parametrize("case", ["small", "colocated"])
+def test_one_resident_substep_is_fh_sph_fused(fh, gpu_ctx, case):
+    """fh_sph_fused_steps with steps = 1 is fh_sph_fused, bit for bit."""
     from forge_hip import workloads
     if case == "small":
         cfg = workloads.small_sph(n=20_000, cols=24)
         rng = np.random.default_rng(8)
         vel = [rng.uniform(-0.5, 0.5, cfg.n).astype(np.float32) for _ in range(3)]
-        steps = 4
-    elif case == "colocated":
+    else:
         cfg, vel = colocated_cfg(seed=35)
-        steps = 3
-    else:  # configs[0]: with the reference's constants (rho << rho0, strongly attractive pressure)
-        # the particles reach the walls within two substeps and the motion is chaotic from then
-        # on, so only two substeps (the second one resident) compare up to rounding
-        cfg, vel = workloads.config0(), None
-        steps = 2
-    print(f"resident substeps {case} n={cfg.n} steps={steps}", flush=True)
-    out = {}
-    for resident in (False, True):
-        acc = torch.zeros((3, cfg.n), dtype=torch.float32, device="cuda")
-        f = fields_from(fh, cfg, vel)
-        p = sph_pipeline(fh, cfg, accel=acc)
-        p.resident = resident
-        set_mode(fh, f, cfg, "fast")
-        torch.cuda.synchronize()
-        p.run(f, cfg.dt, steps)
-        out[resident] = {k: v.cpu().numpy() for k, v in f.f32_fields.items()}
-        out[resident]["accel"] = acc.cpu().numpy()
-    # A particle that ends on a box wall in either run had an ill-conditioned clamp decision
-    # (c3's particles reach the walls within two substeps) and is left out.
-    wall = np.zeros(cfg.n, bool)
-    for r in out.values():
-        for a, nm in enumerate(("pos_x", "pos_y", "pos_z")):
-            wall |= (r[nm] == np.float32(cfg.box_min[a])) | (r[nm] == np.float32(cfg.box_max[a]))
-    print("particles on a wall", int(wall.sum()), flush=True)
-    for k in out[False]:
-        # an acceleration is a sum of pair terms that largely cancel (|a| << sum |terms|), so a
-        # rounding change in the inputs moves it by more, relative to |a|, than the fields
-        ok = close(out[True][k], out[False][k], 10 * REL if k == "accel" else REL)
-        ok |= wall
-        assert ok.all(), (k, int((~ok).sum()))
-    # one substep through fh_sph_fused_steps is fh_sph_fused
     f1, f2 = fields_from(fh, cfg, vel), fields_from(fh, cfg, vel)
     m = sph_pipeline(fh, cfg)._fused_plan()[0]
     torch.cuda.synchronize()
@@ -406,6 +439,69 @@ def test_resident_substeps_match_separate_substeps(fh, gpu_ctx, case):
     f1.context().sync()
     for k in f1.f32_fields:
         assert torch.equal(f1.f32_fields[k], f2.f32_fields[k]), k
+
+
+def resident_case(case):
+    from forge_hip import workloads
+    if case == "small":
+        cfg = workloads.small_sph(n=20_000, cols=24)
+        rng = np.random.default_rng(8)
+        return cfg, [rng.uniform(-0.5, 0.5, cfg.n).astype(np.float32) for _ in range(3)], 4
+    if case == "colocated":
+        cfg, vel = colocated_cfg(seed=35)
+        return cfg, vel, 3
+    if case == "c0":
+        return workloads.config0(), None, 2
+    cfg, vel, _ = viscosity_cfg("groups" if case == "groups_k0" else "lattice")
+    return cfg, vel, 4
+
+
+@pytest.mark.parametrize("case", ["small", "colocated", "c0", "lattice_k0", "groups_k0"])
+def test_resident_substeps_match_oracle(fh, gpu_ctx, oracle, case):
+    """Resident substeps (fh_sph_fused_steps: the state stays in sorted order on the device
+    between substeps, sorted by the previous substep's slots) against the oracle, particle by
+    particle.  A call of k substeps repeats the first k - 1 substeps of the call of k - 1
+    bit for bit, so substep k is checked as one oracle step (or_sph_step) from the fields the
+    (k-1)-substep call returned, at the one-step bar, for k = 1 .. K.  Every substep after the
+    first runs resident.  _k0 cases: gas_constant = 0 (the viscosity term alone, non-chaotic
+    motion), where the K-substep result is also compared with K chained oracle steps from the
+    initial fields, within K times the one-step bound."""
+    cfg, vel, K = resident_case(case)
+    print(f"resident substeps vs oracle: {case} n={cfg.n} K={K}", flush=True)
+    states = [({"pos_x": cfg.x, "pos_y": cfg.y, "pos_z": cfg.z}, vel)]
+    for k in range(1, K + 1):
+        acc = torch.zeros((3, cfg.n), dtype=torch.float32, device="cuda")
+        f = fields_from(fh, cfg, vel)
+        p = sph_pipeline(fh, cfg, accel=acc)
+        p.resident = True
+        set_mode(fh, f, cfg, "fast")
+        torch.cuda.synchronize()
+        p.run(f, cfg.dt, k)
+        got = {nm: t.cpu().numpy() for nm, t in f.f32_fields.items()}
+        prev, pvel = states[-1]
+        fr = assert_oracle_step(oracle, cfg, (prev["pos_x"], prev["pos_y"], prev["pos_z"]),
+                                pvel, got, acc.cpu().numpy())
+        print(f"  substep {k}: bit-exact fractions {fr}", flush=True)
+        states.append((got, [got["vel_x"], got["vel_y"], got["vel_z"]]))
+    if cfg.gas_constant == 0.0:
+        prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                                cfg.rest_density, cfg.viscosity)
+        st = [cfg.x.copy(), cfg.y.copy(), cfg.z.copy()] + [v.copy() for v in vel]
+        vtol = np.zeros((3, cfg.n))
+        for _ in range(K):
+            ocs, osi, _ = oracle.hashgrid_build(*st[:3], cfg.cell_size, (0, 0, 0), cfg.dims)
+            out = oracle.sph_step(prm, 7, cfg.gravity, cfg.box_min, cfg.box_max,
+                                  cfg.restitution, *st, cfg.dt)
+            _, s64, e64 = oracle.sph_force_f64(prm, *st, out[6], ocs, osi)
+            vtol += cfg.dt * (REL * s64 + e64)
+            st = list(out[:6])
+        got = states[-1][0]
+        for a, nm in enumerate(("vel_x", "vel_y", "vel_z")):
+            tol = K * (REL * np.abs(st[3 + a]) + vtol[a]) + 1e-30
+            assert np.all(np.abs(got[nm] - st[3 + a]) <= tol), nm
+        for a, nm in enumerate(("pos_x", "pos_y", "pos_z")):
+            tol = K * (REL * np.abs(st[a]) + cfg.dt * vtol[a]) + 1e-30
+            assert np.all(np.abs(got[nm] - st[a]) <= tol), nm
 
 
 def test_fused_steps_edge_cases(fh, gpu_ctx):

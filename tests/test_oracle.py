@@ -259,7 +259,7 @@ def test_force_closed_forms(oracle):
     st, si = grid(oracle, x, y, z)
     rho = oracle.sph_density(p, x, y, z, st, si)
     vout, acc = oracle.sph_force(p, x, y, z, vx, vy, vz, rho, st, si, 1e-4)
-    a64, s64 = oracle.sph_force_f64(p, x, y, z, vx, vy, vz, rho, st, si)
+    a64, s64, _ = oracle.sph_force_f64(p, x, y, z, vx, vy, vz, rho, st, si)
     for i, j in ((0, 1), (1, 0)):
         exp = pair_accel((x[i], y[i], z[i]), (x[j], y[j], z[j]), (vx[i], vy[i], vz[i]),
                          (vx[j], vy[j], vz[j]), float(rho[i]), float(rho[j]))
@@ -274,6 +274,50 @@ def test_force_closed_forms(oracle):
     assert np.allclose(vout[0], vx + acc[0] * np.float32(1e-4), rtol=0, atol=1e-7)
 
 
+def test_force_viscosity_closed_form_without_pressure(oracle):
+    """gas_constant = 0 removes the pressure term, so the fused force is the viscosity term
+    alone: a_i = sum_j mu m (v_j - v_i) / rho_j * 45 / (pi h^6) (h - r) / rho_i
+    (sph_fused.rs:617-623).  With the reference constants the pressure term is ~10^6 times
+    larger, so only this configuration pins the viscosity half of or_sph_force: a dropped
+    term, a flipped sign, (v_i - v_j) for (v_j - v_i), rho_i for rho_j or a missing (h - r)
+    each move every particle's acceleration by far more than rtol 1e-6."""
+    p0 = oracle.sph_params(H, H, (40, 40, 40), MASS, 0.0, RHO0, MU)
+    x = np.array([0.5, 0.512, 0.495, 0.507, 0.53], np.float32)
+    y = np.array([0.4, 0.405, 0.391, 0.414, 0.40], np.float32)
+    z = np.array([0.3, 0.296, 0.309, 0.288, 0.3], np.float32)
+    vx = np.array([0.1, -0.3, 0.25, 0.7, -0.2], np.float32)
+    vy = np.array([0.0, 0.2, -0.45, 0.15, 0.33], np.float32)
+    vz = np.array([0.5, 0.6, -0.1, 0.05, 0.9], np.float32)
+    st, si = grid(oracle, x, y, z)
+    # densities chosen apart from the poly6 sums, so rho_i and rho_j cannot be exchanged
+    rho = np.array([3.0, 7.5, 11.25, 5.5, 9.0], np.float32)
+    _, acc = oracle.sph_force(p0, x, y, z, vx, vy, vz, rho, st, si, 1e-4)
+    a64, s64, _ = oracle.sph_force_f64(p0, x, y, z, vx, vy, vz, rho, st, si)
+    lap = 45.0 / (PI * H**6)
+    P = np.stack([x, y, z], 1).astype(np.float64)
+    V = np.stack([vx, vy, vz], 1).astype(np.float64)
+    for i in range(5):
+        exp = np.zeros(3)
+        scale = np.zeros(3)  # sum of the terms' magnitudes (float32 rounding is relative to it)
+        pairs = 0
+        for j in range(5):
+            r = np.linalg.norm(P[i] - P[j])
+            if j != i and r < H:
+                t = MU * MASS * (V[j] - V[i]) / float(rho[j]) * lap * (H - r) / float(rho[i])
+                exp += t
+                scale += np.abs(t)
+                pairs += 1
+        assert pairs >= 1
+        # every component is at least 1e-3 of its scale, so flipping its sign (an error of
+        # 2 |exp|), or dropping or mis-scaling a term (an error of a term's size), exceeds the
+        # bound below by more than 10^3
+        assert np.all(np.abs(exp) >= 1e-3 * scale), (i, exp, scale)
+        assert np.all(np.abs(acc[:, i] - exp) <= 1e-6 * scale), (i, acc[:, i], exp)
+        assert np.all(np.abs(a64[:, i] - exp) <= 1e-12 * scale), i
+        # the fp64 error scale is the sum of the viscosity terms' magnitudes alone
+        assert np.allclose(s64[:, i], scale, rtol=1e-9), i
+
+
 def test_force_vs_brute_force_and_f64(oracle):
     rng = np.random.default_rng(14)
     n = 2500
@@ -283,7 +327,7 @@ def test_force_vs_brute_force_and_f64(oracle):
     st, si = grid(oracle, P[:, 0], P[:, 1], P[:, 2])
     rho = oracle.sph_density(p, P[:, 0], P[:, 1], P[:, 2], st, si)
     _, acc = oracle.sph_force(p, *P.T, *V.T, rho, st, si, 1e-4)
-    a64, s64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
+    a64, s64, _ = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
     bf = np.zeros((3, n))
     for i in range(0, n, 97):  # brute force over all particles for a sample of i
         for j in range(n):
@@ -303,11 +347,54 @@ def test_subset_passes_equal_the_full_passes(oracle):
     p = prm(oracle)
     st, si = grid(oracle, P[:, 0], P[:, 1], P[:, 2])
     rho = oracle.sph_density(p, *P.T, st, si)
-    a64, s64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
+    a64, s64, e64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
     which = np.concatenate([rng.permutation(n)[:400], [0, n - 1, 7, 7]]).astype(np.uint32)
     assert np.array_equal(oracle.sph_density_at(p, *P.T, st, si, which), rho[which])
-    b64, t64 = oracle.sph_force_f64_at(p, *P.T, *V.T, rho, st, si, which)
+    b64, t64, f64 = oracle.sph_force_f64_at(p, *P.T, *V.T, rho, st, si, which)
     assert np.array_equal(b64, a64[:, which]) and np.array_equal(t64, s64[:, which])
+    assert np.array_equal(f64, e64[:, which])
+
+
+def test_force_distance_rounding_sensitivity(oracle):
+    """The third output of or_sph_force_f64: per pair, |d term / dr| * 8 * 2^-24 * r / rho_i
+    with d/dr of the pressure factor (h - r)^2 / r * d taken at fixed direction d
+    (-2 (h - r) / r * d) and of the viscosity factor (h - r) (-1).  Checked against the
+    textbook terms of pair_accel for a two-particle pair, then as a bound: on sparse random
+    particles (a few neighbours each, some near r = h, where h - r cancels), the float32
+    oracle is within 1e-5 sum|terms| + sens of the fp64 values for every particle, while
+    without the sensitivity some particles are not."""
+    p = prm(oracle)
+    u = 8.0 * 2.0**-24
+    x = np.array([0.5, 0.512], np.float32)
+    y = np.array([0.4, 0.405], np.float32)
+    z = np.array([0.3, 0.296], np.float32)
+    vx, vy, vz = (np.array([0.1, -0.3], np.float32), np.array([0.0, 0.2], np.float32),
+                  np.array([0.5, 0.5], np.float32))
+    st, si = grid(oracle, x, y, z)
+    rho = oracle.sph_density(p, x, y, z, st, si)
+    _, _, e64 = oracle.sph_force_f64(p, x, y, z, vx, vy, vz, rho, st, si)
+    for i, j in ((0, 1), (1, 0)):
+        d = np.array([x[i], y[i], z[i]], np.float64) - np.array([x[j], y[j], z[j]], np.float64)
+        dv = np.array([vx[j], vy[j], vz[j]], np.float64) - np.array([vx[i], vy[i], vz[i]])
+        r = np.linalg.norm(d)
+        ri, rj = float(rho[i]), float(rho[j])
+        pij = K * (ri - RHO0) + K * (rj - RHO0)
+        dp = np.abs(MASS * pij / (2 * rj) * 45.0 / (PI * H**6) * 2 * (H - r) / r) * np.abs(d)
+        dvv = MU * MASS / rj * 45.0 / (PI * H**6) * np.abs(dv)
+        assert np.allclose(e64[:, i], (dp + dvv) * u * r / ri, rtol=1e-12, atol=0)
+    # as a bound on float32 rounding
+    rng = np.random.default_rng(71)
+    n = 50_000
+    P = (rng.uniform(0, 1, (n, 3)) * [1.0, 2.0, 0.5]).astype(np.float32)
+    V = rng.uniform(-1, 1, (n, 3)).astype(np.float32)
+    p2 = oracle.sph_params(H, 2 * H, (40, 80, 20), MASS, K, RHO0, MU)
+    st, si, _ = oracle.hashgrid_build(*P.T, 2 * H, (0, 0, 0), (40, 80, 20))
+    rho = oracle.sph_density(p2, *P.T, st, si)
+    _, acc = oracle.sph_force(p2, *P.T, *V.T, rho, st, si, 1e-4)
+    a64, s64, e64 = oracle.sph_force_f64(p2, *P.T, *V.T, rho, st, si)
+    err = np.abs(acc - a64)
+    assert np.all(err <= 1e-5 * s64 + e64)
+    assert np.any(err > 1e-5 * s64)
 
 
 def test_epilogue_closed_forms(oracle):
@@ -421,7 +508,7 @@ def test_unfused_vs_brute_force_and_fused(oracle):
     vp = oracle.sph_pressure(p, *P.T, *V.T, rho, st, si, DT)
     vv = oracle.sph_viscosity(p, *P.T, *V.T, rho, st, si, DT)
     vf, _ = oracle.sph_force(p, *P.T, *V.T, rho, st, si, DT)
-    a64, s64 = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
+    a64, s64, _ = oracle.sph_force_f64(p, *P.T, *V.T, rho, st, si)
     # bound of a velocity change: f32 rounding of v + a dt plus 1e-5 of the term magnitudes
     vt = V.T.astype(np.float64)
     ulp = 2 * np.spacing(np.abs(V.T)).astype(np.float64)
