@@ -28,7 +28,8 @@ OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libforge_hip.so"
 ORACLE_DIR = REPO / "oracle"
 
-SOURCES = ["fh_api.hip", "fh_sort.hip", "fh_grid.hip", "fh_sph.hip", "fh_sph_fast.hip"]
+SOURCES = ["fh_api.hip", "fh_sort.hip", "fh_grid.hip", "fh_sph.hip", "fh_sph_fast.hip",
+           "fh_noalloc.hip"]
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

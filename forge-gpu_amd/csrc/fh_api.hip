@@ -117,6 +117,16 @@ hipError_t sph_rebuild_resident(fh_ctx* c, const GridDesc& g, uint32_t cells, ui
 
 }  // namespace
 
+namespace fh {
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+}  // namespace fh
+
 extern "C" {
 
 int fh_abi_version(void) { return FH_ABI_VERSION; }

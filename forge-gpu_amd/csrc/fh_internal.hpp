@@ -258,6 +258,9 @@ inline void tend(fh_ctx* c, KernelId k, hipStream_t s = nullptr) {
     }
 }
 
+// Sets the thread-local message fh_last_error() returns; returns `code`.
+int set_error(int code, const char* fmt, ...);
+
 // ---- launchers (host side, enqueue on ctx->stream; return hipError_t) ------------------------
 
 // Digit histograms of all passes of a num_bits sort of a key array (per-block partials, then

@@ -86,6 +86,7 @@ SIGNATURES = {
     "fh_scratch_bytes": (ctypes.c_size_t, [_P]),
     "fh_hash_cells": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P]),
     "fh_sort_pairs": (_I, [_P, _P, _P, _U32, _U32]),
+    "fh_sort_pairs_noalloc": (_I, [_P, _P, _P, _U32, _U32]),
     "fh_find_cell_boundaries": (_I, [_P, _P, _U32, _U32, _P, _P]),
     "fh_cell_start_csr": (_I, [_P, _P, _U32, _U32, _P]),
     "fh_hashgrid_build": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P, _P]),

@@ -118,6 +118,21 @@ int fh_hash_cells(fh_ctx* ctx, const float* x, const float* y, const float* z, u
  * n > max_n returns FH_ERANGE.  Equal keys keep their input order. */
 int fh_sort_pairs(fh_ctx* ctx, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_t num_bits);
 
+/* fh_sort_pairs without a context, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  Same result as fh_sort_pairs (stable, in place, any 1..32 bits) for at most
+ * FH_NOALLOC_MAX_N pairs (more: FH_ERANGE), queued on `stream` (NULL: the null stream) of the
+ * current device.  All scratch is a fixed device array of FH_NOALLOC_SCRATCH_BYTES bytes in the
+ * library, one copy per GPU held until the process ends; the call allocates nothing (the first
+ * call on a device resolves the array's address).  Every call on one GPU shares that array:
+ * calls ordered on one stream are fine, calls that overlap on one GPU (other streams, other
+ * threads) race and must not be issued.  Errors: 0 / <0 / >0 as everywhere, message in
+ * fh_last_error(). */
+#define FH_NOALLOC_MAX_N 1048576u
+#define FH_NOALLOC_SCRATCH_BYTES 18356480u
+int fh_sort_pairs_noalloc(void* stream, uint32_t* keys, uint32_t* vals, uint32_t n,
+                          uint32_t num_bits);
+
 /* From keys sorted ascending: cell_start[c] = first i with key c, cell_end[c] = last i + 1;
  * cells with no key keep cell_start = 0xFFFFFFFF, cell_end = 0.  Keys >= num_cells are
  * ignored.  Replaces find_cell_boundaries (radix_sort.rs:229-317, kernel :444-466). */
