@@ -6,7 +6,11 @@
 A "step" is one SPH substep of BASELINE.json configs[3]: 1,048,576 particles (dam-break lattice
 block, h = cell = 0.01, 100^3 cells), re-hash + stable radix sort + cell ranges + density +
 fused pressure/viscosity force + gravity / integrate / box, replayed from a captured HIP graph of
-`--graph-substeps` substeps.  Inputs are resident in HBM before the timed region.
+`--graph-substeps` substeps.  Inputs are resident in HBM before the timed region.  Exactly W
+substeps run untimed, then exactly K are timed (K // G graph replays, then the remainder as one
+eager call of the same kernels).  The defaults (W = 100, K = 900) are the survey's c3 protocol
+(1000 substeps, mean of the last 900); with other arguments that protocol is also run on a
+fresh trajectory and reported in extra.c3_protocol_last_900_of_1000.
 
 One JSON line on stdout:
   value        particle-steps/s over the K timed substeps (wall clock between synchronisations)
@@ -15,8 +19,11 @@ One JSON line on stdout:
                eagerly with every kernel bracketed by events, right after the timed region)
   cpu_baseline the single-threaded CPU restatement (oracle/) of the same substep on a bounded
                sample, timed on this host
-  extra.sort_c1  the standalone 16,777,216-pair 32-bit sort: Gkeys/s and the
-               onesweep pass against the HBM roofline
+  extra.sph_c0   configs[0] (50,000 particles) throughput, 2000 substeps after 100
+  extra.sort_c1  the standalone 16,777,216-pair 32-bit sort and the same count of
+               full-entropy 32-bit keys: Gkeys/s, bytes of the survey formula (68 N) and bytes
+               actually moved (passes whose digit is constant move nothing) against the HBM
+               roofline
   extra.query_c2 HashGrid build + neighbour query of configs[2] (4,194,304 points)
   extra.sph_c4   one grid build + density + force pass of configs[4] (8,388,608 particles,
                skewed occupancy): time, candidate tests per second, occupancy max / p99
@@ -167,36 +174,59 @@ def build_pipe(fh, cfg):
     return p
 
 
+def run_substeps(pipe, fields, ctx, dt, count: int, G: int) -> None:
+    """`count` substeps: count // G replays of the captured G-substep graph, then the remainder as
+    one eager fh_sph_fused_steps call (the same kernels)."""
+    if count >= G:
+        pipe.replay(count // G)
+    if count % G:
+        pipe.run_async(fields, dt, count % G)
+
+
+def timed_trajectory(fh, torch, cfg, W: int, K: int, G: int, log):
+    """A fresh dam-break field set: W untimed substeps, then exactly K timed substeps between
+    synchronisations (wall clock and HIP events on the context stream).  Returns the fields,
+    pipeline, context and the two times."""
+    fields = build_fields(fh, cfg, torch)
+    pipe = build_pipe(fh, cfg)
+    ctx = fields.context(cfg.num_cells)
+    torch.cuda.synchronize()
+    pipe.capture(fields, cfg.dt, G)
+    if W:
+        run_substeps(pipe, fields, ctx, cfg.dt, W, G)
+    ctx.sync()
+    torch.cuda.synchronize()
+    ctx.event_record(0)
+    t0 = time.perf_counter()
+    run_substeps(pipe, fields, ctx, cfg.dt, K, G)
+    ctx.event_record(1)
+    ctx.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.event_elapsed_ms(0, 1)
+    log(f"{cfg.name}: {W} warm-up + {K} timed substeps (graph of {G}): wall "
+        f"{wall * 1e3:.2f} ms, events {ev_ms:.2f} ms")
+    return fields, pipe, ctx, wall, ev_ms
+
+
 def bench_sph(args, fh, torch, log):
     from forge_hip import workloads
 
     cfg = workloads.config3()
     C = cfg.num_cells
     passes = (max(1, (C - 1).bit_length()) + 7) // 8
-    G = args.graph_substeps
-    K = max(G, (args.steps // G) * G)
-    W = (args.warmup // G) * G
-    fields = build_fields(fh, cfg, torch)
-    pipe = build_pipe(fh, cfg)
-    ctx = fields.context(C)
-    torch.cuda.synchronize()
-    pipe.capture(fields, cfg.dt, G)  # substeps 1..W are the warm-up replays, then K are timed
-    log(f"captured {G} substeps; warmup {W}")
-    if W:
-        pipe.replay(W // G)
-    ctx.sync()
-    torch.cuda.synchronize()
-    ctx.event_record(0)
-    t0 = time.perf_counter()
-    pipe.replay(K // G)
-    ctx.event_record(1)
-    ctx.sync()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall = t1 - t0
-    ev_ms = ctx.event_elapsed_ms(0, 1)
-    log(f"timed {K} substeps: wall {wall * 1e3:.2f} ms, events {ev_ms:.2f} ms")
-
+    G = max(1, args.graph_substeps)
+    K, W = max(1, args.steps), max(0, args.warmup)
+    fields, pipe, ctx, wall, ev_ms = timed_trajectory(fh, torch, cfg, W, K, G, log)
+    # The survey's c3 protocol (1000 substeps, mean of the last 900) as its own figure, on a
+    # fresh trajectory, unless the arguments already are that protocol.
+    if (W, K) == (100, 900):
+        proto = {"warmup": W, "steps": K, "ms_per_step": wall * 1e3 / K,
+                 "value": cfg.n * K / wall, "same_as_headline": True}
+    else:
+        _, _, _, pwall, _ = timed_trajectory(fh, torch, cfg, 100, 900, G, log)
+        proto = {"warmup": 100, "steps": 900, "ms_per_step": pwall * 1e3 / 900,
+                 "value": cfg.n * 900 / pwall, "same_as_headline": False}
     # Per-kernel durations: the G substeps of the graph once more, launched eagerly on the same
     # stream with every kernel bracketed by HIP events (events recorded by graph nodes cannot be
     # timed on HIP).
@@ -224,13 +254,31 @@ def bench_sph(args, fh, torch, log):
     achieved = pas[dom]["alg_GBs"]
     total_alg = sum(byts.values())
     return dict(cfg=cfg, C=C, passes=passes, G=G, K=K, W=W, wall=wall, ev_ms=ev_ms, kern=kern,
-                pas=pas, dom=dom, achieved=achieved, total_alg=total_alg, digest=cfg.digest())
+                pas=pas, dom=dom, achieved=achieved, total_alg=total_alg, digest=cfg.digest(),
+                proto=proto)
 
 
-def bench_sort(args, fh, torch, log):
+def bench_sph_c0(args, fh, torch, log):
+    """configs[0] (50,000 particles, the scale of the reference's published dam-break figure)
+    as a throughput line: 100 warm-up substeps, then 2000 timed, graph of 10."""
     from forge_hip import workloads
 
-    keys, vals = workloads.config1()
+    cfg = workloads.config0()
+    W, K, G = 100, 2000, 10
+    _, _, ctx, wall, ev_ms = timed_trajectory(fh, torch, cfg, W, K, G, log)
+    return {"workload": "c0: SPH dam-break substep, 50,000 particles, h = cell = 0.025, 40^3 "
+                        "cells, re-hash + sort every substep, hipGraph of 10 substeps",
+            "warmup": W, "steps": K, "ms_per_step": wall * 1e3 / K,
+            "particle_steps_per_s": cfg.n * K / wall, "substep_us_events": ev_ms * 1e3 / K,
+            "input_sha256": cfg.digest(),
+            "reference_published": {"value": 2.22e8, "hardware": "NVIDIA L40",
+                                    "source": "ROADMAP.md:263 (50K particles, its own "
+                                              "random-init manifest; context only)"}}
+
+
+def time_sort(args, fh, torch, log, keys, vals, label):
+    """Median of whole 32-bit fh_sort_pairs calls on (keys, vals) with HIP events, and the
+    per-pass durations of further calls with every kernel bracketed by events."""
     n = keys.size
     ctx = fh.Context(max_n=n, max_cells=1)
     k0, v0 = fh.from_u32(keys), fh.from_u32(vals)
@@ -257,7 +305,6 @@ def bench_sort(args, fh, torch, log):
         sorter.sort(k, v, n, 32, sync=False)
         ctx.event_record(3)
         times.append(ctx.event_elapsed_ms(2, 3))
-    # Per-kernel durations from further sorts with every kernel bracketed by events.
     ctx.time_kernel("sort", 4 * reps)
     ctx.time_kernel("hist", reps)
     for _ in range(reps):
@@ -273,22 +320,42 @@ def bench_sort(args, fh, torch, log):
     # Launches of passes that moved keys (a pass whose digit is equal for every key returns at
     # once: c1's top byte is always 0, so 3 of the 4 passes move keys).
     moving = [x for x in passes_ms if x * 1e3 > 20.0]
+    mp = round(len(moving) / max(reps, 1))
     pass_us = 1e3 * sum(moving) / max(len(moving), 1)
-    pass_bytes = 16 * n
+    moved = (4 + 16 * mp) * n
     out = {
-        "workload": "c1: 16,777,216 (u32 cell key, u32 index) pairs, 32-bit stable LSD sort",
+        "workload": label,
         "median_ms": t, "gkeys_per_s": n / (t * 1e-3) / 1e9,
+        # the survey's formula: a key read for the histograms + 4 passes reading and writing
+        # (key, value), whether or not a pass moves anything
         "alg_bytes": 68 * n, "alg_GBs": 68 * n / (t * 1e-3) / 1e9,
         "frac_of_hbm_peak": 68 * n / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "moving_passes_per_sort": len(moving) / max(reps, 1),
-        "alg_bytes_moving_passes": (4 + 16 * round(len(moving) / max(reps, 1))) * n,
-        "alg_GBs_moving_passes": (4 + 16 * round(len(moving) / max(reps, 1))) * n / (t * 1e-3) / 1e9,
+        # the bytes actually moved: the histogram read + the passes that move keys
+        "moving_passes_per_sort": mp,
+        "moved_bytes": moved, "moved_GBs": moved / (t * 1e-3) / 1e9,
+        "moved_frac_of_hbm_peak": moved / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "onesweep_pass_mean_us": pass_us,
-        "onesweep_pass_GBs": pass_bytes / (pass_us * 1e-6) / 1e9,
+        "onesweep_pass_GBs": 16 * n / (pass_us * 1e-6) / 1e9,
         "hist_mean_us": 1e3 * sum(hist_ms) / max(len(hist_ms), 1),
         "reps": reps,
     }
-    log(f"sort c1: median {t:.3f} ms, {out['gkeys_per_s']:.2f} Gkeys/s")
+    log(f"sort {label[:40]}: median {t:.3f} ms, {out['gkeys_per_s']:.2f} Gkeys/s, "
+        f"{mp} moving passes, moved {out['moved_frac_of_hbm_peak']:.3f} of HBM peak")
+    return out
+
+
+def bench_sort(args, fh, torch, log):
+    """configs[1] (keys < 2^24: the top byte is 0, so 3 of the 4 passes move data), and the same
+    count of full-entropy 32-bit keys (all 4 passes move data)."""
+    from forge_hip import workloads
+
+    keys, vals = workloads.config1()
+    out = time_sort(args, fh, torch, log, keys, vals,
+                    "c1: 16,777,216 (u32 cell key, u32 index) pairs, 32-bit stable LSD sort")
+    full = workloads.u32_stream(workloads.DEFAULT_SEED, 7, keys.size)
+    out["full_entropy"] = time_sort(args, fh, torch, log, full, vals,
+                                    "16,777,216 uniformly random u32 keys (all 4 passes move "
+                                    "data), u32 index values, 32-bit stable LSD sort")
     return out
 
 
@@ -502,6 +569,7 @@ def main(argv=None) -> int:
                           bench_sort(args, fh, torch, log)}), flush=True)
         return 0
     s = bench_sph(args, fh, torch, log)
+    c0 = None if args.no_extra_configs else bench_sph_c0(args, fh, torch, log)
     sort = None if args.no_sort else bench_sort(args, fh, torch, log)
     q2 = None if args.no_extra_configs else bench_query_c2(args, fh, torch, log)
     s4 = None if args.no_extra_configs else bench_sph_c4(args, fh, torch, log)
@@ -529,7 +597,8 @@ def main(argv=None) -> int:
             "workload": "configs[3]: SPH dam-break substep, 1,048,576 particles, h = cell = 0.01, "
                         "100^3 cells, re-hash + sort every substep, hipGraph of "
                         f"{s['G']} substeps (one fh_sph_fused_steps call: state resident in "
-                        "sorted order between them, fields written after the last)",
+                        "sorted order between them, fields written after the last); "
+                        f"{s['W']} warm-up substeps, then {K} timed",
             "particles": cfg.n, "cells": s["C"], "sort_passes": s["passes"],
             "graph_substeps": s["G"], "input_sha256": s["digest"], "parallelism": "single GPU",
         },
@@ -546,6 +615,7 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": cpu,
         "extra": {
+            "c3_protocol_last_900_of_1000": s["proto"],
             "substep_us_events": s["ev_ms"] * 1e3 / K,
             "substep_alg_bytes": s["total_alg"],
             "substep_alg_GBs": s["total_alg"] / (ms_per_step * 1e-3) / 1e9,
@@ -556,6 +626,7 @@ def main(argv=None) -> int:
                         for k in KERNELS},
             "passes": {p: {q: (round(v, 3) if isinstance(v, float) else v) for q, v in d.items()}
                        for p, d in s["pas"].items()},
+            "sph_c0": c0,
             "sort_c1": sort,
             "query_c2": q2,
             "sph_c4": s4,

@@ -1,28 +1,42 @@
-// fh_sph_fast.hip -- LDS-tiled SPH density and pressure/viscosity passes for gfx950.
+// fh_sph_fast.hip -- the fast SPH density and pressure/viscosity passes for gfx950.
 //
-// Work decomposition.  A workgroup (256 lanes) owns 256 consecutive particles of the cell-sorted
-// order (a "tile") and one z-slab dz in {-1, 0, +1} of their 3x3x3 neighbourhood, so every tile
-// is processed by three workgroups whose partial sums land in three separate buffers (summed
-// later in a fixed order: results are deterministic, no atomics).  Splitting by slab divides the
-// critical path of tiles that sit in very dense cells by three.
+// Work items.  Particles are processed in cell-sorted order.  An item is one (sub-tile, z-slab)
+// pair: 64 consecutive sorted particles (one wavefront, one particle per lane) and one slab
+// dz in {-1, 0, +1} of their 3x3x3 neighbourhood.  Each slab's partial sums go to a buffer of
+// their own and k_prep / k_finalize add the three in a fixed order, so results are
+// deterministic (no atomics) and a dense cell's work is split three ways.
 //
-// Neighbour staging.  For a fixed (dy, dz) the three x-adjacent cells of a particle are one
-// contiguous range of the sorted arrays, and because sorted particles have non-decreasing cells
-// the union of those ranges over a tile is itself one contiguous range.  Each of the 3 rows of
-// the slab is streamed through LDS in 512-particle chunks with coalesced float4 loads; every lane
-// then walks only its own sub-range of the chunk, reading LDS (broadcast when lanes share a
-// cell, which is the common case in dense regions).  All loop bounds that contain barriers are
-// workgroup-uniform.
+// Light items (k_density_wave, k_force_wave: 64-lane workgroups, one item each).  For a fixed
+// (dy, dz) the three x-adjacent cells of a particle are one contiguous range of the sorted
+// arrays.  Lanes of one home row (cy, cz) are consecutive (a "segment"), and for each of the
+// slab's three rows the union of a segment's ranges is again one contiguous range.  The wave
+// concatenates the rows of all its segments into one candidate stream and copies it, kWin
+// (192) candidates at a time, into its own LDS slice with coalesced 16-byte loads (no workgroup
+// barrier); every lane then evaluates the intervals of its own rows that fall in the window
+// (fh_stream.hpp, shared with the neighbour query of fh_grid.hip).
 //
-// XCD mapping.  Workgroups are dispatched round-robin over the 8 XCDs; work item ids are
-// remapped so each XCD processes one contiguous block of tiles and its L2 holds that region of
-// the sorted arrays and its neighbour rows.
+// Heavy items (k_density_heavy, k_force_heavy).  An item whose particles face more than
+// kHeavyWork (384) candidates in the slab, or that touches a co-located group, is listed by the
+// plan (k_group_plan) and taken by one of kHeavyGrid (4096) 512-lane workgroups that stride over
+// the list.  Its 8 waves hold the same 64 particles and split the 64-candidate chunks of each
+// segment row round-robin, each through its own LDS slice, and reduce in wave order.  The heavy
+// kernels run on a side stream beside the light ones.
 //
-// Arithmetic.  Same quantities as the reference kernels (sph_density.rs:413-453,
-// sph_fused.rs:552-637) with fused multiply-adds, a hardware reciprocal square root for 1/r and
-// the pressure and viscosity terms summed into one accumulator; the per-slab partials are added
-// as (slab -1 + slab 0) + slab +1.  Differences to the CPU restatement are rounding only
-// (checked against rel 1e-4 on density and 1e-4 * sum|pair terms| on accelerations).
+// Transposed items.  When an item's stream is many times longer than its largest particle's
+// candidate count (sparse particles along a row beside a dense one), it is walked one particle
+// at a time with the candidates across the lanes (coalesced loads, a wave reduction each).
+//
+// Co-located groups.  A cell of >= kCollapseMin (64) particles at one bitwise-identical point
+// (c3's box corners collect thousands) is collapsed: the members are moved to the front of the
+// cell, the first stands for all of them with weight M (and their summed velocity), and the
+// others are finished from it in k_finalize with the viscosity weight of all three slabs.
+//
+// Arithmetic.  The reference's quantities (sph_density.rs:413-453, sph_fused.rs:552-637) with
+// fused multiply-adds, the hardware reciprocal square root for 1/r, and per-particle force
+// records (k_prep) that fold the constants in, so a pair costs one fma for its pressure factor;
+// differences to the CPU restatement are rounding only (rel 1e-4 on density; 1e-4 of the sum of
+// the pair terms' magnitudes, plus their float32 distance-rounding sensitivity, on
+// accelerations).
 #include "fh_internal.hpp"
 #include "fh_stream.hpp"
 
