@@ -220,7 +220,9 @@ def bench_sph(args, fh, torch, log):
     fields, pipe, ctx, wall, ev_ms = timed_trajectory(fh, torch, cfg, W, K, G, log)
     # The survey's c3 protocol (1000 substeps, mean of the last 900) as its own figure, on a
     # fresh trajectory, unless the arguments already are that protocol.
-    if (W, K) == (100, 900):
+    if args.no_protocol:
+        proto = None
+    elif (W, K) == (100, 900):
         proto = {"warmup": W, "steps": K, "ms_per_step": wall * 1e3 / K,
                  "value": cfg.n * K / wall, "same_as_headline": True}
     else:
@@ -533,6 +535,8 @@ def main(argv=None) -> int:
     ap.add_argument("--sort-reps", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-protocol", action="store_true",
+                    help="skip the separate 1000-substep c3 protocol run (for profiling)")
     ap.add_argument("--no-sort", action="store_true", help="skip the c1 sort line")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the c2 (grid build + query) and c4 (skewed SPH pass) lines")
