@@ -67,6 +67,8 @@ int check_grid(fh_ctx* c, float cs, const float* origin, const uint32_t* dims, G
     g->nx = dims[0];
     g->ny = dims[1];
     g->nz = dims[2];
+    g->div_x = make_divu32(dims[0]);
+    g->div_xy = make_divu32(dims[0] * dims[1]);
     *cells = (uint32_t)C;
     return FH_OK;
 }

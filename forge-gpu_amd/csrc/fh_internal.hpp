@@ -100,11 +100,32 @@ struct Control {
     uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
 };
 
+// Division of a 32-bit unsigned value by a fixed divisor d >= 1 with a multiply-high, a
+// subtract, an add and two shifts (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, Figure 4.1): with l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1, t = mulhi(m, x), x / d = (t + ((x - t) >> s1)) >> s2
+// where (s1, s2) = (min(l, 1), max(l - 1, 0)).  Exact for every x < 2^32.
+struct DivU32 {
+    uint32_t m, s1, s2;
+};
+
 struct GridDesc {
     float cs;
     float ox, oy, oz;
     uint32_t nx, ny, nz;
+    DivU32 div_x;   // by nx
+    DivU32 div_xy;  // by nx * ny
 };
+
+inline DivU32 make_divu32(uint32_t d) {
+    uint32_t l = 0;
+    while (l < 32 && (1ull << l) < d) l++;
+    DivU32 r;
+    r.m = (uint32_t)((((1ull << l) - d) << 32) / d + 1);
+    r.s1 = l < 1 ? l : 1;
+    r.s2 = l > 1 ? l - 1 : 0;
+    return r;
+}
 
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
 enum KernelId { KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
@@ -197,6 +218,27 @@ __device__ __forceinline__ uint32_t cell_of(float x, float y, float z, const Gri
     uint32_t cy = cell_coord(y, g.oy, g.cs, g.ny);
     uint32_t cz = cell_coord(z, g.oz, g.cs, g.nz);
     return cx + cy * g.nx + cz * g.nx * g.ny;
+}
+
+__device__ __forceinline__ uint32_t divu32(uint32_t x, DivU32 d) {
+    const uint32_t t = __umulhi(d.m, x);
+    return (t + ((x - t) >> d.s1)) >> d.s2;
+}
+
+// Cell coordinates of a cell key (key = cx + cy * nx + cz * nx * ny, key < nx * ny * nz): the
+// exact inverse of cell_of's linearisation, without the float division.
+struct CellXYZ {
+    int x, y, z;
+};
+__device__ __forceinline__ CellXYZ key_xyz(uint32_t key, const GridDesc& g) {
+    const uint32_t cz = divu32(key, g.div_xy);
+    const uint32_t rem = key - cz * (g.nx * g.ny);
+    const uint32_t cy = divu32(rem, g.div_x);
+    CellXYZ c;
+    c.x = (int)(rem - cy * g.nx);
+    c.y = (int)cy;
+    c.z = (int)cz;
+    return c;
 }
 
 __device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {

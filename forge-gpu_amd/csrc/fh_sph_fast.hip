@@ -63,7 +63,7 @@ __device__ __forceinline__ T load_or(const T* __restrict__ p, uint32_t i, bool o
 
 // The three row ranges [b, e) of slab dz for one particle (cells clamped like the reference,
 // sph_density.rs:421-437); empty ranges for rows outside the grid.
-__device__ __forceinline__ void slab_ranges(const float4& p, bool live, const GridDesc& g,
+__device__ __forceinline__ void slab_ranges(const CellXYZ& c, bool live, const GridDesc& g,
                                             const uint32_t* __restrict__ cstart, uint32_t n,
                                             int dz, uint32_t b[3], uint32_t e[3]) {
 #pragma unroll
@@ -72,10 +72,8 @@ __device__ __forceinline__ void slab_ranges(const float4& p, bool live, const Gr
         e[r] = 0u;
     }
     if (!live) return;
-    const int cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
-    const int cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny);
-    const int cz = (int)cell_coord(p.z, 0.0f, g.cs, g.nz);
-    const int nz = cz + dz;
+    const int cx = c.x, cy = c.y;
+    const int nz = c.z + dz;
     if (nz < 0 || nz >= (int)g.nz) return;
     const uint32_t x0 = (uint32_t)(cx > 0 ? cx - 1 : 0);
     const uint32_t x1 = (uint32_t)(cx + 1 < (int)g.nx ? cx + 1 : (int)g.nx - 1);
@@ -330,13 +328,11 @@ __device__ __forceinline__ void group_work(uint32_t bid, uint32_t nb, const uint
 // Candidates of the possibly grouped cells among the 9 cells of a slab (tagged by
 // k_cell_starts; the group part, which runs beside the plan, decides), as a count to subtract: such a
 // cell of k particles is counted as one (a group of M counts as one candidate, M <= k).
-__device__ __forceinline__ uint32_t grouped_excess(const float4& p, const GridDesc& g,
+__device__ __forceinline__ uint32_t grouped_excess(const CellXYZ& hc, const GridDesc& g,
                                                    const uint64_t* __restrict__ cand_tag,
                                                    const uint32_t* __restrict__ cstart,
                                                    uint32_t epoch, int dz) {
-    const int cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
-    const int cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny);
-    const int cz = (int)cell_coord(p.z, 0.0f, g.cs, g.nz) + dz;
+    const int cx = hc.x, cy = hc.y, cz = hc.z + dz;
     if (cz < 0 || cz >= (int)g.nz) return 0u;
     uint32_t ex = 0;
     for (int y = cy - 1; y <= cy + 1; y++) {
@@ -391,8 +387,8 @@ __device__ __forceinline__ uint32_t pick3(const uint32_t v[3], int r) {
 // one home row (cy, cz) are consecutive lanes, and for each of the slab's 3 rows the union of
 // their neighbour ranges is one contiguous range (x-adjacent cells of that row only): from the
 // first lane's begin to the last lane's end.
-__device__ __forceinline__ uint32_t home_row(const float4& p, const GridDesc& g) {
-    return cell_coord(p.y, 0.0f, g.cs, g.ny) + cell_coord(p.z, 0.0f, g.cs, g.nz) * g.ny;
+__device__ __forceinline__ uint32_t home_row(const CellXYZ& c, const GridDesc& g) {
+    return (uint32_t)c.y + (uint32_t)c.z * g.ny;
 }
 
 // Length of the wave's candidate stream for one slab (the sum over home-row segments of the
@@ -492,7 +488,7 @@ __device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
 // heavy when its largest per-particle candidate count (a cell that may hold a group counting
 // once) exceeds heavy_work or when it touches such a cell, and transposed (heavy) when its
 // stream is much longer than that count.
-__device__ __forceinline__ void plan_work(uint32_t bid, const float4* __restrict__ spos,
+__device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restrict__ skeys,
                                           uint32_t n, GridDesc g,
                                           const uint32_t* __restrict__ cstart,
                                           const uint64_t* __restrict__ cand_tag,
@@ -509,16 +505,16 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const float4* __restrict
     const bool live = s < n;
     uint32_t nh = 0;  // heavy items of this wave, kept in s_item[wave * 3 ...]
     if (sub * kSub < n) {  // wave-uniform
-        const float4 pi = load_or(spos, s, live, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
+        const CellXYZ ci = key_xyz(load_or(skeys, s, live, 0u), g);
         {
             const uint32_t epoch = ctl->epoch;
             for (int slab = 0; slab < 3; slab++) {
                 uint32_t b[3], e[3];
-                slab_ranges(pi, live, g, cstart, n, slab - 1, b, e);
+                slab_ranges(ci, live, g, cstart, n, slab - 1, b, e);
                 uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
                 uint32_t excess = 0;
                 if (cand >= kCollapseMin) {  // a grouped cell holds at least kCollapseMin
-                    excess = grouped_excess(pi, g, cand_tag, cstart, epoch, slab - 1);
+                    excess = grouped_excess(ci, g, cand_tag, cstart, epoch, slab - 1);
                     cand -= excess;
                 }
                 const uint32_t w = wave_max(cand);
@@ -528,7 +524,7 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const float4* __restrict
                 if (direct_mode == 1u) {
                     // a light item only when its stream is far longer (pathologically
                     // disjoint ranges: one window would serve one lane at a time)
-                    const uint32_t T = stream_total(b, e, home_row(pi, g), live, lane);
+                    const uint32_t T = stream_total(b, e, home_row(ci, g), live, lane);
                     trans = hv ? T > kTransRatio * w + kTransOffset
                                : T > kTransLightRatio * w + kTransLightOffset;
                 }
@@ -583,7 +579,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_group_plan(
         group_work(blockIdx.x, kGroupBlocks, big, cap, n, skeys, cstart, spos, svel, sidx, rank,
                    scratch, cell_grp, vrep, skip_tag, ctl);
     else
-        plan_work(blockIdx.x - kGroupBlocks, spos, n, g, cstart, cand_tag, flag, heavy,
+        plan_work(blockIdx.x - kGroupBlocks, skeys, n, g, cstart, cand_tag, flag, heavy,
                   heavy_cap, heavy_work, direct_mode, ctl);
 }
 
@@ -628,6 +624,7 @@ __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
 // Light items hold no co-located group (the plan sends those to the heavy list).
 __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restrict__ spos,
+                                                         const uint32_t* __restrict__ skeys,
                                                          uint32_t n, GridDesc g,
                                                          const uint32_t* __restrict__ cstart,
                                                          float h2, float* __restrict__ dpart,
@@ -644,10 +641,11 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
     const float4 pi = load_or(spos, s, in, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
+    const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
     uint32_t b[3], e[3];
-    slab_ranges(pi, in, g, cstart, n, (int)slab - 1, b, e);
+    slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
     LightStream L;
-    light_stream(L, b, e, home_row(pi, g), in, lane);
+    light_stream(L, b, e, home_row(ci, g), in, lane);
     float4* buf = s_p[wave];
     float acc = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
@@ -749,12 +747,13 @@ __device__ __forceinline__ void row_chunk(const RowPlan& R, uint32_t q, uint32_t
     }
 }
 
-// Cells xa..xb and base index of row r of slab dz for a lane at p (valid = row inside the grid).
-__device__ __forceinline__ bool seg_row(const float4& p, const GridDesc& g, int dz, int r,
+// Cells xa..xb and base index of row r of slab dz for a lane in cell c (valid = row inside the
+// grid).
+__device__ __forceinline__ bool seg_row(const CellXYZ& c, const GridDesc& g, int dz, int r,
                                         uint32_t& rowbase, int& cx) {
-    cx = (int)cell_coord(p.x, 0.0f, g.cs, g.nx);
-    const int cy = (int)cell_coord(p.y, 0.0f, g.cs, g.ny) + r - 1;
-    const int cz = (int)cell_coord(p.z, 0.0f, g.cs, g.nz) + dz;
+    cx = c.x;
+    const int cy = c.y + r - 1;
+    const int cz = c.z + dz;
     rowbase = (uint32_t)cy * g.nx + (uint32_t)cz * g.nx * g.ny;
     return cy >= 0 && cy < (int)g.ny && cz >= 0 && cz < (int)g.nz;
 }
@@ -784,7 +783,7 @@ __device__ __forceinline__ void seg_chunk(const RowPlan R[3], uint32_t t, int& r
 
 // The plans of the 3 rows of a segment (leader / last lane of the segment): the row union,
 // cut around co-located groups when the item touches any (`cut`).
-__device__ __forceinline__ void seg_plans(RowPlan R[3], const float4& pi, const GridDesc& g,
+__device__ __forceinline__ void seg_plans(RowPlan R[3], const CellXYZ& ci, const GridDesc& g,
                                           int dz, const uint32_t b[3], const uint32_t e[3],
                                           int leader, int last, bool cut,
                                           const uint32_t* __restrict__ cstart,
@@ -801,7 +800,7 @@ __device__ __forceinline__ void seg_plans(RowPlan R[3], const float4& pi, const 
         if (cut && lo < hi) {
             uint32_t rowbase;
             int cx;
-            (void)seg_row(pi, g, dz, r, rowbase, cx);
+            (void)seg_row(ci, g, dz, r, rowbase, cx);
             rowbase = (uint32_t)__builtin_amdgcn_readlane((int)rowbase, leader);
             const int xa = max(__builtin_amdgcn_readlane(cx, leader) - 1, 0);
             const int xb = min(__builtin_amdgcn_readlane(cx, last) + 1, (int)g.nx - 1);
@@ -813,7 +812,8 @@ __device__ __forceinline__ void seg_plans(RowPlan R[3], const float4& pi, const 
 
 template <int HW>
 __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
-    const float4* __restrict__ spos, uint32_t n, GridDesc g, const uint32_t* __restrict__ cstart,
+    const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart,
     const uint64_t* __restrict__ cell_grp, float h2, float* __restrict__ dpart, uint32_t stride,
     const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const uint32_t* __restrict__ skip_tag,
     const Control* __restrict__ ctl) {
@@ -833,9 +833,10 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
         const uint32_t s = sub * kSub + (uint32_t)lane;
         const bool live = s < n;
         const float4 pi = load_or(spos, s, live, z4);
+        const CellXYZ ci = key_xyz(load_or(skeys, s, live, 0u), g);
         uint32_t b[3], e[3];
-        slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
-        const uint32_t hr = home_row(pi, g);
+        slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
+        const uint32_t hr = home_row(ci, g);
         float acc = 0.0f;
         if (trans)  // members take their representative's density
             acc = density_trans(spos, b, e, pi, live && !is_member(__float_as_uint(pi.w), s),
@@ -849,7 +850,7 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
             pending &= ~seg;
             const int last = 63 - __clzll((long long)seg);
             RowPlan R[3];
-            seg_plans(R, pi, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
+            seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
                       lane);
             // chunks wave, wave + HW, ... of the segment's three rows; the next is fetched
             // before the current one is evaluated
@@ -1043,6 +1044,7 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
                                                        const float4* __restrict__ svel,
                                                        const float* __restrict__ srho,
                                                        const float4* __restrict__ rec,
+                                                       const uint32_t* __restrict__ skeys,
                                                        uint32_t n, GridDesc g,
                                                        const uint32_t* __restrict__ cstart,
                                                        FastForce K, float* __restrict__ fpart,
@@ -1066,10 +1068,11 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     const float rho_i = load_or(srho, s, in, 0.0f);
     const bool live = in && !(rho_i < 1e-6f);  // sph_fused.rs:550
     const float p_i = K.k * (rho_i - K.rho0);
+    const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
     uint32_t b[3], e[3];
-    slab_ranges(pi, in, g, cstart, n, (int)slab - 1, b, e);
+    slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
     LightStream L;
-    light_stream(L, b, e, home_row(pi, g), in, lane);
+    light_stream(L, b, e, home_row(ci, g), in, lane);
     float4* bp = s_p[wave];
     float4* bv = s_v[wave];
     float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
@@ -1113,7 +1116,8 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
 template <int HW>
 __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
-    const float* __restrict__ srho, const float4* __restrict__ rec, uint32_t n, GridDesc g,
+    const float* __restrict__ srho, const float4* __restrict__ rec,
+    const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
     float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
     const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const uint32_t* __restrict__ skip_tag,
@@ -1139,9 +1143,10 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
         const float rho_i = load_or(srho, s, in, 0.0f);
         const bool live = in && !(rho_i < 1e-6f);
         const float p_i = K.k * (rho_i - K.rho0);
+        const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
         uint32_t b[3], e[3];
-        slab_ranges(pi, live, g, cstart, n, (int)slab - 1, b, e);
-        const uint32_t hr = home_row(pi, g);
+        slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
+        const uint32_t hr = home_row(ci, g);
         float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
         if (trans)  // members are finished from their representative
             force_trans(rec, spos, stride, b, e, pi, p_i,
@@ -1156,7 +1161,7 @@ __global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
             pending &= ~seg;
             const int last = 63 - __clzll((long long)seg);
             RowPlan R[3];
-            seg_plans(R, pi, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
+            seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
                       lane);
             uint32_t t = (uint32_t)wave;
             int r;
@@ -1395,14 +1400,14 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     if (e != hipSuccess) return e;
     tbeg(c, KID_DHEAVY, side_of(c, kSideDensity));
     k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, side_of(c, kSideDensity)>>>(
-        c->spos, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n, c->heavy,
-        c->heavy_cap, c->skip_tag, c->ctl);
+        c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
+        c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
     tend(c, KID_DHEAVY, side_of(c, kSideDensity));
     e = hipGetLastError();
     tbeg(c, KID_DENSITY);
-    k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, a.n, a.g, cell_start, a.h * a.h,
-                                                   c->dpart, c->max_n, items, c->heavy_flag,
-                                                   c->skip_tag, c->ctl);
+    k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->skeys, a.n, a.g, cell_start,
+                                                   a.h * a.h, c->dpart, c->max_n, items,
+                                                   c->heavy_flag, c->skip_tag, c->ctl);
     tend(c, KID_DENSITY);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c, kSideDensity);  // joined even after a failed launch
@@ -1446,14 +1451,15 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     if (e != hipSuccess) return e;
     tbeg(c, KID_FHEAVY, side_of(c, kSideForce));
     k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, side_of(c, kSideForce)>>>(
-        c->spos, c->svel, c->srho, c->sout, a.n, a.g, cell_start, c->cell_grp, K, c->fpart,
-        c->wpart, c->max_n, c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
+        c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
+        c->fpart, c->wpart, c->max_n, c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
     tend(c, KID_FHEAVY, side_of(c, kSideForce));
     e = hipGetLastError();
     tbeg(c, KID_FORCE);
-    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, a.n, a.g,
-                                                 cell_start, K, c->fpart, c->wpart, c->max_n, items,
-                                                 c->heavy_flag, c->skip_tag, c->ctl);
+    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, c->skeys,
+                                                 a.n, a.g, cell_start, K, c->fpart, c->wpart,
+                                                 c->max_n, items, c->heavy_flag, c->skip_tag,
+                                                 c->ctl);
     tend(c, KID_FORCE);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c, kSideForce);
