@@ -957,7 +957,11 @@ __device__ __forceinline__ void force_pair(const float4& q, const float4& w, con
     const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
     const float r2 = fmaf(dz, dz, fmaf(dy, dy, dx * dx));
     const bool ok = r2 < K.h2 && r2 > 1e-12f;
-    const float rinv = __builtin_amdgcn_rsqf(r2);
+    // The empty asm pins 1/r as computed for every candidate: otherwise the compiler moves the
+    // reciprocal square root and the products behind a divergent branch on the pair test, whose
+    // exec-mask bookkeeping costs more than the two selects (10% of k_force_wave on c3).
+    float rinv = __builtin_amdgcn_rsqf(r2);
+    asm volatile("" : "+v"(rinv));
     const float diff = fmaf(-r2, rinv, K.h);
     const float fs = ok ? (fmaf(p_i, w.w, q.w) * diff) * (diff * rinv) : 0.0f;
     const float vs = ok ? diff : 0.0f;
