@@ -263,31 +263,35 @@ __device__ __forceinline__ void group_work(uint32_t bid, uint32_t nb, const uint
         uint32_t tot;
         uint32_t knm = block_exclusive_scan<kGroupWaves>(nm, s_scan, &tot);
         uint32_t kmm = block_exclusive_scan<kGroupWaves>(mm, s_scan, &tot);
-        if (nm) {
-            for (uint32_t t = t0; t < t1 && t < f + M; t += kGroupUnroll) {
-                const uint32_t m = fits ? (bits >> (t - t0)) & 0xFFu : match_bits(spos, t, t1, P);
-                for (uint32_t k = 0; k < kGroupUnroll && t + k < t1 && t + k < f + M; k++)
-                    if (!((m >> k) & 1u)) scratch[f + knm++] = t + k;
+        // The misplaced slots in ascending order: the k-th non-member of [f, f + M) at
+        // scratch[f + k], the k-th member of [f + M, end) at scratch[f + M + k] (k < tot <= M).
+        for (uint32_t t = t0; t < t1; t += kGroupUnroll) {
+            const uint32_t m = fits ? (bits >> (t - t0)) & 0xFFu : match_bits(spos, t, t1, P);
+            for (uint32_t k = 0; k < kGroupUnroll && t + k < t1; k++) {
+                const bool is = (m >> k) & 1u;
+                if (t + k < f + M) {
+                    if (!is) scratch[f + knm++] = t + k;
+                } else if (is) {
+                    scratch[f + M + kmm++] = t + k;
+                }
             }
         }
         __threadfence_block();
         __syncthreads();
-        if (mm) {
-            for (uint32_t t = max(t0, f + M); t < t1; t++) {
-                const bool is = fits ? (bits >> (t - t0)) & 1u : same_pos(spos[t], P);
-                if (!is) continue;
-                const uint32_t u = scratch[f + kmm++];
-                // positions move, the .w index bits stay with the slot
-                const float4 pt = spos[t], pu = spos[u];
-                spos[t] = make_float4(pu.x, pu.y, pu.z, pt.w);
-                spos[u] = make_float4(pt.x, pt.y, pt.z, pu.w);
-                if (svel) swap4(svel, t, u);
-                const uint32_t ti = sidx[t], ui = sidx[u];
-                sidx[t] = ui;
-                sidx[u] = ti;
-                rank[ui] = t;
-                rank[ti] = u;
-            }
+        // Thread k swaps the k-th misplaced member t with the k-th misplaced non-member u: all
+        // pairs at once (their slots are distinct), so the cell costs one round of loads.
+        for (uint32_t k = tid; k < tot; k += kGroupThreads) {
+            const uint32_t t = scratch[f + M + k], u = scratch[f + k];
+            // positions move, the .w index bits stay with the slot
+            const float4 pt = spos[t], pu = spos[u];
+            spos[t] = make_float4(pu.x, pu.y, pu.z, pt.w);
+            spos[u] = make_float4(pt.x, pt.y, pt.z, pu.w);
+            if (svel) swap4(svel, t, u);
+            const uint32_t ti = sidx[t], ui = sidx[u];
+            sidx[t] = ui;
+            sidx[u] = ti;
+            rank[ui] = t;
+            rank[ti] = u;
         }
         __threadfence_block();
         __syncthreads();
