@@ -10,6 +10,9 @@
 //   forge::HashGrid              forge-runtime/src/hashgrid.rs:21-193 (build runs on the GPU)
 //   forge::RadixSorter           forge-runtime/src/radix_sort.rs:26-220
 //   forge::find_cell_boundaries  forge-runtime/src/radix_sort.rs:229-317
+//   forge::cell_start_csr        forge-runtime/src/hashgrid.rs:102-106 (from sorted keys)
+//   forge::frame_bytes, pack_frame, Pipeline::run_streaming
+//                                forge-manifest/src/manifest_runner.rs:145-181, serve.rs:7-10,43-62
 //   forge::FieldSet, SimModule, Pipeline
 //                                forge-manifest/src/modules/mod.rs:12-117
 //   forge::SphFusedModule, SphDensityModule, SphPressureModule, SphViscosityModule,
@@ -22,7 +25,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <chrono>
 #include <cstdint>
+#include <cstring>
 #include <map>
 #include <memory>
 #include <stdexcept>
@@ -227,6 +232,16 @@ inline void find_cell_boundaries(Context& ctx, const Array<uint32_t>& sorted_cel
                                   (uint32_t)num_cells, cell_start.data(), cell_end.data()));
 }
 
+// CSR cell ranges of cell keys the caller already sorted (the prefix sum of hashgrid.rs:102-106):
+// cell_start[c] = number of keys < c for c = 0..num_cells; keys >= num_cells fall in no cell.
+inline void cell_start_csr(Context& ctx, const Array<uint32_t>& sorted_keys, size_t n,
+                           size_t num_cells, Array<uint32_t>& cell_start) {
+    if (cell_start.len() < num_cells + 1)
+        throw Error(FH_EINVAL, "cell_start needs num_cells + 1 entries");
+    check(fh_cell_start_csr(ctx.get(), sorted_keys.data(), (uint32_t)n, (uint32_t)num_cells,
+                            cell_start.data()));
+}
+
 // Named SoA particle fields in original particle order (modules/mod.rs:12-67).
 class FieldSet {
    public:
@@ -279,12 +294,43 @@ struct SphFusedModule : SimModule {
     }
     void execute(FieldSet& fs, float dt) override {
         prepare(fs);
-        fh_sph_params p{smoothing_radius, cell_size, {grid_dims[0], grid_dims[1], grid_dims[2]},
-                        particle_mass, gas_constant, rest_density, viscosity_coefficient};
+        const fh_sph_params p = params();
         check(fh_sph_fused(fs.ctx.get(), &p, has_epilogue ? &epilogue : nullptr,
                            fs.f("pos_x").data(), fs.f("pos_y").data(), fs.f("pos_z").data(),
                            fs.f("vel_x").data(), fs.f("vel_y").data(), fs.f("vel_z").data(),
                            fs.f("density").data(), nullptr, (uint32_t)fs.particle_count, dt));
+    }
+    // `steps` substeps in one call (fh_sph_fused_steps): the state stays on the device in
+    // cell-sorted order between them and the fields are written after the last one.
+    void execute_steps(FieldSet& fs, float dt, uint32_t steps) {
+        prepare(fs);
+        const fh_sph_params p = params();
+        check(fh_sph_fused_steps(fs.ctx.get(), &p, has_epilogue ? &epilogue : nullptr,
+                                 fs.f("pos_x").data(), fs.f("pos_y").data(), fs.f("pos_z").data(),
+                                 fs.f("vel_x").data(), fs.f("vel_y").data(), fs.f("vel_z").data(),
+                                 fs.f("density").data(), nullptr, (uint32_t)fs.particle_count, dt,
+                                 steps));
+    }
+    // The fused force pass alone (sph_fused.rs:519-639) over the grid and densities that a
+    // SphDensityModule left in the field set (u32 cell_start / sorted_indices, f32 density):
+    // v += a dt in place; accel (3 n floats) receives a when non-null.
+    void execute_force(FieldSet& fs, float dt, float* accel = nullptr) {
+        const size_t cells = (size_t)grid_dims[0] * grid_dims[1] * grid_dims[2] + 1;
+        if (fs.u("cell_start").len() != cells)
+            throw Error(FH_EINVAL, "cell_start does not match the module's grid");
+        const fh_sph_params p = params();
+        check(fh_sph_force(fs.ctx.get(), &p, fs.f("pos_x").data(), fs.f("pos_y").data(),
+                           fs.f("pos_z").data(), fs.f("vel_x").data(), fs.f("vel_y").data(),
+                           fs.f("vel_z").data(), fs.f("density").data(), fs.u("cell_start").data(),
+                           fs.u("sorted_indices").data(), accel, (uint32_t)fs.particle_count,
+                           dt));
+    }
+
+   private:
+    fh_sph_params params() const {
+        return fh_sph_params{smoothing_radius, cell_size,
+                             {grid_dims[0], grid_dims[1], grid_dims[2]},
+                             particle_mass, gas_constant, rest_density, viscosity_coefficient};
     }
 };
 
@@ -411,21 +457,56 @@ class Pipeline {
         step_async(fs, dt);
         fs.ctx.sync();
     }
-    void run(FieldSet& fs, float dt, size_t steps) {
-        for (size_t i = 0; i < steps; i++) step(fs, dt);
+    // `steps` substeps queued on the context stream.  When the (fused) plan is a single
+    // SphFusedModule and `resident` is set, they are one fh_sph_fused_steps call: the state stays
+    // in sorted order on the device and the fields are written after the last substep only
+    // (nothing else reads them in between).
+    void run_async(FieldSet& fs, float dt, size_t steps) {
+        plan();
+        if (resident && steps > 1 && plan_.size() == 1) {
+            if (auto* sph = dynamic_cast<SphFusedModule*>(plan_[0])) {
+                sph->execute_steps(fs, dt, (uint32_t)steps);
+                return;
+            }
+        }
+        for (size_t i = 0; i < steps; i++) step_async(fs, dt);
     }
-    // Record `substeps` step_async calls into the context's graph (manifest_runner.rs:57-69)
+    void run(FieldSet& fs, float dt, size_t steps) {  // modules/mod.rs:106-112
+        run_async(fs, dt, steps);
+        fs.ctx.sync();
+    }
+    // Record `substeps` substeps (run_async) into the context's graph (manifest_runner.rs:57-69)
     // and replay it (manifest_runner.rs:74-77).
     void capture(FieldSet& fs, float dt, size_t substeps) {
         plan();
         for (SimModule* m : plan_) m->prepare(fs);
         fs.ctx.sync();
         check(fh_graph_begin(fs.ctx.get()));
-        for (size_t i = 0; i < substeps; i++)
-            for (SimModule* m : plan_) m->execute(fs, dt);
+        try {
+            run_async(fs, dt, substeps);
+        } catch (...) {
+            fh_graph_end(fs.ctx.get());
+            throw;
+        }
         check(fh_graph_end(fs.ctx.get()));
     }
     void replay(FieldSet& fs, uint32_t count) { check(fh_graph_launch(fs.ctx.get(), count)); }
+
+    // run_manifest_streaming's loop (manifest_runner.rs:145-181): each step runs `substeps`
+    // substeps; after step s with s % frame_interval == 0 (an interval of 0 counts as 1) the
+    // binary frame (pack_frame) is copied to the host and passed to on_frame(frame_number,
+    // bytes).  Returns the final positions (interleaved x y z), count, substeps run and elapsed
+    // seconds, as SimResult does.
+    struct StreamResult {
+        std::vector<float> positions;
+        size_t count = 0, steps = 0;
+        double elapsed_secs = 0.0;
+    };
+    template <class OnFrame>
+    StreamResult run_streaming(FieldSet& fs, float dt, size_t total_steps, size_t substeps,
+                               size_t frame_interval, OnFrame on_frame);
+
+    bool resident = true;
 
    private:
     void plan() {
@@ -480,5 +561,59 @@ class Pipeline {
     std::vector<SimModule*> plan_;
     bool fused_ = false;
 };
+
+// The binary position frame of the streaming runner (FrameBuffer::set_frame, serve.rs:7-10,43-62):
+// u32 frame number, u32 particle count n, then x y z per particle as f32, little-endian.
+inline size_t frame_bytes(size_t n) { return 8 + 12 * n; }
+
+// Packs the current positions of `fs` into `out` on the device (fh_pack_frame).  With
+// device_counter (a device u32) the frame number is read from it and incremented there instead,
+// so a captured graph emits consecutive frame numbers on its replays.
+inline void pack_frame(FieldSet& fs, uint32_t frame, Array<uint8_t>& out,
+                       uint32_t* device_counter = nullptr) {
+    if (out.len() < frame_bytes(fs.particle_count))
+        throw Error(FH_EINVAL, "frame buffer too small");
+    check(fh_pack_frame(fs.ctx.get(), fs.f("pos_x").data(), fs.f("pos_y").data(),
+                        fs.f("pos_z").data(), (uint32_t)fs.particle_count, frame, device_counter,
+                        out.data()));
+}
+
+template <class OnFrame>
+Pipeline::StreamResult Pipeline::run_streaming(FieldSet& fs, float dt, size_t total_steps,
+                                               size_t substeps, size_t frame_interval,
+                                               OnFrame on_frame) {
+    const size_t interval = frame_interval ? frame_interval : 1;
+    auto dev = Array<uint8_t>::zeros(frame_bytes(fs.particle_count));
+    StreamResult r;
+    const auto t0 = std::chrono::steady_clock::now();
+    uint32_t frame_num = 0;
+    for (size_t s = 0; s < total_steps; s++) {
+        run_async(fs, dt, substeps);
+        r.steps += substeps;
+        if (s % interval == 0) {
+            pack_frame(fs, frame_num, dev);
+            fs.ctx.sync();
+            const std::vector<uint8_t> host = dev.to_vec();
+            on_frame(frame_num, host);
+            frame_num++;
+        }
+    }
+    fs.ctx.sync();
+    r.elapsed_secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    pack_frame(fs, 0, dev);
+    fs.ctx.sync();
+    const std::vector<uint8_t> host = dev.to_vec();
+    r.count = fs.particle_count;
+    r.positions.resize(3 * fs.particle_count);
+    for (size_t i = 0; i < r.positions.size(); i++) {
+        uint32_t bits = (uint32_t)host[8 + 4 * i] | (uint32_t)host[9 + 4 * i] << 8 |
+                        (uint32_t)host[10 + 4 * i] << 16 | (uint32_t)host[11 + 4 * i] << 24;
+        float f;
+        static_assert(sizeof f == sizeof bits, "f32");
+        std::memcpy(&f, &bits, sizeof f);
+        r.positions[i] = f;
+    }
+    return r;
+}
 
 }  // namespace forge

@@ -5,11 +5,14 @@
 //   tests/radix_sort_test.rs:139-171  test_find_cell_boundaries
 //   tests/hashgrid_test.rs:6-36       test_hashgrid_basic
 //   tests/hashgrid_test.rs:38-88      test_hashgrid_uniform_distribution (exactly 8)
-// plus a dam-break Pipeline step checked against the CPU oracle (oracle/oracle.h) and a graph
-// replay checked against eager steps.  Prints one line per test; exit status 0 iff all pass.
+// plus a dam-break Pipeline step checked against the CPU oracle (oracle/oracle.h), a graph
+// replay checked against eager steps, resident substeps against per-substep ones, the CSR cell
+// ranges of sorted keys, the standalone force pass against the oracle, and the binary frames of
+// the streaming runner.  Prints one line per test; exit status 0 iff all pass.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <numeric>
 #include <vector>
 
@@ -187,6 +190,151 @@ static void test_graph_replay_matches_eager(forge::Context& ctx) {
     std::printf("PASS test_graph_replay_matches_eager\n");
 }
 
+static void test_cell_start_csr(forge::Context& ctx) {
+    // sorted keys, one of them (9) outside the 8-cell grid
+    std::vector<uint32_t> kd = {0, 0, 1, 1, 1, 3, 3, 5, 9};
+    auto keys = Array<uint32_t>::from_vec(kd);
+    auto cs = Array<uint32_t>::zeros(9);
+    forge::cell_start_csr(ctx, keys, kd.size(), 8, cs);
+    ctx.sync();
+    std::vector<uint32_t> exp(9);
+    or_cell_start_csr(kd.data(), (uint32_t)kd.size(), 8, exp.data());
+    const std::vector<uint32_t> lit = {0, 2, 5, 5, 7, 7, 8, 8, 8};
+    EXPECT(exp == lit, "oracle: number of keys below each cell");
+    EXPECT(cs.to_vec() == lit, "cell_start from sorted keys");
+    std::printf("PASS test_cell_start_csr\n");
+}
+
+static void fill(forge::FieldSet& fs, std::vector<float>* st) {
+    const char* names[6] = {"pos_x", "pos_y", "pos_z", "vel_x", "vel_y", "vel_z"};
+    for (int a = 0; a < 6; a++) fs.add_f32(names[a], st[a]);
+}
+
+static void dam_break_pipeline(forge::Pipeline& p, float h, float m) {
+    p.add(std::make_unique<forge::SphFusedModule>(h, h, 40, 40, 40, m, 2000.0f, 1000.0f, 0.01f));
+    p.add(std::make_unique<forge::GravityModule>(0.0f, -9.81f, 0.0f));
+    p.add(std::make_unique<forge::IntegrateModule>());
+    p.add(std::make_unique<forge::BoxColliderModule>(0, 0, 0, 1, 1, 1, 0.3f));
+}
+
+// Pipeline::run keeps the state resident (one fh_sph_fused_steps call); the substeps then visit a
+// cell's particles in the previous substep's order, so results match the per-substep form up to
+// rounding.
+static void test_resident_run_matches_substeps(forge::Context& ctx) {
+    const size_t n = 4096;
+    const float h = 0.025f, m = 1000.0f / (float)n * 0.001f, dt = 1e-4f;
+    std::vector<float> st[6];
+    dam_break(n, st);
+    forge::FieldSet a(ctx, n), b(ctx, n);
+    fill(a, st);
+    fill(b, st);
+    forge::Pipeline pr, ps;
+    dam_break_pipeline(pr, h, m);
+    dam_break_pipeline(ps, h, m);
+    ps.resident = false;
+    pr.run(a, dt, 3);
+    ps.run(b, dt, 3);
+    auto ra = a.f("density").to_vec(), rb = b.f("density").to_vec();
+    for (size_t i = 0; i < n; i++)
+        EXPECT(std::fabs(ra[i] - rb[i]) <= 1e-4f * std::fabs(rb[i]), "density");
+    const char* names[3] = {"pos_x", "pos_y", "pos_z"};
+    for (int q = 0; q < 3; q++) {
+        auto x = a.f(names[q]).to_vec(), y = b.f(names[q]).to_vec();
+        for (size_t i = 0; i < n; i++)
+            EXPECT(std::fabs(x[i] - y[i]) <= 1e-6f + 1e-5f * std::fabs(y[i]), "position");
+    }
+    std::printf("PASS test_resident_run_matches_substeps\n");
+}
+
+// SphFusedModule::execute_force over the grid and densities SphDensityModule left in the field
+// set equals the oracle's fused pass on the same inputs bit for bit (the caller's grid is walked
+// with the reference's expressions and neighbour order).
+static void test_force_after_density_matches_oracle(forge::Context& ctx) {
+    const size_t n = 4096;
+    const float h = 0.025f, m = 1000.0f / (float)n * 0.001f, dt = 1e-4f;
+    std::vector<float> st[6];
+    dam_break(n, st);
+    for (size_t i = 0; i < n; i++) {  // velocities, so the viscosity term is not zero
+        st[3][i] = 0.1f * (float)(i % 11) - 0.5f;
+        st[4][i] = 0.05f * (float)(i % 7);
+        st[5][i] = -0.02f * (float)(i % 5);
+    }
+    forge::FieldSet fs(ctx, n);
+    fill(fs, st);
+    forge::SphDensityModule dens(h, h, 40, 40, 40, m);
+    forge::SphFusedModule sph(h, h, 40, 40, 40, m, 2000.0f, 1000.0f, 0.01f);
+    dens.execute(fs, dt);
+    auto acc = Array<float>::zeros(3 * n);
+    sph.execute_force(fs, dt, acc.data());
+    ctx.sync();
+    auto rho = fs.f("density").to_vec();
+    auto cs = fs.u("cell_start").to_vec(), si = fs.u("sorted_indices").to_vec();
+    or_sph_params p{h, h, {40, 40, 40}, m, 2000.0f, 1000.0f, 0.01f};
+    std::vector<float> vout(3 * n), aout(3 * n);
+    or_sph_force(&p, st[0].data(), st[1].data(), st[2].data(), st[3].data(), st[4].data(),
+                 st[5].data(), rho.data(), (uint32_t)n, cs.data(), si.data(), dt, vout.data(),
+                 aout.data());
+    auto ga = acc.to_vec();
+    const char* names[3] = {"vel_x", "vel_y", "vel_z"};
+    for (int q = 0; q < 3; q++) {
+        auto v = fs.f(names[q]).to_vec();
+        for (size_t i = 0; i < n; i++) {
+            EXPECT(v[i] == vout[(size_t)q * n + i], "velocity vs oracle");
+            EXPECT(ga[(size_t)q * n + i] == aout[(size_t)q * n + i], "acceleration vs oracle");
+        }
+    }
+    std::printf("PASS test_force_after_density_matches_oracle\n");
+}
+
+static std::vector<float> frame_floats(const std::vector<uint8_t>& f, uint32_t* frame,
+                                       uint32_t* count) {
+    auto u32 = [&](size_t o) {
+        return (uint32_t)f[o] | (uint32_t)f[o + 1] << 8 | (uint32_t)f[o + 2] << 16 |
+               (uint32_t)f[o + 3] << 24;
+    };
+    *frame = u32(0);
+    *count = u32(4);
+    std::vector<float> x((f.size() - 8) / 4);
+    for (size_t i = 0; i < x.size(); i++) {
+        const uint32_t b = u32(8 + 4 * i);
+        std::memcpy(&x[i], &b, 4);
+    }
+    return x;
+}
+
+static void test_pack_frame_and_streaming(forge::Context& ctx) {
+    const size_t n = 4096;
+    const float h = 0.025f, m = 1000.0f / (float)n * 0.001f, dt = 1e-4f;
+    std::vector<float> st[6];
+    dam_break(n, st);
+    forge::FieldSet fs(ctx, n);
+    fill(fs, st);
+    auto out = Array<uint8_t>::zeros(forge::frame_bytes(n));
+    forge::pack_frame(fs, 7, out);
+    ctx.sync();
+    uint32_t frame = 0, count = 0;
+    auto x = frame_floats(out.to_vec(), &frame, &count);
+    EXPECT(frame == 7 && count == n, "frame header");
+    for (size_t i = 0; i < n; i++)
+        for (int q = 0; q < 3; q++) EXPECT(x[3 * i + q] == st[q][i], "interleaved positions");
+    forge::Pipeline p;
+    dam_break_pipeline(p, h, m);
+    std::vector<uint32_t> seen;
+    std::vector<float> last;
+    auto r = p.run_streaming(fs, dt, 5, 2, 2, [&](uint32_t f, const std::vector<uint8_t>& bytes) {
+        uint32_t fr = 0, c = 0;
+        last = frame_floats(bytes, &fr, &c);
+        EXPECT(fr == f && c == n, "streamed frame header");
+        seen.push_back(f);
+    });
+    EXPECT(seen == std::vector<uint32_t>({0, 1, 2}), "frames after steps 0, 2 and 4");
+    EXPECT(r.steps == 10 && r.count == n, "substeps run");
+    EXPECT(r.positions == last, "final positions equal the last frame (step 4 is the last)");
+    auto px = fs.f("pos_x").to_vec();
+    for (size_t i = 0; i < n; i++) EXPECT(r.positions[3 * i] == px[i], "final positions");
+    std::printf("PASS test_pack_frame_and_streaming\n");
+}
+
 int main() {
     try {
         forge::Context ctx(1 << 16, 1 << 16);
@@ -197,6 +345,10 @@ int main() {
         test_hashgrid_uniform_distribution(ctx);
         test_pipeline_step_matches_oracle(ctx);
         test_graph_replay_matches_eager(ctx);
+        test_cell_start_csr(ctx);
+        test_resident_run_matches_substeps(ctx);
+        test_force_after_density_matches_oracle(ctx);
+        test_pack_frame_and_streaming(ctx);
     } catch (const forge::Error& e) {
         std::printf("FAIL exception %d: %s\n", e.code(), e.what());
         return 2;

@@ -1,5 +1,7 @@
 """The C++ host mirror (include/forge_hip.hpp) running the reference's hash-grid and radix-sort
-tests and a pipeline step on the GPU (binary built by __graft_entry__.build())."""
+tests, a pipeline step, graph replay, resident substeps, CSR cell ranges from sorted keys, the
+standalone force pass and the streaming frames on the GPU (binary built by
+__graft_entry__.build())."""
 import subprocess
 from pathlib import Path
 
@@ -14,4 +16,4 @@ def test_cpp_mirror_reference_tests():
     r = subprocess.run([str(BIN)], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.count("PASS ") == 7
+    assert r.stdout.count("PASS ") == 11
