@@ -452,18 +452,21 @@ def resident_case(case):
         return cfg, vel, 3
     if case == "c0":
         return workloads.config0(), None, 2
+    if case == "c3":
+        return workloads.config3(), None, 2
     cfg, vel, _ = viscosity_cfg("groups" if case == "groups_k0" else "lattice")
     return cfg, vel, 4
 
 
-@pytest.mark.parametrize("case", ["small", "colocated", "c0", "lattice_k0", "groups_k0"])
+@pytest.mark.parametrize("case", ["small", "colocated", "c0", "lattice_k0", "groups_k0", "c3"])
 def test_resident_substeps_match_oracle(fh, gpu_ctx, oracle, case):
     """Resident substeps (fh_sph_fused_steps: the state stays in sorted order on the device
     between substeps, sorted by the previous substep's slots) against the oracle, particle by
     particle.  A call of k substeps repeats the first k - 1 substeps of the call of k - 1
     bit for bit, so substep k is checked as one oracle step (or_sph_step) from the fields the
     (k-1)-substep call returned, at the one-step bar, for k = 1 .. K.  Every substep after the
-    first runs resident.  _k0 cases: gas_constant = 0 (the viscosity term alone, non-chaotic
+    first runs resident.  c3: the full 1,048,576-particle dam break, whose second substep
+    (resident) already moves most particles to other cells.  _k0 cases: gas_constant = 0 (the viscosity term alone, non-chaotic
     motion), where the K-substep result is also compared with K chained oracle steps from the
     initial fields, within K times the one-step bound."""
     cfg, vel, K = resident_case(case)
