@@ -88,6 +88,21 @@ __device__ __forceinline__ void slab_ranges(const CellXYZ& c, bool live, const G
 }
 
 // ---------------------------------------------------------------------------------------------
+// Workgroup renumbering for the light kernels.  The dispatcher hands workgroup b to XCD b % 8,
+// so consecutive items land on eight different L2s.  Mapping runs of kXcdChunk workgroups to one
+// XCD keeps neighbouring sub-tiles, which read mostly the same candidate cells, on one L2 while
+// every XCD still takes a share of each region of the box (balance matters more than reuse: a
+// contiguous eighth of the items per XCD was slower).  The tail beyond the last whole round of
+// 8 * kXcdChunk workgroups keeps its own numbers, so the mapping is a permutation of [0, nb).
+constexpr uint32_t kXcdChunk = 128, kXcds = 8;
+__device__ __forceinline__ uint32_t xcd_chunked(uint32_t b, uint32_t nb) {
+    const uint32_t full = nb / (kXcds * kXcdChunk) * (kXcds * kXcdChunk);
+    if (b >= full) return b;
+    const uint32_t x = b % kXcds, i = b / kXcds;
+    return ((i / kXcdChunk) * kXcds + x) * kXcdChunk + (i % kXcdChunk);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Load balance.  A (64-particle sub-tile, slab) item whose particles each face more than
 // kHeavyWork candidates -- the box corners of c3 collect thousands of particles at one point --
 // is moved to a heavy list and processed by a 512-lane workgroup in which 8 waves split the
@@ -638,7 +653,7 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
                                                          const Control* __restrict__ ctl) {
     __shared__ float4 s_p[kTileP / kWave][kWin];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
+    const uint32_t item = xcd_chunked(blockIdx.x, gridDim.x) * (kTileP / kWave) + (uint32_t)wave;
     if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
@@ -1064,7 +1079,7 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     __shared__ float4 s_p[kTileP / kWave][kWin];  // x, y, z, p_j
     __shared__ float4 s_v[kTileP / kWave][kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t item = blockIdx.x * (kTileP / kWave) + (uint32_t)wave;
+    const uint32_t item = xcd_chunked(blockIdx.x, gridDim.x) * (kTileP / kWave) + (uint32_t)wave;
     if (item >= items || flag[item] != kItemLight) return;  // whole wave; heavy: k_force_heavy
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
