@@ -68,6 +68,7 @@ def algorithmic_bytes(n: int, cells: int, passes: int, substeps: int = 1) -> dic
     C4 = 4 * (cells + 1)
     entry = {
         "hash": 12 * n + 4 * n,                      # positions in, cell keys out
+        # passes of 8-bit digits, or two of 10-bit digits for 17..20-bit keys (c3):
         # pass 0 reads keys (values are the indices), middle passes read + write (key, value),
         # the last pass writes (key, value) and the rank of each particle
         "sort": 12 * n + 16 * n * max(passes - 2, 0) + 16 * n + 4 * n,
@@ -214,7 +215,7 @@ def bench_sph(args, fh, torch, log):
 
     cfg = workloads.config3()
     C = cfg.num_cells
-    passes = (max(1, (C - 1).bit_length()) + 7) // 8
+    _, passes = fh.RadixSorter.digit_layout(max(1, (C - 1).bit_length()), cfg.n)
     G = max(1, args.graph_substeps)
     K, W = max(1, args.steps), max(0, args.warmup)
     fields, pipe, ctx, wall, ev_ms = timed_trajectory(fh, torch, cfg, W, K, G, log)

@@ -166,8 +166,8 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->va, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->kb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->vb, max_n, &tot);
-    if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)kMaxPasses * c->max_sort_tiles * 256u, &tot);
-    if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)kHistBlocks * kMaxPasses * 256u, &tot);
+    if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)c->max_sort_tiles * kDigitSlots, &tot);
+    if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)kHistBlocks * kDigitSlots, &tot);
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
     if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);
@@ -206,7 +206,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming);
     // One-time clears (outside any capture): look-back words and run tags start untagged
     // (epoch 0 is never current).
-    if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)kMaxPasses * c->max_sort_tiles * 256u * 4u, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)c->max_sort_tiles * kDigitSlots * 4u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->scan_lb, 0, (size_t)c->max_scan_tiles * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->run_tag, 0, (size_t)max_cells * 8u, c->stream);

@@ -29,6 +29,14 @@ constexpr int kSortItemsLarge = 24;                  // keys per thread from kSo
 constexpr int kSortTileLarge = kSortThreads * kSortItemsLarge;
 constexpr uint32_t kSortLargeN = 1u << 22;
 constexpr int kMaxPasses = 4;          // 8-bit digits, up to 32-bit keys
+// Digit layouts of a sort.  8-bit digits in general; 10-bit digits for keys of 17..20 bits
+// below kSortLargeN keys (c3's and c2's cell keys): two passes instead of three.  A pass over
+// that many keys costs about the same at either width -- its time is the look-back chain across
+// the tiles, not its bytes -- so the pass saved is the gain.
+constexpr uint32_t kWideDigitBits = 10;
+// Words per tile of look-back and per row of partial histograms, and Control::hist: the largest
+// passes x bins over the layouts (4 x 256, 2 x 1024).  Pass p's bin d sits at p * bins + d.
+constexpr uint32_t kDigitSlots = 2048;
 constexpr int kHistThreads = 256;
 #ifndef FH_HIST_ITEMS
 #define FH_HIST_ITEMS 16
@@ -97,7 +105,7 @@ struct Control {
     Line heavy_count[kHeavyLists];      // entries in each heavy SPH work sub-list
     Line collapse_count;                // entries in the list of co-located cells
     Line big_count;                     // entries in the list of cells of >= kCollapseMin
-    uint32_t hist[kMaxPasses][256];     // per-pass digit histograms of the current sort
+    uint32_t hist[kDigitSlots];         // digit histograms of the current sort (pass p, bin d: p * bins + d)
 };
 
 // Division of a 32-bit unsigned value by a fixed divisor d >= 1 with a multiply-high, a
@@ -156,8 +164,8 @@ struct fh_ctx {
     uint32_t* va;        // [max_n]
     uint32_t* kb;        // [max_n]
     uint32_t* vb;        // [max_n]
-    uint32_t* sort_lb;   // [kMaxPasses][max_sort_tiles][256] 32-bit look-back words
-    uint32_t* hist_part; // [kHistBlocks][kMaxPasses * 256] per-block digit histograms
+    uint32_t* sort_lb;   // [max_sort_tiles * kDigitSlots] 32-bit look-back words (pass-major)
+    uint32_t* hist_part; // [kHistBlocks][kDigitSlots] per-block digit histograms
     fh::Control* ctl;    // device control block
     // grid scratch
     uint64_t* run_tag;     // [max_cells] epoch << 32 | first sorted index of the cell's run
@@ -403,7 +411,17 @@ hipError_t launch_integrate(fh_ctx* c, float* px, float* py, float* pz, float* v
 hipError_t launch_box(fh_ctx* c, float* px, float* py, float* pz, float* vx, float* vy,
                       float* vz, uint32_t n, const float* mn, const float* mx, float e);
 
-__host__ __device__ inline uint32_t passes_for_bits(uint32_t bits) { return (bits + 7u) / 8u; }
+// Digit width, passes and width of the last pass's digit of a num_bits sort of n keys.
+struct Digits {
+    uint32_t bits, passes, top_bits;
+};
+__host__ __device__ inline Digits digits_for(uint32_t num_bits, uint32_t n) {
+    Digits d;
+    d.bits = (num_bits > 16u && num_bits <= 20u && n < kSortLargeN) ? kWideDigitBits : 8u;
+    d.passes = (num_bits + d.bits - 1u) / d.bits;
+    d.top_bits = num_bits - d.bits * (d.passes ? d.passes - 1u : 0u);
+    return d;
+}
 inline uint32_t bits_for_cells(uint32_t num_cells) {
     uint32_t b = 1;
     while (b < 32 && (1ull << b) < (uint64_t)num_cells) b++;

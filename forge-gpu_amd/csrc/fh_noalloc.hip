@@ -31,12 +31,12 @@ constexpr size_t round_up(size_t b) { return (b + kAlign - 1) / kAlign * kAlign;
 // kSortTile keys; the histogram kernel writes at most ceil(n / kHistChunk) rows.
 constexpr size_t kTiles = (kNoAllocMaxN + kSortTile - 1) / kSortTile;
 constexpr size_t kHistRows = (kNoAllocMaxN + kHistChunk - 1) / kHistChunk;
-constexpr size_t kCtlBytes = 8192;  // a fixed reservation for the control block
+constexpr size_t kCtlBytes = 16384;  // a fixed reservation for the control block
 static_assert(sizeof(Control) <= kCtlBytes, "control block exceeds its reservation");
 constexpr size_t kOffCtl = 0;
 constexpr size_t kOffLb = kOffCtl + kCtlBytes;
-constexpr size_t kOffHist = kOffLb + round_up((size_t)kMaxPasses * kTiles * 256u * 4u);
-constexpr size_t kOffKa = kOffHist + round_up(kHistRows * kMaxPasses * 256u * 4u);
+constexpr size_t kOffHist = kOffLb + round_up(kTiles * kDigitSlots * 4u);
+constexpr size_t kOffKa = kOffHist + round_up(kHistRows * kDigitSlots * 4u);
 constexpr size_t kBuf = round_up((size_t)kNoAllocMaxN * 4u);
 constexpr size_t kOffVa = kOffKa + kBuf;
 constexpr size_t kOffKb = kOffVa + kBuf;

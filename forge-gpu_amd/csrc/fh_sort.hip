@@ -4,18 +4,23 @@
 // re-read every earlier block's histogram per block and every earlier key per key.  Design:
 //   k_begin        bump the look-back epoch, clear histograms and counters, zero the 32-bit
 //                  look-back words of the coming sort
-//   k_hist_keys /  one read of the keys builds the 256-bin histograms of ALL 8-bit passes into
+//   k_hist_keys /  one read of the keys builds the digit histograms of ALL passes into
 //   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
 //                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
 //   k_hist_reduce  sums the partial rows into the histograms
 //   sort_plan      decides which passes run (a pass whose digit is equal for every key is the
 //                  identity and is skipped): k_sort_plan for large sorts, in every workgroup
 //                  of every pass for small ones
-//   k_onesweep     one kernel per 8-bit pass: an 8192-key tile per 512-lane workgroup, ranked
-//                  with 64-lane ballot match-any, digit offsets from a decoupled look-back over
+//   k_onesweep     one kernel per pass: an 8192-key tile per 512-lane workgroup, ranked with
+//                  64-lane ballot match-any, digit offsets from a decoupled look-back over
 //                  dynamically numbered tiles, then staged in LDS in digit order (keys, then
 //                  values through the same buffer) so the global scatter writes contiguous runs
 //   k_sort_finish  copies the result of a one-pass sort in place back from scratch
+// Digits are 8 bits (256 bins), or 10 bits (1024 bins) for keys of 17..20 bits below
+// kSortLargeN keys (digits_for): a pass over a million keys is bound by its look-back chain
+// across the tiles, not by its bytes, so two 10-bit passes beat three 8-bit ones -- provided a
+// tile's 1024 look-back words move as 512 contiguous 64-bit pairs (two digits per thread, one
+// status per pair), not as 1024 strided 32-bit words.
 // Stability: within a tile the rank of a key counts the equal digits before it in input order
 // (earlier items, earlier lanes, earlier waves); across tiles the look-back prefix counts the
 // equal digits of all earlier tiles.  Equal keys therefore keep their input order, which is
@@ -25,6 +30,8 @@
 // few and apart: per-workgroup histogram rows instead of global bin atomics, 32-bit look-back
 // words (a poll moves half the bytes of a 64-bit epoch word), and every hot counter on a line
 // of its own (Control).
+#include <type_traits>
+
 #include "fh_internal.hpp"
 
 namespace fh {
@@ -45,8 +52,7 @@ __device__ __forceinline__ void begin_work(const Begin& b) {
     const uint32_t t = threadIdx.x;
     Control* ctl = b.ctl;
     if (blockIdx.x == 0) {
-        for (uint32_t i = t; i < (uint32_t)kMaxPasses * 256u; i += blockDim.x)
-            (&ctl->hist[0][0])[i] = 0u;
+        for (uint32_t i = t; i < kDigitSlots; i += blockDim.x) ctl->hist[i] = 0u;
         if (t == 0) {
             uint32_t e = (ctl->epoch + 1u) & kEpochMask;
             ctl->epoch = e ? e : 1u;
@@ -61,17 +67,22 @@ __device__ __forceinline__ void begin_work(const Begin& b) {
         b.lb[i] = 0u;
 }
 
+// The look-back words of the passes of a sort of n keys: pass p's tiles take words
+// [p * tiles * bins, (p + 1) * tiles * bins) (counted here with the small tile, which bounds the
+// large one's count).
 static Begin make_begin(fh_ctx* c, bool begin, uint32_t n, uint32_t num_bits) {
     if (!begin) return Begin{nullptr, nullptr, 0u};
+    const Digits L = digits_for(num_bits, n);
     const uint32_t words =
-        n && num_bits ? passes_for_bits(num_bits) * ceil_div(n, (uint32_t)kSortTile) * 256u : 0u;
+        n && num_bits ? L.passes * ceil_div(n, (uint32_t)kSortTile) * (1u << L.bits) : 0u;
     return Begin{c->ctl, c->sort_lb, words};
 }
 
 // ---------------------------------------------------------------------------------------------
 // Histograms.  Each workgroup counts into per-wave LDS histograms; a wave whose valid lanes all
 // hold the same digit (skewed digits: c1's top byte is always 0) adds its population with one
-// LDS atomic instead of 64 conflicting ones.  Digit p of key k is (k >> 8p) & mask_p.
+// LDS atomic instead of 64 conflicting ones.  Digit p of key k is bits [DB p, DB p + DB) of k,
+// the last pass's digit masked by `top`.  A wave's histograms are P rows of 2^DB bins.
 __device__ __forceinline__ void hist_add(uint32_t* h, uint32_t d, bool valid) {
     const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
     const uint64_t other = __ballot(valid && d != d0);
@@ -84,59 +95,59 @@ __device__ __forceinline__ void hist_add(uint32_t* h, uint32_t d, bool valid) {
 }
 
 // P = number of passes (compile time, so the pass loop unrolls); top = mask of the last pass.
-template <int P>
-__device__ __forceinline__ void count_key(uint32_t (*sh)[256], uint32_t k, bool valid,
-                                          uint32_t top) {
+template <int P, int DB>
+__device__ __forceinline__ void count_key(uint32_t* sh, uint32_t k, bool valid, uint32_t top) {
+    constexpr uint32_t NB = 1u << DB;
 #pragma unroll
     for (int p = 0; p < P; p++)
-        hist_add(sh[p], (k >> (8 * p)) & (p == P - 1 ? top : 255u), valid);
+        hist_add(sh + p * NB, (k >> (DB * p)) & (p == P - 1 ? top : NB - 1u), valid);
 }
 
 // A full chunk of this thread's kHistItems keys.  Per pass, a wave whose 64 x kHistItems keys
 // all share one digit (c1's top byte; c3's top digit in most waves) adds their number with one
 // atomic; otherwise every key adds 1, with no per-key uniformity test.  `tb` = bits of the last
 // pass's digit.
-template <int P>
-__device__ __forceinline__ void count_chunk(uint32_t (*sh)[256], const uint32_t (&k)[kHistItems],
+template <int P, int DB>
+__device__ __forceinline__ void count_chunk(uint32_t* sh, const uint32_t (&k)[kHistItems],
                                             uint32_t tb) {
+    constexpr uint32_t NB = 1u << DB;
 #pragma unroll
     for (int p = 0; p < P; p++) {
-        const uint32_t w = p == P - 1 ? tb : 8u;
+        const uint32_t w = p == P - 1 ? tb : (uint32_t)DB;
+        uint32_t* h = sh + p * NB;
         const uint32_t d0 =
-            __builtin_amdgcn_readfirstlane(__builtin_amdgcn_ubfe(k[0], 8u * p, w));
+            __builtin_amdgcn_readfirstlane(__builtin_amdgcn_ubfe(k[0], DB * p, w));
         uint32_t diff = 0;
 #pragma unroll
-        for (int j = 0; j < kHistItems; j++) diff |= __builtin_amdgcn_ubfe(k[j], 8u * p, w) ^ d0;
+        for (int j = 0; j < kHistItems; j++) diff |= __builtin_amdgcn_ubfe(k[j], DB * p, w) ^ d0;
         if (__ballot(diff != 0u) == 0ull) {
-            if ((threadIdx.x & 63u) == 0u) atomicAdd(&sh[p][d0], 64u * kHistItems);
+            if ((threadIdx.x & 63u) == 0u) atomicAdd(&h[d0], 64u * kHistItems);
         } else {
 #pragma unroll
             for (int j = 0; j < kHistItems; j++)
-                atomicAdd(&sh[p][__builtin_amdgcn_ubfe(k[j], 8u * p, w)], 1u);
+                atomicAdd(&h[__builtin_amdgcn_ubfe(k[j], DB * p, w)], 1u);
         }
     }
 }
 
-// Write this workgroup's row of partial histograms (all 256 bins of every pass).
-__device__ __forceinline__ void write_row(uint32_t (*sh)[kMaxPasses][256], uint32_t* part,
-                                          uint32_t passes) {
+// Write this workgroup's row of partial histograms (all bins of every pass, P * 2^DB slots).
+template <int S>
+__device__ __forceinline__ void write_row(uint32_t (*sh)[S], uint32_t* part) {
     __syncthreads();
-    const uint32_t d = threadIdx.x;  // kHistThreads == 256: one bin per thread
-    for (uint32_t p = 0; p < passes; p++)
-        part[(size_t)blockIdx.x * (kMaxPasses * 256u) + p * 256u + d] =
-            sh[0][p][d] + sh[1][p][d] + sh[2][p][d] + sh[3][p][d];
+    for (uint32_t i = threadIdx.x; i < (uint32_t)S; i += kHistThreads)
+        part[(size_t)blockIdx.x * kDigitSlots + i] = sh[0][i] + sh[1][i] + sh[2][i] + sh[3][i];
 }
 
-template <int P>
+template <int P, int DB>
 __global__ __launch_bounds__(kHistThreads) void k_hist_keys(const uint32_t* __restrict__ keys,
                                                             uint32_t n, uint32_t top,
                                                             uint32_t* __restrict__ part,
                                                             Begin bg) {
-    __shared__ uint32_t sh[4][kMaxPasses][256];
+    constexpr int S = P << DB;  // slots of one wave's histograms
+    __shared__ uint32_t sh[4][S];
     const uint32_t wave = threadIdx.x >> 6;
     begin_work(bg);
-    for (uint32_t i = threadIdx.x; i < 4u * kMaxPasses * 256u; i += kHistThreads)
-        (&sh[0][0][0])[i] = 0u;
+    for (uint32_t i = threadIdx.x; i < 4u * S; i += kHistThreads) (&sh[0][0])[i] = 0u;
     __syncthreads();
     const uint32_t chunks = ceil_div(n, (uint32_t)kHistChunk);
     // Striped chunk loads (item j of thread t is key base + 256 j + t); the loads of the next
@@ -156,31 +167,31 @@ __global__ __launch_bounds__(kHistThreads) void k_hist_keys(const uint32_t* __re
             nxt[j] = keys[min(i, n - 1u)];
         }
         if ((c + 1u) * kHistChunk <= n) {  // workgroup-uniform
-            count_chunk<P>(sh[wave], cur, (uint32_t)__popc(top));
+            count_chunk<P, DB>(sh[wave], cur, (uint32_t)__popc(top));
         } else {
 #pragma unroll
             for (int j = 0; j < kHistItems; j++) {
                 const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
-                count_key<P>(sh[wave], cur[j], i < n, top);
+                count_key<P, DB>(sh[wave], cur[j], i < n, top);
             }
         }
 #pragma unroll
         for (int j = 0; j < kHistItems; j++) cur[j] = nxt[j];
     }
-    write_row(sh, part, P);
+    write_row<S>(sh, part);
 }
 
-template <int P>
+template <int P, int DB>
 __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ z,
     uint32_t stride, uint32_t n, GridDesc g, uint32_t top, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ part, Begin bg) {
-    __shared__ uint32_t sh[4][kMaxPasses][256];
+    constexpr int S = (P > 0 ? P : 1) << DB;
+    __shared__ uint32_t sh[4][S];
     const uint32_t wave = threadIdx.x >> 6;
     begin_work(bg);
     if (P > 0) {
-        for (uint32_t i = threadIdx.x; i < 4u * kMaxPasses * 256u; i += kHistThreads)
-            (&sh[0][0][0])[i] = 0u;
+        for (uint32_t i = threadIdx.x; i < 4u * S; i += kHistThreads) (&sh[0][0])[i] = 0u;
         __syncthreads();
     }
     const uint32_t chunks = ceil_div(n, (uint32_t)kHistChunk);
@@ -205,50 +216,52 @@ __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
         }
         if (P > 0) {
             if ((c + 1u) * kHistChunk <= n) {  // workgroup-uniform
-                count_chunk<P>(sh[wave], k, (uint32_t)__popc(top));
+                count_chunk<P, DB>(sh[wave], k, (uint32_t)__popc(top));
             } else {
 #pragma unroll
                 for (int j = 0; j < kHistItems; j++) {
                     const uint32_t i = c * kHistChunk + j * kHistThreads + threadIdx.x;
-                    count_key<P>(sh[wave], k[j], i < n, top);
+                    count_key<P, DB>(sh[wave], k[j], i < n, top);
                 }
             }
         }
     }
-    if (P > 0) write_row(sh, part, P);
+    if (P > 0) write_row<S>(sh, part);
 }
 
-// Sum the partial rows: workgroup (p, r) adds rows r*R .. r*R+R-1 of pass p into the global
-// histogram.  (No fence / last-workgroup election here: an agent-scope release on this part
-// writes the L2 back, which costs tens of microseconds per workgroup; the decision about the
-// passes is a separate one-workgroup kernel, the kernel boundary gives the visibility.)
+// Sum the partial rows: workgroup (r, b) adds rows r*R .. r*R+R-1 of histogram slots
+// 256 b .. 256 b + 255 into the histograms.  (No fence / last-workgroup election here: an
+// agent-scope release on this part writes the L2 back, which costs tens of microseconds per
+// workgroup; the decision about the passes is a separate one-workgroup kernel, the kernel
+// boundary gives the visibility.)
 __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict__ part,
-                                                     uint32_t rows, Control* ctl) {
-    const uint32_t d = threadIdx.x;
-    const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
-    const uint32_t p = blockIdx.x / groups, r0 = (blockIdx.x % groups) * kHistRowsPerReduce;
+                                                     uint32_t rows, uint32_t slot_blocks,
+                                                     Control* ctl) {
+    const uint32_t b = blockIdx.x % slot_blocks, r0 = (blockIdx.x / slot_blocks) * kHistRowsPerReduce;
+    const uint32_t slot = b * 256u + threadIdx.x;
     const uint32_t r1 = min(rows, r0 + (uint32_t)kHistRowsPerReduce);
     uint32_t s = 0;
 #pragma unroll 8
-    for (uint32_t r = r0; r < r1; r++) s += part[(size_t)r * (kMaxPasses * 256u) + p * 256u + d];
-    if (s) atomicAdd(&ctl->hist[p][d], s);
+    for (uint32_t r = r0; r < r1; r++) s += part[(size_t)r * kDigitSlots + slot];
+    if (s) atomicAdd(&ctl->hist[slot], s);
 }
 
 // The passes that run (one bit per pass), derived from the digit histograms (for small sorts
-// by every workgroup of every pass: the same function of the same data, so all agree).  A pass whose digit is
-// equal for every key (one histogram bin holds all n keys) is the identity and is skipped.  Two
-// adjustments leave the result in (kfin, vfin) without a copy kernel: when no pass moves keys
-// and the sort is out of place, pass 0 runs (a stable copy: its digit is constant); when exactly
-// one pass moves keys in place (it has to write scratch) and the sort has another pass, that
-// pass runs as well (also a copy), so the second of the two writes back in place.  Only
-// one-pass sorts in place keep k_sort_finish (which reads ctl->plan, written by pass 0).
-// Threads 0..255 (one bin each) test the bins; s_triv collects the trivial passes.
+// by every workgroup of every pass: the same function of the same data, so all agree).  A pass
+// whose digit is equal for every key (one histogram bin holds all n keys) is the identity and
+// is skipped.  Two adjustments leave the result in (kfin, vfin) without a copy kernel: when no
+// pass moves keys and the sort is out of place, pass 0 runs (a stable copy: its digit is
+// constant); when exactly one pass moves keys in place (it has to write scratch) and the sort
+// has another pass, that pass runs as well (also a copy), so the second of the two writes back
+// in place.  Only one-pass sorts in place keep k_sort_finish (which reads ctl->plan, written by
+// pass 0).  The workgroup's threads test the bins (nb per pass); s_triv collects the trivial
+// passes.
 __device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, uint32_t passes,
-                                              uint32_t n, bool in_place, uint32_t* s_triv) {
-    const uint32_t d = threadIdx.x;
-    if (d < 256u)
-        for (uint32_t q = 0; q < passes; q++)
-            if (ctl->hist[q][d] == n) atomicOr(s_triv, 1u << q);
+                                              uint32_t nb, uint32_t n, bool in_place,
+                                              uint32_t* s_triv) {
+    for (uint32_t q = 0; q < passes; q++)
+        for (uint32_t d = threadIdx.x; d < nb; d += blockDim.x)
+            if (ctl->hist[q * nb + d] == n) atomicOr(s_triv, 1u << q);
     __syncthreads();
     uint32_t plan = ~*s_triv & ((1u << passes) - 1u);
     if (plan == 0u && !in_place) {
@@ -262,18 +275,20 @@ __device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, u
 
 // The same plan as one kernel (256 threads) before the passes: for large sorts, where a load
 // of the histograms and a barrier in each of thousands of workgroups cost more than a launch.
-__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t n, uint32_t in_place,
-                                                   Control* ctl) {
+__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t nb, uint32_t n,
+                                                   uint32_t in_place, Control* ctl) {
     __shared__ uint32_t s_triv;
     if (threadIdx.x == 0) s_triv = 0u;
     __syncthreads();
-    const uint32_t plan = sort_plan(ctl, passes, n, in_place != 0u, &s_triv);
+    const uint32_t plan = sort_plan(ctl, passes, nb, n, in_place != 0u, &s_triv);
     if (threadIdx.x == 0) ctl->plan = plan;
 }
 
-hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t passes) {
+hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots) {
     const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
-    k_hist_reduce<<<passes * groups, 256, 0, c->stream>>>(c->hist_part, rows, c->ctl);
+    const uint32_t slot_blocks = slots / 256u;  // slots = passes * bins, bins >= 256
+    k_hist_reduce<<<groups * slot_blocks, 256, 0, c->stream>>>(c->hist_part, rows, slot_blocks,
+                                                               c->ctl);
     return hipGetLastError();
 }
 
@@ -284,25 +299,25 @@ static uint32_t hist_blocks(uint32_t n) {
     return b;
 }
 
-// Mask of the digit of the last pass of a num_bits sort.
-static uint32_t top_mask(uint32_t num_bits) {
-    const uint32_t b = num_bits - 8u * (passes_for_bits(num_bits) - 1u);
-    return (1u << b) - 1u;
-}
-
 hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits,
                             bool begin) {
-    const uint32_t blocks = hist_blocks(n), top = top_mask(num_bits);
+    const Digits L = digits_for(num_bits, n);
+    const uint32_t blocks = hist_blocks(n), top = (1u << L.top_bits) - 1u;
     const Begin bg = make_begin(c, begin, n, num_bits);
+    uint32_t* part = c->hist_part;
     tbeg(c, KID_HIST);
-    switch (passes_for_bits(num_bits)) {
-        case 1: k_hist_keys<1><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
-        case 2: k_hist_keys<2><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
-        case 3: k_hist_keys<3><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
-        default: k_hist_keys<4><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, c->hist_part, bg); break;
+    if (L.bits == kWideDigitBits) {  // 17..20 bits: two passes
+        k_hist_keys<2, kWideDigitBits><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, part, bg);
+    } else {
+        switch (L.passes) {
+            case 1: k_hist_keys<1, 8><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, part, bg); break;
+            case 2: k_hist_keys<2, 8><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, part, bg); break;
+            case 3: k_hist_keys<3, 8><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, part, bg); break;
+            default: k_hist_keys<4, 8><<<blocks, kHistThreads, 0, c->stream>>>(keys, n, top, part, bg); break;
+        }
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits));
+    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, L.passes << L.bits);
     tend(c, KID_HIST);
     return e;
 }
@@ -310,20 +325,24 @@ hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
                             uint32_t* keys_out, uint32_t* vals_out, bool begin) {
-    const uint32_t blocks = hist_blocks(n), top = num_bits ? top_mask(num_bits) : 0u;
+    const Digits L = digits_for(num_bits, n);
+    const uint32_t blocks = hist_blocks(n), top = num_bits ? (1u << L.top_bits) - 1u : 0u;
     const Begin bg = make_begin(c, begin, n, num_bits);
     uint32_t* part = c->hist_part;
     tbeg(c, KID_HASH);
-    switch (passes_for_bits(num_bits)) {
-        case 0: k_hash_hist<0><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
-        case 1: k_hash_hist<1><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
-        case 2: k_hash_hist<2><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
-        case 3: k_hash_hist<3><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
-        default: k_hash_hist<4><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+    if (num_bits > 0 && L.bits == kWideDigitBits) {
+        k_hash_hist<2, kWideDigitBits><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg);
+    } else {
+        switch (L.passes) {
+            case 0: k_hash_hist<0, 8><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+            case 1: k_hash_hist<1, 8><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+            case 2: k_hash_hist<2, 8><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+            case 3: k_hash_hist<3, 8><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+            default: k_hash_hist<4, 8><<<blocks, kHistThreads, 0, c->stream>>>(x, y, z, stride, n, g, top, keys_out, vals_out, part, bg); break;
+        }
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && num_bits > 0)
-        e = launch_hist_reduce(c, blocks, passes_for_bits(num_bits));
+    if (e == hipSuccess && num_bits > 0) e = launch_hist_reduce(c, blocks, L.passes << L.bits);
     tend(c, KID_HASH);
     return e;
 }
@@ -376,18 +395,19 @@ __device__ __forceinline__ PassBufs pass_bufs(SortIO io, uint32_t plan, uint32_t
     return b;
 }
 
-// Branch-free 64-lane match of an 8-bit digit: bit l of the result is set iff lane l holds the
+// Branch-free 64-lane match of a DB-bit digit: bit l of the result is set iff lane l holds the
 // same digit.  m is 0 or all ones per lane (sign-extended digit bit); ~(ballot ^ m) keeps the
 // lanes that agree with this lane on that bit.
 // Per bit: one signed bit-field extract (m), one compare writing the ballot, and one 3-input
 // bitwise op per half (acc & ~(ballot ^ m), truth table 0x90 over (acc, ballot, m)): 4 VALU
 // per bit.  Left to itself the compiler re-associates the chain into xors and or3s and derives
 // the compare from a separate shift (6 per bit).
-__device__ __forceinline__ void match8(uint32_t d, uint32_t& lo, uint32_t& hi) {
+template <int DB>
+__device__ __forceinline__ void match_digit(uint32_t d, uint32_t& lo, uint32_t& hi) {
     lo = 0xFFFFFFFFu;
     hi = 0xFFFFFFFFu;
 #pragma unroll
-    for (int b = 0; b < 8; b++) {
+    for (int b = 0; b < DB; b++) {
         // m is produced by an opaque v_bfe_i32 so the ballot compares it with zero directly
         // (otherwise the compiler derives the condition with a separate shift).
         uint32_t m;
@@ -431,17 +451,85 @@ __device__ __forceinline__ void load_vals(const uint32_t* __restrict__ vin, uint
     }
 }
 
+// Look-back words of one tile for the DPT digits a thread owns, all with status `st`: one
+// 32-bit word, or -- two digits per thread -- both words in one 64-bit store, so that the pair
+// always carries one status and a single walk serves both digits (and the wave's loads stay
+// contiguous: lane l reads bytes 8l .. 8l + 7 of the tile's row).
+template <int DPT>
+__device__ __forceinline__ void lb_publish(uint32_t* w, uint32_t st, const uint32_t (&v)[DPT]) {
+    static_assert(DPT == 1 || DPT == 2, "one or two digits per thread");
+    if constexpr (DPT == 1) {
+        __hip_atomic_store(w, st | v[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __hip_atomic_store((uint64_t*)w, (uint64_t)(st | v[0]) | ((uint64_t)(st | v[1]) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Windowed decoupled look-back of tile `tile` (> 0) for the thread's digits, whose words are
+// w[t * NB] for tile t: the words of the kLbWin tiles below `t` are loaded together (one round
+// trip instead of kLbWin), then consumed nearest first: aggregates are summed into prefix until
+// an inclusive prefix ends the walk; a word not yet published stops the window and is polled
+// again.  Tiles below 0 are never read (tile 0 publishes inclusive); a bounded poll keeps every
+// wave finite and raises the device error flag instead.
+template <int DPT>
+__device__ __forceinline__ void lb_walk(const uint32_t* __restrict__ w, uint32_t NB, uint32_t tile,
+                                        uint32_t (&prefix)[DPT], Control* ctl) {
+    using Word = typename std::conditional<DPT == 1, uint32_t, uint64_t>::type;
+    uint32_t t = tile, spins = 0;  // the walk continues at tile t - 1
+    for (;;) {
+        Word x[kLbWin];
+#pragma unroll
+        for (int j = 0; j < kLbWin; j++)
+            x[j] = t > (uint32_t)j ? __hip_atomic_load((const Word*)(w + (size_t)(t - 1u - j) * NB),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : (Word)0;
+        uint32_t adv = 0;
+        bool done = false, stop = false;
+#pragma unroll
+        for (int j = 0; j < kLbWin; j++) {
+            const uint32_t st = (uint32_t)x[j] & (3u << 30);
+            if (!stop && !done && t > (uint32_t)j && st != 0u) {
+                prefix[0] += (uint32_t)x[j] & 0x3FFFFFFFu;
+                if constexpr (DPT == 2) prefix[1] += (uint32_t)(x[j] >> 32) & 0x3FFFFFFFu;
+                adv++;
+                done = st == kLb32Inclusive;
+            } else {
+                stop = true;
+            }
+        }
+        if (done) break;
+        t -= adv;
+        if (t == 0) {  // tile 0 always publishes inclusive; never walk below it
+            atomicOr(&ctl->error.v, 2u);
+            break;
+        }
+        if (adv == 0) {
+            if (++spins >= kSpinLimit) {
+                atomicOr(&ctl->error.v, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+}
+
 // Items = keys per thread: a tile holds Items * kSortThreads keys (kSortItems for small sorts,
 // kSortItemsLarge from kSortLargeN keys on: longer per-digit runs in the scatter and half as
-// many look-back words per key, at two workgroups per CU).
-template <int Items>
+// many look-back words per key, at two workgroups per CU).  DB = digit bits: 2^DB bins; in the
+// per-digit phases thread t owns digits t * DPT .. t * DPT + DPT - 1 (the first 256 threads,
+// one digit each, for 8-bit digits; every thread, two digits each, for 10-bit ones).
+template <int Items, int DB>
 __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB) void k_onesweep(
     SortIO io, Control* ctl, uint32_t pass, uint32_t* __restrict__ lookback, uint32_t n,
     uint32_t shift, uint32_t pbits) {
     constexpr uint32_t kTile = (uint32_t)(Items * kSortThreads);
+    constexpr uint32_t NB = 1u << DB;
+    constexpr int DPT = NB > (uint32_t)kSortThreads ? (int)(NB / kSortThreads) : 1;
+    constexpr uint32_t kOwners = NB / DPT;  // threads that own digits
     __shared__ uint32_t s_buf[kTile];
-    __shared__ uint32_t s_wcnt[kSortWaves][256];  // per-wave digit counts, then wave offsets
-    __shared__ uint32_t s_gbase[256];             // global index of tile slot 0 of digit d
+    __shared__ uint32_t s_wcnt[kSortWaves][NB];  // per-wave digit counts, then wave offsets
+    __shared__ uint32_t s_gbase[NB];             // global index of tile slot 0 of digit d
     __shared__ uint32_t s_scan[kSortWaves];
     __shared__ uint32_t s_tile;
     __shared__ uint32_t s_triv;
@@ -451,7 +539,7 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     if (io.plan_in_wg) {  // uniform
         if (tid == 0) s_triv = 0u;
         __syncthreads();
-        plan = sort_plan(ctl, io.passes, n, io.in_place != 0u, &s_triv);
+        plan = sort_plan(ctl, io.passes, NB, n, io.in_place != 0u, &s_triv);
         if (pass == 0u && blockIdx.x == 0u && tid == 0) ctl->plan = plan;  // for k_sort_finish
     } else {
         plan = ctl->plan;
@@ -462,7 +550,7 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
 
     const uint32_t mask = (1u << pbits) - 1u;
     if (tid == 0) s_tile = atomicAdd(&ctl->tile_ctr[pass].v, 1u);
-    for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_wcnt[0][0])[i] = 0u;
+    for (int i = tid; i < kSortWaves * (int)NB; i += kSortThreads) (&s_wcnt[0][0])[i] = 0u;
     __syncthreads();
     const uint32_t tile = s_tile;
     const uint32_t tile_base = tile * kTile;
@@ -482,7 +570,7 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     for (int k = 0; k < Items; k++) {
         const uint32_t d = (keys[k] >> shift) & mask;
         uint32_t lo, hi;
-        match8(d, lo, hi);
+        match_digit<DB>(d, lo, hi);
         const uint32_t before = s_wcnt[wave][d];
         pos[k] = before + (uint32_t)(__popc(lo & lt_lo) + __popc(hi & lt_hi));
         if (((lo & gt_lo) | (hi & gt_hi)) == 0u)  // highest lane of its digit group
@@ -493,32 +581,58 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     }
     __syncthreads();
 
-    // Per digit (threads 0..255): tile count, published at once as this tile's aggregate;
-    // wave offsets; tile-local digit start; global digit start.
-    const uint32_t d = (uint32_t)tid & 255u;
-    uint32_t cnt = 0, wc[kSortWaves];
-    if (tid < 256) {
+    // Per owned digit: tile count, published at once as this tile's aggregate; wave offsets;
+    // tile-local digit start; global digit start.
+    const bool owner = (uint32_t)tid < kOwners;
+    const uint32_t d0 = (uint32_t)tid * DPT;
+    uint32_t cnt[DPT], wc[DPT][kSortWaves], tsum = 0;
 #pragma unroll
-        for (int w = 0; w < kSortWaves; w++) {
-            wc[w] = s_wcnt[w][d];
-            cnt += wc[w];
+    for (int k = 0; k < DPT; k++) {
+        cnt[k] = 0u;
+        if (owner) {
+#pragma unroll
+            for (int w = 0; w < kSortWaves; w++) {
+                wc[k][w] = s_wcnt[w][d0 + k];
+                cnt[k] += wc[k][w];
+            }
         }
-        __hip_atomic_store(lookback + (size_t)tile * 256u + d,
-                           (tile == 0 ? kLb32Inclusive : kLb32Aggregate) | cnt,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        tsum += cnt[k];
     }
+    if (owner) lb_publish<DPT>(lookback + (size_t)tile * NB + d0,
+                               tile == 0 ? kLb32Inclusive : kLb32Aggregate, cnt);
     uint32_t total;
-    const uint32_t dstart = block_exclusive_scan<kSortWaves>(tid < 256 ? cnt : 0u, s_scan, &total);
-    if (tid < 256) {
-        uint32_t run = dstart;
+    uint32_t dstart[DPT];
+    {
+        uint32_t run = block_exclusive_scan<kSortWaves>(owner ? tsum : 0u, s_scan, &total);
 #pragma unroll
-        for (int w = 0; w < kSortWaves; w++) {
-            s_wcnt[w][d] = run;
-            run += wc[w];
+        for (int k = 0; k < DPT; k++) {
+            dstart[k] = run;
+            if (owner) {
+                uint32_t r = run;
+#pragma unroll
+                for (int w = 0; w < kSortWaves; w++) {
+                    s_wcnt[w][d0 + k] = r;
+                    r += wc[k][w];
+                }
+            }
+            run += cnt[k];
         }
     }
-    const uint32_t ghist = (tid < 256 && d <= mask) ? ctl->hist[pass][d] : 0u;
-    const uint32_t gstart = block_exclusive_scan<kSortWaves>(ghist, s_scan, &total);
+    uint32_t gstart[DPT];
+    {
+        uint32_t gh[DPT], gsum = 0;
+#pragma unroll
+        for (int k = 0; k < DPT; k++) {
+            gh[k] = (owner && d0 + k <= mask) ? ctl->hist[pass * NB + d0 + k] : 0u;
+            gsum += gh[k];
+        }
+        uint32_t run = block_exclusive_scan<kSortWaves>(gsum, s_scan, &total);
+#pragma unroll
+        for (int k = 0; k < DPT; k++) {
+            gstart[k] = run;
+            run += gh[k];
+        }
+    }
 
     // Stage the keys in tile-local digit order (that needs only this tile's counts; the scan's
     // barriers published the wave offsets) and issue the value loads, so both overlap the
@@ -535,52 +649,20 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
 #pragma unroll
     for (int k = 0; k < Items; k++) skey[k] = s_buf[k * kSortThreads + tid];
 
-    uint32_t prefix = 0;
-    if (tid < 256 && tile > 0) {
-        // Windowed look-back: the words of the kLbWin tiles below `t` are loaded together (one
-        // round trip instead of kLbWin), then consumed nearest first: aggregates are summed
-        // until an inclusive prefix ends the walk; a word not yet published stops the window
-        // and is polled again.  Tiles below 0 are never read (tile 0 publishes inclusive).
-        uint32_t t = tile, spins = 0;  // the walk continues at tile t - 1
-        for (;;) {
-            uint32_t w[kLbWin];
+    uint32_t prefix[DPT];
 #pragma unroll
-            for (int j = 0; j < kLbWin; j++)
-                w[j] = t > (uint32_t)j
-                           ? __hip_atomic_load(lookback + (size_t)(t - 1u - j) * 256u + d,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : 0u;
-            uint32_t adv = 0;
-            bool done = false, stop = false;
+    for (int k = 0; k < DPT; k++) prefix[k] = 0u;
+    if (owner && tile > 0) {
+        lb_walk<DPT>(lookback + d0, NB, tile, prefix, ctl);
+        uint32_t inc[DPT];
 #pragma unroll
-            for (int j = 0; j < kLbWin; j++) {
-                const uint32_t st = w[j] & (3u << 30);
-                if (!stop && !done && t > (uint32_t)j && st != 0u) {
-                    prefix += w[j] & 0x3FFFFFFFu;
-                    adv++;
-                    done = st == kLb32Inclusive;
-                } else {
-                    stop = true;
-                }
-            }
-            if (done) break;
-            t -= adv;
-            if (t == 0) {  // tile 0 always publishes inclusive; never walk below it
-                atomicOr(&ctl->error.v, 2u);
-                break;
-            }
-            if (adv == 0) {
-                if (++spins >= kSpinLimit) {
-                    atomicOr(&ctl->error.v, 1u);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        __hip_atomic_store(lookback + (size_t)tile * 256u + d, kLb32Inclusive | (prefix + cnt),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < DPT; k++) inc[k] = prefix[k] + cnt[k];
+        lb_publish<DPT>(lookback + (size_t)tile * NB + d0, kLb32Inclusive, inc);
     }
-    if (tid < 256) s_gbase[d] = gstart + prefix - dstart;
+    if (owner) {
+#pragma unroll
+        for (int k = 0; k < DPT; k++) s_gbase[d0 + k] = gstart[k] + prefix[k] - dstart[k];
+    }
     __syncthreads();
 
     // Scatter the keys (contiguous runs per digit), then the values through the same buffer.
@@ -619,8 +701,9 @@ __global__ __launch_bounds__(256) void k_sort_finish(SortIO io, const Control* c
 
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits, uint32_t* rank) {
-    const uint32_t passes = passes_for_bits(num_bits);
-    const bool large = n >= kSortLargeN;
+    const Digits L = digits_for(num_bits, n);
+    const uint32_t passes = L.passes, nb = 1u << L.bits;
+    const bool large = n >= kSortLargeN;  // (10-bit digits only below kSortLargeN)
     const uint32_t tiles = ceil_div(n, (uint32_t)(large ? kSortTileLarge : kSortTile));
     const bool in_place = kfin != nullptr && kfin == k0;
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
@@ -628,20 +711,23 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
               large ? 0u : 1u};
     if (large) {
-        k_sort_plan<<<1, 256, 0, c->stream>>>(passes, n, in_place ? 1u : 0u, c->ctl);
+        k_sort_plan<<<1, 256, 0, c->stream>>>(passes, nb, n, in_place ? 1u : 0u, c->ctl);
         const hipError_t e0 = hipGetLastError();
         if (e0 != hipSuccess) return e0;
     }
     for (uint32_t p = 0; p < passes; p++) {
-        const uint32_t pbits = min(8u, num_bits - 8u * p);
-        uint32_t* lb = c->sort_lb + (size_t)p * tiles * 256u;
+        const uint32_t shift = L.bits * p, pbits = min(L.bits, num_bits - shift);
+        uint32_t* lb = c->sort_lb + (size_t)p * tiles * nb;
         tbeg(c, KID_SORT);
-        if (large)
-            k_onesweep<kSortItemsLarge><<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb,
-                                                                               n, 8u * p, pbits);
+        if (L.bits == kWideDigitBits)
+            k_onesweep<kSortItems, kWideDigitBits><<<tiles, kSortThreads, 0, c->stream>>>(
+                io, c->ctl, p, lb, n, shift, pbits);
+        else if (large)
+            k_onesweep<kSortItemsLarge, 8><<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb,
+                                                                                  n, shift, pbits);
         else
-            k_onesweep<kSortItems><<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb, n,
-                                                                          8u * p, pbits);
+            k_onesweep<kSortItems, 8><<<tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb, n,
+                                                                             shift, pbits);
         tend(c, KID_SORT);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -145,6 +145,16 @@ class HashGrid:
 
 
 class RadixSorter:
+    # Keys of 17..20 bits below this many pairs are sorted in two 10-bit passes, all others in
+    # 8-bit passes (the library's digits_for).
+    WIDE_BELOW_N = 1 << 22
+
+    @staticmethod
+    def digit_layout(num_bits: int, n: int) -> tuple[int, int]:
+        """(digit bits, passes) of a num_bits sort of n pairs."""
+        db = 10 if 16 < num_bits <= 20 and n < RadixSorter.WIDE_BELOW_N else 8
+        return db, (num_bits + db - 1) // db
+
     def __init__(self, max_n: int, device: int = 0, ctx: Context | None = None):
         self.max_n = int(max_n)
         self.ctx = ctx or default_context(self.max_n, 1, device)

@@ -129,7 +129,7 @@ int fh_sort_pairs(fh_ctx* ctx, uint32_t* keys, uint32_t* vals, uint32_t n, uint3
  * threads) race and must not be issued.  Errors: 0 / <0 / >0 as everywhere, message in
  * fh_last_error(). */
 #define FH_NOALLOC_MAX_N 1048576u
-#define FH_NOALLOC_SCRATCH_BYTES 18358272u
+#define FH_NOALLOC_SCRATCH_BYTES 19939328u
 int fh_sort_pairs_noalloc(void* stream, uint32_t* keys, uint32_t* vals, uint32_t n,
                           uint32_t num_bits);
 

@@ -53,7 +53,10 @@ def test_radix_sort_xorshift_streams(fh, gpu_ctx, oracle, name):
 @pytest.mark.parametrize("n,bits", [(0, 8), (1, 32), (2, 1), (3, 5), (4095, 12), (4096, 16),
                                     (4097, 20), (65537, 8), (100_000, 7), (100_000, 32),
                                     (1 << 20, 20), (1_000_003, 24), (2_500_000, 31),
-                                    (1 << 22, 32), (5_000_011, 19)])
+                                    (1 << 22, 32), (5_000_011, 19),
+                                    # 10-bit digits (17..20 bits below 4,194,304 keys)
+                                    (8192, 17), (8193, 18), (70_000, 17), (300_000, 19),
+                                    (1_000_003, 20), (4_194_303, 20)])
 def test_sort_matches_oracle(fh, gpu_ctx, oracle, n, bits):
     rng = np.random.default_rng(n * 131 + bits)
     keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)  # high bits beyond num_bits too
@@ -99,11 +102,33 @@ def test_sort_skips_identity_passes(fh, gpu_ctx, oracle, case):
     assert np.array_equal(k, ok) and np.array_equal(v, ov)
 
 
+@pytest.mark.parametrize("case", ["all_equal", "low_digit_constant", "high_digit_constant",
+                                  "two_values", "low_only"])
+def test_sort_skips_identity_passes_wide(fh, gpu_ctx, oracle, case):
+    """The same for 20-bit sorts, which run two 10-bit passes: an identity pass is skipped and
+    the other one (in place) still leaves the stable sort in the caller's arrays."""
+    n = 200_000
+    rng = np.random.default_rng(13)
+    r = rng.integers(0, 1024, n).astype(np.uint32)
+    keys = {"all_equal": np.full(n, 0xBEEF5, np.uint32),
+            "low_digit_constant": (r << 10) | 0x155,
+            "high_digit_constant": r | (0x2AB << 10),
+            "two_values": np.where(r < 512, 0x3FF, 0xFFC00).astype(np.uint32),
+            "low_only": r}[case]
+    keys = keys | (rng.integers(0, 4096, n).astype(np.uint32) << 20)  # bits above num_bits
+    vals = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    print(f"sort wide skip case {case}", flush=True)
+    k, v = gpu_sort(fh, gpu_ctx, keys, vals, 20)
+    ok, ov = oracle.stable_sort_pairs(keys, vals, 20)
+    assert np.array_equal(k, ok) and np.array_equal(v, ov)
+
+
 def test_sort_back_to_back_sizes(fh, gpu_ctx, oracle):
     """Consecutive sorts of different sizes on one context (look-back words are re-zeroed)."""
     rng = np.random.default_rng(5)
     for n, bits in [(1_000_000, 24), (10_000, 32), (4_200_000, 32), (300_000, 16), (8193, 9),
-                    (4_194_304, 17), (1_000_000, 24)]:
+                    (4_194_304, 17), (1_000_000, 20), (2_000_000, 24), (50_000, 18),
+                    (1_000_000, 24)]:
         keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
         vals = np.arange(n, dtype=np.uint32)
         k, v = gpu_sort(fh, gpu_ctx, keys, vals, bits)

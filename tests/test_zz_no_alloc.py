@@ -26,7 +26,8 @@ def _sort_ctx(fh, ctx, keys, vals, n, bits):
 
 
 @pytest.mark.parametrize("first,second", [((1_048_576, 32), (70_001, 20)),
-                                          ((300_000, 24), (12_345, 7))])
+                                          ((300_000, 24), (12_345, 7)),
+                                          ((1_048_576, 20), (4097, 18))])
 def test_noalloc_sort_equals_fh_sort_pairs(fh, gpu_ctx, first, second):
     lib = fh.load()
     max_n = 1_048_576
