@@ -184,6 +184,9 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
+    if (e == hipSuccess)
+        e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);
+    if (e == hipSuccess) e = alloc(&c->lstream_t, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess) e = alloc(&c->cell_grp, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->big, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
     if (e == hipSuccess) e = alloc(&c->skip_tag, (size_t)ceil_div(max_n, 64u), &tot);
@@ -244,7 +247,7 @@ int fh_destroy(fh_ctx* c) {
     }
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
-                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hist_part,
+                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->lstream, c->lstream_t, c->hist_part,
                     c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout,
                     c->sidx2};
     for (void* b : bufs)

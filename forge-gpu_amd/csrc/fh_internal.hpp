@@ -65,6 +65,11 @@ constexpr uint32_t kGroupHits = 4;
 // The heavy SPH work list is split into kHeavyLists sub-lists with counters on separate lines,
 // so that appends from different workgroups do not serialise on one address.
 constexpr int kHeavyLists = 8;
+// A light item's candidate stream as the density pass leaves it for the force pass: per lane
+// and row, (stream start << 16 | count), then the sorted indices of the first two windows'
+// staging slots (192 each).  Streams longer than two windows (~2 % of c3's light items) are
+// rebuilt by the force pass.
+constexpr uint32_t kLightCacheWords = 3 * 64 + 2 * 192;
 #ifndef FH_PLAN_THREADS
 #define FH_PLAN_THREADS 512
 #endif
@@ -182,6 +187,10 @@ struct fh_ctx {
     uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
     uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
+    uint32_t* lstream;   // [3 * ceil(max_n / 64)][kLightCacheWords] light items' candidate streams
+                         // (lane intervals and window indices) from the density pass, reused by
+                         // the force pass
+    uint32_t* lstream_t; // [3 * ceil(max_n / 64)] stream length of each light item
     uint64_t* cell_grp;  // [max_cells] epoch << 32 | number of co-located leading particles
     uint2* big;          // [ceil(max_n / 64) + 1] (first slot, sample offset) of group cells
     uint32_t* skip_tag;  // [ceil(max_n / 64)] epoch of the rebuild whose sub-tile holds only group members

@@ -640,6 +640,8 @@ __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[
     return r;
 }
 
+static_assert(kLightCacheWords == 3 * kWave + 2 * kWin, "light stream cache layout");
+
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
 // Light items hold no co-located group (the plan sends those to the heavy list).
 __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restrict__ spos,
@@ -650,7 +652,9 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
                                                          uint32_t stride, uint32_t items,
                                                          const uint8_t* __restrict__ flag,
                                                          const uint32_t* __restrict__ skip_tag,
-                                                         const Control* __restrict__ ctl) {
+                                                         const Control* __restrict__ ctl,
+                                                         uint32_t* __restrict__ lstream,
+                                                         uint32_t* __restrict__ lstream_t) {
     __shared__ float4 s_p[kTileP / kWave][kWin];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t item = xcd_chunked(blockIdx.x, gridDim.x) * (kTileP / kWave) + (uint32_t)wave;
@@ -665,11 +669,23 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
     LightStream L;
     light_stream(L, b, e, home_row(ci, g), in, lane);
+    // the stream for the force pass (kLightCacheWords): short streams only
+    const bool keep = L.T <= 2u * kWin;  // uniform
+    uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
+    if (lane == 0) lstream_t[item] = L.T;
+    if (keep) {
+#pragma unroll
+        for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
+    }
     float4* buf = s_p[wave];
     float acc = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
         window_indices(L, w0, lane, j);
+        if (keep) {
+#pragma unroll
+            for (int k = 0; k < kWinLoads; k++) lc[3 * kWave + w0 + k * kWave + lane] = j[k];
+        }
         float4 v[kWinLoads];
 #pragma unroll
         for (int k = 0; k < kWinLoads; k++) v[k] = spos[j[k]];
@@ -1075,7 +1091,9 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
                                                        uint32_t stride, uint32_t items,
                                                        const uint8_t* __restrict__ flag,
                                                        const uint32_t* __restrict__ skip_tag,
-                                                       const Control* __restrict__ ctl) {
+                                                       const Control* __restrict__ ctl,
+                                                       const uint32_t* __restrict__ lstream,
+                                                       const uint32_t* __restrict__ lstream_t) {
     __shared__ float4 s_p[kTileP / kWave][kWin];  // x, y, z, p_j
     __shared__ float4 s_v[kTileP / kWave][kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1091,17 +1109,35 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     const float rho_i = load_or(srho, s, in, 0.0f);
     const bool live = in && !(rho_i < 1e-6f);  // sph_fused.rs:550
     const float p_i = K.k * (rho_i - K.rho0);
-    const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
-    uint32_t b[3], e[3];
-    slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
+    // the candidate stream the density pass left (short streams), else rebuilt
     LightStream L;
-    light_stream(L, b, e, home_row(ci, g), in, lane);
+    L.T = lstream_t[item];
+    const bool kept = L.T <= 2u * kWin;  // uniform
+    const uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
+    if (kept) {
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const uint32_t v = lc[r * kWave + lane];
+            L.S[r] = v >> 16;
+            L.cnt[r] = v & 0xFFFFu;
+        }
+    } else {
+        const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
+        uint32_t b[3], e[3];
+        slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
+        light_stream(L, b, e, home_row(ci, g), in, lane);
+    }
     float4* bp = s_p[wave];
     float4* bv = s_v[wave];
     float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
-        window_indices(L, w0, lane, j);
+        if (kept) {
+#pragma unroll
+            for (int k = 0; k < kWinLoads; k++) j[k] = lc[3 * kWave + w0 + k * kWave + lane];
+        } else {
+            window_indices(L, w0, lane, j);
+        }
         float4 q[kWinLoads], w[kWinLoads];
 #pragma unroll
         for (int k = 0; k < kWinLoads; k++) {
@@ -1430,7 +1466,8 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     tbeg(c, KID_DENSITY);
     k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->skeys, a.n, a.g, cell_start,
                                                    a.h * a.h, c->dpart, c->max_n, items,
-                                                   c->heavy_flag, c->skip_tag, c->ctl);
+                                                   c->heavy_flag, c->skip_tag, c->ctl,
+                                                   c->lstream, c->lstream_t);
     tend(c, KID_DENSITY);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c, kSideDensity);  // joined even after a failed launch
@@ -1482,7 +1519,7 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, c->skeys,
                                                  a.n, a.g, cell_start, K, c->fpart, c->wpart,
                                                  c->max_n, items, c->heavy_flag, c->skip_tag,
-                                                 c->ctl);
+                                                 c->ctl, c->lstream, c->lstream_t);
     tend(c, KID_FORCE);
     if (e == hipSuccess) e = hipGetLastError();
     const hipError_t j = join_side(c, kSideForce);
