@@ -514,7 +514,8 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                                           uint8_t* __restrict__ flag,
                                           uint32_t* __restrict__ heavy, uint32_t heavy_cap,
                                           uint32_t heavy_work, uint32_t direct_mode,
-                                          Control* ctl) {
+                                          Control* ctl, uint32_t* __restrict__ lstream,
+                                          uint32_t* __restrict__ lstream_t) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
     __shared__ uint32_t s_count[kWaves];
@@ -540,16 +541,33 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                 const bool touches = __ballot(excess > 0u) != 0ull;
                 bool hv = w > heavy_work || touches;  // light items hold no group
                 bool trans = direct_mode == 2u;
+                LightStream L;
+                L.T = ~0u;  // no stream built
                 if (direct_mode == 1u) {
                     // a light item only when its stream is far longer (pathologically
-                    // disjoint ranges: one window would serve one lane at a time)
-                    const uint32_t T = stream_total(b, e, home_row(ci, g), live, lane);
+                    // disjoint ranges: one window would serve one lane at a time); the stream
+                    // of a light candidate is built in full, for the passes to reuse
+                    if (!hv) light_stream(L, b, e, home_row(ci, g), live, lane);
+                    const uint32_t T = hv ? stream_total(b, e, home_row(ci, g), live, lane) : L.T;
                     trans = hv ? T > kTransRatio * w + kTransOffset
                                : T > kTransLightRatio * w + kTransLightOffset;
                 }
                 hv = hv || trans;
+                const uint32_t item = sub * 3u + (uint32_t)slab;
+                if (!hv && L.T <= 2u * kWin) {  // uniform: the light stream for both passes
+                    uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
+#pragma unroll
+                    for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
+                    for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // uniform
+                        uint32_t j[kWinLoads];
+                        window_indices(L, w0, lane, j);
+#pragma unroll
+                        for (int k = 0; k < kWinLoads; k++)
+                            lc[3 * kWave + w0 + k * kWave + lane] = j[k];
+                    }
+                }
                 if (lane == 0) {
-                    const uint32_t item = sub * 3u + (uint32_t)slab;
+                    lstream_t[item] = hv ? ~0u : L.T;
                     flag[item] = hv ? kItemHeavy : kItemLight;
                     if (hv)
                         s_item[wave * 3 + (int)nh] =
@@ -593,13 +611,13 @@ __global__ __launch_bounds__(kPlanThreads) void k_group_plan(
     uint64_t* __restrict__ cell_grp, float4* __restrict__ vrep, uint32_t* __restrict__ skip_tag,
     GridDesc g, const uint64_t* __restrict__ cand_tag, uint8_t* __restrict__ flag,
     uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t heavy_work, uint32_t direct_mode,
-    Control* ctl) {
+    Control* ctl, uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t) {
     if (blockIdx.x < kGroupBlocks)
         group_work(blockIdx.x, kGroupBlocks, big, cap, n, skeys, cstart, spos, svel, sidx, rank,
                    scratch, cell_grp, vrep, skip_tag, ctl);
     else
         plan_work(blockIdx.x - kGroupBlocks, skeys, n, g, cstart, cand_tag, flag, heavy,
-                  heavy_cap, heavy_work, direct_mode, ctl);
+                  heavy_cap, heavy_work, direct_mode, ctl, lstream, lstream_t);
 }
 
 // The heavy work lists of this substep as one sequence: entry q of the concatenation of the
@@ -664,27 +682,45 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool in = s < n;
     const float4 pi = load_or(spos, s, in, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
-    const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
-    uint32_t b[3], e[3];
-    slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
+    // the candidate stream the plan built (short streams), else built here and, when short,
+    // kept for the force pass (kLightCacheWords)
     LightStream L;
-    light_stream(L, b, e, home_row(ci, g), in, lane);
-    // the stream for the force pass (kLightCacheWords): short streams only
-    const bool keep = L.T <= 2u * kWin;  // uniform
+    L.T = lstream_t[item];
+    const bool kept = L.T <= 2u * kWin;  // uniform
+    bool keep = false;
     uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
-    if (lane == 0) lstream_t[item] = L.T;
-    if (keep) {
+    if (kept) {
 #pragma unroll
-        for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
+        for (int r = 0; r < 3; r++) {
+            const uint32_t v = lc[r * kWave + lane];
+            L.S[r] = v >> 16;
+            L.cnt[r] = v & 0xFFFFu;
+        }
+    } else {
+        const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
+        uint32_t b[3], e[3];
+        slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
+        light_stream(L, b, e, home_row(ci, g), in, lane);
+        keep = L.T <= 2u * kWin;  // uniform
+        if (lane == 0) lstream_t[item] = L.T;
+        if (keep) {
+#pragma unroll
+            for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
+        }
     }
     float4* buf = s_p[wave];
     float acc = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
-        window_indices(L, w0, lane, j);
-        if (keep) {
+        if (kept) {
 #pragma unroll
-            for (int k = 0; k < kWinLoads; k++) lc[3 * kWave + w0 + k * kWave + lane] = j[k];
+            for (int k = 0; k < kWinLoads; k++) j[k] = lc[3 * kWave + w0 + k * kWave + lane];
+        } else {
+            window_indices(L, w0, lane, j);
+            if (keep) {
+#pragma unroll
+                for (int k = 0; k < kWinLoads; k++) lc[3 * kWave + w0 + k * kWave + lane] = j[k];
+            }
         }
         float4 v[kWinLoads];
 #pragma unroll
@@ -1446,7 +1482,7 @@ hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
                                 c->cell_grp, c->vrep, c->skip_tag, a.g, c->run_tag,
                                 c->heavy_flag, c->heavy, c->heavy_cap,
                                 c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode,
-                                c->ctl);
+                                c->ctl, c->lstream, c->lstream_t);
     tend(c, KID_PLAN);
     return hipGetLastError();
 }
