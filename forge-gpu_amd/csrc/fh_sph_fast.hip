@@ -13,7 +13,11 @@
 // concatenates the rows of all its segments into one candidate stream and copies it, kWin
 // (192) candidates at a time, into its own LDS slice with coalesced 16-byte loads (no workgroup
 // barrier); every lane then evaluates the intervals of its own rows that fall in the window
-// (fh_stream.hpp, shared with the neighbour query of fh_grid.hip).
+// (fh_stream.hpp, shared with the neighbour query of fh_grid.hip).  The plan builds each light
+// item's stream once (the lanes' intervals and the first two windows' staging indices,
+// kLightCacheWords) and both passes read it back; the few longer streams are rebuilt by each
+// pass.  Light workgroups are renumbered so that runs of kXcdChunk consecutive items share one
+// XCD's L2 (neighbouring sub-tiles read mostly the same cells).
 //
 // Heavy items (k_density_heavy, k_force_heavy).  An item whose particles face more than
 // kHeavyWork (384) candidates in the slab, or that touches a co-located group, is listed by the
