@@ -608,7 +608,9 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
 // the cells that may hold a group (tagged by k_cell_starts), not their outcome, and every
 // particle of a cell gives the cell's neighbour ranges whether or not it has been moved yet.
 constexpr uint32_t kGroupBlocks = 64;
-__global__ __launch_bounds__(kPlanThreads) void k_group_plan(
+// 8 waves per SIMD (64 registers, a few spilled): the plan mostly waits on its cell-range loads
+// and the shuffles of the stream build, so occupancy pays more than the registers.
+__global__ __launch_bounds__(kPlanThreads, 8) void k_group_plan(
     const uint2* __restrict__ big, uint32_t cap, uint32_t n, const uint32_t* __restrict__ skeys,
     const uint32_t* __restrict__ cstart, float4* __restrict__ spos, float4* __restrict__ svel,
     uint32_t* __restrict__ sidx, uint32_t* __restrict__ rank, uint32_t* __restrict__ scratch,
