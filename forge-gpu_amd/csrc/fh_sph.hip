@@ -90,36 +90,42 @@ __device__ __forceinline__ void cell_starts_slot(uint32_t s, const uint32_t* __r
     }
     fill_cells(cell_start, lo, hi, s, lane);
     fill_cells(cell_start, lo2, hi2, n, lane);
-    if (cand) {  // rare: a run of at least kCollapseMin
+    // Rare: a run of at least kCollapseMin.  The whole wave takes each such run of its lanes in
+    // turn: lane q < kGroupSamples loads sample q (one round trip for all 16); the middle sample
+    // is tried first as the group's position, then each other in turn (a corner group can fill
+    // all but the middle of a run).
+    uint64_t todo = __ballot(cand);
+    while (todo) {  // uniform
+        const int l = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1ull;
+        const uint32_t rs = (uint32_t)__builtin_amdgcn_readlane((int)s, l);
+        const uint32_t rk = (uint32_t)__builtin_amdgcn_readlane((int)k, l);
         uint32_t L = kCollapseMin;
-        while (L < (1u << 30) && s + 2u * L - 1u < n && skeys[s + 2u * L - 1u] == k) L *= 2u;
-        // The samples are loaded once; the middle one is tried first as the group's position,
-        // then each other in turn (a corner group can fill all but the middle of a run).
-        uint32_t sx[kGroupSamples], sy[kGroupSamples], sz[kGroupSamples];
-#pragma unroll
-        for (uint32_t q = 0; q < kGroupSamples; q++) {
-            const float4 v = pos(s + (q * L) / kGroupSamples);
-            sx[q] = __float_as_uint(v.x);
-            sy[q] = __float_as_uint(v.y);
-            sz[q] = __float_as_uint(v.z);
+        while (L < (1u << 30) && rs + 2u * L - 1u < n && skeys[rs + 2u * L - 1u] == rk) L *= 2u;
+        uint32_t px = 0, py = 0, pz = 0;
+        if ((uint32_t)lane < kGroupSamples) {
+            const float4 v = pos(rs + ((uint32_t)lane * L) / kGroupSamples);
+            px = __float_as_uint(v.x);
+            py = __float_as_uint(v.y);
+            pz = __float_as_uint(v.z);
         }
         uint32_t off = 0, hits = 0;
-#pragma unroll
-        for (uint32_t a = 0; a < kGroupSamples; a++) {
+        for (uint32_t a = 0; a < kGroupSamples; a++) {  // uniform
             const uint32_t qa = a == 0u ? kGroupSamples / 2u : (a <= kGroupSamples / 2u ? a - 1u : a);
-            uint32_t hq = 0;
-#pragma unroll
-            for (uint32_t q = 0; q < kGroupSamples; q++)
-                hq += (sx[q] == sx[qa] && sy[q] == sy[qa] && sz[q] == sz[qa]) ? 1u : 0u;
+            const uint32_t ax = (uint32_t)__builtin_amdgcn_readlane((int)px, (int)qa);
+            const uint32_t ay = (uint32_t)__builtin_amdgcn_readlane((int)py, (int)qa);
+            const uint32_t az = (uint32_t)__builtin_amdgcn_readlane((int)pz, (int)qa);
+            const uint32_t hq = (uint32_t)__popcll(__ballot((uint32_t)lane < kGroupSamples &&
+                                                            px == ax && py == ay && pz == az));
             if (hits < kGroupHits) {
                 hits = hq;
                 off = (qa * L) / kGroupSamples;
             }
         }
-        if (hits >= kGroupHits) {
+        if (hits >= kGroupHits && lane == 0) {
             const uint32_t slot = atomicAdd(&ctl->big_count.v, 1u);
-            if (slot < cap) big[slot] = make_uint2(s, off);
-            cand_tag[k] = (uint64_t)ctl->epoch << 32;  // the plan: this cell may hold a group
+            if (slot < cap) big[slot] = make_uint2(rs, off);
+            cand_tag[rk] = (uint64_t)ctl->epoch << 32;  // the plan: this cell may hold a group
         }
     }
 }
