@@ -503,6 +503,10 @@ __device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
     return out;
 }
 
+// Below this many particles the plan leaves the light streams to the density pass: the
+// plan's waves then run in one round, so the stream build would lengthen it one for one.
+constexpr uint32_t kPlanStreamMinN = 1u << 18;
+
 // Plan, beside the co-located groups (the group part, which tags particles f+1 .. f+M-1 of a grouped
 // cell in spos[s].w with their representative f, f itself with kRepFlag | M, and marks the
 // sub-tiles made only of such non-representative particles in skip_tag: both passes skip them,
@@ -551,8 +555,9 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                     // a light item only when its stream is far longer (pathologically
                     // disjoint ranges: one window would serve one lane at a time); the stream
                     // of a light candidate is built in full, for the passes to reuse
-                    if (!hv) light_stream(L, b, e, home_row(ci, g), live, lane);
-                    const uint32_t T = hv ? stream_total(b, e, home_row(ci, g), live, lane) : L.T;
+                    const bool build = !hv && n >= kPlanStreamMinN;  // uniform
+                    if (build) light_stream(L, b, e, home_row(ci, g), live, lane);
+                    const uint32_t T = build ? L.T : stream_total(b, e, home_row(ci, g), live, lane);
                     trans = hv ? T > kTransRatio * w + kTransOffset
                                : T > kTransLightRatio * w + kTransLightOffset;
                 }
