@@ -168,6 +168,9 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->vb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)c->max_sort_tiles * kDigitSlots, &tot);
     if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)kHistBlocks * kDigitSlots, &tot);
+    if (e == hipSuccess)
+        e = alloc(&c->sort_pre,
+                  ((size_t)c->max_sort_tiles + ceil_div(c->max_sort_tiles, 4u)) * 1024u, &tot);
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
     if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);
@@ -247,7 +250,7 @@ int fh_destroy(fh_ctx* c) {
     }
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
-                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->lstream, c->lstream_t, c->hist_part,
+                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->lstream, c->lstream_t, c->hist_part, c->sort_pre,
                     c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout,
                     c->sidx2};
     for (void* b : bufs)

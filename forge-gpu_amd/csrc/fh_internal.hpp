@@ -171,6 +171,9 @@ struct fh_ctx {
     uint32_t* vb;        // [max_n]
     uint32_t* sort_lb;   // [max_sort_tiles * kDigitSlots] 32-bit look-back words (pass-major)
     uint32_t* hist_part; // [kHistBlocks][kDigitSlots] per-block digit histograms
+    uint32_t* sort_pre;  // first-pass tile prefixes of small sorts: [max_sort_tiles][1024] within
+                         // groups of 4 tiles, then [ceil(max_sort_tiles / 4)][1024] group sums
+                         // (null: the first pass looks back like the others)
     fh::Control* ctl;    // device control block
     // grid scratch
     uint64_t* run_tag;     // [max_cells] epoch << 32 | first sorted index of the cell's run

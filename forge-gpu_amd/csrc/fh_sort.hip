@@ -234,15 +234,33 @@ __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
 // agent-scope release on this part writes the L2 back, which costs tens of microseconds per
 // workgroup; the decision about the passes is a separate one-workgroup kernel, the kernel
 // boundary gives the visibility.)
+// First-pass prefixes (pre != null: a small sort, whose histogram rows are its 4096-key chunks,
+// two per 8192-key tile): for the first pass's digits (slots < nb0), this workgroup's rows are
+// the 4 tiles 4g .. 4g+3, and it also writes each tile's exclusive prefix within them,
+// pre[t * nb0 + d], and their sum, pre[(tiles + g) * nb0 + d].  The first pass of the sort then
+// takes its tiles' global prefixes from these instead of a look-back across the tiles.
+static_assert(kSortTile == 2 * kHistChunk && kHistRowsPerReduce == 8,
+              "first-pass prefixes: two histogram chunks per tile, four tiles per reduce group");
 __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict__ part,
                                                      uint32_t rows, uint32_t slot_blocks,
-                                                     Control* ctl) {
-    const uint32_t b = blockIdx.x % slot_blocks, r0 = (blockIdx.x / slot_blocks) * kHistRowsPerReduce;
+                                                     Control* ctl, uint32_t* __restrict__ pre,
+                                                     uint32_t nb0, uint32_t tiles) {
+    const uint32_t b = blockIdx.x % slot_blocks, g = blockIdx.x / slot_blocks;
+    const uint32_t r0 = g * kHistRowsPerReduce;
     const uint32_t slot = b * 256u + threadIdx.x;
     const uint32_t r1 = min(rows, r0 + (uint32_t)kHistRowsPerReduce);
     uint32_t s = 0;
+    if (pre && slot < nb0) {  // uniform per workgroup (nb0 is a multiple of 256)
 #pragma unroll 8
-    for (uint32_t r = r0; r < r1; r++) s += part[(size_t)r * kDigitSlots + slot];
+        for (uint32_t r = r0; r < r1; r++) {
+            if (!((r - r0) & 1u)) pre[(size_t)(r >> 1) * nb0 + slot] = s;
+            s += part[(size_t)r * kDigitSlots + slot];
+        }
+        pre[((size_t)tiles + g) * nb0 + slot] = s;
+    } else {
+#pragma unroll 8
+        for (uint32_t r = r0; r < r1; r++) s += part[(size_t)r * kDigitSlots + slot];
+    }
     if (s) atomicAdd(&ctl->hist[slot], s);
 }
 
@@ -284,11 +302,19 @@ __global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t nb,
     if (threadIdx.x == 0) ctl->plan = plan;
 }
 
-hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots) {
+// The first-pass prefix buffer of a sort of n keys, or null (large sorts, whose histogram
+// workgroups take several chunks each, and contexts without the buffer).
+static uint32_t* first_pass_pre(fh_ctx* c, uint32_t n) {
+    return n < kSortLargeN ? c->sort_pre : nullptr;
+}
+
+hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots, uint32_t n,
+                              uint32_t nb0) {
     const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
     const uint32_t slot_blocks = slots / 256u;  // slots = passes * bins, bins >= 256
-    k_hist_reduce<<<groups * slot_blocks, 256, 0, c->stream>>>(c->hist_part, rows, slot_blocks,
-                                                               c->ctl);
+    k_hist_reduce<<<groups * slot_blocks, 256, 0, c->stream>>>(
+        c->hist_part, rows, slot_blocks, c->ctl, first_pass_pre(c, n), nb0,
+        ceil_div(n, (uint32_t)kSortTile));
     return hipGetLastError();
 }
 
@@ -317,7 +343,7 @@ hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_
         }
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, L.passes << L.bits);
+    if (e == hipSuccess) e = launch_hist_reduce(c, blocks, L.passes << L.bits, n, 1u << L.bits);
     tend(c, KID_HIST);
     return e;
 }
@@ -342,7 +368,8 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
         }
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && num_bits > 0) e = launch_hist_reduce(c, blocks, L.passes << L.bits);
+    if (e == hipSuccess && num_bits > 0)
+        e = launch_hist_reduce(c, blocks, L.passes << L.bits, n, 1u << L.bits);
     tend(c, KID_HASH);
     return e;
 }
@@ -366,6 +393,8 @@ struct SortIO {
     uint32_t passes;     // passes of the sort
     uint32_t in_place;
     uint32_t plan_in_wg; // 1: every workgroup derives the plan; 0: k_sort_plan wrote ctl->plan
+    const uint32_t* pre; // first-pass tile prefixes (k_hist_reduce), or null
+    uint32_t tiles;      // tiles of a pass (the group sums follow them in pre)
 };
 
 struct PassBufs {
@@ -598,8 +627,10 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
         }
         tsum += cnt[k];
     }
-    if (owner) lb_publish<DPT>(lookback + (size_t)tile * NB + d0,
-                               tile == 0 ? kLb32Inclusive : kLb32Aggregate, cnt);
+    const bool precomputed = pass == 0u && io.pre != nullptr;  // uniform
+    if (owner && !precomputed)
+        lb_publish<DPT>(lookback + (size_t)tile * NB + d0,
+                        tile == 0 ? kLb32Inclusive : kLb32Aggregate, cnt);
     uint32_t total;
     uint32_t dstart[DPT];
     {
@@ -652,7 +683,18 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     uint32_t prefix[DPT];
 #pragma unroll
     for (int k = 0; k < DPT; k++) prefix[k] = 0u;
-    if (owner && tile > 0) {
+    if (owner && tile > 0 && precomputed) {
+        // the first pass reads the input order: the tile's prefix within its group of 4 tiles
+        // plus the sums of the groups before it (k_hist_reduce)
+#pragma unroll
+        for (int k = 0; k < DPT; k++) prefix[k] = io.pre[(size_t)tile * NB + d0 + k];
+        const uint32_t groups = tile >> 2;
+#pragma unroll 8
+        for (uint32_t q = 0; q < groups; q++)
+#pragma unroll
+            for (int k = 0; k < DPT; k++)
+                prefix[k] += io.pre[((size_t)io.tiles + q) * NB + d0 + k];
+    } else if (owner && tile > 0) {
         lb_walk<DPT>(lookback + d0, NB, tile, prefix, ctl);
         uint32_t inc[DPT];
 #pragma unroll
@@ -709,7 +751,7 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
-              large ? 0u : 1u};
+              large ? 0u : 1u, large ? nullptr : first_pass_pre(c, n), tiles};
     if (large) {
         k_sort_plan<<<1, 256, 0, c->stream>>>(passes, nb, n, in_place ? 1u : 0u, c->ctl);
         const hipError_t e0 = hipGetLastError();
