@@ -7,7 +7,9 @@
 //   k_hist_keys /  one read of the keys builds the digit histograms of ALL passes into
 //   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
 //                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
-//   k_hist_reduce  sums the partial rows into the histograms
+//   k_hist_reduce  sums the partial rows into the histograms; for small sorts also the first
+//                  pass's tile prefixes (its input order is the rows' order), so that pass
+//                  needs no look-back
 //   sort_plan      decides which passes run (a pass whose digit is equal for every key is the
 //                  identity and is skipped): k_sort_plan for large sorts, in every workgroup
 //                  of every pass for small ones
