@@ -161,24 +161,32 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
                                              uint32_t jb, uint32_t je, float4 pi, float h2,
                                              float acc) {
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    uint32_t j = jb;
-    for (; j + 4 <= je; j += 4) {
-        const float4 q0 = sp[j - c0], q1 = sp[j + 1 - c0], q2 = sp[j + 2 - c0], q3 = sp[j + 3 - c0];
-        float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
-        float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
-        a0 = fmaf(d * d, d, a0);
-        dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
-        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
-        a1 = fmaf(d * d, d, a1);
-        dx = pi.x - q2.x; dy = pi.y - q2.y; dz = pi.z - q2.z;
-        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
-        a2 = fmaf(d * d, d, a2);
-        dx = pi.x - q3.x; dy = pi.y - q3.y; dz = pi.z - q3.z;
-        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
-        a3 = fmaf(d * d, d, a3);
+    // pointer-stepped: one address and one compare per four candidates.  Callers may pass an
+    // empty range with je < jb (a lane whose range ends before the chunk): the count is clamped
+    // at 0, since je - c0 would wrap around.
+    const float4* p = sp + (jb - c0);
+    const float4* const pe = p + (je > jb ? je - jb : 0u);
+    const float4* const pu = pe - 3;  // p < pu: four more candidates
+    if (p < pu) {
+        do {
+            const float4 q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
+            float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
+            float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+            a0 = fmaf(d * d, d, a0);
+            dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
+            d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+            a1 = fmaf(d * d, d, a1);
+            dx = pi.x - q2.x; dy = pi.y - q2.y; dz = pi.z - q2.z;
+            d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+            a2 = fmaf(d * d, d, a2);
+            dx = pi.x - q3.x; dy = pi.y - q3.y; dz = pi.z - q3.z;
+            d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+            a3 = fmaf(d * d, d, a3);
+            p += 4;
+        } while (p < pu);
     }
-    for (; j < je; j++) {
-        const float4 q = sp[j - c0];
+    for (; p < pe; p++) {
+        const float4 q = *p;
         const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
         const float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a0 = fmaf(d * d, d, a0);
@@ -383,18 +391,23 @@ __device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, ui
                                                uint32_t jb, uint32_t je, float4 pi, float h2,
                                                float acc) {
     float a0 = 0.0f, a1 = 0.0f;
-    uint32_t j = jb;
-    for (; j + 2 <= je; j += 2) {
-        const float4 q0 = sp[j - c0], q1 = sp[j + 1 - c0];
-        float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
-        float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
-        a0 = fmaf(q0.w * d, d * d, a0);
-        dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
-        d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
-        a1 = fmaf(q1.w * d, d * d, a1);
+    const float4* p = sp + (jb - c0);
+    const float4* const pe = p + (je > jb ? je - jb : 0u);  // empty when je <= jb
+    const float4* const pu = pe - 1;  // p < pu: two more candidates
+    if (p < pu) {
+        do {
+            const float4 q0 = p[0], q1 = p[1];
+            float dx = pi.x - q0.x, dy = pi.y - q0.y, dz = pi.z - q0.z;
+            float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+            a0 = fmaf(q0.w * d, d * d, a0);
+            dx = pi.x - q1.x; dy = pi.y - q1.y; dz = pi.z - q1.z;
+            d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
+            a1 = fmaf(q1.w * d, d * d, a1);
+            p += 2;
+        } while (p < pu);
     }
-    if (j < je) {
-        const float4 q = sp[j - c0];
+    if (p < pe) {
+        const float4 q = *p;
         const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
         const float d = fmaxf(fmaf(-dz, dz, fmaf(-dy, dy, fmaf(-dx, dx, h2))), 0.0f);
         a0 = fmaf(q.w * d, d * d, a0);
@@ -950,9 +963,12 @@ __global__ __launch_bounds__(HW * kWave) void k_density_heavy(
                 __builtin_amdgcn_wave_barrier();
                 buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
                 __builtin_amdgcn_wave_barrier();
-                if (mine)
-                    acc = density_run_w(buf, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m),
-                                        pi, h2, acc);
+                if (mine) {
+                    const uint32_t jb = max(pick3(b, r), c0), je = min(pick3(e, r), c0 + m);
+                    // candidate weights other than 1 only in items that touch a group
+                    acc = cut ? density_run_w(buf, c0, jb, je, pi, h2, acc)
+                              : density_run(buf, c0, jb, je, pi, h2, acc);
+                }
                 t += HW;
                 r = nr;
                 c0 = nc0;
@@ -1037,16 +1053,18 @@ __device__ __forceinline__ void force_pair(const float4& q, const float4& w, con
                                            float p_i, const FastForce& K, float& ax, float& ay,
                                            float& az, float& wa) {
     const float dx = pi.x - q.x, dy = pi.y - q.y, dz = pi.z - q.z;
-    const float r2 = fmaf(dz, dz, fmaf(dy, dy, dx * dx));
+    // r^2 + 1e-30: identical for every pair that passes the test (r^2 > 1e-12), and never 0, so
+    // 1/r stays finite and a rejected pair's zeroed (h - r) zeroes its pressure factor as well
+    // (one select instead of two)
+    const float r2 = fmaf(dz, dz, fmaf(dy, dy, fmaf(dx, dx, 1e-30f)));
     const bool ok = r2 < K.h2 && r2 > 1e-12f;
     // The empty asm pins 1/r as computed for every candidate: otherwise the compiler moves the
     // reciprocal square root and the products behind a divergent branch on the pair test, whose
-    // exec-mask bookkeeping costs more than the two selects (10% of k_force_wave on c3).
+    // exec-mask bookkeeping costs more than the select (10% of k_force_wave on c3).
     float rinv = __builtin_amdgcn_rsqf(r2);
     asm volatile("" : "+v"(rinv));
-    const float diff = fmaf(-r2, rinv, K.h);
-    const float fs = ok ? (fmaf(p_i, w.w, q.w) * diff) * (diff * rinv) : 0.0f;
-    const float vs = ok ? diff : 0.0f;
+    const float vs = ok ? fmaf(-r2, rinv, K.h) : 0.0f;
+    const float fs = (fmaf(p_i, w.w, q.w) * vs) * (vs * rinv);
     wa = fmaf(vs, w.w, wa);
     ax = fmaf(vs, w.x, fmaf(fs, dx, ax));
     ay = fmaf(vs, w.y, fmaf(fs, dy, ay));
@@ -1060,20 +1078,29 @@ __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
                                           uint32_t jb, uint32_t je, float4 pi, float p_i,
                                           const FastForce& K, float& ax, float& ay, float& az,
                                           float& wv) {
-    uint32_t j = jb;
+    // pointer-stepped: the loop keeps one address and one compare per U candidates; empty when
+    // je <= jb (je may lie before the chunk, where je - c0 would wrap around)
+    const float4* p = sp + (jb - c0);
+    const float4* v = sv + (jb - c0);
+    const float4* const pe = p + (je > jb ? je - jb : 0u);
     if (U > 1) {
-        for (; j + U <= je; j += U) {
-            float4 q[U], w[U];
+        const float4* const pu = pe - (U - 1);  // p < pu: U more candidates
+        if (p < pu) {
+            do {
+                float4 q[U], w[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                q[u] = sp[j + u - c0];
-                w[u] = sv[j + u - c0];
-            }
+                for (int u = 0; u < U; u++) {
+                    q[u] = p[u];
+                    w[u] = v[u];
+                }
 #pragma unroll
-            for (int u = 0; u < U; u++) force_pair(q[u], w[u], pi, p_i, K, ax, ay, az, wv);
+                for (int u = 0; u < U; u++) force_pair(q[u], w[u], pi, p_i, K, ax, ay, az, wv);
+                p += U;
+                v += U;
+            } while (p < pu);
         }
     }
-    for (; j < je; j++) force_pair(sp[j - c0], sv[j - c0], pi, p_i, K, ax, ay, az, wv);
+    for (; p < pe; p++, v++) force_pair(*p, *v, pi, p_i, K, ax, ay, az, wv);
 }
 
 // Transposed force walk of the item's particles taken by this wave: in the lane of each such
