@@ -187,6 +187,10 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
+    // partial sums of the heavy parts: per list slot, 8 parts x 4 components x 64 lanes
+    if (e == hipSuccess)
+        e = alloc(&c->hpart, (size_t)kHeavyLists * c->heavy_cap * 8u * 4u * 64u, &tot);
+    if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess)
         e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);
     if (e == hipSuccess) e = alloc(&c->lstream_t, 3 * (size_t)ceil_div(max_n, 64u), &tot);
@@ -250,7 +254,8 @@ int fh_destroy(fh_ctx* c) {
     }
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
                     c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
-                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->lstream, c->lstream_t, c->hist_part, c->sort_pre,
+                    c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hpart, c->hslot, c->lstream, c->lstream_t, c->hist_part,
+                    c->sort_pre,
                     c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout,
                     c->sidx2};
     for (void* b : bufs)

@@ -190,6 +190,8 @@ struct fh_ctx {
     uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
     uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
+    float* hpart;        // heavy work partials: per heavy-list slot, 8 parts x 4 x 64 floats
+    uint32_t* hslot;     // [3 * ceil(max_n / 64)] heavy list slot of each heavy item
     uint32_t* lstream;   // [3 * ceil(max_n / 64)][kLightCacheWords] light items' candidate streams
                          // (lane intervals and window indices) from the density pass, reused by
                          // the force pass

@@ -124,6 +124,8 @@ constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transpose
 // Item flags (the plan): light (one wavefront), heavy (heavy list), every particle co-located
 // (skipped by both passes).
 constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
+// hslot[item]: the heavy list slot of a heavy item (where its partial sums are), else kNoSlot.
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
 // Transposed heavy items: the particles' candidate ranges overlap little (sparse particles
 // spread along a row beside a dense one), so the union of a segment's ranges -- what the shared
 // walk stages and every lane steps through -- is many times longer than any one particle's
@@ -536,7 +538,8 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                                           uint32_t* __restrict__ heavy, uint32_t heavy_cap,
                                           uint32_t heavy_work, uint32_t direct_mode,
                                           Control* ctl, uint32_t* __restrict__ lstream,
-                                          uint32_t* __restrict__ lstream_t) {
+                                          uint32_t* __restrict__ lstream_t,
+                                          uint32_t* __restrict__ hslot) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
     __shared__ uint32_t s_count[kWaves];
@@ -591,6 +594,7 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                 if (lane == 0) {
                     lstream_t[item] = hv ? ~0u : L.T;
                     flag[item] = hv ? kItemHeavy : kItemLight;
+                    if (!hv) hslot[item] = kNoSlot;
                     if (hv)
                         s_item[wave * 3 + (int)nh] =
                             item | (touches ? kCutFlag : 0u) | (trans ? kTransFlag : 0u);
@@ -615,8 +619,10 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
         for (int v = 0; v < w; v++) off += s_count[v];
         if ((uint32_t)k < s_count[w]) {
             const uint32_t pos = s_base + off + (uint32_t)k;
-            if (pos < heavy_cap)
-                heavy[(size_t)(bid % kHeavyLists) * heavy_cap + pos] = s_item[w * 3 + k];
+            const uint32_t ent = s_item[w * 3 + k];
+            const uint32_t slot = (bid % kHeavyLists) * heavy_cap + pos;
+            if (pos < heavy_cap) heavy[slot] = ent;
+            hslot[ent & ~(kCutFlag | kTransFlag)] = pos < heavy_cap ? slot : kNoSlot;
         }
     }
 }
@@ -635,13 +641,14 @@ __global__ __launch_bounds__(kPlanThreads, 8) void k_group_plan(
     uint64_t* __restrict__ cell_grp, float4* __restrict__ vrep, uint32_t* __restrict__ skip_tag,
     GridDesc g, const uint64_t* __restrict__ cand_tag, uint8_t* __restrict__ flag,
     uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t heavy_work, uint32_t direct_mode,
-    Control* ctl, uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t) {
+    Control* ctl, uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
+    uint32_t* __restrict__ hslot) {
     if (blockIdx.x < kGroupBlocks)
         group_work(blockIdx.x, kGroupBlocks, big, cap, n, skeys, cstart, spos, svel, sidx, rank,
                    scratch, cell_grp, vrep, skip_tag, ctl);
     else
         plan_work(blockIdx.x - kGroupBlocks, skeys, n, g, cstart, cand_tag, flag, heavy,
-                  heavy_cap, heavy_work, direct_mode, ctl, lstream, lstream_t);
+                  heavy_cap, heavy_work, direct_mode, ctl, lstream, lstream_t, hslot);
 }
 
 // The heavy work lists of this substep as one sequence: entry q of the concatenation of the
@@ -686,20 +693,17 @@ static_assert(kLightCacheWords == 3 * kWave + 2 * kWin, "light stream cache layo
 
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
 // Light items hold no co-located group (the plan sends those to the heavy list).
-__global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restrict__ spos,
-                                                         const uint32_t* __restrict__ skeys,
-                                                         uint32_t n, GridDesc g,
-                                                         const uint32_t* __restrict__ cstart,
-                                                         float h2, float* __restrict__ dpart,
-                                                         uint32_t stride, uint32_t items,
-                                                         const uint8_t* __restrict__ flag,
-                                                         const uint32_t* __restrict__ skip_tag,
-                                                         const Control* __restrict__ ctl,
-                                                         uint32_t* __restrict__ lstream,
-                                                         uint32_t* __restrict__ lstream_t) {
-    __shared__ float4 s_p[kTileP / kWave][kWin];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t item = xcd_chunked(blockIdx.x, gridDim.x) * (kTileP / kWave) + (uint32_t)wave;
+__device__ __forceinline__ void density_light(uint32_t item, int lane, float4* buf,
+                                              const float4* __restrict__ spos,
+                                              const uint32_t* __restrict__ skeys, uint32_t n,
+                                              GridDesc g, const uint32_t* __restrict__ cstart,
+                                              float h2, float* __restrict__ dpart,
+                                              uint32_t stride, uint32_t items,
+                                              const uint8_t* __restrict__ flag,
+                                              const uint32_t* __restrict__ skip_tag,
+                                              const Control* __restrict__ ctl,
+                                              uint32_t* __restrict__ lstream,
+                                              uint32_t* __restrict__ lstream_t) {
     if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
@@ -732,7 +736,6 @@ __global__ __launch_bounds__(kTileP) void k_density_wave(const float4* __restric
             for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
         }
     }
-    float4* buf = s_p[wave];
     float acc = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
@@ -905,86 +908,154 @@ __device__ __forceinline__ void seg_plans(RowPlan R[3], const CellXYZ& ci, const
 }
 
 
+// One virtual wave (`wave` of HW) of heavy entry `entry`: its partial density sums (chunks
+// wave, wave + HW, ... of each segment row; the transposed walk's lanes trans_lanes(wave, HW)).
+// False when the item is skipped (only group members).
 template <int HW>
-__global__ __launch_bounds__(HW * kWave) void k_density_heavy(
-    const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
-    const uint32_t* __restrict__ cstart,
-    const uint64_t* __restrict__ cell_grp, float h2, float* __restrict__ dpart, uint32_t stride,
-    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const uint32_t* __restrict__ skip_tag,
-    const Control* __restrict__ ctl) {
-    __shared__ float4 s_p[HW][kWave];
-    __shared__ float s_acc[HW][kSub];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
+__device__ __forceinline__ bool density_heavy_wave(
+    uint32_t entry, int wave, int lane, float4* buf, const float4* __restrict__ spos,
+    const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
+    const uint32_t* __restrict__ skip_tag, uint32_t epoch, float& out) {
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float4* buf = s_p[wave];
-    for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
-        const uint32_t entry = heavy_entry(heavy, ctl, heavy_cap, it);
-        const bool cut = (entry & kCutFlag) != 0u;  // the item touches a co-located group
-        const bool trans = (entry & kTransFlag) != 0u;
-        const uint32_t item = entry & ~(kCutFlag | kTransFlag);
-        const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
-        if (skip_tag[sub] == epoch) continue;  // uniform: only group members
-        const uint32_t s = sub * kSub + (uint32_t)lane;
-        const bool live = s < n;
-        const float4 pi = load_or(spos, s, live, z4);
-        const CellXYZ ci = key_xyz(load_or(skeys, s, live, 0u), g);
-        uint32_t b[3], e[3];
-        slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
-        const uint32_t hr = home_row(ci, g);
-        float acc = 0.0f;
-        if (trans)  // members take their representative's density
-            acc = density_trans(spos, b, e, pi, live && !is_member(__float_as_uint(pi.w), s),
-                                h2, trans_lanes(wave, HW), lane);
-        uint64_t pending = trans ? 0ull : __ballot(live);
-        while (pending) {  // uniform, identical in every wave
-            const int leader = __ffsll((unsigned long long)pending) - 1;
-            const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
-            const bool mine = live && hr == row;
-            const uint64_t seg = __ballot(mine);
-            pending &= ~seg;
-            const int last = 63 - __clzll((long long)seg);
-            RowPlan R[3];
-            seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
-                      lane);
-            // chunks wave, wave + HW, ... of the segment's three rows; the next is fetched
-            // before the current one is evaluated
-            uint32_t t = (uint32_t)wave;
-            int r;
-            uint32_t c0, m;
-            seg_chunk(R, t, r, c0, m);
-            float4 v = r < 3 ? chunk_load(spos, c0, m, lane) : z4;
-            while (r < 3) {  // uniform within the wave
-                int nr;
-                uint32_t nc0, nm;
-                seg_chunk(R, t + HW, nr, nc0, nm);
-                const float4 nv = nr < 3 ? chunk_load(spos, nc0, nm, lane) : z4;
-                const uint32_t j = c0 + (uint32_t)lane;
-                __builtin_amdgcn_wave_barrier();
-                buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
-                __builtin_amdgcn_wave_barrier();
-                if (mine) {
-                    const uint32_t jb = max(pick3(b, r), c0), je = min(pick3(e, r), c0 + m);
-                    // candidate weights other than 1 only in items that touch a group
-                    acc = cut ? density_run_w(buf, c0, jb, je, pi, h2, acc)
-                              : density_run(buf, c0, jb, je, pi, h2, acc);
-                }
-                t += HW;
-                r = nr;
-                c0 = nc0;
-                m = nm;
-                v = nv;
+    const bool cut = (entry & kCutFlag) != 0u;  // the item touches a co-located group
+    const bool trans = (entry & kTransFlag) != 0u;
+    const uint32_t item = entry & ~(kCutFlag | kTransFlag);
+    const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
+    if (skip_tag[sub] == epoch) return false;  // uniform: only group members
+    const uint32_t s = sub * kSub + (uint32_t)lane;
+    const bool live = s < n;
+    const float4 pi = load_or(spos, s, live, z4);
+    const CellXYZ ci = key_xyz(load_or(skeys, s, live, 0u), g);
+    uint32_t b[3], e[3];
+    slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
+    const uint32_t hr = home_row(ci, g);
+    float acc = 0.0f;
+    if (trans)  // members take their representative's density
+        acc = density_trans(spos, b, e, pi, live && !is_member(__float_as_uint(pi.w), s), h2,
+                            trans_lanes(wave, HW), lane);
+    uint64_t pending = trans ? 0ull : __ballot(live);
+    while (pending) {  // uniform, identical in every wave
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
+        const bool mine = live && hr == row;
+        const uint64_t seg = __ballot(mine);
+        pending &= ~seg;
+        const int last = 63 - __clzll((long long)seg);
+        RowPlan R[3];
+        seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
+                  lane);
+        // chunks wave, wave + HW, ... of the segment's three rows; the next is fetched before
+        // the current one is evaluated
+        uint32_t t = (uint32_t)wave;
+        int r;
+        uint32_t c0, m;
+        seg_chunk(R, t, r, c0, m);
+        float4 v = r < 3 ? chunk_load(spos, c0, m, lane) : z4;
+        while (r < 3) {  // uniform within the wave
+            int nr;
+            uint32_t nc0, nm;
+            seg_chunk(R, t + HW, nr, nc0, nm);
+            const float4 nv = nr < 3 ? chunk_load(spos, nc0, nm, lane) : z4;
+            const uint32_t j = c0 + (uint32_t)lane;
+            __builtin_amdgcn_wave_barrier();
+            buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
+            __builtin_amdgcn_wave_barrier();
+            if (mine) {
+                const uint32_t jb = max(pick3(b, r), c0), je = min(pick3(e, r), c0 + m);
+                // candidate weights other than 1 only in items that touch a group
+                acc = cut ? density_run_w(buf, c0, jb, je, pi, h2, acc)
+                          : density_run(buf, c0, jb, je, pi, h2, acc);
             }
+            t += HW;
+            r = nr;
+            c0 = nc0;
+            m = nm;
+            v = nv;
         }
-        s_acc[wave][lane] = acc;
-        __syncthreads();
-        if (wave == 0) {
-            float t = 0.0f;
-            for (int w = 0; w < HW; w++) t += s_acc[w][lane];
-            if (live) dpart[(size_t)slab * stride + s] = t;
-        }
-        __syncthreads();
     }
+    out = acc;
+    return true;
+}
+
+// The heavy work partials: part p of heavy entry slot q (the entry's position in its list)
+// holds, per lane, kHeavyComps floats at hpart[((q * HW + p) * kHeavyComps + c) * 64 + lane].
+constexpr int kHeavyComps = 4;
+__device__ __forceinline__ size_t hpart_at(uint32_t slot, int part, int comp, int lane) {
+    return (((size_t)slot * kHeavyWaves + (uint32_t)part) * kHeavyComps + (uint32_t)comp) * 64u +
+           (uint32_t)lane;
+}
+
+// Heavy entry q of the concatenated lists and its slot (list k, position i: k * cap + i).
+__device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict__ heavy,
+                                                     const Control* __restrict__ ctl,
+                                                     uint32_t cap, uint32_t q, uint32_t& slot) {
+    int k = 0;
+    for (; k < kHeavyLists - 1; k++) {
+        const uint32_t c = min(ctl->heavy_count[k].v, cap);
+        if (q < c) break;
+        q -= c;
+    }
+    slot = (uint32_t)k * cap + q;
+    return heavy[(size_t)k * cap + q];
+}
+
+// Heavy parts of a pass: workgroups 0 .. kHeavyParts - 1 of the pass kernel, one wave each;
+// the kHeavyWaves parts of one heavy entry are workgroups on one XCD (b % 8 is the XCD), so
+// they share its L2: b = (q / 8) * 64 + part * 8 + q % 8 for entries q < kHeavyGrid, and the
+// same workgroup takes q + kHeavyGrid, ... after that.
+constexpr uint32_t kHeavyParts = (uint32_t)kHeavyGrid * kHeavyWaves;
+static_assert(kHeavyWaves == 8 && kHeavyGrid % 8 == 0, "heavy part numbering");
+__device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t& q0, int& part) {
+    q0 = (b >> 6) * 8u + (b & 7u);
+    part = (int)((b >> 3) & 7u);
+}
+
+// Density pass, one launch: heavy parts first (they are the long work), then one light item per
+// wave.  The parts leave their partial sums in hpart; k_heavy_sum adds them in part order.
+__global__ __launch_bounds__(kWave) void k_density_pass(
+    const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
+    float* __restrict__ dpart, uint32_t stride, uint32_t items, const uint8_t* __restrict__ flag,
+    const uint32_t* __restrict__ skip_tag, const Control* __restrict__ ctl,
+    uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, float* __restrict__ hpart) {
+    __shared__ float4 s_p[kWin];
+    const int lane = threadIdx.x;
+    const uint32_t b = blockIdx.x;
+    if (b < kHeavyParts) {  // uniform
+        uint32_t q0;
+        int part;
+        heavy_part_of(b, q0, part);
+        const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
+        for (uint32_t q = q0; q < count; q += kHeavyGrid) {  // uniform
+            uint32_t slot;
+            const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
+            float acc;
+            if (density_heavy_wave<kHeavyWaves>(entry, part, lane, s_p, spos, skeys, n, g, cstart,
+                                                cell_grp, h2, skip_tag, epoch, acc))
+                hpart[hpart_at(slot, part, 0, lane)] = acc;
+        }
+        return;
+    }
+    const uint32_t nl = gridDim.x - kHeavyParts;
+    density_light(xcd_chunked(b - kHeavyParts, nl), lane, s_p, spos, skeys, n, g, cstart, h2,
+                  dpart, stride, items, flag, skip_tag, ctl, lstream, lstream_t);
+}
+
+// A slab partial of particle j: written to its plane (`plane`, already offset to the slab and
+// component) by a light item, or, for a particle of a heavy item (hslot[item] = its list slot),
+// the sum of the item's kHeavyWaves part partials of component `comp` in part order.
+__device__ __forceinline__ float slab_part(const float* __restrict__ plane,
+                                           const uint32_t* __restrict__ hslot,
+                                           const float* __restrict__ hpart, uint32_t slab,
+                                           int comp, uint32_t j) {
+    const uint32_t sl = hslot[(j / kSub) * 3u + slab];
+    if (sl == kNoSlot) return plane[j];
+    float t = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kHeavyWaves; p++) t += hpart[hpart_at(sl, p, comp, j % kSub)];
+    return t;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -996,8 +1067,11 @@ struct FastForce {
 };
 
 __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_t stride,
-                                        uint32_t j, float mc) {
-    return mc * ((dpart[j] + dpart[stride + j]) + dpart[2u * stride + j]);
+                                        uint32_t j, float mc, const uint32_t* __restrict__ hslot,
+                                        const float* __restrict__ hpart) {
+    return mc * ((slab_part(dpart, hslot, hpart, 0u, 0, j) +
+                  slab_part(dpart + stride, hslot, hpart, 1u, 0, j)) +
+                 slab_part(dpart + 2u * stride, hslot, hpart, 2u, 0, j));
 }
 
 // Force records, made once per substep after the density pass (k_prep), one pair per sorted
@@ -1017,7 +1091,9 @@ __global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
                                               const float* __restrict__ dpart, uint32_t n,
                                               uint32_t stride, float mc, float k, float rho0,
                                               float fp, float fv, float* __restrict__ srho,
-                                              float4* __restrict__ rec) {
+                                              float4* __restrict__ rec,
+                                              const uint32_t* __restrict__ hslot,
+                                              const float* __restrict__ hpart) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const float4 p = spos[s];
@@ -1033,7 +1109,7 @@ __global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
         wt = 0.0f;
         u = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    const float rho = rho_of(dpart, stride, r, mc);
+    const float rho = rho_of(dpart, stride, r, mc, hslot, hpart);
     const float inv = rho < 1e-6f ? 0.0f : 1.0f / rho;
     srho[s] = rho;
     const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z);
@@ -1153,26 +1229,21 @@ __device__ __forceinline__ void force_trans(const float4* __restrict__ rec,
 // Acceleration partials: fpart[slab][c][s] = sum over the slab's neighbours j of the pressure
 // and viscosity pair terms (sph_fused.rs:604-623), not yet divided by rho_i.  Same windowed
 // stream as k_density_wave; the window is staged by copying force records (k_prep).
-__global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict__ spos,
-                                                       const float4* __restrict__ svel,
-                                                       const float* __restrict__ srho,
-                                                       const float4* __restrict__ rec,
-                                                       const uint32_t* __restrict__ skeys,
-                                                       uint32_t n, GridDesc g,
-                                                       const uint32_t* __restrict__ cstart,
-                                                       FastForce K, float* __restrict__ fpart,
-                                                       float* __restrict__ wpart,
-                                                       uint32_t stride, uint32_t items,
-                                                       const uint8_t* __restrict__ flag,
-                                                       const uint32_t* __restrict__ skip_tag,
-                                                       const Control* __restrict__ ctl,
-                                                       const uint32_t* __restrict__ lstream,
-                                                       const uint32_t* __restrict__ lstream_t) {
-    __shared__ float4 s_p[kTileP / kWave][kWin];  // x, y, z, p_j
-    __shared__ float4 s_v[kTileP / kWave][kWin];  // u/rho_j, w/rho_j
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t item = xcd_chunked(blockIdx.x, gridDim.x) * (kTileP / kWave) + (uint32_t)wave;
-    if (item >= items || flag[item] != kItemLight) return;  // whole wave; heavy: k_force_heavy
+__device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp, float4* bv,
+                                            const float4* __restrict__ spos,
+                                            const float4* __restrict__ svel,
+                                            const float* __restrict__ srho,
+                                            const float4* __restrict__ rec,
+                                            const uint32_t* __restrict__ skeys, uint32_t n,
+                                            GridDesc g, const uint32_t* __restrict__ cstart,
+                                            const FastForce& K, float* __restrict__ fpart,
+                                            float* __restrict__ wpart, uint32_t stride,
+                                            uint32_t items, const uint8_t* __restrict__ flag,
+                                            const uint32_t* __restrict__ skip_tag,
+                                            const Control* __restrict__ ctl,
+                                            const uint32_t* __restrict__ lstream,
+                                            const uint32_t* __restrict__ lstream_t) {
+    if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
     const uint32_t s = sub * kSub + (uint32_t)lane;
@@ -1201,8 +1272,6 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
         slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
         light_stream(L, b, e, home_row(ci, g), in, lane);
     }
-    float4* bp = s_p[wave];
-    float4* bv = s_v[wave];
     float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
@@ -1246,105 +1315,125 @@ __global__ __launch_bounds__(kTileP) void k_force_wave(const float4* __restrict_
     }
 }
 
+// One virtual wave (`wave` of HW) of heavy entry `entry` in the force pass: its partial
+// acceleration (with the -wv v_i viscosity part, which adds linearly) and viscosity weight.
+// False when the item is skipped (only group members).
 template <int HW>
-__global__ __launch_bounds__(HW * kWave, FH_HMINW) void k_force_heavy(
+__device__ __forceinline__ bool force_heavy_wave(
+    uint32_t entry, int wave, int lane, float4* bp, float4* bv, const float4* __restrict__ spos,
+    const float4* __restrict__ svel, const float* __restrict__ srho,
+    const float4* __restrict__ rec, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp,
+    const FastForce& K, uint32_t stride, const uint32_t* __restrict__ skip_tag, uint32_t epoch,
+    float out[4]) {
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const bool cut = (entry & kCutFlag) != 0u;
+    const bool trans = (entry & kTransFlag) != 0u;
+    const uint32_t item = entry & ~(kCutFlag | kTransFlag);
+    const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
+    if (skip_tag[sub] == epoch) return false;  // uniform: only group members
+    const uint32_t s = sub * kSub + (uint32_t)lane;
+    const bool in = s < n;
+    const float4 pi = load_or(spos, s, in, z4);
+    const float rho_i = load_or(srho, s, in, 0.0f);
+    const bool live = in && !(rho_i < 1e-6f);
+    const float p_i = K.k * (rho_i - K.rho0);
+    const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
+    uint32_t b[3], e[3];
+    slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
+    const uint32_t hr = home_row(ci, g);
+    float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
+    if (trans)  // members are finished from their representative
+        force_trans(rec, spos, stride, b, e, pi, p_i,
+                    live && !is_member(__float_as_uint(pi.w), s), K, trans_lanes(wave, HW), lane,
+                    ax, ay, az, wv);
+    uint64_t pending = trans ? 0ull : __ballot(live);
+    while (pending) {  // uniform, identical in every wave
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
+        const bool mine = live && hr == row;
+        const uint64_t seg = __ballot(mine);
+        pending &= ~seg;
+        const int last = 63 - __clzll((long long)seg);
+        RowPlan R[3];
+        seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
+                  lane);
+        uint32_t t = (uint32_t)wave;
+        int r;
+        uint32_t c0, m;
+        seg_chunk(R, t, r, c0, m);
+        // records of chunk t (lanes past the chunk load a valid index; their slots are never
+        // read), the next chunk's fetched before the current one is evaluated
+        float4 q = load_or(rec, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
+        float4 w = load_or(rec + stride, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
+        while (r < 3) {  // uniform within the wave
+            int nr;
+            uint32_t nc0, nm;
+            seg_chunk(R, t + HW, nr, nc0, nm);
+            const float4 nq = load_or(rec, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
+            const float4 nw = load_or(rec + stride, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
+            __builtin_amdgcn_wave_barrier();
+            bp[lane] = q;
+            bv[lane] = w;
+            __builtin_amdgcn_wave_barrier();
+            if (mine)
+                force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m), pi,
+                                 p_i, K, ax, ay, az, wv);
+            t += HW;
+            r = nr;
+            c0 = nc0;
+            m = nm;
+            q = nq;
+            w = nw;
+        }
+    }
+    // the -wv v_i part of the viscosity sum (wave partials add linearly)
+    wv *= K.fr;
+    const float4 vi = load_or(svel, s, in, z4);
+    out[0] = fmaf(-wv, vi.x, ax);
+    out[1] = fmaf(-wv, vi.y, ay);
+    out[2] = fmaf(-wv, vi.z, az);
+    out[3] = wv;
+    return true;
+}
+
+// Force pass, one launch: heavy parts first, then one light item per wave (as k_density_pass).
+__global__ __launch_bounds__(kWave) void k_force_pass(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
     const float* __restrict__ srho, const float4* __restrict__ rec,
     const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
-    float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
-    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, const uint32_t* __restrict__ skip_tag,
-    const Control* __restrict__ ctl) {
-    __shared__ float4 s_p[HW][kWave];
-    __shared__ float4 s_v[HW][kWave];
-    __shared__ float s_acc[4][HW][kSub];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float4* bp = s_p[wave];
-    float4* bv = s_v[wave];
-    for (uint32_t it = blockIdx.x; it < count; it += gridDim.x) {  // uniform
-        const uint32_t entry = heavy_entry(heavy, ctl, heavy_cap, it);
-        const bool cut = (entry & kCutFlag) != 0u;
-        const bool trans = (entry & kTransFlag) != 0u;
-        const uint32_t item = entry & ~(kCutFlag | kTransFlag);
-        const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
-        if (skip_tag[sub] == epoch) continue;  // uniform: only group members
-        const uint32_t s = sub * kSub + (uint32_t)lane;
-        const bool in = s < n;
-        const float4 pi = load_or(spos, s, in, z4);
-        const float rho_i = load_or(srho, s, in, 0.0f);
-        const bool live = in && !(rho_i < 1e-6f);
-        const float p_i = K.k * (rho_i - K.rho0);
-        const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
-        uint32_t b[3], e[3];
-        slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
-        const uint32_t hr = home_row(ci, g);
-        float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
-        if (trans)  // members are finished from their representative
-            force_trans(rec, spos, stride, b, e, pi, p_i,
-                        live && !is_member(__float_as_uint(pi.w), s), K, trans_lanes(wave, HW),
-                        lane, ax, ay, az, wv);
-        uint64_t pending = trans ? 0ull : __ballot(live);
-        while (pending) {  // uniform, identical in every wave
-            const int leader = __ffsll((unsigned long long)pending) - 1;
-            const uint32_t row = (uint32_t)__shfl((int)hr, leader, kWave);
-            const bool mine = live && hr == row;
-            const uint64_t seg = __ballot(mine);
-            pending &= ~seg;
-            const int last = 63 - __clzll((long long)seg);
-            RowPlan R[3];
-            seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
-                      lane);
-            uint32_t t = (uint32_t)wave;
-            int r;
-            uint32_t c0, m;
-            seg_chunk(R, t, r, c0, m);
-            // records of chunk t (lanes past the chunk load a valid index; their slots are
-            // never read), the next chunk's fetched before the current one is evaluated
-            float4 q = load_or(rec, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
-            float4 w = load_or(rec + stride, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
-            while (r < 3) {  // uniform within the wave
-                int nr;
-                uint32_t nc0, nm;
-                seg_chunk(R, t + HW, nr, nc0, nm);
-                const float4 nq = load_or(rec, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
-                const float4 nw =
-                    load_or(rec + stride, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
-                __builtin_amdgcn_wave_barrier();
-                bp[lane] = q;
-                bv[lane] = w;
-                __builtin_amdgcn_wave_barrier();
-                if (mine)
-                    force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m),
-                                     pi, p_i, K, ax, ay, az, wv);
-                t += HW;
-                r = nr;
-                c0 = nc0;
-                m = nm;
-                q = nq;
-                w = nw;
+    float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride, uint32_t items,
+    const uint8_t* __restrict__ flag, const uint32_t* __restrict__ skip_tag,
+    const Control* __restrict__ ctl, const uint32_t* __restrict__ lstream,
+    const uint32_t* __restrict__ lstream_t, const uint32_t* __restrict__ heavy,
+    uint32_t heavy_cap, float* __restrict__ hpart) {
+    __shared__ float4 s_p[kWin];  // x, y, z, p_j
+    __shared__ float4 s_v[kWin];  // u/rho_j, w/rho_j
+    const int lane = threadIdx.x;
+    const uint32_t b = blockIdx.x;
+    if (b < kHeavyParts) {  // uniform
+        uint32_t q0;
+        int part;
+        heavy_part_of(b, q0, part);
+        const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
+        for (uint32_t q = q0; q < count; q += kHeavyGrid) {  // uniform
+            uint32_t slot;
+            const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
+            float o[4];
+            if (force_heavy_wave<kHeavyWaves>(entry, part, lane, s_p, s_v, spos, svel, srho, rec,
+                                              skeys, n, g, cstart, cell_grp, K, stride, skip_tag,
+                                              epoch, o)) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) hpart[hpart_at(slot, part, c, lane)] = o[c];
             }
         }
-        // the -wv v_i part of the viscosity sum (wave partials add linearly)
-        wv *= K.fr;
-        const float4 vi = load_or(svel, s, in, z4);
-        s_acc[0][wave][lane] = fmaf(-wv, vi.x, ax);
-        s_acc[1][wave][lane] = fmaf(-wv, vi.y, ay);
-        s_acc[2][wave][lane] = fmaf(-wv, vi.z, az);
-        s_acc[3][wave][lane] = wv;
-        __syncthreads();
-        if (wave < 3) {  // wave c reduces component c in wave order
-            float t = 0.0f;
-            for (int w = 0; w < HW; w++) t += s_acc[wave][w][lane];
-            if (in) fpart[((size_t)slab * 3u + (uint32_t)wave) * stride + s] = t;
-        } else if (wave == 3 && in && (__float_as_uint(pi.w) & kRepFlag)) {
-            float t = 0.0f;
-            for (int w = 0; w < HW; w++) t += s_acc[3][w][lane];
-            wpart[(size_t)slab * stride + s] = t;
-        }
-        __syncthreads();
+        return;
     }
+    const uint32_t nl = gridDim.x - kHeavyParts;
+    force_light(xcd_chunked(b - kHeavyParts, nl), lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
+                g, cstart, K, fpart, wpart, stride, items, flag, skip_tag, ctl, lstream,
+                lstream_t);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1369,7 +1458,10 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
                                                   const float* __restrict__ wpart, uint32_t n,
                                                   uint32_t stride, Finish F, bool want_accel,
                                                   float4* __restrict__ sout, GridDesc g,
-                                                  uint32_t* __restrict__ keys_out) {
+                                                  uint32_t* __restrict__ keys_out,
+                                                  const uint32_t* __restrict__ hslot,
+                                                  const float* __restrict__ hpart,
+                                                  const float* __restrict__ srho) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const float4 p = spos[s];
@@ -1379,7 +1471,10 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     const uint32_t wb = __float_as_uint(p.w);
     uint32_t r = (wb & kRepFlag) ? s : wb;
     if (r >= n) r = s;
-    const float rho = rho_of(dpart, stride, r, F.mc);
+    // after a force pass k_prep has left rho (of r) in srho, and the force pass has reused the
+    // heavy parts' partial buffer, so the density partials are summed only when density is all
+    const float rho = (F.flags & kDensityOnly) ? rho_of(dpart, stride, r, F.mc, hslot, hpart)
+                                               : srho[s];
     if (F.flags & kDensityOnly) {
         sout[2u * s] = make_float4(p.x, p.y, p.z, rho);
         return;
@@ -1390,11 +1485,19 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     if (!(rho < 1e-6f)) {
         const float inv = 1.0f / rho;
         const size_t S = stride;
-        float fx = (fpart[r] + fpart[3 * S + r]) + fpart[6 * S + r];
-        float fy = (fpart[S + r] + fpart[4 * S + r]) + fpart[7 * S + r];
-        float fz = (fpart[2 * S + r] + fpart[5 * S + r]) + fpart[8 * S + r];
+        float fx = (slab_part(fpart, hslot, hpart, 0u, 0, r) +
+                    slab_part(fpart + 3 * S, hslot, hpart, 1u, 0, r)) +
+                   slab_part(fpart + 6 * S, hslot, hpart, 2u, 0, r);
+        float fy = (slab_part(fpart + S, hslot, hpart, 0u, 1, r) +
+                    slab_part(fpart + 4 * S, hslot, hpart, 1u, 1, r)) +
+                   slab_part(fpart + 7 * S, hslot, hpart, 2u, 1, r);
+        float fz = (slab_part(fpart + 2 * S, hslot, hpart, 0u, 2, r) +
+                    slab_part(fpart + 5 * S, hslot, hpart, 1u, 2, r)) +
+                   slab_part(fpart + 8 * S, hslot, hpart, 2u, 2, r);
         if (r != s) {
-            const float W = (wpart[r] + wpart[S + r]) + wpart[2 * S + r];
+            const float W = (slab_part(wpart, hslot, hpart, 0u, 3, r) +
+                             slab_part(wpart + S, hslot, hpart, 1u, 3, r)) +
+                            slab_part(wpart + 2 * S, hslot, hpart, 2u, 3, r);
             const float4 vr = svel[r];
             fx = fmaf(W, vr.x - v.x, fx);
             fy = fmaf(W, vr.y - v.y, fy);
@@ -1520,7 +1623,7 @@ hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
                                 c->cell_grp, c->vrep, c->skip_tag, a.g, c->run_tag,
                                 c->heavy_flag, c->heavy, c->heavy_cap,
                                 c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode,
-                                c->ctl, c->lstream, c->lstream_t);
+                                c->ctl, c->lstream, c->lstream_t, c->hslot);
     tend(c, KID_PLAN);
     return hipGetLastError();
 }
@@ -1529,23 +1632,13 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     if (a.n == 0) return hipSuccess;
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
-    hipError_t e = fork_side(c, kSideDensity);
-    if (e != hipSuccess) return e;
-    tbeg(c, KID_DHEAVY, side_of(c, kSideDensity));
-    k_density_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, side_of(c, kSideDensity)>>>(
-        c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
-        c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
-    tend(c, KID_DHEAVY, side_of(c, kSideDensity));
-    e = hipGetLastError();
     tbeg(c, KID_DENSITY);
-    k_density_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->skeys, a.n, a.g, cell_start,
-                                                   a.h * a.h, c->dpart, c->max_n, items,
-                                                   c->heavy_flag, c->skip_tag, c->ctl,
-                                                   c->lstream, c->lstream_t);
+    k_density_pass<<<kHeavyParts + grid, kWave, 0, c->stream>>>(
+        c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
+        items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
+        c->heavy_cap, c->hpart);
     tend(c, KID_DENSITY);
-    if (e == hipSuccess) e = hipGetLastError();
-    const hipError_t j = join_side(c, kSideDensity);  // joined even after a failed launch
-    return e != hipSuccess ? e : j;
+    return hipGetLastError();
 }
 
 
@@ -1571,7 +1664,7 @@ hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
     tbeg(c, KID_PREP);
     k_prep<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
                                                        c->max_n, K.mc, a.k, a.rho0, K.fp, K.fv,
-                                                       c->srho, c->sout);
+                                                       c->srho, c->sout, c->hslot, c->hpart);
     tend(c, KID_PREP);
     return hipGetLastError();
 }
@@ -1581,23 +1674,13 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     const FastForce K = fast_force(a);
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
-    hipError_t e = fork_side(c, kSideForce);
-    if (e != hipSuccess) return e;
-    tbeg(c, KID_FHEAVY, side_of(c, kSideForce));
-    k_force_heavy<kHeavyWaves><<<kHeavyGrid, kHeavyThreads, 0, side_of(c, kSideForce)>>>(
-        c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
-        c->fpart, c->wpart, c->max_n, c->heavy, c->heavy_cap, c->skip_tag, c->ctl);
-    tend(c, KID_FHEAVY, side_of(c, kSideForce));
-    e = hipGetLastError();
     tbeg(c, KID_FORCE);
-    k_force_wave<<<grid, kTileP, 0, c->stream>>>(c->spos, c->svel, c->srho, c->sout, c->skeys,
-                                                 a.n, a.g, cell_start, K, c->fpart, c->wpart,
-                                                 c->max_n, items, c->heavy_flag, c->skip_tag,
-                                                 c->ctl, c->lstream, c->lstream_t);
+    k_force_pass<<<kHeavyParts + grid, kWave, 0, c->stream>>>(
+        c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
+        c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
+        c->lstream_t, c->heavy, c->heavy_cap, c->hpart);
     tend(c, KID_FORCE);
-    if (e == hipSuccess) e = hipGetLastError();
-    const hipError_t j = join_side(c, kSideForce);
-    return e != hipSuccess ? e : j;
+    return hipGetLastError();
 }
 
 // rank[id] = s for the particle id carried in the new state of slot s (sout[2 s + 1].w): the
@@ -1631,7 +1714,8 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     k_finalize<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
                                                            c->wpart, a.n, c->max_n, F,
                                                            accel != nullptr, c->sout, a.g,
-                                                           density_only ? nullptr : next_keys);
+                                                           density_only ? nullptr : next_keys,
+                                                           c->hslot, c->hpart, c->srho);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && to_particles && rebuild_rank) {
         k_rank_of<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->sout, a.n, c->rank);
