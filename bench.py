@@ -45,17 +45,15 @@ for _p in (REPO, REPO / "forge-gpu_amd"):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 METRIC = "SPH particle-steps/s @1M; radix sort Gkeys/s; achieved HBM GB/s vs peak"
-KERNELS = ["hash", "hist", "sort", "gather", "scan", "plan", "density", "density_heavy",
-           "prep", "force", "force_heavy", "finalize"]
+KERNELS = ["hash", "hist", "sort", "gather", "scan", "plan", "density", "prep", "force",
+           "finalize"]
 # A "pass" groups the kernels of one stage of the substep; its duration per substep is the sum
-# of its kernels' launch durations, or its wall time for the two passes whose kernels overlap
-# (the heavy kernels of a pass process the items its light kernel skips, so the pair moves the
-# pass's bytes together).
+# of its kernels' launch durations, or, for the two neighbour passes, its wall time from the
+# pass timers (the density pass: one launch of heavy parts and light items; the force pass:
+# k_prep and that launch).
 PASSES = {"hash": ["hash", "hist"], "sort": ["sort"], "gather": ["gather"], "scan": ["scan"],
-          "plan": ["plan"], "density": ["density", "density_heavy"],
-          "force": ["prep", "force", "force_heavy"], "finalize": ["finalize"]}
-# The density and force passes run their light and heavy kernels concurrently on two streams:
-# their duration is the pass's wall time (first launch to the join), from these timers.
+          "plan": ["plan"], "density": ["density"], "force": ["prep", "force"],
+          "finalize": ["finalize"]}
 PASS_TIMERS = {"density": "density_pass", "force": "force_pass"}
 
 
@@ -246,7 +244,7 @@ def bench_sph(args, fh, torch, log):
     byts = algorithmic_bytes(cfg.n, C, passes, G)
     pas = {}
     for p, ks in PASSES.items():
-        # a pass whose kernels overlap on two streams is timed as a whole (wall time)
+        # the neighbour passes are timed as a whole (wall time)
         us = kern[PASS_TIMERS[p]]["per_substep_us"] if p in PASS_TIMERS else \
             sum(kern[k]["per_substep_us"] for k in ks)
         pas[p] = {"kernels": ks, "per_substep_us": us,
@@ -467,7 +465,7 @@ def bench_sph_c4(args, fh, torch, log):
     ctx.event_record(8)
     ctx.sync()
     ms = ctx.event_elapsed_ms(7, 8) / reps
-    ks = ["density", "density_heavy", "force", "force_heavy"]
+    ks = ["density", "force"]
     for k in ks:
         ctx.time_kernel(k, 1)
     p.step_async(f, cfg.dt)

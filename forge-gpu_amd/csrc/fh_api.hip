@@ -211,9 +211,6 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
             c->own_stream = e == hipSuccess;
         }
     }
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming);
     // One-time clears (outside any capture): look-back words and run tags start untagged
     // (epoch 0 is never current).
     if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)c->max_sort_tiles * kDigitSlots * 4u, c->stream);
@@ -239,7 +236,6 @@ int fh_destroy(fh_ctx* c) {
     if (!c) return FH_OK;
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    if (c->side) (void)hipStreamSynchronize(c->side);
     if (c->exec) (void)hipGraphExecDestroy(c->exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
     for (int q = 0; q < kEvents; q++)
@@ -262,9 +258,6 @@ int fh_destroy(fh_ctx* c) {
         if (b) (void)hipFree(b);
     if (c->h_error) (void)hipHostFree(c->h_error);
     if (c->own_stream && c->stream) (void)hipStreamDestroy(c->stream);
-    if (c->side) (void)hipStreamDestroy(c->side);
-    if (c->fork_ev) (void)hipEventDestroy(c->fork_ev);
-    if (c->join_ev) (void)hipEventDestroy(c->join_ev);
     delete c;
     return FH_OK;
 }
@@ -465,7 +458,7 @@ static int sph_fused_steps(fh_ctx* c, const fh_sph_params* prm, const fh_epilogu
             continue;
         }
         FH_CHECK_HIP(launch_group_plan(c, a, true));
-        // pass timers: first launch to the join of the side stream (wall time of the pass)
+        // pass timers: wall time of each pass (the force pass with its k_prep)
         tbeg(c, KID_DPASS);
         FH_CHECK_HIP(launch_density_fast(c, a, c->cell_start));
         tend(c, KID_DPASS);
@@ -665,9 +658,8 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
 
 static const char* const kKernelNames[KID_COUNT] = {"hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
-                                                    "finalize", "runs", "plan",
-                                                    "density_heavy", "force_heavy",
-                                                    "prep", "density_pass", "force_pass"};
+                                                    "finalize", "runs", "plan", "prep",
+                                                    "density_pass", "force_pass"};
 
 static int kernel_id(const char* name) {
     if (!name) return -1;

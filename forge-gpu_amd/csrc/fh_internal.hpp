@@ -142,8 +142,8 @@ inline DivU32 make_divu32(uint32_t d) {
 
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
 enum KernelId { KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
-                KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_DHEAVY, KID_FHEAVY,
-                KID_PREP, KID_DPASS, KID_FPASS, KID_COUNT };
+                KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_PREP, KID_DPASS,
+                KID_FPASS, KID_COUNT };
 
 // Event pairs bracketing the first `max` launches of one kernel after it was armed; when the
 // launches are captured, every replay of the graph re-records the same events.
@@ -158,10 +158,6 @@ struct fh_ctx {
     int device;
     hipStream_t stream;
     bool own_stream;
-    // The heavy SPH kernels run on `side`, forked from and joined back into `stream` with the
-    // two events, so they overlap the light kernels (default priority, like `stream`).
-    hipStream_t side;
-    hipEvent_t fork_ev, join_ev;
     uint32_t max_n, max_cells;
     uint32_t max_sort_tiles, max_scan_tiles;
     // sort scratch

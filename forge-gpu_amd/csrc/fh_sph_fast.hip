@@ -6,7 +6,7 @@
 // their own and k_prep / k_finalize add the three in a fixed order, so results are
 // deterministic (no atomics) and a dense cell's work is split three ways.
 //
-// Light items (k_density_wave, k_force_wave: 64-lane workgroups, one item each).  For a fixed
+// Light items (density_light, force_light: one wavefront per item).  For a fixed
 // (dy, dz) the three x-adjacent cells of a particle are one contiguous range of the sorted
 // arrays.  Lanes of one home row (cy, cz) are consecutive (a "segment"), and for each of the
 // slab's three rows the union of a segment's ranges is again one contiguous range.  The wave
@@ -19,12 +19,15 @@
 // pass.  Light workgroups are renumbered so that runs of kXcdChunk consecutive items share one
 // XCD's L2 (neighbouring sub-tiles read mostly the same cells).
 //
-// Heavy items (k_density_heavy, k_force_heavy).  An item whose particles face more than
-// kHeavyWork (384) candidates in the slab, or that touches a co-located group, is listed by the
-// plan (k_group_plan) and taken by one of kHeavyGrid (4096) 512-lane workgroups that stride over
-// the list.  Its 8 waves hold the same 64 particles and split the 64-candidate chunks of each
-// segment row round-robin, each through its own LDS slice, and reduce in wave order.  The heavy
-// kernels run on a side stream beside the light ones.
+// Heavy items.  An item whose particles face more than kHeavyWork (384) candidates in the slab,
+// or that touches a co-located group, is listed by the plan (k_group_plan) and split into 8
+// parts: single-wave workgroups that hold the same 64 particles and take the 64-candidate chunks
+// of each segment row round-robin (part p: chunks p, p + 8, ...).  Each part leaves its partial
+// sums in hpart (by the item's list slot, hslot[item]), and k_prep / k_finalize add the parts in
+// part order.  Heavy parts and light items share one launch per pass (k_density_pass,
+// k_force_pass): the parts first, on workgroups 0 .. kHeavyParts - 1, the 8 parts of an item on
+// one XCD; light items after them.  (Two launches on two streams, a heavy kernel of 512-lane
+// workgroups beside the light one, cost ~5 us of cross-queue wait at each fork and join.)
 //
 // Transposed items.  When an item's stream is many times longer than its largest particle's
 // candidate count (sparse particles along a row beside a dense one), it is walked one particle
@@ -109,15 +112,14 @@ __device__ __forceinline__ uint32_t xcd_chunked(uint32_t b, uint32_t nb) {
 // ---------------------------------------------------------------------------------------------
 // Load balance.  A (64-particle sub-tile, slab) item whose particles each face more than
 // kHeavyWork candidates -- the box corners of c3 collect thousands of particles at one point --
-// is moved to a heavy list and processed by a 512-lane workgroup in which 8 waves split the
-// candidates of the same 64 particles and reduce their partial sums in wave order.  The light
-// kernels skip those items.  The plan is made once per substep and serves both passes.
+// is moved to a heavy list and processed in 8 single-wave parts that split the candidates of the
+// same 64 particles; their partial sums are added in part order.  The light items skip those
+// items.  The plan is made once per substep and serves both passes.
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
 #ifndef FH_HW
 #define FH_HW 8
 #endif
 constexpr int kHeavyWaves = FH_HW;      // waves per heavy workgroup (one item at a time)
-constexpr int kHeavyThreads = kHeavyWaves * kWave;
 constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
 constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
 constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transposed
@@ -152,9 +154,6 @@ constexpr uint32_t kTransLightRatio = FH_TRANS_LIGHT_RATIO, kTransLightOffset = 
 constexpr uint32_t kHeavyGrid = FH_HGRID;  // heavy workgroups (grid-stride over the list)
 #ifndef FH_HU
 #define FH_HU 2
-#endif
-#ifndef FH_HMINW
-#define FH_HMINW 6
 #endif
 
 // Candidate density accumulation of one lane over [jb, je) of a staged chunk, four candidates
@@ -659,17 +658,6 @@ __device__ __forceinline__ uint32_t heavy_total(const Control* __restrict__ ctl,
     for (int q = 0; q < kHeavyLists; q++) t += min(ctl->heavy_count[q].v, cap);
     return t;
 }
-__device__ __forceinline__ uint32_t heavy_entry(const uint32_t* __restrict__ heavy,
-                                                const Control* __restrict__ ctl, uint32_t cap,
-                                                uint32_t q) {
-    int k = 0;
-    for (; k < kHeavyLists - 1; k++) {
-        const uint32_t c = min(ctl->heavy_count[k].v, cap);
-        if (q < c) break;
-        q -= c;
-    }
-    return heavy[(size_t)k * cap + q];
-}
 
 // ---------------------------------------------------------------------------------------------
 // Lane `lane` of a chunk of m (>= 1) candidates starting at c0: a global load from a clamped,
@@ -765,11 +753,12 @@ __device__ __forceinline__ void density_light(uint32_t item, int lane, float4* b
     if (in) dpart[(size_t)slab * stride + s] = acc;
 }
 
-// Heavy items: the 8 waves of a workgroup hold the same 64 particles of one (sub-tile, slab)
-// and walk the same home-row segments as k_density_wave, but split each segment row's chunks
-// round-robin (wave w takes chunks w, w + 8, ...), each through its own LDS slice (no
-// workgroup barrier until the final reduction in wave order).  The members of co-located groups
-// in a segment row are cut out of its candidate range (the representative stays, with weight M).
+// Heavy items: the 8 parts of an item (single-wave workgroups) hold the same 64 particles of one
+// (sub-tile, slab) and walk the same home-row segments as density_light, but split each segment
+// row's chunks round-robin (part w takes chunks w, w + 8, ...), each through its own LDS; their
+// partial sums are added in part order by the passes' consumers.  The members of co-located
+// groups in a segment row are cut out of its candidate range (the representative stays, with
+// weight M).
 constexpr int kMaxCut = 4;  // groups cut out per segment row (further ones are staged, weight 0)
 
 struct RowPlan {
@@ -1136,7 +1125,7 @@ __device__ __forceinline__ void force_pair(const float4& q, const float4& w, con
     const bool ok = r2 < K.h2 && r2 > 1e-12f;
     // The empty asm pins 1/r as computed for every candidate: otherwise the compiler moves the
     // reciprocal square root and the products behind a divergent branch on the pair test, whose
-    // exec-mask bookkeeping costs more than the select (10% of k_force_wave on c3).
+    // exec-mask bookkeeping costs more than the select (10% of the light force work on c3).
     float rinv = __builtin_amdgcn_rsqf(r2);
     asm volatile("" : "+v"(rinv));
     const float vs = ok ? fmaf(-r2, rinv, K.h) : 0.0f;
@@ -1228,7 +1217,7 @@ __device__ __forceinline__ void force_trans(const float4* __restrict__ rec,
 
 // Acceleration partials: fpart[slab][c][s] = sum over the slab's neighbours j of the pressure
 // and viscosity pair terms (sph_fused.rs:604-623), not yet divided by rho_i.  Same windowed
-// stream as k_density_wave; the window is staged by copying force records (k_prep).
+// stream as density_light; the window is staged by copying force records (k_prep).
 __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp, float4* bv,
                                             const float4* __restrict__ spos,
                                             const float4* __restrict__ svel,
@@ -1589,29 +1578,6 @@ static float poly6_mc(float h, float mass) {
 }
 
 
-
-// Fork the side stream off the main one (heavy kernels go there), and join it back.
-#ifndef FH_SIDE_MODE
-#define FH_SIDE_MODE 7
-#endif
-// Which concurrent pairs use the side stream (bit 0: unused since groups and plan share one
-// launch, bit 1: the heavy
-// density kernel beside the light one, bit 2: the same for the force pass); otherwise the pair
-// runs one after the other on the context stream.
-constexpr uint32_t kSideGroup = 1u, kSideDensity = 2u, kSideForce = 4u;
-static hipStream_t side_of(fh_ctx* c, uint32_t use) {
-    return (FH_SIDE_MODE & use) ? c->side : c->stream;
-}
-static hipError_t fork_side(fh_ctx* c, uint32_t use) {
-    if (!(FH_SIDE_MODE & use)) return hipSuccess;
-    hipError_t e = hipEventRecord(c->fork_ev, c->stream);
-    return e == hipSuccess ? hipStreamWaitEvent(c->side, c->fork_ev, 0) : e;
-}
-static hipError_t join_side(fh_ctx* c, uint32_t use) {
-    if (!(FH_SIDE_MODE & use)) return hipSuccess;
-    hipError_t e = hipEventRecord(c->join_ev, c->side);
-    return e == hipSuccess ? hipStreamWaitEvent(c->stream, c->join_ev, 0) : e;
-}
 
 hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
     if (a.n == 0) return hipSuccess;

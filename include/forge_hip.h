@@ -257,13 +257,13 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
 #define FH_OPT_SPH_EXACT 1
 /* FH_OPT_HEAVY_WORK = 2: work split of the fast passes.  A (64-particle, z-slab) item whose
  * particles face more than `value` candidates (a co-located group counting as one) is processed
- * by a 512-lane workgroup (8 wavefronts) instead of one wavefront; value 0 restores the default
- * (384).
+ * by 8 wavefronts that split its candidates instead of one wavefront; value 0 restores the
+ * default (384).
  * Results differ only by rounding. */
 #define FH_OPT_HEAVY_WORK 2
 /* FH_OPT_DIRECT_ITEMS = 3: items whose particles' candidate ranges barely overlap (sparse
  * particles along a row, or beside a dense one) are walked transposed: one particle at a time,
- * its candidates across the lanes of a 512-lane workgroup, instead of all particles through a
+ * its candidates across the lanes of a wavefront, instead of all particles through a
  * shared LDS-staged stream.  0: never, 1: chosen per item from the stream and per-particle
  * lengths (default), 2: every item.  Results differ only by rounding. */
 #define FH_OPT_DIRECT_ITEMS 3
@@ -310,9 +310,9 @@ int fh_event_record(fh_ctx* ctx, uint32_t slot);
 int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
 
 /* Per-kernel timing.  Arm kernel `name` (one of "hist", "hash", "scan", "sort",
- * "gather", "density", "force", "query", "finalize", "runs", "plan", "density_heavy",
- * "force_heavy", "prep"; or a whole fast pass of fh_sph_fused, "density_pass" or
- * "force_pass", from its first launch to the join of its side stream) so that its next
+ * "gather", "density", "force", "query", "finalize", "runs", "plan", "prep"; or a whole fast
+ * pass of fh_sph_fused, "density_pass" or "force_pass", from its first launch to its last) so
+ * that its next
  * `max_launches` launches on the
  * context stream are bracketed by HIP events; launches captured into a graph record the events
  * on every replay.  max_launches = 0 disarms.  Arming allocates events: call outside capture.
