@@ -1001,8 +1001,11 @@ __device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t& q0, int& par
 }
 
 // Density pass, one launch: heavy parts first (they are the long work), then one light item per
-// wave.  The parts leave their partial sums in hpart; k_heavy_sum adds them in part order.
-__global__ __launch_bounds__(kWave) void k_density_pass(
+// wave.  The parts leave their partial sums in hpart; k_prep and k_finalize add them in part
+// order.  Held to 8 waves per SIMD (the SGPRs of both paths otherwise limit it to 7; fixed c3
+// state 492 -> 489 us per substep).
+__global__ __attribute__((amdgpu_flat_work_group_size(kWave, kWave), amdgpu_waves_per_eu(8, 8)))
+void k_density_pass(
     const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
     float* __restrict__ dpart, uint32_t stride, uint32_t items, const uint8_t* __restrict__ flag,
