@@ -187,9 +187,10 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
-    // partial sums of the heavy parts: per list slot, 8 parts x 4 components x 64 lanes
+    // partial sums of the heavy parts: per list slot, kHeavyWaves parts x kHeavyComps x 64 lanes
     if (e == hipSuccess)
-        e = alloc(&c->hpart, (size_t)kHeavyLists * c->heavy_cap * 8u * 4u * 64u, &tot);
+        e = alloc(&c->hpart,
+                  (size_t)kHeavyLists * c->heavy_cap * kHeavyWaves * kHeavyComps * 64u, &tot);
     if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess)
         e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);

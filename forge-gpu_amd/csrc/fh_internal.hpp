@@ -65,6 +65,11 @@ constexpr uint32_t kGroupHits = 4;
 // The heavy SPH work list is split into kHeavyLists sub-lists with counters on separate lines,
 // so that appends from different workgroups do not serialise on one address.
 constexpr int kHeavyLists = 8;
+#ifndef FH_HW
+#define FH_HW 4
+#endif
+constexpr int kHeavyWaves = FH_HW;  // single-wave parts of a heavy SPH item
+constexpr int kHeavyComps = 4;      // partial sums per lane and part: a_x, a_y, a_z, w (density: 1)
 // A light item's candidate stream as the density pass leaves it for the force pass: per lane
 // and row, (stream start << 16 | count), then the sorted indices of the first two windows'
 // staging slots (192 each).  Streams longer than two windows (~2 % of c3's light items) are
@@ -186,7 +191,7 @@ struct fh_ctx {
     uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
     uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
-    float* hpart;        // heavy work partials: per heavy-list slot, 8 parts x 4 x 64 floats
+    float* hpart;        // heavy work partials: per heavy-list slot, kHeavyWaves x 4 x 64 floats
     uint32_t* hslot;     // [3 * ceil(max_n / 64)] heavy list slot of each heavy item
     uint32_t* lstream;   // [3 * ceil(max_n / 64)][kLightCacheWords] light items' candidate streams
                          // (lane intervals and window indices) from the density pass, reused by

@@ -20,14 +20,16 @@
 // XCD's L2 (neighbouring sub-tiles read mostly the same cells).
 //
 // Heavy items.  An item whose particles face more than kHeavyWork (384) candidates in the slab,
-// or that touches a co-located group, is listed by the plan (k_group_plan) and split into 8
-// parts: single-wave workgroups that hold the same 64 particles and take the 64-candidate chunks
-// of each segment row round-robin (part p: chunks p, p + 8, ...).  Each part leaves its partial
-// sums in hpart (by the item's list slot, hslot[item]), and k_prep / k_finalize add the parts in
-// part order.  Heavy parts and light items share one launch per pass (k_density_pass,
-// k_force_pass): the parts first, on workgroups 0 .. kHeavyParts - 1, the 8 parts of an item on
-// one XCD; light items after them.  (Two launches on two streams, a heavy kernel of 512-lane
-// workgroups beside the light one, cost ~5 us of cross-queue wait at each fork and join.)
+// or that touches a co-located group, is listed by the plan (k_group_plan) and split into
+// kHeavyWaves (4) parts: single-wave workgroups that hold the same 64 particles and take the
+// 64-candidate chunks of each segment row round-robin (part p: chunks p, p + 4, ...).  Each part
+// leaves its partial sums in hpart (by the item's list slot, hslot[item]), and k_prep /
+// k_finalize add the parts in part order.  Heavy parts and light items share one launch per
+// pass (k_density_pass, k_force_pass): the parts first, on workgroups 0 .. kHeavyParts - 1, the
+// parts of an item on one XCD; light items after them.  (Two launches on two streams, a heavy
+// kernel of 512-lane workgroups beside the light one, cost ~5 us of cross-queue wait at each
+// fork and join.  8 parts per item were 2 % slower on c3 but 8 % faster on c4, whose dense clumps
+// make long items; 2 or 16 parts 5 % and 8 % slower on c3.)
 //
 // Transposed items.  When an item's stream is many times longer than its largest particle's
 // candidate count (sparse particles along a row beside a dense one), it is walked one particle
@@ -112,17 +114,14 @@ __device__ __forceinline__ uint32_t xcd_chunked(uint32_t b, uint32_t nb) {
 // ---------------------------------------------------------------------------------------------
 // Load balance.  A (64-particle sub-tile, slab) item whose particles each face more than
 // kHeavyWork candidates -- the box corners of c3 collect thousands of particles at one point --
-// is moved to a heavy list and processed in 8 single-wave parts that split the candidates of the
+// is moved to a heavy list and processed in 4 single-wave parts that split the candidates of the
 // same 64 particles; their partial sums are added in part order.  The light items skip those
 // items.  The plan is made once per substep and serves both passes.
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
-#ifndef FH_HW
-#define FH_HW 8
-#endif
-constexpr int kHeavyWaves = FH_HW;      // waves per heavy workgroup (one item at a time)
 constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
 constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
 constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transposed
+constexpr uint32_t kEntryFlags = kCutFlag | kTransFlag;
 // Item flags (the plan): light (one wavefront), heavy (heavy list), every particle co-located
 // (skipped by both passes).
 constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
@@ -457,7 +456,7 @@ __device__ __forceinline__ bool is_member(uint32_t bits, uint32_t j) {
     return !(bits & kRepFlag) && bits != j;
 }
 
-// Lanes w, w + HW, w + 2 HW, ... of a wave (the particles wave w takes in a transposed walk).
+// Lanes w, w + hw, w + 2 hw, ... of a wave (the particles wave w takes in a transposed walk).
 __device__ __forceinline__ uint64_t trans_lanes(int wave, int hw) {
     uint64_t m = 0;
     for (int l = wave; l < kWave; l += hw) m |= 1ull << l;
@@ -621,7 +620,7 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
             const uint32_t ent = s_item[w * 3 + k];
             const uint32_t slot = (bid % kHeavyLists) * heavy_cap + pos;
             if (pos < heavy_cap) heavy[slot] = ent;
-            hslot[ent & ~(kCutFlag | kTransFlag)] = pos < heavy_cap ? slot : kNoSlot;
+            hslot[ent & ~kEntryFlags] = pos < heavy_cap ? slot : kNoSlot;
         }
     }
 }
@@ -753,9 +752,9 @@ __device__ __forceinline__ void density_light(uint32_t item, int lane, float4* b
     if (in) dpart[(size_t)slab * stride + s] = acc;
 }
 
-// Heavy items: the 8 parts of an item (single-wave workgroups) hold the same 64 particles of one
+// Heavy items: the parts of an item (single-wave workgroups) hold the same 64 particles of one
 // (sub-tile, slab) and walk the same home-row segments as density_light, but split each segment
-// row's chunks round-robin (part w takes chunks w, w + 8, ...), each through its own LDS; their
+// row's chunks round-robin (part w takes chunks w, w + 4, ...), each through its own LDS; their
 // partial sums are added in part order by the passes' consumers.  The members of co-located
 // groups in a segment row are cut out of its candidate range (the representative stays, with
 // weight M).
@@ -897,19 +896,19 @@ __device__ __forceinline__ void seg_plans(RowPlan R[3], const CellXYZ& ci, const
 }
 
 
-// One virtual wave (`wave` of HW) of heavy entry `entry`: its partial density sums (chunks
-// wave, wave + HW, ... of each segment row; the transposed walk's lanes trans_lanes(wave, HW)).
+// One virtual wave (`wave` of hw) of heavy entry `entry`: its partial density sums (chunks
+// wave, wave + hw, ... of each segment row; the transposed walk's lanes trans_lanes(wave, hw)),
+// hw = the item's part count.
 // False when the item is skipped (only group members).
-template <int HW>
 __device__ __forceinline__ bool density_heavy_wave(
-    uint32_t entry, int wave, int lane, float4* buf, const float4* __restrict__ spos,
+    uint32_t entry, int wave, int hw, int lane, float4* buf, const float4* __restrict__ spos,
     const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
     const uint32_t* __restrict__ skip_tag, uint32_t epoch, float& out) {
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const bool cut = (entry & kCutFlag) != 0u;  // the item touches a co-located group
     const bool trans = (entry & kTransFlag) != 0u;
-    const uint32_t item = entry & ~(kCutFlag | kTransFlag);
+    const uint32_t item = entry & ~kEntryFlags;
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == epoch) return false;  // uniform: only group members
     const uint32_t s = sub * kSub + (uint32_t)lane;
@@ -922,7 +921,7 @@ __device__ __forceinline__ bool density_heavy_wave(
     float acc = 0.0f;
     if (trans)  // members take their representative's density
         acc = density_trans(spos, b, e, pi, live && !is_member(__float_as_uint(pi.w), s), h2,
-                            trans_lanes(wave, HW), lane);
+                            trans_lanes(wave, hw), lane);
     uint64_t pending = trans ? 0ull : __ballot(live);
     while (pending) {  // uniform, identical in every wave
         const int leader = __ffsll((unsigned long long)pending) - 1;
@@ -934,7 +933,7 @@ __device__ __forceinline__ bool density_heavy_wave(
         RowPlan R[3];
         seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
                   lane);
-        // chunks wave, wave + HW, ... of the segment's three rows; the next is fetched before
+        // chunks wave, wave + hw, ... of the segment's three rows; the next is fetched before
         // the current one is evaluated
         uint32_t t = (uint32_t)wave;
         int r;
@@ -944,7 +943,7 @@ __device__ __forceinline__ bool density_heavy_wave(
         while (r < 3) {  // uniform within the wave
             int nr;
             uint32_t nc0, nm;
-            seg_chunk(R, t + HW, nr, nc0, nm);
+            seg_chunk(R, t + (uint32_t)hw, nr, nc0, nm);
             const float4 nv = nr < 3 ? chunk_load(spos, nc0, nm, lane) : z4;
             const uint32_t j = c0 + (uint32_t)lane;
             __builtin_amdgcn_wave_barrier();
@@ -956,7 +955,7 @@ __device__ __forceinline__ bool density_heavy_wave(
                 acc = cut ? density_run_w(buf, c0, jb, je, pi, h2, acc)
                           : density_run(buf, c0, jb, je, pi, h2, acc);
             }
-            t += HW;
+            t += (uint32_t)hw;
             r = nr;
             c0 = nc0;
             m = nm;
@@ -969,7 +968,6 @@ __device__ __forceinline__ bool density_heavy_wave(
 
 // The heavy work partials: part p of heavy entry slot q (the entry's position in its list)
 // holds, per lane, kHeavyComps floats at hpart[((q * HW + p) * kHeavyComps + c) * 64 + lane].
-constexpr int kHeavyComps = 4;
 __device__ __forceinline__ size_t hpart_at(uint32_t slot, int part, int comp, int lane) {
     return (((size_t)slot * kHeavyWaves + (uint32_t)part) * kHeavyComps + (uint32_t)comp) * 64u +
            (uint32_t)lane;
@@ -990,14 +988,14 @@ __device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict_
 }
 
 // Heavy parts of a pass: workgroups 0 .. kHeavyParts - 1 of the pass kernel, one wave each;
-// the kHeavyWaves parts of one heavy entry are workgroups on one XCD (b % 8 is the XCD), so
-// they share its L2: b = (q / 8) * 64 + part * 8 + q % 8 for entries q < kHeavyGrid, and the
+// the kHeavyWaves (P) parts of one heavy entry are workgroups on one XCD (b % 8 is the XCD), so
+// they share its L2: b = (q / 8) * 8P + part * 8 + q % 8 for entries q < kHeavyGrid, and the
 // same workgroup takes q + kHeavyGrid, ... after that.
 constexpr uint32_t kHeavyParts = (uint32_t)kHeavyGrid * kHeavyWaves;
-static_assert(kHeavyWaves == 8 && kHeavyGrid % 8 == 0, "heavy part numbering");
+static_assert(kHeavyGrid % 8 == 0, "heavy part numbering");
 __device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t& q0, int& part) {
-    q0 = (b >> 6) * 8u + (b & 7u);
-    part = (int)((b >> 3) & 7u);
+    q0 = (b / (8u * kHeavyWaves)) * 8u + (b & 7u);
+    part = (int)((b >> 3) % (uint32_t)kHeavyWaves);
 }
 
 // Density pass, one launch: heavy parts first (they are the long work), then one light item per
@@ -1024,8 +1022,8 @@ void k_density_pass(
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             float acc;
-            if (density_heavy_wave<kHeavyWaves>(entry, part, lane, s_p, spos, skeys, n, g, cstart,
-                                                cell_grp, h2, skip_tag, epoch, acc))
+            if (density_heavy_wave(entry, part, kHeavyWaves, lane, s_p, spos, skeys, n, g, cstart, cell_grp,
+                                   h2, skip_tag, epoch, acc))
                 hpart[hpart_at(slot, part, 0, lane)] = acc;
         }
         return;
@@ -1307,12 +1305,11 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
     }
 }
 
-// One virtual wave (`wave` of HW) of heavy entry `entry` in the force pass: its partial
+// One virtual wave (`wave` of hw) of heavy entry `entry` in the force pass: its partial
 // acceleration (with the -wv v_i viscosity part, which adds linearly) and viscosity weight.
 // False when the item is skipped (only group members).
-template <int HW>
 __device__ __forceinline__ bool force_heavy_wave(
-    uint32_t entry, int wave, int lane, float4* bp, float4* bv, const float4* __restrict__ spos,
+    uint32_t entry, int wave, int hw, int lane, float4* bp, float4* bv, const float4* __restrict__ spos,
     const float4* __restrict__ svel, const float* __restrict__ srho,
     const float4* __restrict__ rec, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp,
@@ -1321,7 +1318,7 @@ __device__ __forceinline__ bool force_heavy_wave(
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const bool cut = (entry & kCutFlag) != 0u;
     const bool trans = (entry & kTransFlag) != 0u;
-    const uint32_t item = entry & ~(kCutFlag | kTransFlag);
+    const uint32_t item = entry & ~kEntryFlags;
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == epoch) return false;  // uniform: only group members
     const uint32_t s = sub * kSub + (uint32_t)lane;
@@ -1337,7 +1334,7 @@ __device__ __forceinline__ bool force_heavy_wave(
     float ax = 0.0f, ay = 0.0f, az = 0.0f, wv = 0.0f;
     if (trans)  // members are finished from their representative
         force_trans(rec, spos, stride, b, e, pi, p_i,
-                    live && !is_member(__float_as_uint(pi.w), s), K, trans_lanes(wave, HW), lane,
+                    live && !is_member(__float_as_uint(pi.w), s), K, trans_lanes(wave, hw), lane,
                     ax, ay, az, wv);
     uint64_t pending = trans ? 0ull : __ballot(live);
     while (pending) {  // uniform, identical in every wave
@@ -1361,7 +1358,7 @@ __device__ __forceinline__ bool force_heavy_wave(
         while (r < 3) {  // uniform within the wave
             int nr;
             uint32_t nc0, nm;
-            seg_chunk(R, t + HW, nr, nc0, nm);
+            seg_chunk(R, t + (uint32_t)hw, nr, nc0, nm);
             const float4 nq = load_or(rec, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
             const float4 nw = load_or(rec + stride, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
             __builtin_amdgcn_wave_barrier();
@@ -1371,7 +1368,7 @@ __device__ __forceinline__ bool force_heavy_wave(
             if (mine)
                 force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m), pi,
                                  p_i, K, ax, ay, az, wv);
-            t += HW;
+            t += (uint32_t)hw;
             r = nr;
             c0 = nc0;
             m = nm;
@@ -1413,9 +1410,8 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             float o[4];
-            if (force_heavy_wave<kHeavyWaves>(entry, part, lane, s_p, s_v, spos, svel, srho, rec,
-                                              skeys, n, g, cstart, cell_grp, K, stride, skip_tag,
-                                              epoch, o)) {
+            if (force_heavy_wave(entry, part, kHeavyWaves, lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
+                                 g, cstart, cell_grp, K, stride, skip_tag, epoch, o)) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) hpart[hpart_at(slot, part, c, lane)] = o[c];
             }

@@ -257,7 +257,7 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
 #define FH_OPT_SPH_EXACT 1
 /* FH_OPT_HEAVY_WORK = 2: work split of the fast passes.  A (64-particle, z-slab) item whose
  * particles face more than `value` candidates (a co-located group counting as one) is processed
- * by 8 wavefronts that split its candidates instead of one wavefront; value 0 restores the
+ * by 4 wavefronts that split its candidates instead of one wavefront; value 0 restores the
  * default (384).
  * Results differ only by rounding. */
 #define FH_OPT_HEAVY_WORK 2

@@ -42,9 +42,9 @@ def rel_err(a, b):
 
 
 def set_mode(fh, f, cfg, mode):
-    """fast: default work split; heavy: every (sub-tile, slab) item through the 1024-lane
-    kernels; light: none of them (one wavefront per item, shared stream); direct: every item
-    walked lane by lane; exact: the bit-exact passes."""
+    """fast: default work split; heavy: every (sub-tile, slab) item split into single-wave parts
+    whose partials are added afterwards; light: none of them (one wavefront per item, shared
+    stream); direct: every item walked lane by lane; exact: the bit-exact passes."""
     ctx = f.context(cfg.num_cells)
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, {"heavy": 1, "light": 1 << 30}.get(mode, 0))
