@@ -115,6 +115,7 @@ struct Control {
     Line heavy_count[kHeavyLists];      // entries in each heavy SPH work sub-list
     Line collapse_count;                // entries in the list of co-located cells
     Line big_count;                     // entries in the list of cells of >= kCollapseMin
+    Line triv;                          // bit p: one digit of sort pass p holds all n keys
     uint32_t hist[kDigitSlots];         // digit histograms of the current sort (pass p, bin d: p * bins + d)
 };
 

@@ -7,12 +7,11 @@
 //   k_hist_keys /  one read of the keys builds the digit histograms of ALL passes into
 //   k_hash_hist    per-workgroup partial rows (k_hash_hist computes the keys from positions on
 //                  the fly: the hash of HashGrid::build, hashgrid.rs:89-92, fused)
-//   k_hist_reduce  sums the partial rows into the histograms; for small sorts also the first
-//                  pass's tile prefixes (its input order is the rows' order), so that pass
-//                  needs no look-back
-//   sort_plan      decides which passes run (a pass whose digit is equal for every key is the
-//                  identity and is skipped): k_sort_plan for large sorts, in every workgroup
-//                  of every pass for small ones
+//   k_hist_reduce  sums the partial rows into the histograms and marks the passes whose digit
+//                  is equal for every key; for small sorts also the first pass's tile prefixes
+//                  (its input order is the rows' order), so that pass needs no look-back
+//   sort_plan      decides which passes run (an identity pass is skipped), in every workgroup
+//                  of every pass from the marks
 //   k_onesweep     one kernel per pass: an 8192-key tile per 512-lane workgroup, ranked with
 //                  64-lane ballot match-any, digit offsets from a decoupled look-back over
 //                  dynamically numbered tiles, then staged in LDS in digit order (keys, then
@@ -63,6 +62,7 @@ __device__ __forceinline__ void begin_work(const Begin& b) {
             for (int q = 0; q < kHeavyLists; q++) ctl->heavy_count[q].v = 0u;
             ctl->collapse_count.v = 0u;
             ctl->big_count.v = 0u;
+            ctl->triv.v = 0u;
         }
     }
     for (uint32_t i = blockIdx.x * blockDim.x + t; i < b.lb_words; i += gridDim.x * blockDim.x)
@@ -246,7 +246,7 @@ static_assert(kSortTile == 2 * kHistChunk && kHistRowsPerReduce == 8,
 __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict__ part,
                                                      uint32_t rows, uint32_t slot_blocks,
                                                      Control* ctl, uint32_t* __restrict__ pre,
-                                                     uint32_t nb0, uint32_t tiles) {
+                                                     uint32_t nb0, uint32_t tiles, uint32_t n) {
     const uint32_t b = blockIdx.x % slot_blocks, g = blockIdx.x / slot_blocks;
     const uint32_t r0 = g * kHistRowsPerReduce;
     const uint32_t slot = b * 256u + threadIdx.x;
@@ -263,27 +263,25 @@ __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict_
 #pragma unroll 8
         for (uint32_t r = r0; r < r1; r++) s += part[(size_t)r * kDigitSlots + slot];
     }
-    if (s) atomicAdd(&ctl->hist[slot], s);
+    if (s) {
+        // the add that completes a bin holding every key marks its pass as the identity (exactly
+        // one add sees the count reach n: counts only grow)
+        if (atomicAdd(&ctl->hist[slot], s) + s == n) atomicOr(&ctl->triv.v, 1u << (slot / nb0));
+    }
 }
 
-// The passes that run (one bit per pass), derived from the digit histograms (for small sorts
-// by every workgroup of every pass: the same function of the same data, so all agree).  A pass
-// whose digit is equal for every key (one histogram bin holds all n keys) is the identity and
-// is skipped.  Two adjustments leave the result in (kfin, vfin) without a copy kernel: when no
-// pass moves keys and the sort is out of place, pass 0 runs (a stable copy: its digit is
+// The passes that run (one bit per pass), derived by every workgroup of every pass from the
+// trivial-pass bits k_hist_reduce left (the same function of the same word, so all agree).  A
+// pass whose digit is equal for every key (one histogram bin holds all n keys) is the identity
+// and is skipped.  Two adjustments leave the result in (kfin, vfin) without a copy kernel: when
+// no pass moves keys and the sort is out of place, pass 0 runs (a stable copy: its digit is
 // constant); when exactly one pass moves keys in place (it has to write scratch) and the sort
 // has another pass, that pass runs as well (also a copy), so the second of the two writes back
 // in place.  Only one-pass sorts in place keep k_sort_finish (which reads ctl->plan, written by
-// pass 0).  The workgroup's threads test the bins (nb per pass); s_triv collects the trivial
-// passes.
+// pass 0).
 __device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, uint32_t passes,
-                                              uint32_t nb, uint32_t n, bool in_place,
-                                              uint32_t* s_triv) {
-    for (uint32_t q = 0; q < passes; q++)
-        for (uint32_t d = threadIdx.x; d < nb; d += blockDim.x)
-            if (ctl->hist[q * nb + d] == n) atomicOr(s_triv, 1u << q);
-    __syncthreads();
-    uint32_t plan = ~*s_triv & ((1u << passes) - 1u);
+                                              bool in_place) {
+    uint32_t plan = ~ctl->triv.v & ((1u << passes) - 1u);
     if (plan == 0u && !in_place) {
         plan = 1u;
     } else if (__popc(plan) == 1 && in_place && passes >= 2u) {
@@ -293,16 +291,6 @@ __device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, u
     return plan;
 }
 
-// The same plan as one kernel (256 threads) before the passes: for large sorts, where a load
-// of the histograms and a barrier in each of thousands of workgroups cost more than a launch.
-__global__ __launch_bounds__(256) void k_sort_plan(uint32_t passes, uint32_t nb, uint32_t n,
-                                                   uint32_t in_place, Control* ctl) {
-    __shared__ uint32_t s_triv;
-    if (threadIdx.x == 0) s_triv = 0u;
-    __syncthreads();
-    const uint32_t plan = sort_plan(ctl, passes, nb, n, in_place != 0u, &s_triv);
-    if (threadIdx.x == 0) ctl->plan = plan;
-}
 
 // The first-pass prefix buffer of a sort of n keys, or null (large sorts, whose histogram
 // workgroups take several chunks each, and contexts without the buffer).
@@ -316,7 +304,7 @@ hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots, uint32_t
     const uint32_t slot_blocks = slots / 256u;  // slots = passes * bins, bins >= 256
     k_hist_reduce<<<groups * slot_blocks, 256, 0, c->stream>>>(
         c->hist_part, rows, slot_blocks, c->ctl, first_pass_pre(c, n), nb0,
-        ceil_div(n, (uint32_t)kSortTile));
+        ceil_div(n, (uint32_t)kSortTile), n);
     return hipGetLastError();
 }
 
@@ -394,7 +382,6 @@ struct SortIO {
     uint32_t* rank;      // non-null: the last pass also writes rank[value] = output index
     uint32_t passes;     // passes of the sort
     uint32_t in_place;
-    uint32_t plan_in_wg; // 1: every workgroup derives the plan; 0: k_sort_plan wrote ctl->plan
     const uint32_t* pre; // first-pass tile prefixes (k_hist_reduce), or null
     uint32_t tiles;      // tiles of a pass (the group sums follow them in pre)
 };
@@ -563,18 +550,10 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     __shared__ uint32_t s_gbase[NB];             // global index of tile slot 0 of digit d
     __shared__ uint32_t s_scan[kSortWaves];
     __shared__ uint32_t s_tile;
-    __shared__ uint32_t s_triv;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint32_t plan;
-    if (io.plan_in_wg) {  // uniform
-        if (tid == 0) s_triv = 0u;
-        __syncthreads();
-        plan = sort_plan(ctl, io.passes, NB, n, io.in_place != 0u, &s_triv);
-        if (pass == 0u && blockIdx.x == 0u && tid == 0) ctl->plan = plan;  // for k_sort_finish
-    } else {
-        plan = ctl->plan;
-    }
+    const uint32_t plan = sort_plan(ctl, io.passes, io.in_place != 0u);
+    if (pass == 0u && blockIdx.x == 0u && tid == 0) ctl->plan = plan;  // for k_sort_finish
     if (!((plan >> pass) & 1u)) return;  // the pass does not run (workgroup-uniform)
     const PassBufs bf = pass_bufs(io, plan, pass);
     const bool last = (plan >> (pass + 1u)) == 0u;
@@ -753,12 +732,7 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
-              large ? 0u : 1u, large ? nullptr : first_pass_pre(c, n), tiles};
-    if (large) {
-        k_sort_plan<<<1, 256, 0, c->stream>>>(passes, nb, n, in_place ? 1u : 0u, c->ctl);
-        const hipError_t e0 = hipGetLastError();
-        if (e0 != hipSuccess) return e0;
-    }
+              large ? nullptr : first_pass_pre(c, n), tiles};
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t shift = L.bits * p, pbits = min(L.bits, num_bits - shift);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * nb;
