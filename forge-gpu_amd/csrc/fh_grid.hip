@@ -312,16 +312,31 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
             for (int r = 0; r < 3; r++) {
                 const uint32_t jb = max(L.S[r], w0);
                 const uint32_t je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin);
-                for (uint32_t t = jb; t < je; t++) {
-                    const float4 p = s_p[t - w0];
+                // branch-free, two candidates per step of the LDS address: a candidate beyond
+                // the radius adds 0 to the count and +0.0f to the weight sum, which starts at +0
+                // and only grows, so w + 0.0f == w bit for bit and the sum (in candidate order)
+                // is the reference's
+                const float4* c = s_p + (jb - w0);
+                const float4* const ce = c + (je > jb ? je - jb : 0u);
+                const float4* const cu = ce - 1;
+                const auto test = [&](const float4& p) {
                     const float dx = p.x - q.x, dy2 = p.y - q.y, dz2 = p.z - q.z;
                     const float dist_sq = dx * dx + dy2 * dy2 + dz2 * dz2;
-                    if (dist_sq <= radius_sq) {
-                        const float diff = radius_sq - dist_sq;
-                        cnt++;
-                        w += coeff * diff * diff * diff;
-                    }
+                    const bool ok = dist_sq <= radius_sq;
+                    const float diff = radius_sq - dist_sq;
+                    const float t = coeff * diff * diff * diff;
+                    cnt += ok ? 1u : 0u;
+                    w += ok ? t : 0.0f;
+                };
+                if (c < cu) {
+                    do {
+                        const float4 p0 = c[0], p1 = c[1];
+                        test(p0);
+                        test(p1);
+                        c += 2;
+                    } while (c < cu);
                 }
+                if (c < ce) test(*c);
             }
             __builtin_amdgcn_wave_barrier();
         }
