@@ -18,7 +18,7 @@
 //                  values through the same buffer) so the global scatter writes contiguous runs
 //   k_sort_finish  copies the result of a one-pass sort in place back from scratch
 // Digits are 8 bits (256 bins), or 10 bits (1024 bins) for keys of 17..20 bits below
-// kSortLargeN keys (digits_for): a pass over a million keys is bound by its look-back chain
+// kWideMaxN keys (digits_for): a pass over a million keys is bound by its look-back chain
 // across the tiles, not by its bytes, so two 10-bit passes beat three 8-bit ones -- provided a
 // tile's 1024 look-back words move as 512 contiguous 64-bit pairs (two digits per thread, one
 // status per pair), not as 1024 strided 32-bit words.
@@ -292,10 +292,11 @@ __device__ __forceinline__ uint32_t sort_plan(const Control* __restrict__ ctl, u
 }
 
 
-// The first-pass prefix buffer of a sort of n keys, or null (large sorts, whose histogram
-// workgroups take several chunks each, and contexts without the buffer).
+// The first-pass prefix buffer of a sort of n keys, or null (sorts of more than 4,194,304 keys,
+// whose histogram workgroups take several chunks each).
 static uint32_t* first_pass_pre(fh_ctx* c, uint32_t n) {
-    return n < kSortLargeN ? c->sort_pre : nullptr;
+    // the prefixes need one partial histogram row per 4096-key chunk of the input
+    return n <= (uint32_t)kHistBlocks * kHistChunk ? c->sort_pre : nullptr;
 }
 
 hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots, uint32_t n,
@@ -532,8 +533,8 @@ __device__ __forceinline__ void lb_walk(const uint32_t* __restrict__ w, uint32_t
     }
 }
 
-// Items = keys per thread: a tile holds Items * kSortThreads keys (kSortItems for small sorts,
-// kSortItemsLarge from kSortLargeN keys on: longer per-digit runs in the scatter and half as
+// Items = keys per thread: a tile holds Items * kSortThreads keys (kSortItems for small sorts
+// and 10-bit digits, kSortItemsLarge for 8-bit digits from kSortLargeN keys on: longer per-digit runs in the scatter and half as
 // many look-back words per key, at two workgroups per CU).  DB = digit bits: 2^DB bins; in the
 // per-digit phases thread t owns digits t * DPT .. t * DPT + DPT - 1 (the first 256 threads,
 // one digit each, for 8-bit digits; every thread, two digits each, for 10-bit ones).
@@ -726,7 +727,8 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits, uint32_t* rank) {
     const Digits L = digits_for(num_bits, n);
     const uint32_t passes = L.passes, nb = 1u << L.bits;
-    const bool large = n >= kSortLargeN;  // (10-bit digits only below kSortLargeN)
+    // large 8-bit sorts: 12,288-key tiles and the plan without first-pass prefixes
+    const bool large = n >= kSortLargeN && L.bits != kWideDigitBits;
     const uint32_t tiles = ceil_div(n, (uint32_t)(large ? kSortTileLarge : kSortTile));
     const bool in_place = kfin != nullptr && kfin == k0;
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)

@@ -147,7 +147,7 @@ class HashGrid:
 class RadixSorter:
     # Keys of 17..20 bits below this many pairs are sorted in two 10-bit passes, all others in
     # 8-bit passes (the library's digits_for).
-    WIDE_BELOW_N = 1 << 22
+    WIDE_BELOW_N = 1 << 23
 
     @staticmethod
     def digit_layout(num_bits: int, n: int) -> tuple[int, int]:

@@ -69,12 +69,14 @@ def test_product_path_has_no_oracle_dependency():
 
 def test_sort_digit_layout(fh):
     """Digit layout of a sort (the library's digits_for): two 10-bit passes for 17..20-bit keys
-    below 4,194,304 pairs, 8-bit passes otherwise; bench.py counts passes with it."""
+    below 8,388,608 pairs, 8-bit passes otherwise; bench.py counts passes with it."""
     lay = fh.RadixSorter.digit_layout
     assert lay(20, 1 << 20) == (10, 2)       # c3: 10^6 cells
     assert lay(17, 100) == (10, 2)
     assert lay(20, (1 << 22) - 1) == (10, 2)
-    assert lay(20, 1 << 22) == (8, 3)         # large sorts keep 8-bit digits
+    assert lay(20, 1 << 22) == (10, 2)        # c2: 82^3 cells, 4,194,304 points
+    assert lay(20, (1 << 23) - 1) == (10, 2)
+    assert lay(20, 1 << 23) == (8, 3)         # larger sorts keep 8-bit digits
     assert lay(16, 1 << 20) == (8, 2)         # c0: 40^3 cells
     assert lay(21, 1 << 20) == (8, 3)
     assert lay(32, 1 << 24) == (8, 4)         # c1

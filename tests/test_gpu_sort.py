@@ -54,9 +54,11 @@ def test_radix_sort_xorshift_streams(fh, gpu_ctx, oracle, name):
                                     (4097, 20), (65537, 8), (100_000, 7), (100_000, 32),
                                     (1 << 20, 20), (1_000_003, 24), (2_500_000, 31),
                                     (1 << 22, 32), (5_000_011, 19),
-                                    # 10-bit digits (17..20 bits below 4,194,304 keys)
+                                    # 10-bit digits (17..20 bits below 8,388,608 keys; first
+                                    # pass without look-back up to 4,194,304 keys)
                                     (8192, 17), (8193, 18), (70_000, 17), (300_000, 19),
-                                    (1_000_003, 20), (4_194_303, 20)])
+                                    (1_000_003, 20), (4_194_303, 20), (4_194_304, 20),
+                                    (4_194_305, 20), (8_388_607, 20), (8_388_608, 20)])
 def test_sort_matches_oracle(fh, gpu_ctx, oracle, n, bits):
     rng = np.random.default_rng(n * 131 + bits)
     keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)  # high bits beyond num_bits too
