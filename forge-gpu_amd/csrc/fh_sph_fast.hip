@@ -25,7 +25,7 @@
 // 64-candidate chunks of each segment row round-robin (part p: chunks p, p + 4, ...).  Each part
 // leaves its partial sums in hpart (by the item's list slot, hslot[item]), and k_prep /
 // k_finalize add the parts in part order.  Heavy parts and light items share one launch per
-// pass (k_density_pass, k_force_pass): the parts first, on workgroups 0 .. kHeavyParts - 1, the
+// pass (k_density_pass, k_force_pass): the parts first, on workgroups 0 .. hparts - 1, the
 // parts of an item on one XCD; light items after them.  (Two launches on two streams, a heavy
 // kernel of 512-lane workgroups beside the light one, cost ~5 us of cross-queue wait at each
 // fork and join.  8 parts per item were 2 % slower on c3 but 8 % faster on c4, whose dense clumps
@@ -987,12 +987,17 @@ __device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict_
     return heavy[(size_t)k * cap + q];
 }
 
-// Heavy parts of a pass: workgroups 0 .. kHeavyParts - 1 of the pass kernel, one wave each;
-// the kHeavyWaves (P) parts of one heavy entry are workgroups on one XCD (b % 8 is the XCD), so
-// they share its L2: b = (q / 8) * 8P + part * 8 + q % 8 for entries q < kHeavyGrid, and the
-// same workgroup takes q + kHeavyGrid, ... after that.
-constexpr uint32_t kHeavyParts = (uint32_t)kHeavyGrid * kHeavyWaves;
+// Heavy parts of a pass: workgroups 0 .. hparts - 1 of the pass kernel (hparts = hgrid * P), one
+// wave each; the P = kHeavyWaves parts of one heavy entry are workgroups on one XCD (b % 8 is
+// the XCD), so they share its L2: b = (q / 8) * 8P + part * 8 + q % 8 for entries q < hgrid, and
+// the same workgroup takes q + hgrid, ... after that.  hgrid (a multiple of 8, at most
+// kHeavyGrid) follows the item count, so that a small system does not dispatch thousands of
+// idle parts (c0's 50,000 particles: 2,346 items).
 static_assert(kHeavyGrid % 8 == 0, "heavy part numbering");
+static uint32_t heavy_grid(uint32_t items) {
+    const uint32_t g = (items / 8u + 7u) / 8u * 8u;
+    return g < 64u ? 64u : (g > (uint32_t)kHeavyGrid ? (uint32_t)kHeavyGrid : g);
+}
 __device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t& q0, int& part) {
     q0 = (b / (8u * kHeavyWaves)) * 8u + (b & 7u);
     part = (int)((b >> 3) % (uint32_t)kHeavyWaves);
@@ -1009,16 +1014,17 @@ void k_density_pass(
     float* __restrict__ dpart, uint32_t stride, uint32_t items, const uint8_t* __restrict__ flag,
     const uint32_t* __restrict__ skip_tag, const Control* __restrict__ ctl,
     uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
-    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, float* __restrict__ hpart) {
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, float* __restrict__ hpart,
+    uint32_t hgrid) {
     __shared__ float4 s_p[kWin];
     const int lane = threadIdx.x;
-    const uint32_t b = blockIdx.x;
-    if (b < kHeavyParts) {  // uniform
+    const uint32_t b = blockIdx.x, hparts = hgrid * kHeavyWaves;
+    if (b < hparts) {  // uniform
         uint32_t q0;
         int part;
         heavy_part_of(b, q0, part);
         const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-        for (uint32_t q = q0; q < count; q += kHeavyGrid) {  // uniform
+        for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             float acc;
@@ -1028,8 +1034,8 @@ void k_density_pass(
         }
         return;
     }
-    const uint32_t nl = gridDim.x - kHeavyParts;
-    density_light(xcd_chunked(b - kHeavyParts, nl), lane, s_p, spos, skeys, n, g, cstart, h2,
+    const uint32_t nl = gridDim.x - hparts;
+    density_light(xcd_chunked(b - hparts, nl), lane, s_p, spos, skeys, n, g, cstart, h2,
                   dpart, stride, items, flag, skip_tag, ctl, lstream, lstream_t);
 }
 
@@ -1396,17 +1402,17 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
     const uint8_t* __restrict__ flag, const uint32_t* __restrict__ skip_tag,
     const Control* __restrict__ ctl, const uint32_t* __restrict__ lstream,
     const uint32_t* __restrict__ lstream_t, const uint32_t* __restrict__ heavy,
-    uint32_t heavy_cap, float* __restrict__ hpart) {
+    uint32_t heavy_cap, float* __restrict__ hpart, uint32_t hgrid) {
     __shared__ float4 s_p[kWin];  // x, y, z, p_j
     __shared__ float4 s_v[kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x;
-    const uint32_t b = blockIdx.x;
-    if (b < kHeavyParts) {  // uniform
+    const uint32_t b = blockIdx.x, hparts = hgrid * kHeavyWaves;
+    if (b < hparts) {  // uniform
         uint32_t q0;
         int part;
         heavy_part_of(b, q0, part);
         const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-        for (uint32_t q = q0; q < count; q += kHeavyGrid) {  // uniform
+        for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             float o[4];
@@ -1418,8 +1424,8 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
         }
         return;
     }
-    const uint32_t nl = gridDim.x - kHeavyParts;
-    force_light(xcd_chunked(b - kHeavyParts, nl), lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
+    const uint32_t nl = gridDim.x - hparts;
+    force_light(xcd_chunked(b - hparts, nl), lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
                 g, cstart, K, fpart, wpart, stride, items, flag, skip_tag, ctl, lstream,
                 lstream_t);
 }
@@ -1598,10 +1604,11 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_DENSITY);
-    k_density_pass<<<kHeavyParts + grid, kWave, 0, c->stream>>>(
+    const uint32_t hgrid = heavy_grid(items);
+    k_density_pass<<<hgrid * kHeavyWaves + grid, kWave, 0, c->stream>>>(
         c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
         items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
-        c->heavy_cap, c->hpart);
+        c->heavy_cap, c->hpart, hgrid);
     tend(c, KID_DENSITY);
     return hipGetLastError();
 }
@@ -1640,10 +1647,11 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     uint32_t items;
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_FORCE);
-    k_force_pass<<<kHeavyParts + grid, kWave, 0, c->stream>>>(
+    const uint32_t hgrid = heavy_grid(items);
+    k_force_pass<<<hgrid * kHeavyWaves + grid, kWave, 0, c->stream>>>(
         c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
         c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
-        c->lstream_t, c->heavy, c->heavy_cap, c->hpart);
+        c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid);
     tend(c, KID_FORCE);
     return hipGetLastError();
 }
