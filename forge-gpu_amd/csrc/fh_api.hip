@@ -187,10 +187,10 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
-    // partial sums of the heavy parts: per list slot, kHeavyWaves parts x kHeavyComps x 64 lanes
+    // partial sums of the heavy parts: per list slot, kHeavyWavesMax parts x kHeavyComps x 64 lanes
     if (e == hipSuccess)
         e = alloc(&c->hpart,
-                  (size_t)kHeavyLists * c->heavy_cap * kHeavyWaves * kHeavyComps * 64u, &tot);
+                  (size_t)kHeavyLists * c->heavy_cap * kHeavyWavesMax * kHeavyComps * 64u, &tot);
     if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess)
         e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);
@@ -574,6 +574,12 @@ int fh_set_option(fh_ctx* c, int option, int value) {
             if (value < 0 || value > 2)
                 return fail(FH_EINVAL, "fh_set_option: direct items mode %d outside 0..2", value);
             c->direct_mode = (uint32_t)value;
+            return FH_OK;
+        case FH_OPT_HEAVY_PARTS:
+            if (value != 0 && value != kHeavyWaves && value != kHeavyWavesMax)
+                return fail(FH_EINVAL, "fh_set_option: heavy parts %d is not 0, %d or %d", value,
+                            kHeavyWaves, kHeavyWavesMax);
+            c->heavy_parts = (uint32_t)value;
             return FH_OK;
         default:
             return fail(FH_EINVAL, "fh_set_option: unknown option %d", option);

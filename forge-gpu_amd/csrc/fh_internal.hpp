@@ -70,7 +70,9 @@ constexpr int kHeavyLists = 8;
 #ifndef FH_HW
 #define FH_HW 4
 #endif
-constexpr int kHeavyWaves = FH_HW;  // single-wave parts of a heavy SPH item
+// single-wave parts of a heavy SPH item: kHeavyWaves by default, up to kHeavyWavesMax (the
+// partial-sum slots are sized for the maximum) with FH_OPT_HEAVY_PARTS
+constexpr int kHeavyWaves = FH_HW, kHeavyWavesMax = 8;
 constexpr int kHeavyComps = 4;      // partial sums per lane and part: a_x, a_y, a_z, w (density: 1)
 // A light item's candidate stream as the density pass leaves it for the force pass: per lane
 // and row, (stream start << 16 | count), then the sorted indices of the first two windows'
@@ -213,6 +215,7 @@ struct fh_ctx {
     bool sph_exact;      // FH_OPT_SPH_EXACT
     uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
     uint32_t direct_mode; // FH_OPT_DIRECT_ITEMS: 0 never, 1 automatic (default), 2 always
+    uint32_t heavy_parts; // FH_OPT_HEAVY_PARTS (0: kHeavyWaves)
     uint32_t* h_error;   // pinned host word for the device error flag
     size_t scratch_bytes;
     hipGraph_t graph;

@@ -967,9 +967,11 @@ __device__ __forceinline__ bool density_heavy_wave(
 }
 
 // The heavy work partials: part p of heavy entry slot q (the entry's position in its list)
-// holds, per lane, kHeavyComps floats at hpart[((q * HW + p) * kHeavyComps + c) * 64 + lane].
-__device__ __forceinline__ size_t hpart_at(uint32_t slot, int part, int comp, int lane) {
-    return (((size_t)slot * kHeavyWaves + (uint32_t)part) * kHeavyComps + (uint32_t)comp) * 64u +
+// holds, per lane, kHeavyComps floats at hpart[((q * hw + p) * kHeavyComps + c) * 64 + lane],
+// hw = the parts per item (the buffer is sized for kHeavyWavesMax).
+__device__ __forceinline__ size_t hpart_at(uint32_t slot, uint32_t hw, int part, int comp,
+                                         int lane) {
+    return (((size_t)slot * hw + (uint32_t)part) * kHeavyComps + (uint32_t)comp) * 64u +
            (uint32_t)lane;
 }
 
@@ -988,25 +990,30 @@ __device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict_
 }
 
 // Heavy parts of a pass: workgroups 0 .. hparts - 1 of the pass kernel (hparts = hgrid * P), one
-// wave each; the P = kHeavyWaves parts of one heavy entry are workgroups on one XCD (b % 8 is
+// wave each; the P = hw parts of one heavy entry are workgroups on one XCD (b % 8 is
 // the XCD), so they share its L2: b = (q / 8) * 8P + part * 8 + q % 8 for entries q < hgrid, and
 // the same workgroup takes q + hgrid, ... after that.  hgrid (a multiple of 8, at most
 // kHeavyGrid) follows the item count, so that a small system does not dispatch thousands of
 // idle parts (c0's 50,000 particles: 2,346 items).
 static_assert(kHeavyGrid % 8 == 0, "heavy part numbering");
+// The pass kernels are compiled for the default part count and for 8.
+static uint32_t heavy_parts(const fh_ctx* c) {
+    return c->heavy_parts == 8u ? 8u : (uint32_t)kHeavyWaves;
+}
 static uint32_t heavy_grid(uint32_t items) {
     const uint32_t g = (items / 8u + 7u) / 8u * 8u;
     return g < 64u ? 64u : (g > (uint32_t)kHeavyGrid ? (uint32_t)kHeavyGrid : g);
 }
-__device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t& q0, int& part) {
-    q0 = (b / (8u * kHeavyWaves)) * 8u + (b & 7u);
-    part = (int)((b >> 3) % (uint32_t)kHeavyWaves);
+__device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t hw, uint32_t& q0, int& part) {
+    q0 = (b / (8u * hw)) * 8u + (b & 7u);
+    part = (int)((b >> 3) % hw);
 }
 
 // Density pass, one launch: heavy parts first (they are the long work), then one light item per
 // wave.  The parts leave their partial sums in hpart; k_prep and k_finalize add them in part
 // order.  Held to 8 waves per SIMD (the SGPRs of both paths otherwise limit it to 7; fixed c3
 // state 492 -> 489 us per substep).
+template <uint32_t HW>
 __global__ __attribute__((amdgpu_flat_work_group_size(kWave, kWave), amdgpu_waves_per_eu(8, 8)))
 void k_density_pass(
     const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
@@ -1016,21 +1023,22 @@ void k_density_pass(
     uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
     const uint32_t* __restrict__ heavy, uint32_t heavy_cap, float* __restrict__ hpart,
     uint32_t hgrid) {
+    constexpr uint32_t hw = HW;
     __shared__ float4 s_p[kWin];
     const int lane = threadIdx.x;
-    const uint32_t b = blockIdx.x, hparts = hgrid * kHeavyWaves;
+    const uint32_t b = blockIdx.x, hparts = hgrid * hw;
     if (b < hparts) {  // uniform
         uint32_t q0;
         int part;
-        heavy_part_of(b, q0, part);
+        heavy_part_of(b, hw, q0, part);
         const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
         for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             float acc;
-            if (density_heavy_wave(entry, part, kHeavyWaves, lane, s_p, spos, skeys, n, g, cstart, cell_grp,
+            if (density_heavy_wave(entry, part, (int)hw, lane, s_p, spos, skeys, n, g, cstart, cell_grp,
                                    h2, skip_tag, epoch, acc))
-                hpart[hpart_at(slot, part, 0, lane)] = acc;
+                hpart[hpart_at(slot, hw, part, 0, lane)] = acc;
         }
         return;
     }
@@ -1041,7 +1049,8 @@ void k_density_pass(
 
 // A slab partial of particle j: written to its plane (`plane`, already offset to the slab and
 // component) by a light item, or, for a particle of a heavy item (hslot[item] = its list slot),
-// the sum of the item's kHeavyWaves part partials of component `comp` in part order.
+// the sum of the item's hw part partials of component `comp` in part order.
+template <uint32_t HW>
 __device__ __forceinline__ float slab_part(const float* __restrict__ plane,
                                            const uint32_t* __restrict__ hslot,
                                            const float* __restrict__ hpart, uint32_t slab,
@@ -1050,7 +1059,7 @@ __device__ __forceinline__ float slab_part(const float* __restrict__ plane,
     if (sl == kNoSlot) return plane[j];
     float t = 0.0f;
 #pragma unroll
-    for (int p = 0; p < kHeavyWaves; p++) t += hpart[hpart_at(sl, p, comp, j % kSub)];
+    for (int p = 0; p < (int)HW; p++) t += hpart[hpart_at(sl, HW, p, comp, j % kSub)];
     return t;
 }
 
@@ -1062,12 +1071,13 @@ struct FastForce {
     float fr;  // fv / fp (0 when fp = 0, i.e. mass = 0, where fv = 0 as well)
 };
 
+template <uint32_t HW>
 __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_t stride,
                                         uint32_t j, float mc, const uint32_t* __restrict__ hslot,
                                         const float* __restrict__ hpart) {
-    return mc * ((slab_part(dpart, hslot, hpart, 0u, 0, j) +
-                  slab_part(dpart + stride, hslot, hpart, 1u, 0, j)) +
-                 slab_part(dpart + 2u * stride, hslot, hpart, 2u, 0, j));
+    return mc * ((slab_part<HW>(dpart, hslot, hpart, 0u, 0, j) +
+                  slab_part<HW>(dpart + stride, hslot, hpart, 1u, 0, j)) +
+                 slab_part<HW>(dpart + 2u * stride, hslot, hpart, 2u, 0, j));
 }
 
 // Force records, made once per substep after the density pass (k_prep), one pair per sorted
@@ -1081,6 +1091,7 @@ __device__ __forceinline__ float rho_of(const float* __restrict__ dpart, uint32_
 // with it passes the distance test and the branch-free pair loop never multiplies by NaN.
 // srho[j] = rho_j; members take their representative's density (they sit at its position).
 // The force kernels then only copy records into LDS.
+template <uint32_t HW>
 __global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
                                               const float4* __restrict__ svel,
                                               const float4* __restrict__ vrep,
@@ -1105,7 +1116,7 @@ __global__ __launch_bounds__(256) void k_prep(const float4* __restrict__ spos,
         wt = 0.0f;
         u = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    const float rho = rho_of(dpart, stride, r, mc, hslot, hpart);
+    const float rho = rho_of<HW>(dpart, stride, r, mc, hslot, hpart);
     const float inv = rho < 1e-6f ? 0.0f : 1.0f / rho;
     srho[s] = rho;
     const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z);
@@ -1393,6 +1404,7 @@ __device__ __forceinline__ bool force_heavy_wave(
 }
 
 // Force pass, one launch: heavy parts first, then one light item per wave (as k_density_pass).
+template <uint32_t HW>
 __global__ __launch_bounds__(kWave) void k_force_pass(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
     const float* __restrict__ srho, const float4* __restrict__ rec,
@@ -1403,23 +1415,24 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
     const Control* __restrict__ ctl, const uint32_t* __restrict__ lstream,
     const uint32_t* __restrict__ lstream_t, const uint32_t* __restrict__ heavy,
     uint32_t heavy_cap, float* __restrict__ hpart, uint32_t hgrid) {
+    constexpr uint32_t hw = HW;
     __shared__ float4 s_p[kWin];  // x, y, z, p_j
     __shared__ float4 s_v[kWin];  // u/rho_j, w/rho_j
     const int lane = threadIdx.x;
-    const uint32_t b = blockIdx.x, hparts = hgrid * kHeavyWaves;
+    const uint32_t b = blockIdx.x, hparts = hgrid * hw;
     if (b < hparts) {  // uniform
         uint32_t q0;
         int part;
-        heavy_part_of(b, q0, part);
+        heavy_part_of(b, hw, q0, part);
         const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
         for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             float o[4];
-            if (force_heavy_wave(entry, part, kHeavyWaves, lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
+            if (force_heavy_wave(entry, part, (int)hw, lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
                                  g, cstart, cell_grp, K, stride, skip_tag, epoch, o)) {
 #pragma unroll
-                for (int c = 0; c < 4; c++) hpart[hpart_at(slot, part, c, lane)] = o[c];
+                for (int c = 0; c < 4; c++) hpart[hpart_at(slot, hw, part, c, lane)] = o[c];
             }
         }
         return;
@@ -1445,6 +1458,7 @@ constexpr uint32_t kDensityOnly = 1u << 31;
 // contiguous bytes) and,
 // when accelerations are asked for, to sout[2 stride + s] = (ax, ay, az, 0).  k_scatter then
 // moves it to particle order.
+template <uint32_t HW>
 __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spos,
                                                   const float4* __restrict__ svel,
                                                   const float* __restrict__ dpart,
@@ -1467,7 +1481,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     if (r >= n) r = s;
     // after a force pass k_prep has left rho (of r) in srho, and the force pass has reused the
     // heavy parts' partial buffer, so the density partials are summed only when density is all
-    const float rho = (F.flags & kDensityOnly) ? rho_of(dpart, stride, r, F.mc, hslot, hpart)
+    const float rho = (F.flags & kDensityOnly) ? rho_of<HW>(dpart, stride, r, F.mc, hslot, hpart)
                                                : srho[s];
     if (F.flags & kDensityOnly) {
         sout[2u * s] = make_float4(p.x, p.y, p.z, rho);
@@ -1479,19 +1493,19 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     if (!(rho < 1e-6f)) {
         const float inv = 1.0f / rho;
         const size_t S = stride;
-        float fx = (slab_part(fpart, hslot, hpart, 0u, 0, r) +
-                    slab_part(fpart + 3 * S, hslot, hpart, 1u, 0, r)) +
-                   slab_part(fpart + 6 * S, hslot, hpart, 2u, 0, r);
-        float fy = (slab_part(fpart + S, hslot, hpart, 0u, 1, r) +
-                    slab_part(fpart + 4 * S, hslot, hpart, 1u, 1, r)) +
-                   slab_part(fpart + 7 * S, hslot, hpart, 2u, 1, r);
-        float fz = (slab_part(fpart + 2 * S, hslot, hpart, 0u, 2, r) +
-                    slab_part(fpart + 5 * S, hslot, hpart, 1u, 2, r)) +
-                   slab_part(fpart + 8 * S, hslot, hpart, 2u, 2, r);
+        float fx = (slab_part<HW>(fpart, hslot, hpart, 0u, 0, r) +
+                    slab_part<HW>(fpart + 3 * S, hslot, hpart, 1u, 0, r)) +
+                   slab_part<HW>(fpart + 6 * S, hslot, hpart, 2u, 0, r);
+        float fy = (slab_part<HW>(fpart + S, hslot, hpart, 0u, 1, r) +
+                    slab_part<HW>(fpart + 4 * S, hslot, hpart, 1u, 1, r)) +
+                   slab_part<HW>(fpart + 7 * S, hslot, hpart, 2u, 1, r);
+        float fz = (slab_part<HW>(fpart + 2 * S, hslot, hpart, 0u, 2, r) +
+                    slab_part<HW>(fpart + 5 * S, hslot, hpart, 1u, 2, r)) +
+                   slab_part<HW>(fpart + 8 * S, hslot, hpart, 2u, 2, r);
         if (r != s) {
-            const float W = (slab_part(wpart, hslot, hpart, 0u, 3, r) +
-                             slab_part(wpart + S, hslot, hpart, 1u, 3, r)) +
-                            slab_part(wpart + 2 * S, hslot, hpart, 2u, 3, r);
+            const float W = (slab_part<HW>(wpart, hslot, hpart, 0u, 3, r) +
+                             slab_part<HW>(wpart + S, hslot, hpart, 1u, 3, r)) +
+                            slab_part<HW>(wpart + 2 * S, hslot, hpart, 2u, 3, r);
             const float4 vr = svel[r];
             fx = fmaf(W, vr.x - v.x, fx);
             fy = fmaf(W, vr.y - v.y, fy);
@@ -1605,7 +1619,9 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_DENSITY);
     const uint32_t hgrid = heavy_grid(items);
-    k_density_pass<<<hgrid * kHeavyWaves + grid, kWave, 0, c->stream>>>(
+    const uint32_t hw = heavy_parts(c);
+    const auto kernel = hw == 8u ? k_density_pass<8> : k_density_pass<kHeavyWaves>;
+    kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
         items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
         c->heavy_cap, c->hpart, hgrid);
@@ -1634,7 +1650,8 @@ hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
     if (a.n == 0) return hipSuccess;
     const FastForce K = fast_force(a);
     tbeg(c, KID_PREP);
-    k_prep<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
+    const auto kernel = heavy_parts(c) == 8u ? k_prep<8> : k_prep<kHeavyWaves>;
+    kernel<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
                                                        c->max_n, K.mc, a.k, a.rho0, K.fp, K.fv,
                                                        c->srho, c->sout, c->hslot, c->hpart);
     tend(c, KID_PREP);
@@ -1648,7 +1665,9 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_FORCE);
     const uint32_t hgrid = heavy_grid(items);
-    k_force_pass<<<hgrid * kHeavyWaves + grid, kWave, 0, c->stream>>>(
+    const uint32_t hw = heavy_parts(c);
+    const auto kernel = hw == 8u ? k_force_pass<8> : k_force_pass<kHeavyWaves>;
+    kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
         c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
         c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid);
@@ -1684,7 +1703,8 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     }
     F.e = epi ? epi->restitution : 0.0f;
     tbeg(c, KID_FINAL);
-    k_finalize<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
+    const auto fin = heavy_parts(c) == 8u ? k_finalize<8> : k_finalize<kHeavyWaves>;
+    fin<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
                                                            c->wpart, a.n, c->max_n, F,
                                                            accel != nullptr, c->sout, a.g,
                                                            density_only ? nullptr : next_keys,

@@ -27,6 +27,7 @@ FH_EPI_BOX = 4
 FH_OPT_SPH_EXACT = 1
 FH_OPT_HEAVY_WORK = 2
 FH_OPT_DIRECT_ITEMS = 3
+FH_OPT_HEAVY_PARTS = 4
 
 
 class LibraryNotBuilt(RuntimeError):

@@ -267,6 +267,11 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * shared LDS-staged stream.  0: never, 1: chosen per item from the stream and per-particle
  * lengths (default), 2: every item.  Results differ only by rounding. */
 #define FH_OPT_DIRECT_ITEMS 3
+/* FH_OPT_HEAVY_PARTS = 4: wavefronts (4 or 8) that split each heavy item of the fast passes; 0
+ * restores the default (4).  More parts shorten the longest items (dense clumps: c4 is ~8 %
+ * faster with 8), fewer cost less per item (c3 is ~2 % faster with 4).  Results differ only by
+ * rounding. */
+#define FH_OPT_HEAVY_PARTS 4
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
 /* GravityModule (gravity.rs:31-34): v += g * dt. */

@@ -44,11 +44,14 @@ def rel_err(a, b):
 def set_mode(fh, f, cfg, mode):
     """fast: default work split; heavy: every (sub-tile, slab) item split into single-wave parts
     whose partials are added afterwards; light: none of them (one wavefront per item, shared
-    stream); direct: every item walked lane by lane; exact: the bit-exact passes."""
+    stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; direct:
+    every item walked lane by lane; exact: the bit-exact passes."""
     ctx = f.context(cfg.num_cells)
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
-    ctx.set_option(fh.FH_OPT_HEAVY_WORK, {"heavy": 1, "light": 1 << 30}.get(mode, 0))
-    ctx.set_option(fh.FH_OPT_DIRECT_ITEMS, {"heavy": 0, "light": 0, "direct": 2}.get(mode, 1))
+    ctx.set_option(fh.FH_OPT_HEAVY_WORK, {"heavy": 1, "heavy8": 1, "light": 1 << 30}.get(mode, 0))
+    ctx.set_option(fh.FH_OPT_DIRECT_ITEMS,
+                   {"heavy": 0, "heavy8": 0, "light": 0, "direct": 2}.get(mode, 1))
+    ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode == "heavy8" else 0)
 
 
 def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast", visible=None):
@@ -132,7 +135,7 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "light", "direct"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
     from forge_hip import workloads
@@ -152,7 +155,7 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "light", "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
@@ -212,7 +215,7 @@ def colocated_cfg(n=40_000, seed=33):
     return cfg, vel
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "light", "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
@@ -262,7 +265,7 @@ def viscosity_cfg(case):
 
 
 @pytest.mark.parametrize("case", ["lattice", "groups", "colocated"])
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "light", "direct"])
 def test_viscosity_without_pressure_matches_oracle(fh, gpu_ctx, oracle, case, mode):
     """The fused force's viscosity half (sph_fused.rs:617-623) on its own, in every work split:
     plain lattice particles, and members of co-located groups, which are finished from their
@@ -542,3 +545,13 @@ def test_fused_steps_edge_cases(fh, gpu_ctx):
         assert torch.equal(f1.f32_fields[k], f2.f32_fields[k]), k
     for ff in (f1, f2):
         ff.context(cfg.num_cells).set_option(fh.FH_OPT_SPH_EXACT, 0)
+
+
+def test_heavy_parts_option(fh, gpu_ctx):
+    """FH_OPT_HEAVY_PARTS takes 0 (default), 4 or 8; other values are refused."""
+    for v in (0, 4, 8):
+        gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, v)
+    for bad in (1, 3, 16, -1):
+        with pytest.raises(fh.ForgeError):
+            gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, bad)
+    gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
