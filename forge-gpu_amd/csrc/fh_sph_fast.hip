@@ -743,24 +743,8 @@ __device__ __forceinline__ void density_light(uint32_t item, int lane, float4* b
 #pragma unroll
         for (int k = 0; k < kWinLoads; k++) buf[k * kWave + lane] = v[k];
         __builtin_amdgcn_wave_barrier();
-        // each lane's three row intervals in the window, longest first (as in force_light)
         uint32_t jb[3], je[3];
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-            jb[r] = max(L.S[r], w0);
-            je[r] = max(min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin), jb[r]);
-        }
-        const auto cswap = [&](int a, int b) {
-            const bool sw = je[b] - jb[b] > je[a] - jb[a];
-            const uint32_t tb = jb[a], te = je[a];
-            jb[a] = sw ? jb[b] : jb[a];
-            je[a] = sw ? je[b] : je[a];
-            jb[b] = sw ? tb : jb[b];
-            je[b] = sw ? te : je[b];
-        };
-        cswap(0, 1);
-        cswap(0, 2);
-        cswap(1, 2);
+        window_rows(L, w0, jb, je);
 #pragma unroll
         for (int r = 0; r < 3; r++)
             if (jb[r] < je[r]) acc = density_run(buf, w0, jb[r], je[r], pi, h2, acc);
@@ -1318,26 +1302,8 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
         }
         __builtin_amdgcn_wave_barrier();
         if (live) {
-            // each lane's three row intervals in the window, longest first: the r-th loop runs
-            // as long as the longest r-th interval over the lanes, and lanes whose long row is
-            // not the same one then share the first loop
             uint32_t jb[3], je[3];
-#pragma unroll
-            for (int r = 0; r < 3; r++) {
-                jb[r] = max(L.S[r], w0);
-                je[r] = max(min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin), jb[r]);
-            }
-            const auto cswap = [&](int a, int b) {
-                const bool sw = je[b] - jb[b] > je[a] - jb[a];
-                const uint32_t tb = jb[a], te = je[a];
-                jb[a] = sw ? jb[b] : jb[a];
-                je[a] = sw ? je[b] : je[a];
-                jb[b] = sw ? tb : jb[b];
-                je[b] = sw ? te : je[b];
-            };
-            cswap(0, 1);
-            cswap(0, 2);
-            cswap(1, 2);
+            window_rows(L, w0, jb, je);
 #pragma unroll
             for (int r = 0; r < 3; r++)
                 if (jb[r] < je[r]) force_run<2>(bp, bv, w0, jb[r], je[r], pi, p_i, K, ax, ay, az, wv);

@@ -131,4 +131,27 @@ __device__ __forceinline__ void window_indices(const LightStream& L, uint32_t w0
         j[k] = stream_index(L, min(w0 + (uint32_t)(k * kWave + lane), L.T - 1u));
 }
 
+// The lane's three row intervals clipped to the window [w0, w0 + kWin), as [jb[r], je[r]) with
+// the longest first (three compare-swaps): a wave's r-th loop then runs as long as the longest
+// r-th interval over its lanes, and lanes whose long row is not the same one share the first.
+__device__ __forceinline__ void window_rows(const LightStream& L, uint32_t w0, uint32_t jb[3],
+                                            uint32_t je[3]) {
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        jb[r] = max(L.S[r], w0);
+        je[r] = max(min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin), jb[r]);
+    }
+    const auto cswap = [&](int a, int b) {
+        const bool sw = je[b] - jb[b] > je[a] - jb[a];
+        const uint32_t tb = jb[a], te = je[a];
+        jb[a] = sw ? jb[b] : jb[a];
+        je[a] = sw ? je[b] : je[a];
+        jb[b] = sw ? tb : jb[b];
+        je[b] = sw ? te : je[b];
+    };
+    cswap(0, 1);
+    cswap(0, 2);
+    cswap(1, 2);
+}
+
 }  // namespace fh
