@@ -143,6 +143,33 @@ def copy_calibration(torch, log, mib: int = 1024) -> None:
     log(f"copy calibration: 3 launches, {mib} MiB read + {mib} MiB written each")
 
 
+def stream_ceiling(torch, log, mib: int = 1024, reps: int = 10) -> dict:
+    """A STREAM-style copy ceiling measured on this GPU: `mib` MiB read and written by one
+    device copy, median of `reps` with HIP events; GB/s counts the bytes read plus written."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    t = sorted(ts)[len(ts) // 2]
+    gbs = 2 * mib * (1 << 20) / (t * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    log(f"copy ceiling: {mib} MiB copy in {t:.3f} ms -> {gbs:.0f} GB/s")
+    return {"GBs": gbs, "bytes": 2 * mib * (1 << 20), "ms": t, "reps": reps,
+            "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+            "kernel": "torch copy_ of a 1 GiB float32 tensor (read + write counted)"}
+
+
 def cpu_info() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -316,12 +343,14 @@ def time_sort(args, fh, torch, log, keys, vals, label):
         ctx.sync()  # the next copy_ must not overlap this sort
     passes_ms = ctx.kernel_times_ms("sort")
     hist_ms = ctx.kernel_times_ms("hist")
+    # The device's pass plan (fh_sort_plan, bit p: pass p moved keys; a pass whose digit is
+    # equal for every key returns at once: c1's top byte is always 0, so 3 of the 4 passes move
+    # keys).  The timed launches are the 4 passes of each sort in order.
+    plan = ctx.sort_plan()
     ctx.close()
     t = sorted(times)[len(times) // 2]
-    # Launches of passes that moved keys (a pass whose digit is equal for every key returns at
-    # once: c1's top byte is always 0, so 3 of the 4 passes move keys).
-    moving = [x for x in passes_ms if x * 1e3 > 20.0]
-    mp = round(len(moving) / max(reps, 1))
+    moving = [x for q, x in enumerate(passes_ms) if (plan >> (q % 4)) & 1]
+    mp = bin(plan & 0xF).count("1")
     pass_us = 1e3 * sum(moving) / max(len(moving), 1)
     moved = (4 + 16 * mp) * n
     out = {
@@ -332,7 +361,7 @@ def time_sort(args, fh, torch, log, keys, vals, label):
         "alg_bytes": 68 * n, "alg_GBs": 68 * n / (t * 1e-3) / 1e9,
         "frac_of_hbm_peak": 68 * n / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
         # the bytes actually moved: the histogram read + the passes that move keys
-        "moving_passes_per_sort": mp,
+        "moving_passes_per_sort": mp, "pass_plan": plan,
         "moved_bytes": moved, "moved_GBs": moved / (t * 1e-3) / 1e9,
         "moved_frac_of_hbm_peak": moved / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "onesweep_pass_mean_us": pass_us,
@@ -527,6 +556,47 @@ def valu_block(insts, us):
             "frac": insts / (us * 1e-6) / VALU_PEAK_INSTS, "source": "profiles/valu_c3.txt"}
 
 
+# Survey bytes per particle of each neighbour pass: density reads the
+# sorted float4 positions and writes rho (20 B); force + epilogue read two float4 records and
+# write the new position, velocity and index (60 B).
+SURVEY_PASS_BYTES = {"density": 20, "force": 60}
+
+
+def roofline_block(s, dom, n, stream):
+    """The dominant pass against the HBM roofline (algorithmic bytes / its measured time), with
+    the survey's byte count beside the builder's, the measured HBM traffic, the copy ceiling
+    measured on this GPU, and the VALU issue fraction; `bound` names the resource closest to
+    its limit."""
+    p = s["pas"][dom]
+    us = p["per_substep_us"]
+    traffic = read_traffic(dom)
+    valu = valu_block(read_valu(dom), us)
+    frac = s["achieved"] / HBM_PEAK_GBS
+    dram_frac = traffic / (us * 1e-6) / 1e9 / HBM_PEAK_GBS if traffic and us else None
+    hbm_frac = max(frac, dram_frac or 0.0)
+    bound = "valu" if valu and valu["frac"] > hbm_frac else "hbm"
+    sb = SURVEY_PASS_BYTES.get(dom)
+    out = {
+        "bound": bound, "kernel": dom + " pass (" + " + ".join(p["kernels"]) + ")",
+        "achieved": s["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": frac,
+        "traffic": traffic,
+        "alg_bytes_per_launch": p["alg_bytes"], "mean_launch_us": us,
+        # the survey's per-particle bytes for the same pass (BASELINE.md section 3)
+        "survey_bytes_per_launch": sb * n if sb else None,
+        "survey_frac": sb * n / (us * 1e-6) / 1e9 / HBM_PEAK_GBS if sb and us else None,
+        "dram_frac": dram_frac,
+        # the SPH passes are limited by vector ALU issue, not HBM: VALU wave instructions of
+        # the pass (PMC, profiles/valu_c3.txt) over the time measured here, against the issue
+        # rate of 256 CUs at 2.4 GHz
+        "valu": valu,
+    }
+    if stream:
+        out["stream_ceiling_GBs"] = stream["GBs"]
+        out["frac_of_stream_ceiling"] = s["achieved"] / stream["GBs"]
+        out["stream_ceiling"] = stream
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -541,6 +611,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-sort", action="store_true", help="skip the c1 sort line")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the c2 (grid build + query) and c4 (skewed SPH pass) lines")
+    ap.add_argument("--no-stream", action="store_true", help="skip the copy-ceiling measurement")
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--sort-only", action="store_true",
                     help="only the c1 sort line (for a profile of the sort alone)")
@@ -573,6 +644,7 @@ def main(argv=None) -> int:
         print(json.dumps({"metric": "radix sort Gkeys/s (configs[1])", "sort_c1":
                           bench_sort(args, fh, torch, log)}), flush=True)
         return 0
+    stream = None if args.no_stream else stream_ceiling(torch, log)
     s = bench_sph(args, fh, torch, log)
     c0 = None if args.no_extra_configs else bench_sph_c0(args, fh, torch, log)
     sort = None if args.no_sort else bench_sort(args, fh, torch, log)
@@ -607,17 +679,7 @@ def main(argv=None) -> int:
             "particles": cfg.n, "cells": s["C"], "sort_passes": s["passes"],
             "graph_substeps": s["G"], "input_sha256": s["digest"], "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm", "kernel": dom + " pass (" + " + ".join(s["pas"][dom]["kernels"]) + ")",
-            "achieved": s["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": s["achieved"] / HBM_PEAK_GBS, "traffic": read_traffic(dom),
-            "alg_bytes_per_launch": s["pas"][dom]["alg_bytes"],
-            "mean_launch_us": s["pas"][dom]["per_substep_us"],
-            # the SPH passes are limited by vector ALU issue, not HBM: VALU wave instructions of
-            # the pass (PMC, profiles/valu_c3.txt) over the time measured here, against the
-            # issue rate of 256 CUs at 2.4 GHz
-            "valu": valu_block(read_valu(dom), s["pas"][dom]["per_substep_us"]),
-        },
+        "roofline": roofline_block(s, dom, cfg.n, stream),
         "cpu_baseline": cpu,
         "extra": {
             "c3_protocol_last_900_of_1000": s["proto"],

@@ -120,6 +120,51 @@ hipError_t sph_rebuild_resident(fh_ctx* c, const GridDesc& g, uint32_t cells, ui
 }  // namespace
 
 namespace fh {
+// Epoch renewal: every tag array back to "untagged" (0) and the epoch to 0, so the next start
+// makes it 1 again.  Queued by the host between starts (never captured).
+__global__ __launch_bounds__(256) void k_epoch_reset(Control* ctl, uint64_t* run_tag,
+                                                     uint64_t* cell_grp, uint32_t cells,
+                                                     uint32_t* skip_tag, uint32_t subs,
+                                                     uint64_t* scan_lb, uint32_t scan_tiles) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < cells; i += stride) {
+        run_tag[i] = 0ull;
+        cell_grp[i] = 0ull;
+    }
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < subs; i += stride)
+        skip_tag[i] = 0u;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < scan_tiles; i += stride)
+        scan_lb[i] = 0ull;
+    if (blockIdx.x == 0 && threadIdx.x == 0) ctl->epoch = 0u;
+}
+
+static hipError_t launch_epoch_reset(fh_ctx* c) {
+    uint32_t blocks = ceil_div(c->max_cells, 256u * 4u);
+    if (blocks > 2048u) blocks = 2048u;
+    if (blocks < 1u) blocks = 1u;
+    tbeg(c, KID_EPOCH);
+    k_epoch_reset<<<blocks, 256, 0, c->stream>>>(c->ctl, c->run_tag, c->cell_grp, c->max_cells,
+                                                 c->skip_tag, ceil_div(c->max_n, 64u), c->scan_lb,
+                                                 c->max_scan_tiles);
+    tend(c, KID_EPOCH);
+    return hipGetLastError();
+}
+
+hipError_t note_begin(fh_ctx* c) {
+    if (!c->epoch_period) return hipSuccess;
+    if (c->capturing) {  // replays are counted by fh_graph_launch
+        c->capture_begins++;
+        return hipSuccess;
+    }
+    if (c->begins + 1u > c->epoch_period) {
+        const hipError_t e = launch_epoch_reset(c);
+        if (e != hipSuccess) return e;
+        c->begins = 0;
+    }
+    c->begins++;
+    return hipSuccess;
+}
+
 int set_error(int code, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -158,6 +203,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     c->max_n = max_n;
     c->max_cells = max_cells;
     c->direct_mode = 1u;
+    c->epoch_period = kEpochPeriod;
     c->max_sort_tiles = ceil_div(max_n, (uint32_t)kSortTile);
     c->max_scan_tiles = ceil_div(max_cells, (uint32_t)kScanTile);
     size_t tot = 0;
@@ -309,6 +355,18 @@ int fh_sort_pairs(fh_ctx* c, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_
     FH_CHECK_HIP(launch_hist_keys(c, keys, n, num_bits, true));
     // In place: the last pass that runs writes the caller's buffers (see sort_plan).
     FH_CHECK_HIP(launch_sort_passes(c, keys, vals, keys, vals, n, num_bits));
+    return FH_OK;
+}
+
+int fh_sort_plan(fh_ctx* c, uint32_t* plan) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!plan) return fail(FH_EINVAL, "fh_sort_plan: null output");
+    if (c->capturing) return fail(FH_ESTATE, "fh_sort_plan: stream is being captured");
+    FH_CHECK_HIP(hipMemcpyAsync(c->h_error, &c->ctl->plan, sizeof(uint32_t),
+                                hipMemcpyDeviceToHost, c->stream));
+    FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+    *plan = *c->h_error;
     return FH_OK;
 }
 
@@ -581,6 +639,23 @@ int fh_set_option(fh_ctx* c, int option, int value) {
                             kHeavyWaves, kHeavyWavesMax);
             c->heavy_parts = (uint32_t)value;
             return FH_OK;
+        case FH_OPT_EPOCH_PERIOD:
+            if (value < 0 || (uint32_t)value > kEpochPeriod)
+                return fail(FH_EINVAL, "fh_set_option: epoch period %d outside 0..%u", value,
+                            kEpochPeriod);
+            c->epoch_period = value ? (uint32_t)value : kEpochPeriod;
+            // renew now, so the count of the new period starts from the next start
+            FH_CHECK_HIP(launch_epoch_reset(c));
+            c->begins = 0;
+            return FH_OK;
+        case FH_OPT_SPIN_LIMIT: {
+            if (value < 0) return fail(FH_EINVAL, "fh_set_option: spin limit %d < 0", value);
+            const uint32_t v = (uint32_t)value;
+            FH_CHECK_HIP(hipMemcpyAsync(&c->ctl->spin_limit, &v, sizeof(v), hipMemcpyHostToDevice,
+                                        c->stream));
+            FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+            return FH_OK;
+        }
         default:
             return fail(FH_EINVAL, "fh_set_option: unknown option %d", option);
     }
@@ -622,6 +697,7 @@ int fh_graph_begin(fh_ctx* c) {
     if (c->capturing) return fail(FH_ESTATE, "fh_graph_begin: already capturing");
     FH_CHECK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
     c->capturing = true;
+    c->capture_begins = 0;
     return FH_OK;
 }
 
@@ -642,6 +718,8 @@ int fh_graph_end(fh_ctx* c) {
     if (c->graph) (void)hipGraphDestroy(c->graph);
     c->graph = graph;
     c->exec = exec;
+    c->graph_begins = c->capture_begins;
+    c->capture_begins = 0;
     FH_CHECK_HIP(hipGraphUpload(c->exec, c->stream));
     return FH_OK;
 }
@@ -651,7 +729,17 @@ int fh_graph_launch(fh_ctx* c, uint32_t count) {
     if (rc) return rc;
     if (!c->exec) return fail(FH_ESTATE, "fh_graph_launch: no captured graph");
     if (c->capturing) return fail(FH_ESTATE, "fh_graph_launch: stream is being captured");
-    for (uint32_t q = 0; q < count; q++) FH_CHECK_HIP(hipGraphLaunch(c->exec, c->stream));
+    // Each replay starts graph_begins sorts / rebuilds: renew the epoch between replays before
+    // the count since the last renewal would pass the period.
+    for (uint32_t q = 0; q < count; q++) {
+        if (c->epoch_period && c->graph_begins &&
+            c->begins + c->graph_begins > c->epoch_period) {
+            FH_CHECK_HIP(launch_epoch_reset(c));
+            c->begins = 0;
+        }
+        FH_CHECK_HIP(hipGraphLaunch(c->exec, c->stream));
+        c->begins += c->graph_begins;
+    }
     return FH_OK;
 }
 
@@ -666,7 +754,8 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
 static const char* const kKernelNames[KID_COUNT] = {"hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
                                                     "finalize", "runs", "plan", "prep",
-                                                    "density_pass", "force_pass"};
+                                                    "density_pass", "force_pass",
+                                                    "epoch_reset"};
 
 static int kernel_id(const char* name) {
     if (!name) return -1;

@@ -99,6 +99,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_starts(const uint64_t* __
         } else {
             lb_store(my, lb_word(kLbAggregate, epoch, total));
             uint32_t t = tile - 1u, spins = 0;
+            const uint32_t limit = ctl->spin_limit ? ctl->spin_limit : kSpinLimit;
             for (;;) {
                 const uint64_t w = lb_load(lookback + t);
                 const uint64_t st = w & (3ull << 62);
@@ -110,13 +111,14 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_starts(const uint64_t* __
                         break;
                     }
                     t--;
-                } else {
-                    if (++spins >= kSpinLimit) {
-                        atomicOr(&ctl->error.v, 1u);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
                 }
+                // every poll counts (a walk over the most scan tiles needs at most 2^20 of them)
+                if (++spins >= limit) {
+                    atomicOr(&ctl->error.v, 1u);
+                    break;
+                }
+                if (!(st != 0 && ((uint32_t)(w >> 32) & kEpochMask) == epoch))
+                    __builtin_amdgcn_s_sleep(1);
             }
             lb_store(my, lb_word(kLbInclusive, epoch, min(prefix, total)));
         }

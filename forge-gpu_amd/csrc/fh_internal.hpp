@@ -112,7 +112,8 @@ struct Line {
 struct Control {
     uint32_t epoch;                     // bumped by k_begin before each sort / scan
     uint32_t plan;                      // bit p: sort pass p runs (written by pass 0)
-    uint32_t pad0[30];
+    uint32_t spin_limit;                // look-back polls before giving up (0: kSpinLimit)
+    uint32_t pad0[29];
     Line error;                         // nonzero: a look-back spin limit was hit
     Line tile_ctr[kMaxPasses];          // dynamic tile ids of the sort passes
     Line scan_ctr;                      // dynamic tile id of the cell scan
@@ -153,7 +154,7 @@ inline DivU32 make_divu32(uint32_t d) {
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
 enum KernelId { KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
                 KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_PREP, KID_DPASS,
-                KID_FPASS, KID_COUNT };
+                KID_FPASS, KID_EPOCH, KID_COUNT };
 
 // Event pairs bracketing the first `max` launches of one kernel after it was armed; when the
 // launches are captured, every replay of the graph re-records the same events.
@@ -217,6 +218,13 @@ struct fh_ctx {
     uint32_t direct_mode; // FH_OPT_DIRECT_ITEMS: 0 never, 1 automatic (default), 2 always
     uint32_t heavy_parts; // FH_OPT_HEAVY_PARTS (0: kHeavyWaves)
     uint32_t* h_error;   // pinned host word for the device error flag
+    // Epoch renewal.  Tags compare 30-bit epochs, so a tag left 2^30 - 1 starts ago would match
+    // again; the host counts the starts it queues (graph replays included) and, before the
+    // count reaches epoch_period, queues k_epoch_reset (tags cleared, epoch back to 0).
+    uint32_t epoch_period;   // 0: no renewal (the no-alloc sort, which reads no tags)
+    uint64_t begins;         // starts queued since the last renewal
+    uint32_t capture_begins; // starts recorded by the capture in progress
+    uint32_t graph_begins;   // starts per replay of the instantiated graph
     size_t scratch_bytes;
     hipGraph_t graph;
     hipGraphExec_t exec;
@@ -331,6 +339,10 @@ inline void tend(fh_ctx* c, KernelId k, hipStream_t s = nullptr) {
 
 // Sets the thread-local message fh_last_error() returns; returns `code`.
 int set_error(int code, const char* fmt, ...);
+// Account for one start of a sort / rebuild about to be queued (renews the epoch when due).
+hipError_t note_begin(fh_ctx* c);
+// Default renewal period: every tag epoch stays below the 30-bit wrap.
+constexpr uint32_t kEpochPeriod = kEpochMask - 1u;
 
 // ---- launchers (host side, enqueue on ctx->stream; return hipError_t) ------------------------
 

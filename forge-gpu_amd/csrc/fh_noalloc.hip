@@ -16,6 +16,8 @@
 // calls that follow one another on a stream need nothing else, while calls that overlap on
 // one GPU (different streams, or threads) race on the array and must not be issued.
 #include <mutex>
+#include <stddef.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "fh_internal.hpp"
@@ -56,7 +58,9 @@ bool g_gfx950[kMaxDevices];
 
 }  // namespace
 
-// Address of this device's copy of `scratch` (device `dev` current), resolved once.
+// Address of this device's copy of `scratch` (device `dev` current), resolved once.  The
+// FH_DEBUG_SPIN_LIMIT environment variable (diagnostics and tests only) sets the look-back
+// poll limit of the sorts on this device at that point, like FH_OPT_SPIN_LIMIT for a context.
 static int scratch_of(int dev, unsigned char** base) {
     if (dev < 0 || dev >= kMaxDevices) return FH_ENODEV;
     std::lock_guard<std::mutex> lock(g_mu);
@@ -70,6 +74,12 @@ static int scratch_of(int dev, unsigned char** base) {
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return (int)e;
         if (!p) return (int)hipErrorInvalidSymbol;
+        if (const char* lim = getenv("FH_DEBUG_SPIN_LIMIT")) {
+            const uint32_t v = (uint32_t)strtoul(lim, nullptr, 10);
+            e = hipMemcpy((unsigned char*)p + kOffCtl + offsetof(Control, spin_limit), &v,
+                          sizeof(v), hipMemcpyHostToDevice);
+            if (e != hipSuccess) return (int)e;
+        }
         g_base[dev] = (unsigned char*)p;
     }
     *base = g_base[dev];
@@ -112,4 +122,35 @@ extern "C" int fh_sort_pairs_noalloc(void* stream, uint32_t* keys, uint32_t* val
     if (e != hipSuccess)
         return set_error((int)e, "fh_sort_pairs_noalloc: %s (%d)", hipGetErrorString(e), (int)e);
     return FH_OK;
+}
+
+// The device error flag of this device's fixed scratch (raised by a look-back that gave up):
+// read after the caller's stream drains, then cleared, so each failure is reported once.
+extern "C" int fh_noalloc_status(void* stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error((int)e, "fh_noalloc_status: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(FH_ENODEV, "fh_noalloc_status: device %d", dev);
+    unsigned char* base;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        base = g_base[dev];
+    }
+    if (!base) return FH_OK;  // no no-alloc sort has run on this device
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing((hipStream_t)stream, &cs);
+    if (e == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return set_error(FH_ESTATE, "fh_noalloc_status: the stream is being captured");
+    e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return set_error((int)e, "fh_noalloc_status: %s", hipGetErrorString(e));
+    unsigned char* flag = base + kOffCtl + offsetof(Control, error);
+    uint32_t word = 0;
+    e = hipMemcpy(&word, flag, sizeof(word), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return set_error((int)e, "fh_noalloc_status: %s", hipGetErrorString(e));
+    if (!word) return FH_OK;
+    const uint32_t zero = 0;
+    e = hipMemcpy(flag, &zero, sizeof(zero), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return set_error((int)e, "fh_noalloc_status: %s", hipGetErrorString(e));
+    return set_error(FH_ESTATE, "fh_noalloc_status: a no-alloc sort on device %d gave up in its "
+                     "look-back (code %u); its output is wrong", dev, word);
 }

@@ -318,6 +318,10 @@ static uint32_t hist_blocks(uint32_t n) {
 
 hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_t num_bits,
                             bool begin) {
+    if (begin) {
+        const hipError_t e = note_begin(c);
+        if (e != hipSuccess) return e;
+    }
     const Digits L = digits_for(num_bits, n);
     const uint32_t blocks = hist_blocks(n), top = (1u << L.top_bits) - 1u;
     const Begin bg = make_begin(c, begin, n, num_bits);
@@ -342,6 +346,10 @@ hipError_t launch_hist_keys(fh_ctx* c, const uint32_t* keys, uint32_t n, uint32_
 hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const float* z,
                             uint32_t stride, uint32_t n, const GridDesc& g, uint32_t num_bits,
                             uint32_t* keys_out, uint32_t* vals_out, bool begin) {
+    if (begin) {
+        const hipError_t e = note_begin(c);
+        if (e != hipSuccess) return e;
+    }
     const Digits L = digits_for(num_bits, n);
     const uint32_t blocks = hist_blocks(n), top = num_bits ? (1u << L.top_bits) - 1u : 0u;
     const Begin bg = make_begin(c, begin, n, num_bits);
@@ -489,13 +497,14 @@ __device__ __forceinline__ void lb_publish(uint32_t* w, uint32_t st, const uint3
 // w[t * NB] for tile t: the words of the kLbWin tiles below `t` are loaded together (one round
 // trip instead of kLbWin), then consumed nearest first: aggregates are summed into prefix until
 // an inclusive prefix ends the walk; a word not yet published stops the window and is polled
-// again.  Tiles below 0 are never read (tile 0 publishes inclusive); a bounded poll keeps every
-// wave finite and raises the device error flag instead.
+// again.  Tiles below 0 are never read (tile 0 publishes inclusive); a bounded number of polls
+// keeps every wave finite and raises the device error flag instead.
 template <int DPT>
 __device__ __forceinline__ void lb_walk(const uint32_t* __restrict__ w, uint32_t NB, uint32_t tile,
                                         uint32_t (&prefix)[DPT], Control* ctl) {
     using Word = typename std::conditional<DPT == 1, uint32_t, uint64_t>::type;
     uint32_t t = tile, spins = 0;  // the walk continues at tile t - 1
+    const uint32_t limit = ctl->spin_limit ? ctl->spin_limit : kSpinLimit;
     for (;;) {
         Word x[kLbWin];
 #pragma unroll
@@ -523,13 +532,12 @@ __device__ __forceinline__ void lb_walk(const uint32_t* __restrict__ w, uint32_t
             atomicOr(&ctl->error.v, 2u);
             break;
         }
-        if (adv == 0) {
-            if (++spins >= kSpinLimit) {
-                atomicOr(&ctl->error.v, 1u);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+        // every poll counts (a walk over the most tiles of a context needs < 2^15 of them)
+        if (++spins >= limit) {
+            atomicOr(&ctl->error.v, 1u);
+            break;
         }
+        if (adv == 0) __builtin_amdgcn_s_sleep(1);
     }
 }
 

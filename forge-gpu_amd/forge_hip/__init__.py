@@ -7,8 +7,9 @@ SPH / gravity / integrate / box modules).  Importing it never loads a CPU fallba
 none.
 """
 from ._lib import (FH_EINVAL, FH_ENODEV, FH_EPI_BOX, FH_EPI_GRAVITY, FH_EPI_INTEGRATE,
-                   FH_ERANGE, FH_ESTATE, FH_OK, FH_OPT_DIRECT_ITEMS, FH_OPT_HEAVY_PARTS, FH_OPT_HEAVY_WORK,
-                   FH_OPT_SPH_EXACT, ForgeError, LibraryNotBuilt, load)
+                   FH_ERANGE, FH_ESTATE, FH_OK, FH_OPT_DIRECT_ITEMS, FH_OPT_EPOCH_PERIOD,
+                   FH_OPT_HEAVY_PARTS, FH_OPT_HEAVY_WORK, FH_OPT_SPH_EXACT, FH_OPT_SPIN_LIMIT,
+                   ForgeError, LibraryNotBuilt, load)
 from .hashgrid import HashGrid, RadixSorter, cell_start_csr, find_cell_boundaries
 from .modules import (BoxColliderModule, FieldSet, GravityModule, IntegrateModule, Pipeline,
                       SimModule, SphDensityModule, SphFusedModule, SphPressureModule,
@@ -18,7 +19,9 @@ from .runtime import Context, default_context, from_u32, to_u32, u32_empty
 
 __all__ = [
     "FH_OK", "FH_EINVAL", "FH_ERANGE", "FH_ESTATE", "FH_ENODEV", "FH_EPI_GRAVITY",
-    "FH_EPI_INTEGRATE", "FH_EPI_BOX", "FH_OPT_SPH_EXACT", "FH_OPT_HEAVY_WORK", "FH_OPT_DIRECT_ITEMS", "FH_OPT_HEAVY_PARTS", "ForgeError", "LibraryNotBuilt", "load", "HashGrid",
+    "FH_EPI_INTEGRATE", "FH_EPI_BOX", "FH_OPT_SPH_EXACT", "FH_OPT_HEAVY_WORK",
+    "FH_OPT_DIRECT_ITEMS", "FH_OPT_HEAVY_PARTS", "FH_OPT_EPOCH_PERIOD", "FH_OPT_SPIN_LIMIT",
+    "ForgeError", "LibraryNotBuilt", "load", "HashGrid",
     "RadixSorter", "find_cell_boundaries", "cell_start_csr", "FieldSet", "SimModule", "Pipeline",
     "SphDensityModule", "SphFusedModule", "SphPressureModule", "SphViscosityModule",
     "GravityModule", "IntegrateModule",

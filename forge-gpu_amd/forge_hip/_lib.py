@@ -28,6 +28,8 @@ FH_OPT_SPH_EXACT = 1
 FH_OPT_HEAVY_WORK = 2
 FH_OPT_DIRECT_ITEMS = 3
 FH_OPT_HEAVY_PARTS = 4
+FH_OPT_EPOCH_PERIOD = 5
+FH_OPT_SPIN_LIMIT = 6
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -87,7 +89,9 @@ SIGNATURES = {
     "fh_scratch_bytes": (ctypes.c_size_t, [_P]),
     "fh_hash_cells": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P]),
     "fh_sort_pairs": (_I, [_P, _P, _P, _U32, _U32]),
+    "fh_sort_plan": (_I, [_P, ctypes.POINTER(_U32)]),
     "fh_sort_pairs_noalloc": (_I, [_P, _P, _P, _U32, _U32]),
+    "fh_noalloc_status": (_I, [_P]),
     "fh_find_cell_boundaries": (_I, [_P, _P, _U32, _U32, _P, _P]),
     "fh_cell_start_csr": (_I, [_P, _P, _U32, _U32, _P]),
     "fh_hashgrid_build": (_I, [_P, _P, _P, _P, _U32, _U32, _F32, _F3, _U3, _P, _P, _P]),

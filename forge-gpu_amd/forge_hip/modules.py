@@ -596,9 +596,10 @@ def run_streaming(pipeline: Pipeline, fields: FieldSet, dt: float, total_steps: 
     """run_manifest_streaming's loop (manifest_runner.rs:145-181): each step runs `substeps`
     substeps; after step s with s % frame_interval == 0 (interval at least 1) the frame
     (u32 frame number, u32 count, interleaved f32 positions) is packed on the device, copied
-    into pinned host memory and passed to on_frame(frame_number, frame) as a uint8 array (the
-    positions are frame[8:].view(float32)).  Returns the final positions (interleaved), count,
-    substeps run and elapsed seconds, as SimResult does."""
+    into pinned host memory and passed to on_frame(frame_number, frame) as a uint8 array of its
+    own (the positions are frame[8:].view(float32)): the callback may keep it, as the Rust
+    mirror's callback receives the frame by value.  Returns the final positions (interleaved),
+    count, substeps run and elapsed seconds, as SimResult does."""
     import time
 
     n = fields.particle_count
@@ -617,7 +618,8 @@ def run_streaming(pipeline: Pipeline, fields: FieldSet, dt: float, total_steps: 
             with torch.cuda.stream(ctx.torch_stream()):
                 host.copy_(dev, non_blocking=True)
             ctx.sync()
-            on_frame(frame_num, host.numpy())
+            # a copy: the pinned staging buffer is reused by the next frame
+            on_frame(frame_num, host.numpy().copy())
             frame_num += 1
     ctx.sync()
     elapsed = time.perf_counter() - start

@@ -97,6 +97,12 @@ class Context:
         check(_lib.load().fh_event_elapsed_ms(self.handle, int(a), int(b), ctypes.byref(ms)))
         return float(ms.value)
 
+    def sort_plan(self) -> int:
+        """Bit p set: digit pass p of the last sort moved data (fh_sort_plan; synchronises)."""
+        v = ctypes.c_uint32()
+        check(_lib.load().fh_sort_plan(self.handle, ctypes.byref(v)))
+        return int(v.value)
+
     def set_option(self, option: int, value: int) -> None:
         """fh_set_option, e.g. set_option(FH_OPT_SPH_EXACT, 1) for the bit-exact SPH passes."""
         check(_lib.load().fh_set_option(self.handle, int(option), int(value)))

@@ -16,7 +16,7 @@
 
 use std::os::raw::{c_char, c_int, c_void};
 
-pub const FH_ABI_VERSION: c_int = 2;
+pub const FH_ABI_VERSION: c_int = 3;
 
 pub const FH_OK: c_int = 0;
 pub const FH_EINVAL: c_int = -1;
@@ -32,6 +32,8 @@ pub const FH_OPT_SPH_EXACT: c_int = 1;
 pub const FH_OPT_HEAVY_WORK: c_int = 2;
 pub const FH_OPT_DIRECT_ITEMS: c_int = 3;
 pub const FH_OPT_HEAVY_PARTS: c_int = 4;
+pub const FH_OPT_EPOCH_PERIOD: c_int = 5;
+pub const FH_OPT_SPIN_LIMIT: c_int = 6;
 
 pub const FH_NOALLOC_MAX_N: u32 = 1_048_576;
 pub const FH_NOALLOC_SCRATCH_BYTES: u32 = 19_939_328;
@@ -83,8 +85,10 @@ extern "C" {
                          dims: *const u32, keys: *mut u32, vals: *mut u32) -> c_int;
     pub fn fh_sort_pairs(ctx: *mut fh_ctx, keys: *mut u32, vals: *mut u32, n: u32,
                          num_bits: u32) -> c_int;
+    pub fn fh_sort_plan(ctx: *mut fh_ctx, plan: *mut u32) -> c_int;
     pub fn fh_sort_pairs_noalloc(stream: *mut c_void, keys: *mut u32, vals: *mut u32, n: u32,
                                  num_bits: u32) -> c_int;
+    pub fn fh_noalloc_status(stream: *mut c_void) -> c_int;
     pub fn fh_find_cell_boundaries(ctx: *mut fh_ctx, sorted_keys: *const u32, n: u32,
                                    num_cells: u32, cell_start: *mut u32,
                                    cell_end: *mut u32) -> c_int;

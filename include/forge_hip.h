@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 2
+#define FH_ABI_VERSION 3
 
 /* ---- status codes (negative: argument errors detected on the host) ------------------------- */
 #define FH_OK 0
@@ -117,6 +117,11 @@ int fh_hash_cells(fh_ctx* ctx, const float* x, const float* y, const float* z, u
  * required num_bits % 4 == 0 and panicked on n > max_n; here any 1..32 is accepted and
  * n > max_n returns FH_ERANGE.  Equal keys keep their input order. */
 int fh_sort_pairs(fh_ctx* ctx, uint32_t* keys, uint32_t* vals, uint32_t n, uint32_t num_bits);
+/* The pass plan of the context's last sort (fh_sort_pairs, or the sort of a build / rebuild):
+ * bit p set = digit pass p moved data; a pass whose digit is equal for every key is skipped
+ * (for example the top byte of keys below 2^24).  No counterpart in the reference (whose every
+ * 4-bit pass runs); for measurement.  Synchronises the stream. */
+int fh_sort_plan(fh_ctx* ctx, uint32_t* plan);
 
 /* fh_sort_pairs without a context, for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
@@ -132,6 +137,13 @@ int fh_sort_pairs(fh_ctx* ctx, uint32_t* keys, uint32_t* vals, uint32_t n, uint3
 #define FH_NOALLOC_SCRATCH_BYTES 19939328u
 int fh_sort_pairs_noalloc(void* stream, uint32_t* keys, uint32_t* vals, uint32_t n,
                           uint32_t num_bits);
+/* Device-side status of the no-alloc sorts on the current device: waits for `stream` (NULL: the
+ * null stream), then reads and clears the device error flag of the fixed scratch.  FH_OK when
+ * no no-alloc sort on this device gave up in a look-back since the last query (or none ran);
+ * FH_ESTATE when one did (its output is wrong; fh_last_error() names the failure).  Like
+ * fh_sync for a context, it is not legal during stream capture.  Allocates nothing (a 4-byte
+ * copy each way). */
+int fh_noalloc_status(void* stream);
 
 /* From keys sorted ascending: cell_start[c] = first i with key c, cell_end[c] = last i + 1;
  * cells with no key keep cell_start = 0xFFFFFFFF, cell_end = 0.  Keys >= num_cells are
@@ -272,6 +284,20 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * faster with 8), fewer cost less per item (c3 is ~2 % faster with 4).  Results differ only by
  * rounding. */
 #define FH_OPT_HEAVY_PARTS 4
+/* FH_OPT_EPOCH_PERIOD = 5: the work tags of the rebuilds (co-located groups, skipped sub-tiles,
+ * cell runs, scan look-back) compare a 30-bit epoch that every sort / rebuild start bumps on the
+ * device, so a tag left 2^30 - 1 starts earlier would match again.  The context counts the
+ * starts it queues (graph replays included) and, before the count reaches the period, queues a
+ * renewal (tags cleared, epoch back to 0) between two calls or replays.  value = the period in
+ * starts (1..2^30 - 2; 0 restores the default 2^30 - 2); setting it renews at once.  Short
+ * periods exercise the renewal in tests; results do not change. */
+#define FH_OPT_EPOCH_PERIOD 5
+/* FH_OPT_SPIN_LIMIT = 6 (diagnostics): polls a radix-sort or scan look-back walk makes before
+ * it gives up and raises the device error flag that fh_sync reports (0 restores the default,
+ * 2^22, far above what any walk needs).  A limit of 1 forces that failure path without a fault
+ * (every walk that needs a second poll gives up; the scatter stays in bounds, the output is
+ * wrong and fh_sync returns FH_ESTATE).  Synchronises the stream. */
+#define FH_OPT_SPIN_LIMIT 6
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
 /* GravityModule (gravity.rs:31-34): v += g * dt. */
@@ -315,8 +341,9 @@ int fh_event_record(fh_ctx* ctx, uint32_t slot);
 int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
 
 /* Per-kernel timing.  Arm kernel `name` (one of "hist", "hash", "scan", "sort",
- * "gather", "density", "force", "query", "finalize", "runs", "plan", "prep"; or a whole fast
- * pass of fh_sph_fused, "density_pass" or "force_pass", from its first launch to its last) so
+ * "gather", "density", "force", "query", "finalize", "runs", "plan", "prep", "epoch_reset";
+ * or a whole fast pass of fh_sph_fused, "density_pass" or "force_pass", from its first launch
+ * to its last) so
  * that its next
  * `max_launches` launches on the
  * context stream are bracketed by HIP events; launches captured into a graph record the events

@@ -28,7 +28,7 @@ def test_ctypes_signatures_match_header(fh):
 
 
 def test_abi_version(fh):
-    assert fh.load().fh_abi_version() == 2
+    assert fh.load().fh_abi_version() == 3
 
 
 def test_null_context_is_an_argument_error(fh):

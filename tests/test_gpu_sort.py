@@ -23,6 +23,19 @@ def xorshift32(seed, n, mask):
     return out
 
 
+def expected_plan(keys, digit_bits, passes):
+    """The passes an in-place sort runs: those whose digit is not the same for every key; when
+    that is exactly one of two or more passes, its neighbour runs as well (a copy), so the
+    second of the two writes the caller's arrays (sort_plan in fh_sort.hip)."""
+    m = (1 << digit_bits) - 1
+    plan = sum(1 << p for p in range(passes)
+               if np.unique((keys >> (digit_bits * p)) & m).size > 1)
+    if bin(plan).count("1") == 1 and passes >= 2:
+        p = plan.bit_length() - 1
+        plan |= 1 << (p - 1 if p > 0 else 1)
+    return plan
+
+
 def gpu_sort(fh, ctx, keys, vals, bits):
     k = fh.from_u32(keys)
     v = fh.from_u32(vals)
@@ -102,6 +115,9 @@ def test_sort_skips_identity_passes(fh, gpu_ctx, oracle, case):
     k, v = gpu_sort(fh, gpu_ctx, keys, vals, 32)
     ok, ov = oracle.stable_sort_pairs(keys, vals, 32)
     assert np.array_equal(k, ok) and np.array_equal(v, ov)
+    # the device's pass plan (fh_sort_plan)
+    want = expected_plan(keys, 8, 4)
+    assert gpu_ctx.sort_plan() == want, (case, gpu_ctx.sort_plan(), want)
 
 
 @pytest.mark.parametrize("case", ["all_equal", "low_digit_constant", "high_digit_constant",
@@ -123,6 +139,8 @@ def test_sort_skips_identity_passes_wide(fh, gpu_ctx, oracle, case):
     k, v = gpu_sort(fh, gpu_ctx, keys, vals, 20)
     ok, ov = oracle.stable_sort_pairs(keys, vals, 20)
     assert np.array_equal(k, ok) and np.array_equal(v, ov)
+    want = expected_plan(keys & 0xFFFFF, 10, 2)
+    assert gpu_ctx.sort_plan() == want, (case, gpu_ctx.sort_plan(), want)
 
 
 def test_sort_back_to_back_sizes(fh, gpu_ctx, oracle):

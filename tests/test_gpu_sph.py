@@ -372,14 +372,16 @@ def test_standalone_modules_match_oracle(fh, gpu_ctx, oracle):
         assert np.array_equal(gpu, o), nm
 
 
-def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle):
+@pytest.mark.parametrize("parts", [4, 8])
+def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts):
     """configs[4] at full size (8,388,608 particles, 64 Gaussian clumps + 10 % uniform, cells of
     0 to ~27,000 particles): one HashGrid build (bit-exact), then one fused SPH pass.  The full
     CPU passes would take ~1.3e11 candidate tests each, so the oracle evaluates a sample: 4096
     random particles, 512 of the densest cell and 512 of the sparsest occupied cells.  Density
     is checked against or_sph_density_at (rel 1e-4); the acceleration against
     or_sph_force_f64_at evaluated on the GPU's densities (themselves checked on the sample),
-    within 1e-4 * sum|pair terms|.  Random velocities make the viscosity term non-zero."""
+    within 1e-4 * sum|pair terms|.  Random velocities make the viscosity term non-zero.
+    parts: wavefronts per heavy item (FH_OPT_HEAVY_PARTS), the default and the bench's."""
     from forge_hip import workloads
     cfg = workloads.config4()
     n = cfg.n
@@ -402,9 +404,14 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle):
     m.accel = accel
     p.add(m)
     torch.cuda.synchronize()
-    print(f"c4 fused pass: max occupancy {occ.max()}, p99 {np.percentile(occ, 99):.0f}",
-          flush=True)
-    p.step(f, cfg.dt)
+    print(f"c4 fused pass ({parts} parts): max occupancy {occ.max()}, "
+          f"p99 {np.percentile(occ, 99):.0f}", flush=True)
+    ctx = f.context(cfg.num_cells)
+    ctx.set_option(fh.FH_OPT_HEAVY_PARTS, parts)
+    try:
+        p.step(f, cfg.dt)
+    finally:
+        ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
     rho = f.f32_fields["density"].cpu().numpy()
     acc = accel.cpu().numpy().astype(np.float64)
     dense = int(np.argmax(occ))
