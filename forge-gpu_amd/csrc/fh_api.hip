@@ -124,8 +124,7 @@ namespace fh {
 // makes it 1 again.  Queued by the host between starts (never captured).
 __global__ __launch_bounds__(256) void k_epoch_reset(Control* ctl, uint64_t* run_tag,
                                                      uint64_t* cell_grp, uint32_t cells,
-                                                     uint32_t* skip_tag, uint32_t subs,
-                                                     uint64_t* scan_lb, uint32_t scan_tiles) {
+                                                     uint32_t* skip_tag, uint32_t subs) {
     const uint32_t stride = gridDim.x * blockDim.x;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < cells; i += stride) {
         run_tag[i] = 0ull;
@@ -133,8 +132,6 @@ __global__ __launch_bounds__(256) void k_epoch_reset(Control* ctl, uint64_t* run
     }
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < subs; i += stride)
         skip_tag[i] = 0u;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < scan_tiles; i += stride)
-        scan_lb[i] = 0ull;
     if (blockIdx.x == 0 && threadIdx.x == 0) ctl->epoch = 0u;
 }
 
@@ -144,8 +141,7 @@ static hipError_t launch_epoch_reset(fh_ctx* c) {
     if (blocks < 1u) blocks = 1u;
     tbeg(c, KID_EPOCH);
     k_epoch_reset<<<blocks, 256, 0, c->stream>>>(c->ctl, c->run_tag, c->cell_grp, c->max_cells,
-                                                 c->skip_tag, ceil_div(c->max_n, 64u), c->scan_lb,
-                                                 c->max_scan_tiles);
+                                                 c->skip_tag, ceil_div(c->max_n, 64u));
     tend(c, KID_EPOCH);
     return hipGetLastError();
 }
@@ -205,7 +201,6 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     c->direct_mode = 1u;
     c->epoch_period = kEpochPeriod;
     c->max_sort_tiles = ceil_div(max_n, (uint32_t)kSortTile);
-    c->max_scan_tiles = ceil_div(max_cells, (uint32_t)kScanTile);
     size_t tot = 0;
     hipError_t e = hipSuccess;
     if (e == hipSuccess) e = alloc(&c->ka, max_n, &tot);
@@ -220,7 +215,6 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
     if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);
-    if (e == hipSuccess) e = alloc(&c->scan_lb, c->max_scan_tiles, &tot);
     if (e == hipSuccess) e = alloc(&c->skeys, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sidx, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->spos, max_n, &tot);
@@ -233,10 +227,12 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
-    // partial sums of the heavy parts: per list slot, kHeavyWavesMax parts x kHeavyComps x 64 lanes
+    // partial sums of the heavy parts: per list slot, kHeavyWaves parts x kHeavyComps x 64 lanes
+    // (room for kHeavyWavesMax parts is made when FH_OPT_HEAVY_PARTS asks for it)
+    c->hpart_parts = kHeavyWaves;
     if (e == hipSuccess)
         e = alloc(&c->hpart,
-                  (size_t)kHeavyLists * c->heavy_cap * kHeavyWavesMax * kHeavyComps * 64u, &tot);
+                  (size_t)kHeavyLists * c->heavy_cap * kHeavyWaves * kHeavyComps * 64u, &tot);
     if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess)
         e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);
@@ -261,7 +257,6 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     // One-time clears (outside any capture): look-back words and run tags start untagged
     // (epoch 0 is never current).
     if (e == hipSuccess) e = hipMemsetAsync(c->sort_lb, 0, (size_t)c->max_sort_tiles * kDigitSlots * 4u, c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(c->scan_lb, 0, (size_t)c->max_scan_tiles * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->ctl, 0, sizeof(Control), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->run_tag, 0, (size_t)max_cells * 8u, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->cell_grp, 0, (size_t)max_cells * 8u, c->stream);
@@ -296,7 +291,7 @@ int fh_destroy(fh_ctx* c) {
         }
     }
     void* bufs[] = {c->ka, c->va, c->kb, c->vb, c->sort_lb, c->ctl, c->run_tag,
-                    c->cell_start, c->scan_lb, c->skeys, c->sidx, c->spos, c->svel,
+                    c->cell_start, c->skeys, c->sidx, c->spos, c->svel,
                     c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hpart, c->hslot, c->lstream, c->lstream_t, c->hist_part,
                     c->sort_pre,
                     c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout,
@@ -407,11 +402,14 @@ int fh_hashgrid_build(fh_ctx* c, const float* x, const float* y, const float* z,
     if ((rc = check_grid(c, cell_size, origin, dims, &g, &cells, "fh_hashgrid_build"))) return rc;
     const uint32_t bits = bits_for_cells(cells);
     FH_CHECK_HIP(launch_hash_hist(c, x, y, z, stride, n, g, bits, cell_indices, nullptr, true));
-    if (n > 0) {
+    if (n > 0)
         FH_CHECK_HIP(launch_sort_passes(c, cell_indices, nullptr, c->skeys, sorted_indices, n, bits));
-        FH_CHECK_HIP(launch_runs(c, c->skeys, n));
-    }
-    FH_CHECK_HIP(launch_scan_starts(c, cells, n, cell_start));
+    // CSR straight from the sorted keys (each run start fills the empty cells before it): no
+    // count, no scan
+    tbeg(c, KID_SCAN);
+    const hipError_t e = launch_csr_from_sorted(c, c->skeys, n, cells, cell_start);
+    tend(c, KID_SCAN);
+    FH_CHECK_HIP(e);
     return FH_OK;
 }
 
@@ -637,6 +635,21 @@ int fh_set_option(fh_ctx* c, int option, int value) {
             if (value != 0 && value != kHeavyWaves && value != kHeavyWavesMax)
                 return fail(FH_EINVAL, "fh_set_option: heavy parts %d is not 0, %d or %d", value,
                             kHeavyWaves, kHeavyWavesMax);
+            if ((uint32_t)value > c->hpart_parts) {
+                // the partial sums of every heavy list slot for `value` parts: a larger buffer,
+                // made once (outside capture, checked above)
+                const size_t words = (size_t)kHeavyLists * c->heavy_cap * (uint32_t)value *
+                                     kHeavyComps * 64u;
+                FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+                float* p = nullptr;
+                const hipError_t ae = hipMalloc((void**)&p, words * sizeof(float));
+                if (ae != hipSuccess) return hip_fail(ae, "fh_set_option: heavy part buffer");
+                (void)hipFree(c->hpart);
+                c->scratch_bytes += (words - (size_t)kHeavyLists * c->heavy_cap * c->hpart_parts *
+                                                 kHeavyComps * 64u) * sizeof(float);
+                c->hpart = p;
+                c->hpart_parts = (uint32_t)value;
+            }
             c->heavy_parts = (uint32_t)value;
             return FH_OK;
         case FH_OPT_EPOCH_PERIOD:
@@ -753,7 +766,7 @@ int fh_event_record(fh_ctx* c, uint32_t slot) {
 
 static const char* const kKernelNames[KID_COUNT] = {"hist", "hash", "scan", "sort",
                                                     "gather", "density", "force", "query",
-                                                    "finalize", "runs", "plan", "prep",
+                                                    "finalize", "plan", "prep",
                                                     "density_pass", "force_pass",
                                                     "epoch_reset"};
 

@@ -1,13 +1,9 @@
-// fh_grid.hip -- cell ranges and the 3x3x3 neighbour query for gfx950.
+// fh_grid.hip -- cell ranges and the 3x3x3 neighbour query for gfx950.  (The CSR cell_start
+// of HashGrid::build comes from the sorted keys directly, k_csr_from_sorted in fh_sph.hip.)
 //
-//   k_runs +       CSR cell_start[0..C] (hashgrid.rs:95-106) from the sorted keys: the first
-//   k_scan_starts  index of each key run is tagged at its cell, then a single-pass reverse
-//                  minimum scan with a decoupled look-back fills every cell with the first
-//                  sorted index at or after it (no atomics per particle, no clearing: the tags
-//                  carry the build's epoch, so the build is graph-safe).
 //   k_fill_u32 +   find_cell_boundaries (radix_sort.rs:229-317): sentinel fill, then one
 //   k_boundaries   thread per sorted key marks the first / last index of its run.
-//   k_nbr_query    HashGrid::query_neighbors (hashgrid.rs:145-193) for every point of a built
+//   k_nbr_stream   HashGrid::query_neighbors (hashgrid.rs:145-193) for every point of a built
 //                  grid: the 3 x-adjacent cells of one (dy, dz) row are contiguous in the
 //                  sorted order, so the 27-cell walk is 9 contiguous ranges visited in the
 //                  reference's dz, dy, dx order.
@@ -15,136 +11,6 @@
 #include "fh_stream.hpp"
 
 namespace fh {
-
-// Run marking: the first sorted index of every run of equal keys is stored, tagged with the
-// current epoch, at run_tag[key] (untagged cells hold no particle; nothing needs clearing).
-__global__ void k_runs(const uint32_t* __restrict__ keys, uint32_t n,
-                       uint64_t* __restrict__ run_tag, const Control* __restrict__ ctl) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= n) return;
-    const uint32_t k = keys[s];
-    if (s == 0 || keys[s - 1] != k) run_tag[k] = ((uint64_t)ctl->epoch << 32) | s;
-}
-
-hipError_t launch_runs(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n) {
-    if (n == 0) return hipSuccess;
-    tbeg(c, KID_RUNS);
-    k_runs<<<ceil_div(n, 256u), 256, 0, c->stream>>>(sorted_keys, n, c->run_tag, c->ctl);
-    tend(c, KID_RUNS);
-    return hipGetLastError();
-}
-
-// Suffix minimum (inclusive) of one value per lane over a wavefront.
-__device__ __forceinline__ uint32_t wave_suffix_min(uint32_t v, int lane) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        uint32_t t = __shfl_down(v, off, kWave);
-        if (lane + off < kWave) v = min(v, t);
-    }
-    return v;
-}
-
-// cell_start[c] = min over cells c' >= c of (first sorted index of c' if c' holds particles),
-// i.e. the first sorted index with key >= c; n where none.  Tiles of 4096 cells are numbered
-// dynamically from the END of the grid, and a decoupled look-back carries the minimum over all
-// later cells; each lane owns 16 consecutive cells.  This equals the exclusive prefix sum of
-// the per-cell counts of hashgrid.rs:102-106.
-__global__ __launch_bounds__(kScanThreads) void k_scan_starts(const uint64_t* __restrict__ run_tag,
-                                                              uint32_t* __restrict__ cell_start,
-                                                              uint64_t* __restrict__ lookback,
-                                                              Control* ctl, uint32_t C, uint32_t n) {
-    __shared__ uint32_t s_tile;
-    __shared__ uint32_t s_wave[4];
-    __shared__ uint32_t s_prefix;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_tile = atomicAdd(&ctl->scan_ctr.v, 1u);
-    __syncthreads();
-    const uint32_t tile = s_tile;
-    const uint32_t epoch = ctl->epoch;
-    const uint32_t hi = C - tile * (uint32_t)kScanTile;  // cells [hi - 4096, hi), clipped at 0
-    const int64_t first = (int64_t)hi - kScanTile + (int64_t)tid * kScanItems;
-
-    uint32_t v[kScanItems];
-#pragma unroll
-    for (int q = 0; q < kScanItems; q++) {
-        const int64_t c = first + q;
-        uint32_t x = 0xFFFFFFFFu;
-        if (c >= 0) {
-            const uint64_t t = run_tag[c];
-            if ((uint32_t)(t >> 32) == epoch) x = (uint32_t)t;
-        }
-        v[q] = x;
-    }
-    // lane-local suffix minimum
-    uint32_t m = 0xFFFFFFFFu;
-#pragma unroll
-    for (int q = kScanItems - 1; q >= 0; q--) {
-        m = min(m, v[q]);
-        v[q] = m;
-    }
-    // minimum over the later lanes of the workgroup
-    const uint32_t inc = wave_suffix_min(m, lane);
-    uint32_t later = __shfl_down(inc, 1, kWave);
-    if (lane == 63) later = 0xFFFFFFFFu;
-    if (lane == 0) s_wave[wave] = inc;
-    __syncthreads();
-    for (int w = wave + 1; w < 4; w++) later = min(later, s_wave[w]);
-    const uint32_t total = min(min(s_wave[0], s_wave[1]), min(s_wave[2], s_wave[3]));
-
-    if (tid == 0) {
-        uint64_t* my = lookback + tile;
-        uint32_t prefix = 0xFFFFFFFFu;
-        if (tile == 0) {
-            lb_store(my, lb_word(kLbInclusive, epoch, total));
-        } else {
-            lb_store(my, lb_word(kLbAggregate, epoch, total));
-            uint32_t t = tile - 1u, spins = 0;
-            const uint32_t limit = ctl->spin_limit ? ctl->spin_limit : kSpinLimit;
-            for (;;) {
-                const uint64_t w = lb_load(lookback + t);
-                const uint64_t st = w & (3ull << 62);
-                if (st != 0 && ((uint32_t)(w >> 32) & kEpochMask) == epoch) {
-                    prefix = min(prefix, (uint32_t)w);
-                    if (st == kLbInclusive) break;
-                    if (t == 0) {
-                        atomicOr(&ctl->error.v, 2u);
-                        break;
-                    }
-                    t--;
-                }
-                // every poll counts (a walk over the most scan tiles needs at most 2^20 of them)
-                if (++spins >= limit) {
-                    atomicOr(&ctl->error.v, 1u);
-                    break;
-                }
-                if (!(st != 0 && ((uint32_t)(w >> 32) & kEpochMask) == epoch))
-                    __builtin_amdgcn_s_sleep(1);
-            }
-            lb_store(my, lb_word(kLbInclusive, epoch, min(prefix, total)));
-        }
-        s_prefix = prefix;
-    }
-    __syncthreads();
-    const uint32_t after = min(later, s_prefix);
-#pragma unroll
-    for (int q = 0; q < kScanItems; q++) {
-        const int64_t c = first + q;
-        if (c >= 0) {
-            const uint32_t x = min(v[q], after);
-            cell_start[c] = x == 0xFFFFFFFFu ? n : x;
-        }
-    }
-    if (tile == 0 && tid == 0) cell_start[C] = n;
-}
-
-hipError_t launch_scan_starts(fh_ctx* c, uint32_t num_cells, uint32_t n, uint32_t* cell_start) {
-    const uint32_t tiles = ceil_div(num_cells, (uint32_t)kScanTile);
-    tbeg(c, KID_SCAN);
-    k_scan_starts<<<tiles, kScanThreads, 0, c->stream>>>(c->run_tag, cell_start, c->scan_lb,
-                                                         c->ctl, num_cells, n);
-    tend(c, KID_SCAN);
-    return hipGetLastError();
-}
 
 // ---------------------------------------------------------------------------------------------
 __global__ void k_fill_u32(uint32_t* __restrict__ p, uint32_t value, uint32_t n) {
@@ -189,76 +55,41 @@ __device__ __forceinline__ int32_t rust_as_i32(float f) {
     return (int32_t)f;
 }
 
-// Gather of the point positions into sorted order (float4), so the query walks contiguous
-// memory.
-__global__ void k_gather_pos(const float* __restrict__ x, const float* __restrict__ y,
-                             const float* __restrict__ z, uint32_t stride,
-                             const uint32_t* __restrict__ sidx, uint32_t n,
-                             float4* __restrict__ spos) {
-    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+// The point positions in sorted order (float4), so the query walks contiguous memory.  A
+// gather through sorted_indices would read three scattered words per point (a cache line each);
+// instead the inverse permutation is taken first (k_rank_of_sidx: coalesced read, one scattered
+// word written per point), and then every point is read in its own order and stored once, as a
+// float4, at its sorted slot (k_scatter_pos).
+__global__ __launch_bounds__(256) void k_rank_of_sidx(const uint32_t* __restrict__ sidx,
+                                                      uint32_t n, uint32_t* __restrict__ rank) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
-    uint32_t i = sidx[s];
-    if (i >= n) i = 0;  // never taken for a grid built over these n points
-    size_t o = (size_t)i * stride;
+    const uint32_t i = sidx[s];
+    if (i < n) rank[i] = s;  // always, for a grid built over these n points
+}
+
+__global__ __launch_bounds__(256) void k_scatter_pos(const float* __restrict__ x,
+                                                     const float* __restrict__ y,
+                                                     const float* __restrict__ z,
+                                                     uint32_t stride,
+                                                     const uint32_t* __restrict__ rank,
+                                                     uint32_t n, float4* __restrict__ spos) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t s = rank[i];
+    if (s >= n) return;  // never taken for a permutation
+    const size_t o = (size_t)i * stride;
     spos[s] = make_float4(x[o], y[o], z[o], 0.0f);
 }
 
-// One thread per sorted point.  Arithmetic is exactly the reference's (the library is built
-// with -ffp-contract=off): diff = p_j - q, dist_sq = (dx*dx + dy*dy) + dz*dz, `<=` against
-// radius*radius, weight coeff*diff*diff*diff summed in visiting order, so counts and weight
-// sums are bit-identical to the CPU restatement.
-__global__ __launch_bounds__(256) void k_nbr_query(const float4* __restrict__ spos,
-                                                   const uint32_t* __restrict__ sidx, uint32_t n,
-                                                   GridDesc g,
-                                                   const uint32_t* __restrict__ cell_start,
-                                                   float radius_sq, float coeff,
-                                                   uint32_t* __restrict__ counts,
-                                                   float* __restrict__ wsum) {
-    uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= n) return;
-    const float4 q = spos[s];
-    // Query cell is not clamped (hashgrid.rs:155-157).
-    const int64_t cx = rust_as_i32(floorf((q.x - g.ox) / g.cs));
-    const int64_t cy = rust_as_i32(floorf((q.y - g.oy) / g.cs));
-    const int64_t cz = rust_as_i32(floorf((q.z - g.oz) / g.cs));
-    const int64_t x0 = cx - 1 < 0 ? 0 : cx - 1;
-    const int64_t x1 = cx + 1 > (int64_t)g.nx - 1 ? (int64_t)g.nx - 1 : cx + 1;
-    uint32_t cnt = 0;
-    float w = 0.0f;
-    for (int dz = -1; dz <= 1; dz++) {
-        int64_t nz = cz + dz;
-        if (nz < 0 || nz >= (int64_t)g.nz) continue;
-        for (int dy = -1; dy <= 1; dy++) {
-            int64_t ny = cy + dy;
-            if (ny < 0 || ny >= (int64_t)g.ny) continue;
-            if (x0 > x1) continue;
-            uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
-            uint32_t b = cell_start[row + (uint32_t)x0];
-            uint32_t e = min(cell_start[row + (uint32_t)x1 + 1u], n);
-            for (uint32_t j = b; j < e; j++) {
-                float4 p = spos[j];
-                float dx = p.x - q.x, dy2 = p.y - q.y, dz2 = p.z - q.z;
-                float dist_sq = dx * dx + dy2 * dy2 + dz2 * dz2;
-                if (dist_sq <= radius_sq) {
-                    float diff = radius_sq - dist_sq;
-                    cnt++;
-                    w += coeff * diff * diff * diff;
-                }
-            }
-        }
-    }
-    uint32_t i = sidx[s];
-    if (i >= n) return;
-    counts[i] = cnt;
-    if (wsum) wsum[i] = w;
-}
-
-// The same query, with the neighbour candidates of 64 consecutive sorted points staged through
-// LDS (the wave candidate stream of fh_stream.hpp, one z-slab at a time): each lane still visits
-// its own candidates in the reference's order (dz, dy, then ascending sorted index) with the
-// reference's expressions, so counts and weight sums stay bit-identical; the staging turns the
-// per-lane scattered reads into shared, coalesced ones.  Points whose query cell lies outside
-// the grid (the reference does not clamp it) take the per-lane walk of k_nbr_query afterwards.
+// HashGrid::query_neighbors for every point of a built grid, with the neighbour candidates of 64
+// consecutive sorted points staged through LDS (the wave candidate stream of fh_stream.hpp, one
+// z-slab at a time).  Arithmetic is exactly the reference's (the library is built with
+// -ffp-contract=off): diff = p_j - q, dist_sq = (dx*dx + dy*dy) + dz*dz, `<=` against
+// radius*radius, weight coeff*diff*diff*diff summed in visiting order; each lane visits its own
+// candidates in the reference's order (dz, dy, then ascending sorted index), so counts and
+// weight sums are bit-identical to the CPU restatement.  Points whose query cell lies outside
+// the grid (the reference does not clamp it) take a per-lane walk around that cell afterwards.
 __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__ spos,
                                                       const uint32_t* __restrict__ sidx,
                                                       uint32_t n, GridDesc g,
@@ -445,9 +276,12 @@ hipError_t launch_neighbor_query(fh_ctx* c, const float* x, const float* y, cons
                                  const uint32_t* cell_start, const uint32_t* sorted_indices,
                                  float radius, uint32_t* counts, float* wsum) {
     if (n == 0) return hipSuccess;
-    k_gather_pos<<<ceil_div(n, 256u), 256, 0, c->stream>>>(x, y, z, stride, sorted_indices, n,
-                                                           c->spos);
+    k_rank_of_sidx<<<ceil_div(n, 256u), 256, 0, c->stream>>>(sorted_indices, n, c->rank);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_scatter_pos<<<ceil_div(n, 256u), 256, 0, c->stream>>>(x, y, z, stride, c->rank, n,
+                                                            c->spos);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Same float expressions as sph_density.rs:413-416 with h = radius.
     float h = radius;

@@ -84,19 +84,14 @@ constexpr uint32_t kLightCacheWords = 3 * 64 + 2 * 192;
 #endif
 // k_group_plan workgroup: a co-located group, or 8 sub-tiles = 24 (sub-tile, slab) items
 constexpr int kPlanThreads = FH_PLAN_THREADS;
-constexpr int kScanThreads = 256;
-constexpr int kScanItems = 16;
-constexpr int kScanTile = kScanThreads * kScanItems;  // 4096 cells per scan tile
 constexpr int kEvents = 16;
 
-// Look-back words of the cell scan: [63:62] status, [61:32] epoch, [31:0] value.  A word whose
-// epoch differs from the current one is "not ready", so the array never needs clearing.
-// (The sort's look-back words are 32-bit, [31:30] status, [29:0] value, and are zeroed by
-// k_begin: half the bytes per poll, which is what the look-back walk is bound by.)
+// The sort's look-back words are 32-bit, [31:30] status, [29:0] value, zeroed by k_begin at
+// the start of each sort (half the bytes per poll of a 64-bit word, which is what the walk is
+// bound by).  Work tags (co-located groups, skipped sub-tiles, candidate group cells) carry a
+// 30-bit epoch that every start bumps; the context renews it before it wraps.
 constexpr uint32_t kLb32Aggregate = 1u << 30;
 constexpr uint32_t kLb32Inclusive = 2u << 30;
-constexpr uint64_t kLbAggregate = 1ull << 62;
-constexpr uint64_t kLbInclusive = 2ull << 62;
 constexpr uint32_t kEpochMask = 0x3FFFFFFFu;
 // Bound on look-back polls before a tile gives up and raises the device error flag; keeps
 // every wave finite even if an invariant were broken (each poll sleeps ~64 clocks).
@@ -153,7 +148,7 @@ inline DivU32 make_divu32(uint32_t d) {
 
 // Kernels that can be timed with fh_time_kernel (names in kKernelNames).
 enum KernelId { KID_HIST, KID_HASH, KID_SCAN, KID_SORT, KID_GATHER, KID_DENSITY,
-                KID_FORCE, KID_NBR, KID_FINAL, KID_RUNS, KID_PLAN, KID_PREP, KID_DPASS,
+                KID_FORCE, KID_NBR, KID_FINAL, KID_PLAN, KID_PREP, KID_DPASS,
                 KID_FPASS, KID_EPOCH, KID_COUNT };
 
 // Event pairs bracketing the first `max` launches of one kernel after it was armed; when the
@@ -170,7 +165,7 @@ struct fh_ctx {
     hipStream_t stream;
     bool own_stream;
     uint32_t max_n, max_cells;
-    uint32_t max_sort_tiles, max_scan_tiles;
+    uint32_t max_sort_tiles;
     // sort scratch
     uint32_t* ka;        // [max_n]
     uint32_t* va;        // [max_n]
@@ -183,9 +178,9 @@ struct fh_ctx {
                          // (null: the first pass looks back like the others)
     fh::Control* ctl;    // device control block
     // grid scratch
-    uint64_t* run_tag;     // [max_cells] epoch << 32 | first sorted index of the cell's run
+    uint64_t* run_tag;     // [max_cells] epoch << 32: the cell may hold a co-located group
+                           // (k_cell_starts' candidates, read by the plan)
     uint32_t* cell_start;  // [max_cells + 1]
-    uint64_t* scan_lb;     // [max_scan_tiles]
     uint32_t* skeys;       // [max_n] sorted keys (cells)
     uint32_t* sidx;        // [max_n] sorted particle ids
     // SPH scratch (sorted order)
@@ -197,7 +192,8 @@ struct fh_ctx {
     uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
     uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
-    float* hpart;        // heavy work partials: per heavy-list slot, kHeavyWaves x 4 x 64 floats
+    float* hpart;        // heavy work partials: per heavy-list slot, hpart_parts x 4 x 64 floats
+    uint32_t hpart_parts; // parts per slot the buffer has room for (kHeavyWaves until 8 are asked for)
     uint32_t* hslot;     // [3 * ceil(max_n / 64)] heavy list slot of each heavy item
     uint32_t* lstream;   // [3 * ceil(max_n / 64)][kLightCacheWords] light items' candidate streams
                          // (lane intervals and window indices) from the density pass, reused by
@@ -278,15 +274,6 @@ __device__ __forceinline__ CellXYZ key_xyz(uint32_t key, const GridDesc& g) {
     return c;
 }
 
-__device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t lb_word(uint64_t status, uint32_t epoch, uint32_t value) {
-    return status | ((uint64_t)(epoch & kEpochMask) << 32) | (uint64_t)value;
-}
 
 // Inclusive scan of one value per thread across a 64-lane wavefront.
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int lane) {
@@ -364,11 +351,6 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits,
                               uint32_t* rank = nullptr);
-// Mark the first index of every run of equal sorted keys in c->run_tag (epoch-tagged).
-hipError_t launch_runs(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n);
-// CSR cell_start[0..C] from the run tags: cell_start[c] = first sorted index with key >= c
-// (a reverse minimum scan over the cells), cell_start[C] = n.
-hipError_t launch_scan_starts(fh_ctx* c, uint32_t num_cells, uint32_t n, uint32_t* cell_start);
 hipError_t launch_fill_u32(fh_ctx* c, uint32_t* p, uint32_t value, uint32_t n);
 hipError_t launch_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
                              uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end);

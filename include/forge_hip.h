@@ -282,21 +282,23 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
 /* FH_OPT_HEAVY_PARTS = 4: wavefronts (4 or 8) that split each heavy item of the fast passes; 0
  * restores the default (4).  More parts shorten the longest items (dense clumps: c4 is ~8 %
  * faster with 8), fewer cost less per item (c3 is ~2 % faster with 4).  Results differ only by
- * rounding. */
+ * rounding.  The context holds the parts' partial sums for 4 parts; the first time 8 are set
+ * it makes room for 8 (one allocation of ~192 bytes per particle of max_n, so set it outside
+ * capture; fh_scratch_bytes counts it). */
 #define FH_OPT_HEAVY_PARTS 4
-/* FH_OPT_EPOCH_PERIOD = 5: the work tags of the rebuilds (co-located groups, skipped sub-tiles,
- * cell runs, scan look-back) compare a 30-bit epoch that every sort / rebuild start bumps on the
- * device, so a tag left 2^30 - 1 starts earlier would match again.  The context counts the
- * starts it queues (graph replays included) and, before the count reaches the period, queues a
- * renewal (tags cleared, epoch back to 0) between two calls or replays.  value = the period in
- * starts (1..2^30 - 2; 0 restores the default 2^30 - 2); setting it renews at once.  Short
- * periods exercise the renewal in tests; results do not change. */
+/* FH_OPT_EPOCH_PERIOD = 5: the work tags of the SPH rebuilds (co-located groups, skipped
+ * sub-tiles, candidate group cells) compare a 30-bit epoch that every sort / rebuild start
+ * bumps on the device, so a tag left 2^30 - 1 starts earlier would match again.  The context
+ * counts the starts it queues (graph replays included) and, before the count reaches the
+ * period, queues a renewal (tags cleared, epoch back to 0) between two calls or replays.
+ * value = the period in starts (1..2^30 - 2; 0 restores the default 2^30 - 2); setting it
+ * renews at once.  Short periods exercise the renewal in tests; results do not change. */
 #define FH_OPT_EPOCH_PERIOD 5
-/* FH_OPT_SPIN_LIMIT = 6 (diagnostics): polls a radix-sort or scan look-back walk makes before
- * it gives up and raises the device error flag that fh_sync reports (0 restores the default,
- * 2^22, far above what any walk needs).  A limit of 1 forces that failure path without a fault
- * (every walk that needs a second poll gives up; the scatter stays in bounds, the output is
- * wrong and fh_sync returns FH_ESTATE).  Synchronises the stream. */
+/* FH_OPT_SPIN_LIMIT = 6 (diagnostics): polls a radix-sort look-back walk makes before it gives
+ * up and raises the device error flag that fh_sync reports (0 restores the default, 2^22, far
+ * above what any walk needs).  A limit of 1 forces that failure path without a fault (every
+ * walk that needs a second poll gives up; the scatter stays in bounds, the output is wrong and
+ * fh_sync returns FH_ESTATE).  Synchronises the stream. */
 #define FH_OPT_SPIN_LIMIT 6
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
@@ -341,7 +343,7 @@ int fh_event_record(fh_ctx* ctx, uint32_t slot);
 int fh_event_elapsed_ms(fh_ctx* ctx, uint32_t slot_start, uint32_t slot_end, float* ms);
 
 /* Per-kernel timing.  Arm kernel `name` (one of "hist", "hash", "scan", "sort",
- * "gather", "density", "force", "query", "finalize", "runs", "plan", "prep", "epoch_reset";
+ * "gather", "density", "force", "query", "finalize", "plan", "prep", "epoch_reset";
  * or a whole fast pass of fh_sph_fused, "density_pass" or "force_pass", from its first launch
  * to its last) so
  * that its next

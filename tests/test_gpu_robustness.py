@@ -73,8 +73,8 @@ def test_epoch_renewal_keeps_sph_results(fh, gpu_ctx, period):
 
 
 def test_epoch_renewal_keeps_hashgrid_builds(fh, gpu_ctx, oracle):
-    """fh_hashgrid_build (epoch-tagged cell runs and scan look-back words) on 6 point sets in
-    a context renewing every 2 starts, against the oracle."""
+    """fh_hashgrid_build (each build is a start) on 6 point sets in a context renewing every 2
+    starts, against the oracle: the renewals run between builds and change nothing."""
     ctx = fh.Context(max_n=50_000, max_cells=40 ** 3)
     ctx.set_option(fh.FH_OPT_EPOCH_PERIOD, 2)
     ctx.time_kernel("epoch_reset", 100)
