@@ -99,7 +99,9 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
                                                       float* __restrict__ wsum) {
     __shared__ float4 s_p[kWin];
     const int lane = threadIdx.x;
-    const uint32_t s = blockIdx.x * kWave + (uint32_t)lane;
+    // runs of consecutive sub-tiles on one XCD: neighbouring sub-tiles read mostly the same
+    // candidate rows, which then stay in that XCD's L2
+    const uint32_t s = xcd_chunked(blockIdx.x, gridDim.x) * kWave + (uint32_t)lane;
     const bool in = s < n;
     const float4 q = spos[in ? s : 0u];
     // the sort's (clamped) cell, and the reference's unclamped query cell

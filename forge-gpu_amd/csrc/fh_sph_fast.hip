@@ -97,21 +97,6 @@ __device__ __forceinline__ void slab_ranges(const CellXYZ& c, bool live, const G
 }
 
 // ---------------------------------------------------------------------------------------------
-// Workgroup renumbering for the light kernels.  The dispatcher hands workgroup b to XCD b % 8,
-// so consecutive items land on eight different L2s.  Mapping runs of kXcdChunk workgroups to one
-// XCD keeps neighbouring sub-tiles, which read mostly the same candidate cells, on one L2 while
-// every XCD still takes a share of each region of the box (balance matters more than reuse: a
-// contiguous eighth of the items per XCD was slower).  The tail beyond the last whole round of
-// 8 * kXcdChunk workgroups keeps its own numbers, so the mapping is a permutation of [0, nb).
-constexpr uint32_t kXcdChunk = 128, kXcds = 8;
-__device__ __forceinline__ uint32_t xcd_chunked(uint32_t b, uint32_t nb) {
-    const uint32_t full = nb / (kXcds * kXcdChunk) * (kXcds * kXcdChunk);
-    if (b >= full) return b;
-    const uint32_t x = b % kXcds, i = b / kXcds;
-    return ((i / kXcdChunk) * kXcds + x) * kXcdChunk + (i % kXcdChunk);
-}
-
-// ---------------------------------------------------------------------------------------------
 // Load balance.  A (64-particle sub-tile, slab) item whose particles each face more than
 // kHeavyWork candidates -- the box corners of c3 collect thousands of particles at one point --
 // is moved to a heavy list and processed in 4 single-wave parts that split the candidates of the

@@ -27,6 +27,22 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
     return v;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Workgroup renumbering for the one-wave-per-item kernels (SPH light items, neighbour query).
+// The dispatcher hands workgroup b to XCD b % 8, so consecutive items land on eight different
+// L2s.  Mapping runs of kXcdChunk workgroups to one
+// XCD keeps neighbouring sub-tiles, which read mostly the same candidate cells, on one L2 while
+// every XCD still takes a share of each region of the box (balance matters more than reuse: a
+// contiguous eighth of the items per XCD was slower).  The tail beyond the last whole round of
+// 8 * kXcdChunk workgroups keeps its own numbers, so the mapping is a permutation of [0, nb).
+constexpr uint32_t kXcdChunk = 128, kXcds = 8;
+__device__ __forceinline__ uint32_t xcd_chunked(uint32_t b, uint32_t nb) {
+    const uint32_t full = nb / (kXcds * kXcdChunk) * (kXcds * kXcdChunk);
+    if (b >= full) return b;
+    const uint32_t x = b % kXcds, i = b / kXcds;
+    return ((i / kXcdChunk) * kXcds + x) * kXcdChunk + (i % kXcdChunk);
+}
+
 // Light items.  The candidates of a wave are laid out as one stream: for each home-row segment
 // in lane order, the unions of its rows 0, 1, 2.  Every lane's own range of row r is then one
 // contiguous interval [S[r], S[r] + cnt[r]) of the stream.  The stream is staged through the
