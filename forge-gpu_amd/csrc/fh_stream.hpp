@@ -138,24 +138,27 @@ __device__ __forceinline__ uint32_t stream_index(const LightStream& L, uint32_t 
     return u < L0 ? lo0 + u : (u < L0 + L1 ? lo1 + (u - L0) : lo2 + (u - L0 - L1));
 }
 
-// Sorted indices of the window's staging slots: slot k * 64 + lane holds stream position
-// w0 + k * 64 + lane; positions past the stream repeat its last element.
+// Sorted indices of the staging slots of a window of W candidates: slot k * 64 + lane holds
+// stream position w0 + k * 64 + lane; positions past the stream repeat its last element.
+template <int W = kWin>
 __device__ __forceinline__ void window_indices(const LightStream& L, uint32_t w0, int lane,
-                                               uint32_t j[kWinLoads]) {
+                                               uint32_t j[W / kWave]) {
+    static_assert(W % kWave == 0, "windows are whole rows of the wave");
 #pragma unroll
-    for (int k = 0; k < kWinLoads; k++)
+    for (int k = 0; k < W / kWave; k++)
         j[k] = stream_index(L, min(w0 + (uint32_t)(k * kWave + lane), L.T - 1u));
 }
 
-// The lane's three row intervals clipped to the window [w0, w0 + kWin), as [jb[r], je[r]) with
+// The lane's three row intervals clipped to the window [w0, w0 + W), as [jb[r], je[r]) with
 // the longest first (three compare-swaps): a wave's r-th loop then runs as long as the longest
 // r-th interval over its lanes, and lanes whose long row is not the same one share the first.
+template <int W = kWin>
 __device__ __forceinline__ void window_rows(const LightStream& L, uint32_t w0, uint32_t jb[3],
                                             uint32_t je[3]) {
 #pragma unroll
     for (int r = 0; r < 3; r++) {
         jb[r] = max(L.S[r], w0);
-        je[r] = max(min(L.S[r] + L.cnt[r], w0 + (uint32_t)kWin), jb[r]);
+        je[r] = max(min(L.S[r] + L.cnt[r], w0 + (uint32_t)W), jb[r]);
     }
     const auto cswap = [&](int a, int b) {
         const bool sw = je[b] - jb[b] > je[a] - jb[a];
