@@ -85,13 +85,12 @@ __global__ __launch_bounds__(256) void k_scatter_pos(const float* __restrict__ x
 // HashGrid::query_neighbors for every point of a built grid, with the neighbour candidates of 64
 // consecutive sorted points staged through LDS (the wave candidate stream of fh_stream.hpp, one
 // z-slab at a time, kQueryWin candidates per window: a slab's stream of uniform points, ~240
-// candidates, fits one window, so a lane's rows are not cut by window edges).  The predicate is
-// exactly the reference's (the library is built with -ffp-contract=off): diff = p_j - q,
-// dist_sq = (dx*dx + dy*dy) + dz*dz, `<=` against radius*radius, so the counts are bit-identical
-// to the CPU restatement.  The weight sum accumulates d^3, d = max(radius^2 - dist_sq, 0) (0 for
-// every candidate beyond the radius, NaN included), in the reference's visiting order (dz, dy,
-// ascending sorted index) with one fused multiply-add per candidate, and is scaled by the poly6
-// coefficient once at the end: within a few ulp of the reference's sum of coeff * d^3 terms.
+// candidates, mostly fits one window, so a lane's rows are rarely cut by a window edge and the
+// row loops, which run as long as their longest lane, run once per slab).  Arithmetic is exactly
+// the reference's (the library is built with -ffp-contract=off): diff = p_j - q, dist_sq =
+// (dx*dx + dy*dy) + dz*dz, `<=` against radius*radius, weight coeff*diff*diff*diff summed in
+// visiting order; each lane visits its own candidates in the reference's order (dz, dy, then
+// ascending sorted index), so counts and weight sums are bit-identical to the CPU restatement.
 // Points whose query cell lies outside the grid (the reference does not clamp it) take a
 // per-lane walk around that cell afterwards.
 #ifndef FH_QWIN
@@ -99,13 +98,18 @@ __global__ __launch_bounds__(256) void k_scatter_pos(const float* __restrict__ x
 #endif
 constexpr int kQueryWin = FH_QWIN;
 
+// One candidate: a candidate beyond the radius adds 0 to the count and +0.0f to the weight sum,
+// which starts at +0 and only grows, so w + 0.0f == w bit for bit and the sum over the
+// candidates is the reference's sum over its neighbours.
 __device__ __forceinline__ void nbr_pair(const float4& p, const float4& q, float radius_sq,
-                                         uint32_t& cnt, float& w3) {
+                                         float coeff, uint32_t& cnt, float& w) {
     const float dx = p.x - q.x, dy = p.y - q.y, dz = p.z - q.z;
     const float dist_sq = dx * dx + dy * dy + dz * dz;
-    cnt += dist_sq <= radius_sq ? 1u : 0u;
-    const float d = fmaxf(radius_sq - dist_sq, 0.0f);
-    w3 = __builtin_fmaf(d * d, d, w3);
+    const bool ok = dist_sq <= radius_sq;
+    const float diff = radius_sq - dist_sq;
+    const float t = coeff * diff * diff * diff;
+    cnt += ok ? 1u : 0u;
+    w += ok ? t : 0.0f;
 }
 
 __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__ spos,
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
     const uint32_t x0 = cxc > 0u ? cxc - 1u : 0u;
     const uint32_t x1 = cxc + 1u < g.nx ? cxc + 1u : g.nx - 1u;
     uint32_t cnt = 0;
-    float w3 = 0.0f;
+    float w = 0.0f;
     for (int dz = -1; dz <= 1; dz++) {  // uniform
         uint32_t b[3], e[3];
         const int nz = (int)czc + dz;
@@ -146,12 +150,18 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
             if (in && nz >= 0 && nz < (int)g.nz && ny >= 0 && ny < (int)g.ny) {
                 const uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
                 b[r] = cell_start[row + x0];
-                // outside points: an empty range at their place in the row (walked later)
-                e[r] = inside ? min(cell_start[row + x1 + 1u], n) : b[r];
+                e[r] = min(cell_start[row + x1 + 1u], n);
             }
         }
+        // a segment's row union runs from its first lane's begin to its last lane's end, which
+        // holds because the lanes' clamped ranges grow along the row; an outside point keeps its
+        // clamped ranges for the union and evaluates none of them (it is walked later)
         LightStream L;
         light_stream(L, b, e, hr, in, lane);
+        if (!inside) {
+#pragma unroll
+            for (int r = 0; r < 3; r++) L.cnt[r] = 0u;
+        }
         for (uint32_t w0 = 0; w0 < L.T; w0 += kQueryWin) {  // uniform
             uint32_t j[kLoads];
             window_indices<kQueryWin>(L, w0, lane, j);
@@ -162,32 +172,32 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
 #pragma unroll
             for (int k = 0; k < kLoads; k++) s_p[k * kWave + lane] = v[k];
             __builtin_amdgcn_wave_barrier();
-            // the rows longest first: a lane then adds its rows to the weight sum in another
-            // order than the reference's dy order (the count does not depend on the order)
-            uint32_t jb[3], je[3];
-            window_rows<kQueryWin>(L, w0, jb, je);
+            // the rows in the reference's dy order (walking them longest first would change
+            // the order of the weight sum)
 #pragma unroll
             for (int r = 0; r < 3; r++) {
+                const uint32_t jb = max(L.S[r], w0);
+                const uint32_t je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kQueryWin);
                 // two candidates per step of the LDS address
-                const float4* c = s_p + (jb[r] - w0);
-                const float4* const ce = c + (je[r] - jb[r]);
+                const float4* c = s_p + (jb - w0);
+                const float4* const ce = c + (je > jb ? je - jb : 0u);
                 const float4* const cu = ce - 1;
                 if (c < cu) {
                     do {
                         const float4 p0 = c[0], p1 = c[1];
-                        nbr_pair(p0, q, radius_sq, cnt, w3);
-                        nbr_pair(p1, q, radius_sq, cnt, w3);
+                        nbr_pair(p0, q, radius_sq, coeff, cnt, w);
+                        nbr_pair(p1, q, radius_sq, coeff, cnt, w);
                         c += 2;
                     } while (c < cu);
                 }
-                if (c < ce) nbr_pair(*c, q, radius_sq, cnt, w3);
+                if (c < ce) nbr_pair(*c, q, radius_sq, coeff, cnt, w);
             }
             __builtin_amdgcn_wave_barrier();
         }
     }
     if (in && !inside) {  // rare: the reference's walk around an unclamped query cell
         cnt = 0;
-        w3 = 0.0f;
+        w = 0.0f;
         const int64_t lx0 = cxu - 1 < 0 ? 0 : cxu - 1;
         const int64_t lx1 = cxu + 1 > (int64_t)g.nx - 1 ? (int64_t)g.nx - 1 : cxu + 1;
         for (int dz = -1; dz <= 1; dz++) {
@@ -199,7 +209,7 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
                 const uint32_t row = (uint32_t)ny * g.nx + (uint32_t)nz * g.nx * g.ny;
                 const uint32_t jb = cell_start[row + (uint32_t)lx0];
                 const uint32_t je = min(cell_start[row + (uint32_t)lx1 + 1u], n);
-                for (uint32_t j = jb; j < je; j++) nbr_pair(spos[j], q, radius_sq, cnt, w3);
+                for (uint32_t j = jb; j < je; j++) nbr_pair(spos[j], q, radius_sq, coeff, cnt, w);
             }
         }
     }
@@ -207,7 +217,7 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
     const uint32_t i = sidx[s];
     if (i >= n) return;
     counts[i] = cnt;
-    if (wsum) wsum[i] = coeff * w3;
+    if (wsum) wsum[i] = w;
 }
 
 // Batched HashGrid::query_neighbors: one thread per query, neighbour positions read through
