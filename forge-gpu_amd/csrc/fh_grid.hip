@@ -56,30 +56,30 @@ __device__ __forceinline__ int32_t rust_as_i32(float f) {
 }
 
 // The point positions in sorted order (float4), so the query walks contiguous memory.  A
-// gather through sorted_indices would read three scattered words per point (a cache line each);
-// instead the inverse permutation is taken first (k_rank_of_sidx: coalesced read, one scattered
-// word written per point), and then every point is read in its own order and stored once, as a
-// float4, at its sorted slot (k_scatter_pos).
-__global__ __launch_bounds__(256) void k_rank_of_sidx(const uint32_t* __restrict__ sidx,
-                                                      uint32_t n, uint32_t* __restrict__ rank) {
+// gather through sorted_indices from the caller's three arrays would read three scattered
+// words per point (a cache line each), and a scatter to the sorted slots (through the inverse
+// permutation) writes partial cache lines twice (rank, then the float4); instead the points are
+// packed once as float4 in their own order (k_pack_pos: coalesced reads and writes), and every
+// sorted slot then reads one 16-byte record (k_gather_pos: coalesced sidx reads and writes, one
+// scattered 16-byte read per point, mostly served from the MALL, which holds the packed copy).
+__global__ __launch_bounds__(256) void k_pack_pos(const float* __restrict__ x,
+                                                  const float* __restrict__ y,
+                                                  const float* __restrict__ z, uint32_t stride,
+                                                  uint32_t n, float4* __restrict__ packed) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const size_t o = (size_t)i * stride;
+    packed[i] = make_float4(x[o], y[o], z[o], 0.0f);
+}
+
+__global__ __launch_bounds__(256) void k_gather_pos(const float4* __restrict__ packed,
+                                                    const uint32_t* __restrict__ sidx,
+                                                    uint32_t n, float4* __restrict__ spos) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const uint32_t i = sidx[s];
-    if (i < n) rank[i] = s;  // always, for a grid built over these n points
-}
-
-__global__ __launch_bounds__(256) void k_scatter_pos(const float* __restrict__ x,
-                                                     const float* __restrict__ y,
-                                                     const float* __restrict__ z,
-                                                     uint32_t stride,
-                                                     const uint32_t* __restrict__ rank,
-                                                     uint32_t n, float4* __restrict__ spos) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t s = rank[i];
-    if (s >= n) return;  // never taken for a permutation
-    const size_t o = (size_t)i * stride;
-    spos[s] = make_float4(x[o], y[o], z[o], 0.0f);
+    // a grid built over these n points holds a permutation of 0..n-1
+    spos[s] = i < n ? packed[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 // HashGrid::query_neighbors for every point of a built grid, with the neighbour candidates of 64
@@ -288,11 +288,11 @@ hipError_t launch_neighbor_query(fh_ctx* c, const float* x, const float* y, cons
                                  const uint32_t* cell_start, const uint32_t* sorted_indices,
                                  float radius, uint32_t* counts, float* wsum) {
     if (n == 0) return hipSuccess;
-    k_rank_of_sidx<<<ceil_div(n, 256u), 256, 0, c->stream>>>(sorted_indices, n, c->rank);
+    // c->sout (3 float4 per point) is free between SPH calls: the packed copy goes there
+    k_pack_pos<<<ceil_div(n, 256u), 256, 0, c->stream>>>(x, y, z, stride, n, c->sout);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_scatter_pos<<<ceil_div(n, 256u), 256, 0, c->stream>>>(x, y, z, stride, c->rank, n,
-                                                            c->spos);
+    k_gather_pos<<<ceil_div(n, 256u), 256, 0, c->stream>>>(c->sout, sorted_indices, n, c->spos);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Same float expressions as sph_density.rs:413-416 with h = radius.
