@@ -227,12 +227,13 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
-    // partial sums of the heavy parts: per list slot, kHeavyWaves parts x kHeavyComps x 64 lanes
-    // (room for kHeavyWavesMax parts is made when FH_OPT_HEAVY_PARTS asks for it)
+    // partial sums of the heavy parts: a slot for every item by default (FH_OPT_HEAVY_SLOTS
+    // caps it), kHeavyWaves parts x kHeavyComps x 64 lanes each (room for kHeavyWavesMax parts
+    // is made when FH_OPT_HEAVY_PARTS asks for it)
     c->hpart_parts = kHeavyWaves;
+    c->hslot_cap = kHeavyLists * c->heavy_cap;
     if (e == hipSuccess)
-        e = alloc(&c->hpart,
-                  (size_t)kHeavyLists * c->heavy_cap * kHeavyWaves * kHeavyComps * 64u, &tot);
+        e = alloc(&c->hpart, (size_t)c->hslot_cap * kHeavyWaves * kHeavyComps * 64u, &tot);
     if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess)
         e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);
@@ -614,6 +615,30 @@ int fh_sph_viscosity(fh_ctx* c, const fh_sph_params* prm, const float* px, const
                    n, dt);
 }
 
+// The heavy parts' partial-sum buffer for `slots` slots of `parts` parts each: one allocation
+// (callers have checked that no capture is in progress), the old buffer freed after the stream
+// has drained.  The context's captured graph holds the old buffer and slot count, so it is
+// dropped (fh_graph_launch then fails with FH_ESTATE until a graph is captured again).
+static int resize_hpart(fh_ctx* c, uint32_t slots, uint32_t parts) {
+    const size_t words = (size_t)slots * parts * kHeavyComps * 64u;
+    const size_t old_words = (size_t)c->hslot_cap * c->hpart_parts * kHeavyComps * 64u;
+    FH_CHECK_HIP(hipStreamSynchronize(c->stream));
+    if (c->exec) (void)hipGraphExecDestroy(c->exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->exec = nullptr;
+    c->graph = nullptr;
+    c->graph_begins = 0;
+    float* p = nullptr;
+    const hipError_t ae = hipMalloc((void**)&p, (words ? words : 1u) * sizeof(float));
+    if (ae != hipSuccess) return hip_fail(ae, "fh_set_option: heavy part buffer");
+    (void)hipFree(c->hpart);
+    c->scratch_bytes = c->scratch_bytes - old_words * sizeof(float) + words * sizeof(float);
+    c->hpart = p;
+    c->hslot_cap = slots;
+    c->hpart_parts = parts;
+    return FH_OK;
+}
+
 int fh_set_option(fh_ctx* c, int option, int value) {
     int rc = check_ctx(c);
     if (rc) return rc;
@@ -636,22 +661,23 @@ int fh_set_option(fh_ctx* c, int option, int value) {
                 return fail(FH_EINVAL, "fh_set_option: heavy parts %d is not 0, %d or %d", value,
                             kHeavyWaves, kHeavyWavesMax);
             if ((uint32_t)value > c->hpart_parts) {
-                // the partial sums of every heavy list slot for `value` parts: a larger buffer,
-                // made once (outside capture, checked above)
-                const size_t words = (size_t)kHeavyLists * c->heavy_cap * (uint32_t)value *
-                                     kHeavyComps * 64u;
-                FH_CHECK_HIP(hipStreamSynchronize(c->stream));
-                float* p = nullptr;
-                const hipError_t ae = hipMalloc((void**)&p, words * sizeof(float));
-                if (ae != hipSuccess) return hip_fail(ae, "fh_set_option: heavy part buffer");
-                (void)hipFree(c->hpart);
-                c->scratch_bytes += (words - (size_t)kHeavyLists * c->heavy_cap * c->hpart_parts *
-                                                 kHeavyComps * 64u) * sizeof(float);
-                c->hpart = p;
-                c->hpart_parts = (uint32_t)value;
+                // the partial sums of every slot for `value` parts: a larger buffer, made once
+                // (outside capture, checked above)
+                const int rc2 = resize_hpart(c, c->hslot_cap, (uint32_t)value);
+                if (rc2) return rc2;
             }
             c->heavy_parts = (uint32_t)value;
             return FH_OK;
+        case FH_OPT_HEAVY_SLOTS: {
+            if (value < 0) return fail(FH_EINVAL, "fh_set_option: heavy slots %d < 0", value);
+            const uint32_t all = kHeavyLists * c->heavy_cap;
+            const uint32_t cap = value == 0 || (uint32_t)value > all ? all : (uint32_t)value;
+            if (cap != c->hslot_cap) {
+                const int rc2 = resize_hpart(c, cap, c->hpart_parts);
+                if (rc2) return rc2;
+            }
+            return FH_OK;
+        }
         case FH_OPT_EPOCH_PERIOD:
             if (value < 0 || (uint32_t)value > kEpochPeriod)
                 return fail(FH_EINVAL, "fh_set_option: epoch period %d outside 0..%u", value,
@@ -830,6 +856,7 @@ int fh_event_elapsed_ms(fh_ctx* c, uint32_t a, uint32_t b, float* ms) {
     if (rc) return rc;
     if (a >= (uint32_t)kEvents || b >= (uint32_t)kEvents || !ms)
         return fail(FH_EINVAL, "fh_event_elapsed_ms: bad slot or null output");
+    if (c->capturing) return fail(FH_ESTATE, "fh_event_elapsed_ms: stream is being captured");
     FH_CHECK_HIP(hipEventSynchronize(c->ev[b]));
     FH_CHECK_HIP(hipEventElapsedTime(ms, c->ev[a], c->ev[b]));
     return FH_OK;

@@ -192,9 +192,10 @@ struct fh_ctx {
     uint32_t* heavy;     // [kHeavyLists][heavy_cap] heavy (64-particle tile, slab) work items
     uint32_t heavy_cap;  // entries per heavy sub-list
     uint8_t* heavy_flag; // [3 * ceil(max_n / 64)] 1: heavy list, 2: co-located, skipped
-    float* hpart;        // heavy work partials: per heavy-list slot, hpart_parts x 4 x 64 floats
+    float* hpart;        // heavy work partials: per slot, hpart_parts x 4 x 64 floats
     uint32_t hpart_parts; // parts per slot the buffer has room for (kHeavyWaves until 8 are asked for)
-    uint32_t* hslot;     // [3 * ceil(max_n / 64)] heavy list slot of each heavy item
+    uint32_t hslot_cap;  // partial-sum slots in hpart (FH_OPT_HEAVY_SLOTS; default: every item)
+    uint32_t* hslot;     // [3 * ceil(max_n / 64)] partial-sum slot of each heavy item, or kNoSlot
     uint32_t* lstream;   // [3 * ceil(max_n / 64)][kLightCacheWords] light items' candidate streams
                          // (lane intervals and window indices) from the density pass, reused by
                          // the force pass

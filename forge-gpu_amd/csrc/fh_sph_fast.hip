@@ -112,6 +112,11 @@ constexpr uint32_t kEntryFlags = kCutFlag | kTransFlag;
 constexpr uint8_t kItemLight = 0, kItemHeavy = 1, kItemSkip = 2;
 // hslot[item]: the heavy list slot of a heavy item (where its partial sums are), else kNoSlot.
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+// Partial-sum slot of the heavy entry at position pos of sub-list k: the lists interleaved, so a
+// cap on the slots (FH_OPT_HEAVY_SLOTS) leaves every list its first entries.
+__device__ __forceinline__ uint32_t heavy_slot(uint32_t k, uint32_t pos) {
+    return pos * kHeavyLists + k;
+}
 // Transposed heavy items: the particles' candidate ranges overlap little (sparse particles
 // spread along a row beside a dense one), so the union of a segment's ranges -- what the shared
 // walk stages and every lane steps through -- is many times longer than any one particle's
@@ -522,7 +527,7 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                                           uint32_t heavy_work, uint32_t direct_mode,
                                           Control* ctl, uint32_t* __restrict__ lstream,
                                           uint32_t* __restrict__ lstream_t,
-                                          uint32_t* __restrict__ hslot) {
+                                          uint32_t* __restrict__ hslot, uint32_t hslot_cap) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
     __shared__ uint32_t s_count[kWaves];
@@ -588,7 +593,9 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
     }
     if (lane == 0) s_count[wave] = nh;
     __syncthreads();
-    // one append per workgroup, to sub-list blockIdx % kHeavyLists, in wave order
+    // one append per workgroup, to sub-list blockIdx % kHeavyLists, in wave order; the entry
+    // at position pos of list k has partial-sum slot heavy_slot(k, pos) if that is below
+    // hslot_cap, else none (kNoSlot: the spill kernels walk it)
     __shared__ uint32_t s_base;
     if (threadIdx.x == 0) {
         uint32_t tot = 0;
@@ -603,9 +610,10 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
         if ((uint32_t)k < s_count[w]) {
             const uint32_t pos = s_base + off + (uint32_t)k;
             const uint32_t ent = s_item[w * 3 + k];
-            const uint32_t slot = (bid % kHeavyLists) * heavy_cap + pos;
-            if (pos < heavy_cap) heavy[slot] = ent;
-            hslot[ent & ~kEntryFlags] = pos < heavy_cap ? slot : kNoSlot;
+            const uint32_t slot = heavy_slot(bid % kHeavyLists, pos);
+            // the sub-lists hold every item of the context (heavy_cap): pos < heavy_cap always
+            if (pos < heavy_cap) heavy[(bid % kHeavyLists) * heavy_cap + pos] = ent;
+            hslot[ent & ~kEntryFlags] = pos < heavy_cap && slot < hslot_cap ? slot : kNoSlot;
         }
     }
 }
@@ -625,13 +633,13 @@ __global__ __launch_bounds__(kPlanThreads, 8) void k_group_plan(
     GridDesc g, const uint64_t* __restrict__ cand_tag, uint8_t* __restrict__ flag,
     uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t heavy_work, uint32_t direct_mode,
     Control* ctl, uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
-    uint32_t* __restrict__ hslot) {
+    uint32_t* __restrict__ hslot, uint32_t hslot_cap) {
     if (blockIdx.x < kGroupBlocks)
         group_work(blockIdx.x, kGroupBlocks, big, cap, n, skeys, cstart, spos, svel, sidx, rank,
                    scratch, cell_grp, vrep, skip_tag, ctl);
     else
         plan_work(blockIdx.x - kGroupBlocks, skeys, n, g, cstart, cand_tag, flag, heavy,
-                  heavy_cap, heavy_work, direct_mode, ctl, lstream, lstream_t, hslot);
+                  heavy_cap, heavy_work, direct_mode, ctl, lstream, lstream_t, hslot, hslot_cap);
 }
 
 // The heavy work lists of this substep as one sequence: entry q of the concatenation of the
@@ -960,7 +968,8 @@ __device__ __forceinline__ size_t hpart_at(uint32_t slot, uint32_t hw, int part,
            (uint32_t)lane;
 }
 
-// Heavy entry q of the concatenated lists and its slot (list k, position i: k * cap + i).
+// Heavy entry q of the concatenated lists and its partial-sum slot (slots at or above the
+// context's hslot_cap do not exist).
 __device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict__ heavy,
                                                      const Control* __restrict__ ctl,
                                                      uint32_t cap, uint32_t q, uint32_t& slot) {
@@ -970,7 +979,7 @@ __device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict_
         if (q < c) break;
         q -= c;
     }
-    slot = (uint32_t)k * cap + q;
+    slot = heavy_slot((uint32_t)k, q);
     return heavy[(size_t)k * cap + q];
 }
 
@@ -1007,7 +1016,7 @@ void k_density_pass(
     const uint32_t* __restrict__ skip_tag, const Control* __restrict__ ctl,
     uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
     const uint32_t* __restrict__ heavy, uint32_t heavy_cap, float* __restrict__ hpart,
-    uint32_t hgrid) {
+    uint32_t hgrid, uint32_t hslot_cap) {
     constexpr uint32_t hw = HW;
     __shared__ float4 s_p[kWin];
     const int lane = threadIdx.x;
@@ -1020,9 +1029,10 @@ void k_density_pass(
         for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
+            if (slot >= hslot_cap) continue;  // uniform: no partial-sum slot (k_density_spill)
             float acc;
-            if (density_heavy_wave(entry, part, (int)hw, lane, s_p, spos, skeys, n, g, cstart, cell_grp,
-                                   h2, skip_tag, epoch, acc))
+            if (density_heavy_wave(entry, part, (int)hw, lane, s_p, spos, skeys, n, g, cstart,
+                                   cell_grp, h2, skip_tag, epoch, acc))
                 hpart[hpart_at(slot, hw, part, 0, lane)] = acc;
         }
         return;
@@ -1398,7 +1408,7 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
     const uint8_t* __restrict__ flag, const uint32_t* __restrict__ skip_tag,
     const Control* __restrict__ ctl, const uint32_t* __restrict__ lstream,
     const uint32_t* __restrict__ lstream_t, const uint32_t* __restrict__ heavy,
-    uint32_t heavy_cap, float* __restrict__ hpart, uint32_t hgrid) {
+    uint32_t heavy_cap, float* __restrict__ hpart, uint32_t hgrid, uint32_t hslot_cap) {
     constexpr uint32_t hw = HW;
     __shared__ float4 s_p[kWin];  // x, y, z, p_j
     __shared__ float4 s_v[kWin];  // u/rho_j, w/rho_j
@@ -1412,9 +1422,10 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
         for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
+            if (slot >= hslot_cap) continue;  // uniform: no partial-sum slot (k_force_spill)
             float o[4];
-            if (force_heavy_wave(entry, part, (int)hw, lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
-                                 g, cstart, cell_grp, K, stride, skip_tag, epoch, o)) {
+            if (force_heavy_wave(entry, part, (int)hw, lane, s_p, s_v, spos, svel, srho, rec, skeys,
+                                 n, g, cstart, cell_grp, K, stride, skip_tag, epoch, o)) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) hpart[hpart_at(slot, hw, part, c, lane)] = o[c];
             }
@@ -1425,6 +1436,92 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
     force_light(xcd_chunked(b - hparts, nl), lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
                 g, cstart, K, fpart, wpart, stride, items, flag, skip_tag, ctl, lstream,
                 lstream_t);
+}
+
+// Heavy items that got no partial-sum slot (FH_OPT_HEAVY_SLOTS caps the slots): one workgroup
+// of HW wavefronts per item, wave p computing part p as the pass kernels do; the parts meet in
+// LDS and are added in part order, as k_prep / k_finalize add a slotted item's (slab_part), so
+// the sums do not depend on which items got slots.  The result goes to the item's slab plane
+// like a light item's.  Launched only when the context has fewer slots than items.
+constexpr uint32_t kSpillGrid = 1024;
+template <uint32_t HW>
+__global__ __launch_bounds__(kWave * HW) void k_density_spill(
+    const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
+    float* __restrict__ dpart, uint32_t stride, const uint32_t* __restrict__ skip_tag,
+    const Control* __restrict__ ctl, const uint32_t* __restrict__ heavy, uint32_t heavy_cap,
+    uint32_t hslot_cap) {
+    __shared__ float4 s_p[HW][kWin];
+    __shared__ float s_sum[HW][kWave];
+    const int lane = threadIdx.x % kWave;
+    const int part = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
+    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform in the workgroup
+        uint32_t slot;
+        const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
+        if (slot < hslot_cap) continue;  // the pass kernel's parts have it
+        float acc = 0.0f;
+        // false in every part or in none (only group members are skipped)
+        const bool any = density_heavy_wave(entry, part, (int)HW, lane, s_p[part], spos, skeys,
+                                            n, g, cstart, cell_grp, h2, skip_tag, epoch, acc);
+        s_sum[part][lane] = acc;
+        __syncthreads();
+        const uint32_t item = entry & ~kEntryFlags;
+        const uint32_t s = (item / 3u) * kSub + (uint32_t)lane;
+        if (part == 0 && any && s < n) {
+            float t = 0.0f;
+#pragma unroll
+            for (int p = 0; p < (int)HW; p++) t += s_sum[p][lane];
+            dpart[(size_t)(item % 3u) * stride + s] = t;
+        }
+        __syncthreads();
+    }
+}
+
+template <uint32_t HW>
+__global__ __launch_bounds__(kWave * HW) void k_force_spill(
+    const float4* __restrict__ spos, const float4* __restrict__ svel,
+    const float* __restrict__ srho, const float4* __restrict__ rec,
+    const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
+    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
+    float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
+    const uint32_t* __restrict__ skip_tag, const Control* __restrict__ ctl,
+    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t hslot_cap) {
+    __shared__ float4 s_p[HW][kWin];
+    __shared__ float4 s_v[HW][kWin];
+    __shared__ float s_sum[HW][kHeavyComps][kWave];
+    const int lane = threadIdx.x % kWave;
+    const int part = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
+    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform in the workgroup
+        uint32_t slot;
+        const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
+        if (slot < hslot_cap) continue;
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const bool any = force_heavy_wave(entry, part, (int)HW, lane, s_p[part], s_v[part], spos,
+                                          svel, srho, rec, skeys, n, g, cstart, cell_grp, K,
+                                          stride, skip_tag, epoch, o);
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_sum[part][c][lane] = o[c];
+        __syncthreads();
+        const uint32_t item = entry & ~kEntryFlags;
+        const uint32_t s = (item / 3u) * kSub + (uint32_t)lane;
+        if (part == 0 && any && s < n) {
+            float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 0; p < (int)HW; p++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) t[c] += s_sum[p][c][lane];
+            const uint32_t slab = item % 3u;
+            float* f = fpart + (size_t)slab * 3u * stride;
+            f[s] = t[0];
+            f[stride + s] = t[1];
+            f[2u * (size_t)stride + s] = t[2];
+            // read only for a group representative (k_finalize finishes its members)
+            wpart[(size_t)slab * stride + s] = t[3];
+        }
+        __syncthreads();
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1592,7 +1689,7 @@ hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
                                 c->cell_grp, c->vrep, c->skip_tag, a.g, c->run_tag,
                                 c->heavy_flag, c->heavy, c->heavy_cap,
                                 c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode,
-                                c->ctl, c->lstream, c->lstream_t, c->hslot);
+                                c->ctl, c->lstream, c->lstream_t, c->hslot, c->hslot_cap);
     tend(c, KID_PLAN);
     return hipGetLastError();
 }
@@ -1608,9 +1705,17 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
         items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
-        c->heavy_cap, c->hpart, hgrid);
+        c->heavy_cap, c->hpart, hgrid, c->hslot_cap);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && c->hslot_cap < kHeavyLists * c->heavy_cap) {  // items may lack slots
+        const auto spill = hw == 8u ? k_density_spill<8> : k_density_spill<kHeavyWaves>;
+        spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
+            c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
+            c->skip_tag, c->ctl, c->heavy, c->heavy_cap, c->hslot_cap);
+        e = hipGetLastError();
+    }
     tend(c, KID_DENSITY);
-    return hipGetLastError();
+    return e;
 }
 
 
@@ -1654,9 +1759,18 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
         c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
-        c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid);
+        c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid, c->hslot_cap);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && c->hslot_cap < kHeavyLists * c->heavy_cap) {  // items may lack slots
+        const auto spill = hw == 8u ? k_force_spill<8> : k_force_spill<kHeavyWaves>;
+        spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
+            c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
+            c->fpart, c->wpart, c->max_n, c->skip_tag, c->ctl, c->heavy, c->heavy_cap,
+            c->hslot_cap);
+        e = hipGetLastError();
+    }
     tend(c, KID_FORCE);
-    return hipGetLastError();
+    return e;
 }
 
 // rank[id] = s for the particle id carried in the new state of slot s (sout[2 s + 1].w): the

@@ -30,6 +30,7 @@ FH_OPT_DIRECT_ITEMS = 3
 FH_OPT_HEAVY_PARTS = 4
 FH_OPT_EPOCH_PERIOD = 5
 FH_OPT_SPIN_LIMIT = 6
+FH_OPT_HEAVY_SLOTS = 7
 
 
 class LibraryNotBuilt(RuntimeError):

@@ -283,8 +283,9 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * restores the default (4).  More parts shorten the longest items (dense clumps: c4 is ~8 %
  * faster with 8), fewer cost less per item (c3 is ~2 % faster with 4).  Results differ only by
  * rounding.  The context holds the parts' partial sums for 4 parts; the first time 8 are set
- * it makes room for 8 (one allocation of ~192 bytes per particle of max_n, so set it outside
- * capture; fh_scratch_bytes counts it). */
+ * it makes room for 8 (one allocation, twice the FH_OPT_HEAVY_SLOTS buffer below, so set it
+ * outside capture; fh_scratch_bytes counts it; the context's captured graph is dropped and any
+ * graph captured on its stream before must be captured again). */
 #define FH_OPT_HEAVY_PARTS 4
 /* FH_OPT_EPOCH_PERIOD = 5: the work tags of the SPH rebuilds (co-located groups, skipped
  * sub-tiles, candidate group cells) compare a 30-bit epoch that every sort / rebuild start
@@ -300,6 +301,16 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * walk that needs a second poll gives up; the scatter stays in bounds, the output is wrong and
  * fh_sync returns FH_ESTATE).  Synchronises the stream. */
 #define FH_OPT_SPIN_LIMIT 6
+/* FH_OPT_HEAVY_SLOTS = 7: partial-sum slots of the fast passes' heavy items (4 KB each with 4
+ * parts, 8 KB with 8).  By default every (64-particle, z-slab) item of max_n has one (~192 bytes
+ * per particle of max_n with 4 parts); a smaller number bounds the context's memory.  A heavy
+ * item that gets no slot in a substep is walked by one wavefront of an extra kernel, part after
+ * part, and its parts are added in the same order as a slotted item's: the results are the same
+ * bit for bit, only that item is slower.  value = slots (0 or more than the items restores one
+ * per item).  One allocation, made at once: set it outside capture; fh_scratch_bytes counts it;
+ * the context's captured graph is dropped and any graph captured on its stream before must be
+ * captured again. */
+#define FH_OPT_HEAVY_SLOTS 7
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
 /* GravityModule (gravity.rs:31-34): v += g * dt. */

@@ -44,14 +44,18 @@ def rel_err(a, b):
 def set_mode(fh, f, cfg, mode):
     """fast: default work split; heavy: every (sub-tile, slab) item split into single-wave parts
     whose partials are added afterwards; light: none of them (one wavefront per item, shared
-    stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; direct:
-    every item walked lane by lane; exact: the bit-exact passes."""
+    stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; spill,
+    spill8: as heavy and heavy8 with 5 partial-sum slots (FH_OPT_HEAVY_SLOTS), so nearly every
+    item is walked by the spill kernels; direct: every item walked lane by lane; exact: the
+    bit-exact passes."""
     ctx = f.context(cfg.num_cells)
+    heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1}
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
-    ctx.set_option(fh.FH_OPT_HEAVY_WORK, {"heavy": 1, "heavy8": 1, "light": 1 << 30}.get(mode, 0))
+    ctx.set_option(fh.FH_OPT_HEAVY_WORK, heavy.get(mode, 1 << 30 if mode == "light" else 0))
     ctx.set_option(fh.FH_OPT_DIRECT_ITEMS,
-                   {"heavy": 0, "heavy8": 0, "light": 0, "direct": 2}.get(mode, 1))
-    ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode == "heavy8" else 0)
+                   0 if mode in heavy or mode == "light" else 2 if mode == "direct" else 1)
+    ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode in ("heavy8", "spill8") else 0)
+    ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 5 if mode in ("spill", "spill8") else 0)
 
 
 def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast", visible=None):
@@ -135,7 +139,8 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "spill", "light",
+                                  "direct"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
     from forge_hip import workloads
@@ -155,7 +160,8 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "light",
+                                  "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
@@ -215,7 +221,8 @@ def colocated_cfg(n=40_000, seed=33):
     return cfg, vel
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "light",
+                                  "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
@@ -562,3 +569,72 @@ def test_heavy_parts_option(fh, gpu_ctx):
         with pytest.raises(fh.ForgeError):
             gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, bad)
     gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
+
+
+def test_heavy_slots_option(fh, gpu_ctx):
+    """FH_OPT_HEAVY_SLOTS: a negative count is refused; a cap shrinks the context's scratch by
+    its partial-sum buffer and 0 (or more slots than items) restores it."""
+    full = gpu_ctx.scratch_bytes
+    with pytest.raises(fh.ForgeError):
+        gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, -1)
+    gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 1)
+    assert gpu_ctx.scratch_bytes < full
+    gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 2**31 - 1)
+    assert gpu_ctx.scratch_bytes == full
+    gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 3)
+    gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 0)
+    assert gpu_ctx.scratch_bytes == full
+
+
+@pytest.mark.parametrize("case", ["colocated", "c3"])
+def test_heavy_slot_cap_is_bit_identical(fh, gpu_ctx, case):
+    """With a few partial-sum slots (FH_OPT_HEAVY_SLOTS) most heavy items are walked part after
+    part by the spill kernels, whose parts are added in the order the slotted items' are: three
+    substeps equal the uncapped ones bit for bit, for the default split and for every item
+    heavy with 4 and 8 parts.  A graph captured with a cap replays to the eager fields, and a
+    later change of the cap drops the context's graph: the replay is refused rather than run on
+    the freed buffer.  c3: the 1M-particle dam break (co-located corner groups, transposed
+    items)."""
+    from forge_hip import workloads
+    if case == "c3":
+        cfg, vel = workloads.config3(), None
+    else:
+        cfg, vel = colocated_cfg()
+    for mode, cap in (("fast", 3), ("heavy", 1), ("heavy8", 17)):
+        print(f"heavy slot cap {case} {mode} cap={cap}", flush=True)
+        outs = []
+        for slots in (0, cap):
+            f = fields_from(fh, cfg, vel)
+            p = sph_pipeline(fh, cfg)
+            set_mode(fh, f, cfg, mode)
+            f.context(cfg.num_cells).set_option(fh.FH_OPT_HEAVY_SLOTS, slots)
+            torch.cuda.synchronize()
+            try:
+                p.run(f, cfg.dt, 3)
+            finally:
+                set_mode(fh, f, cfg, "fast")
+            outs.append(f.f32_fields)
+        for k in outs[0]:
+            assert torch.equal(outs[0][k], outs[1][k]), (mode, k)
+    print(f"heavy slot cap {case}: graph", flush=True)
+    f_e = fields_from(fh, cfg, vel)
+    f_g = fields_from(fh, cfg, vel)
+    p_e = sph_pipeline(fh, cfg)
+    p_g = sph_pipeline(fh, cfg)
+    ctx = f_g.context(cfg.num_cells)
+    ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 2)
+    try:
+        torch.cuda.synchronize()
+        p_g.capture(f_g, cfg.dt, 3)
+        assert f_g.context(cfg.num_cells) is ctx  # the capped context, not a grown one
+        for rep in range(2):
+            p_e.run(f_e, cfg.dt, 3)
+            p_g.replay(1)
+            ctx.sync()
+            for k in f_e.f32_fields:
+                assert torch.equal(f_e.f32_fields[k], f_g.f32_fields[k]), (rep, k)
+    finally:
+        ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 0)
+    with pytest.raises(fh.ForgeError) as e:
+        p_g.replay(1)
+    assert e.value.code == fh.FH_ESTATE
