@@ -69,6 +69,7 @@ int check_grid(fh_ctx* c, float cs, const float* origin, const uint32_t* dims, G
     g->nz = dims[2];
     g->div_x = make_divu32(dims[0]);
     g->div_xy = make_divu32(dims[0] * dims[1]);
+    g->sb = 0u;
     *cells = (uint32_t)C;
     return FH_OK;
 }
@@ -92,13 +93,15 @@ hipError_t alloc(T** p, size_t count, size_t* total) {
 // skeys / sidx (ascending id within a cell) and rank (its inverse), the gather into sorted
 // float4 order, and the CSR cell_start from the sorted keys (with the candidate co-located
 // groups of the fast passes).
+// g.sb > 0 (the fused module's fast path): the keys carry the sub-cell below the cell
+// (sort_key_of), and the last sort pass drops it, so skeys holds cells.
 hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float* px,
                        const float* py, const float* pz, const float* vx, const float* vy,
                        const float* vz, uint32_t n, bool with_vel) {
-    const uint32_t bits = bits_for_cells(cells);
+    const uint32_t bits = bits_for_cells(cells) + g.sb;
     hipError_t e = launch_hash_hist(c, px, py, pz, 1, n, g, bits, c->kb, nullptr, true);
     if (e == hipSuccess && n > 0)
-        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits, c->rank);
+        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx, n, bits, c->rank, g.sb);
     if (e == hipSuccess)
         e = launch_gather(c, g, cells, px, py, pz, vx, vy, vz, n, with_vel, !c->sph_exact);
     return e;
@@ -108,11 +111,10 @@ hipError_t sph_rebuild(fh_ctx* c, const GridDesc& g, uint32_t cells, const float
 // the place of particle ids as sort values; its cells were written to c->kb by the previous
 // substep's k_finalize, so only their histograms remain to be counted.
 hipError_t sph_rebuild_resident(fh_ctx* c, const GridDesc& g, uint32_t cells, uint32_t n) {
-    (void)g;
-    const uint32_t bits = bits_for_cells(cells);
+    const uint32_t bits = bits_for_cells(cells) + g.sb;
     hipError_t e = n ? launch_hist_keys(c, c->kb, n, bits, true) : hipSuccess;
     if (e == hipSuccess && n > 0)
-        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx2, n, bits);
+        e = launch_sort_passes(c, c->kb, nullptr, c->skeys, c->sidx2, n, bits, nullptr, g.sb);
     if (e == hipSuccess) e = launch_gather_resident(c, cells, n);
     return e;
 }
@@ -500,6 +502,8 @@ static int sph_fused_steps(fh_ctx* c, const fh_sph_params* prm, const fh_epilogu
     GridDesc g;
     uint32_t cells;
     if ((rc = check_sph(c, prm, &g, &cells, what))) return rc;
+    // FH_OPT_SUBCELL: the fast rebuilds order each cell by sub-cell (keys that still fit 32 bits)
+    if (!c->sph_exact && bits_for_cells(cells) + c->sub_bits <= 32u) g.sb = c->sub_bits;
     SphArgs a{g, prm->smoothing_radius, prm->particle_mass, prm->gas_constant,
               prm->rest_density, prm->viscosity_coefficient, dt, n};
     for (uint32_t k = 0; k < steps; k++) {
@@ -678,6 +682,12 @@ int fh_set_option(fh_ctx* c, int option, int value) {
             }
             return FH_OK;
         }
+        case FH_OPT_SUBCELL:
+            if (value != 0 && value != 2 && value != 4 && value != 8)
+                return fail(FH_EINVAL, "fh_set_option: sub-cells per axis %d is not 0, 2, 4 or 8",
+                            value);
+            c->sub_bits = value == 8 ? 9u : value == 4 ? 6u : value == 2 ? 3u : 0u;
+            return FH_OK;
         case FH_OPT_EPOCH_PERIOD:
             if (value < 0 || (uint32_t)value > kEpochPeriod)
                 return fail(FH_EINVAL, "fh_set_option: epoch period %d outside 0..%u", value,

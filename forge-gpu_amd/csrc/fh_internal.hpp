@@ -134,6 +134,7 @@ struct GridDesc {
     uint32_t nx, ny, nz;
     DivU32 div_x;   // by nx
     DivU32 div_xy;  // by nx * ny
+    uint32_t sb;    // sub-cell bits below the cell in the fast SPH path's sort keys (0, 3, 6, 9)
 };
 
 inline DivU32 make_divu32(uint32_t d) {
@@ -214,6 +215,7 @@ struct fh_ctx {
     uint32_t heavy_work; // FH_OPT_HEAVY_WORK (0: default)
     uint32_t direct_mode; // FH_OPT_DIRECT_ITEMS: 0 never, 1 automatic (default), 2 always
     uint32_t heavy_parts; // FH_OPT_HEAVY_PARTS (0: kHeavyWaves)
+    uint32_t sub_bits;    // FH_OPT_SUBCELL: sub-cell key bits of the fused module's fast rebuilds
     uint32_t* h_error;   // pinned host word for the device error flag
     // Epoch renewal.  Tags compare 30-bit epochs, so a tag left 2^30 - 1 starts ago would match
     // again; the host counts the starts it queues (graph replays included) and, before the
@@ -252,6 +254,29 @@ __device__ __forceinline__ uint32_t cell_of(float x, float y, float z, const Gri
     uint32_t cy = cell_coord(y, g.oy, g.cs, g.ny);
     uint32_t cz = cell_coord(z, g.oz, g.cs, g.nz);
     return cx + cy * g.nx + cz * g.nx * g.ny;
+}
+
+// Sort key of the fast SPH path: the cell, then (g.sb = 3, 6 or 9) the position's sub-cell,
+// B = 2, 4 or 8 per axis, in Morton order, so that the particles of a cell lie in compact runs and a
+// chunk of consecutive candidates covers a small box.  g.sb = 0: the cell (cell_of).  Positions
+// outside the grid keep their clamped cell and a sub-cell clamped to 0..B-1.
+__device__ __forceinline__ uint32_t sub_coord(float p, float o, float cs, uint32_t B) {
+    const float f = (p - o) / cs;
+    const float t = (f - floorf(f)) * (float)B;
+    if (!(t >= 0.0f)) return 0u;
+    return t >= (float)(B - 1u) ? B - 1u : (uint32_t)t;
+}
+__device__ __forceinline__ uint32_t sort_key_of(float x, float y, float z, const GridDesc& g) {
+    const uint32_t cell = cell_of(x, y, z, g);
+    if (g.sb == 0u) return cell;
+    const uint32_t B = 1u << (g.sb / 3u);
+    const uint32_t sx = sub_coord(x, g.ox, g.cs, B), sy = sub_coord(y, g.oy, g.cs, B),
+                   sz = sub_coord(z, g.oz, g.cs, B);
+    // interleave: bit b of each coordinate goes to bits 3b, 3b + 1, 3b + 2
+    uint32_t m = 0u;
+    for (uint32_t b = 0; b < g.sb / 3u; b++)
+        m |= (((sx >> b) & 1u) | (((sy >> b) & 1u) << 1) | (((sz >> b) & 1u) << 2)) << (3u * b);
+    return (cell << g.sb) | m;
 }
 
 __device__ __forceinline__ uint32_t divu32(uint32_t x, DivU32 d) {
@@ -351,7 +376,7 @@ hipError_t launch_hash_hist(fh_ctx* c, const float* x, const float* y, const flo
 // the device; the others ping-pong through the context's scratch.
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
                               uint32_t* vfin, uint32_t n, uint32_t num_bits,
-                              uint32_t* rank = nullptr);
+                              uint32_t* rank = nullptr, uint32_t kshift = 0);
 hipError_t launch_fill_u32(fh_ctx* c, uint32_t* p, uint32_t value, uint32_t n);
 hipError_t launch_boundaries(fh_ctx* c, const uint32_t* sorted_keys, uint32_t n,
                              uint32_t num_cells, uint32_t* cell_start, uint32_t* cell_end);

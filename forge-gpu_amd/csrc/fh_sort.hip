@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
             k[j] = 0u;
             if (i < n) {
                 const size_t o = (size_t)i * stride;
-                k[j] = cell_of(x[o], y[o], z[o], g);
+                k[j] = sort_key_of(x[o], y[o], z[o], g);
             }
         }
 #pragma unroll
@@ -393,6 +393,7 @@ struct SortIO {
     uint32_t in_place;
     const uint32_t* pre; // first-pass tile prefixes (k_hist_reduce), or null
     uint32_t tiles;      // tiles of a pass (the group sums follow them in pre)
+    uint32_t kshift;     // the last pass writes key >> kshift to kfin (sub-cell bits dropped)
 };
 
 struct PassBufs {
@@ -706,7 +707,8 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
     for (int k = 0; k < Items; k++) {
         const uint32_t i = (uint32_t)(k * kSortThreads + tid);
         dst[k] = s_gbase[(skey[k] >> shift) & mask] + i;
-        if ((full || i < valid) && dst[k] < n && bf.kout) bf.kout[dst[k]] = skey[k];
+        if ((full || i < valid) && dst[k] < n && bf.kout)
+            bf.kout[dst[k]] = last ? skey[k] >> io.kshift : skey[k];
     }
 #pragma unroll
     for (int k = 0; k < Items; k++) s_buf[pos[k]] = vals[k];
@@ -732,7 +734,8 @@ __global__ __launch_bounds__(256) void k_sort_finish(SortIO io, const Control* c
 }
 
 hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0, uint32_t* kfin,
-                              uint32_t* vfin, uint32_t n, uint32_t num_bits, uint32_t* rank) {
+                              uint32_t* vfin, uint32_t n, uint32_t num_bits, uint32_t* rank,
+                              uint32_t kshift) {
     const Digits L = digits_for(num_bits, n);
     const uint32_t passes = L.passes, nb = 1u << L.bits;
     // large 8-bit sorts: 12,288-key tiles and the plan without first-pass prefixes
@@ -742,7 +745,7 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
-              large ? nullptr : first_pass_pre(c, n), tiles};
+              large ? nullptr : first_pass_pre(c, n), tiles, kshift};
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t shift = L.bits * p, pbits = min(L.bits, num_bits - shift);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * nb;

@@ -662,6 +662,69 @@ __device__ __forceinline__ float4 chunk_load(const float4* __restrict__ spos, ui
     return (uint32_t)lane < m ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
+// Bounding box of the positions of the lanes with `on` (uniform; no such lane: lo = +inf,
+// hi = -inf, which no candidate is near).  NaN coordinates are ignored (fminf / fmaxf); a lane
+// whose coordinate is NaN has no pair at all.
+struct Box {
+    float lx, ly, lz, hx, hy, hz;
+};
+// (the reduced value is the same in every lane: read from lane 0 into a scalar register)
+__device__ __forceinline__ float wave_fmin(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ float wave_fmax(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ Box lane_box(const float4& p, bool on) {
+    const float inf = __builtin_inff();
+    Box b;
+    b.lx = wave_fmin(on ? p.x : inf);
+    b.ly = wave_fmin(on ? p.y : inf);
+    b.lz = wave_fmin(on ? p.z : inf);
+    b.hx = wave_fmax(on ? p.x : -inf);
+    b.hy = wave_fmax(on ? p.y : -inf);
+    b.hz = wave_fmax(on ? p.z : -inf);
+    return b;
+}
+
+// The lanes whose candidate of a chunk (this lane's v, if `valid`) lies within sqrt(lim) of
+// the box (a chunk with none is skipped).  The distance of a pair is at least its candidate's distance to the box of the other
+// particles, so a chunk with no candidate within h of the item's box holds no pair of its
+// particles; lim = h^2 (1 + 2^-10) leaves room for the rounding of either computation.  A NaN
+// candidate coordinate counts as near (the pair test rejects it).
+__device__ __forceinline__ uint64_t near_mask(const float4& v, bool valid, const Box& b,
+                                              float lim) {
+    const float dx = fmaxf(fmaxf(b.lx - v.x, v.x - b.hx), 0.0f);
+    const float dy = fmaxf(fmaxf(b.ly - v.y, v.y - b.hy), 0.0f);
+    const float dz = fmaxf(fmaxf(b.lz - v.z, v.z - b.hz), 0.0f);
+    return __ballot(valid && fmaf(dz, dz, fmaf(dy, dy, dx * dx)) <= lim);
+}
+
+// Rows (bit r) whose interval [b[r], e[r]) is the same in every lane of the segment: each chunk
+// of such a row lies inside every lane's interval, so it can be compacted to its candidates near
+// the item's box (near_mask) before the pair loop.
+__device__ __forceinline__ uint32_t same_rows(const uint32_t b[3], const uint32_t e[3], bool mine,
+                                              int leader) {
+    uint32_t same = 0u;
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b[r], leader);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)e[r], leader);
+        if (__ballot(mine && (b[r] != lo || e[r] != hi)) == 0ull) same |= 1u << r;
+    }
+    return same;
+}
+
+// Position of this lane among the set bits of `mask` below it.
+__device__ __forceinline__ uint32_t mask_rank(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 // Next non-empty row after r (3 if none) of a segment whose row r spans [lo[r], hi[r]).
 __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[3], int r) {
     for (r = r + 1; r < 3; r++)
@@ -893,6 +956,7 @@ __device__ __forceinline__ void seg_plans(RowPlan R[3], const CellXYZ& ci, const
 // wave, wave + hw, ... of each segment row; the transposed walk's lanes trans_lanes(wave, hw)),
 // hw = the item's part count.
 // False when the item is skipped (only group members).
+template <bool CULL>
 __device__ __forceinline__ bool density_heavy_wave(
     uint32_t entry, int wave, int hw, int lane, float4* buf, const float4* __restrict__ spos,
     const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
@@ -907,6 +971,10 @@ __device__ __forceinline__ bool density_heavy_wave(
     const uint32_t s = sub * kSub + (uint32_t)lane;
     const bool live = s < n;
     const float4 pi = load_or(spos, s, live, z4);
+    // the item's box, for skipping chunks far from all of its particles (chunk_near); taken
+    // here, where few values are live (per segment it would cost registers in the force pass)
+    const Box box = CULL ? lane_box(pi, live) : Box{};
+    const float lim = h2 * (1.0f + 0x1p-10f);
     const CellXYZ ci = key_xyz(load_or(skeys, s, live, 0u), g);
     uint32_t b[3], e[3];
     slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
@@ -927,26 +995,40 @@ __device__ __forceinline__ bool density_heavy_wave(
         seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
                   lane);
         // chunks wave, wave + hw, ... of the segment's three rows; the next is fetched before
-        // the current one is evaluated
+        // the current one is evaluated; a chunk with no candidate near the item is skipped
+        const uint32_t same = CULL ? same_rows(b, e, mine, leader) : 0u;
         uint32_t t = (uint32_t)wave;
         int r;
         uint32_t c0, m;
         seg_chunk(R, t, r, c0, m);
         float4 v = r < 3 ? chunk_load(spos, c0, m, lane) : z4;
         while (r < 3) {  // uniform within the wave
+            const uint64_t near = CULL ? near_mask(v, (uint32_t)lane < m, box, lim) : ~0ull;
+            const bool go = near != 0ull;
             int nr;
             uint32_t nc0, nm;
             seg_chunk(R, t + (uint32_t)hw, nr, nc0, nm);
             const float4 nv = nr < 3 ? chunk_load(spos, nc0, nm, lane) : z4;
             const uint32_t j = c0 + (uint32_t)lane;
-            __builtin_amdgcn_wave_barrier();
-            buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
-            __builtin_amdgcn_wave_barrier();
-            if (mine) {
-                const uint32_t jb = max(pick3(b, r), c0), je = min(pick3(e, r), c0 + m);
-                // candidate weights other than 1 only in items that touch a group
-                acc = cut ? density_run_w(buf, c0, jb, je, pi, h2, acc)
-                          : density_run(buf, c0, jb, je, pi, h2, acc);
+            if (CULL && go && ((same >> r) & 1u)) {  // uniform: the near candidates only
+                __builtin_amdgcn_wave_barrier();
+                if ((near >> lane) & 1ull)
+                    buf[mask_rank(near)] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
+                __builtin_amdgcn_wave_barrier();
+                const uint32_t k = (uint32_t)__popcll(near);
+                if (mine)
+                    acc = cut ? density_run_w(buf, 0u, 0u, k, pi, h2, acc)
+                              : density_run(buf, 0u, 0u, k, pi, h2, acc);
+            } else if (go) {  // uniform
+                __builtin_amdgcn_wave_barrier();
+                buf[lane] = make_float4(v.x, v.y, v.z, candidate_weight(v.w, j));
+                __builtin_amdgcn_wave_barrier();
+                if (mine) {
+                    const uint32_t jb = max(pick3(b, r), c0), je = min(pick3(e, r), c0 + m);
+                    // candidate weights other than 1 only in items that touch a group
+                    acc = cut ? density_run_w(buf, c0, jb, je, pi, h2, acc)
+                              : density_run(buf, c0, jb, je, pi, h2, acc);
+                }
             }
             t += (uint32_t)hw;
             r = nr;
@@ -1007,7 +1089,7 @@ __device__ __forceinline__ void heavy_part_of(uint32_t b, uint32_t hw, uint32_t&
 // wave.  The parts leave their partial sums in hpart; k_prep and k_finalize add them in part
 // order.  Held to 8 waves per SIMD (the SGPRs of both paths otherwise limit it to 7; fixed c3
 // state 492 -> 489 us per substep).
-template <uint32_t HW>
+template <uint32_t HW, bool CULL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kWave, kWave), amdgpu_waves_per_eu(8, 8)))
 void k_density_pass(
     const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
@@ -1031,7 +1113,7 @@ void k_density_pass(
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             if (slot >= hslot_cap) continue;  // uniform: no partial-sum slot (k_density_spill)
             float acc;
-            if (density_heavy_wave(entry, part, (int)hw, lane, s_p, spos, skeys, n, g, cstart,
+            if (density_heavy_wave<CULL>(entry, part, (int)hw, lane, s_p, spos, skeys, n, g, cstart,
                                    cell_grp, h2, skip_tag, epoch, acc))
                 hpart[hpart_at(slot, hw, part, 0, lane)] = acc;
         }
@@ -1319,6 +1401,7 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
 // One virtual wave (`wave` of hw) of heavy entry `entry` in the force pass: its partial
 // acceleration (with the -wv v_i viscosity part, which adds linearly) and viscosity weight.
 // False when the item is skipped (only group members).
+template <bool CULL>
 __device__ __forceinline__ bool force_heavy_wave(
     uint32_t entry, int wave, int hw, int lane, float4* bp, float4* bv, const float4* __restrict__ spos,
     const float4* __restrict__ svel, const float* __restrict__ srho,
@@ -1338,6 +1421,8 @@ __device__ __forceinline__ bool force_heavy_wave(
     const float rho_i = load_or(srho, s, in, 0.0f);
     const bool live = in && !(rho_i < 1e-6f);
     const float p_i = K.k * (rho_i - K.rho0);
+    const Box box = CULL ? lane_box(pi, live) : Box{};  // as in density_heavy_wave
+    const float lim = K.h2 * (1.0f + 0x1p-10f);
     const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
     uint32_t b[3], e[3];
     slab_ranges(ci, live, g, cstart, n, (int)slab - 1, b, e);
@@ -1358,6 +1443,7 @@ __device__ __forceinline__ bool force_heavy_wave(
         RowPlan R[3];
         seg_plans(R, ci, g, (int)slab - 1, b, e, leader, last, cut, cstart, cell_grp, epoch,
                   lane);
+        const uint32_t same = CULL ? same_rows(b, e, mine, leader) : 0u;  // as in density
         uint32_t t = (uint32_t)wave;
         int r;
         uint32_t c0, m;
@@ -1367,18 +1453,35 @@ __device__ __forceinline__ bool force_heavy_wave(
         float4 q = load_or(rec, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
         float4 w = load_or(rec + stride, c0 + min((uint32_t)lane, m - 1u), r < 3, z4);
         while (r < 3) {  // uniform within the wave
+            // a chunk with no record near the item is skipped (chunk_near); decided before
+            // the next chunk's loads are issued, so its temporaries are not live beside them
+            const uint64_t near = CULL ? near_mask(q, (uint32_t)lane < m, box, lim) : ~0ull;
+            const bool go = near != 0ull;
             int nr;
             uint32_t nc0, nm;
             seg_chunk(R, t + (uint32_t)hw, nr, nc0, nm);
             const float4 nq = load_or(rec, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
             const float4 nw = load_or(rec + stride, nc0 + min((uint32_t)lane, nm - 1u), nr < 3, z4);
-            __builtin_amdgcn_wave_barrier();
-            bp[lane] = q;
-            bv[lane] = w;
-            __builtin_amdgcn_wave_barrier();
-            if (mine)
-                force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m), pi,
-                                 p_i, K, ax, ay, az, wv);
+            if (CULL && go && ((same >> r) & 1u)) {  // uniform: the near records only
+                __builtin_amdgcn_wave_barrier();
+                if ((near >> lane) & 1ull) {
+                    const uint32_t x = mask_rank(near);
+                    bp[x] = q;
+                    bv[x] = w;
+                }
+                __builtin_amdgcn_wave_barrier();
+                if (mine)
+                    force_run<FH_HU>(bp, bv, 0u, 0u, (uint32_t)__popcll(near), pi, p_i, K, ax, ay,
+                                     az, wv);
+            } else if (go) {  // uniform
+                __builtin_amdgcn_wave_barrier();
+                bp[lane] = q;
+                bv[lane] = w;
+                __builtin_amdgcn_wave_barrier();
+                if (mine)
+                    force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m),
+                                     pi, p_i, K, ax, ay, az, wv);
+            }
             t += (uint32_t)hw;
             r = nr;
             c0 = nc0;
@@ -1398,8 +1501,10 @@ __device__ __forceinline__ bool force_heavy_wave(
 }
 
 // Force pass, one launch: heavy parts first, then one light item per wave (as k_density_pass).
-template <uint32_t HW>
-__global__ __launch_bounds__(kWave) void k_force_pass(
+// With the chunk tests (CULL) at least 6 waves per SIMD (80 registers): held to 7 it spills 2
+// registers to scratch, which was 3 % slower on configs[4].
+template <uint32_t HW, bool CULL>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(CULL ? 6 : 1, 8))) void k_force_pass(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
     const float* __restrict__ srho, const float4* __restrict__ rec,
     const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
@@ -1424,7 +1529,7 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
             if (slot >= hslot_cap) continue;  // uniform: no partial-sum slot (k_force_spill)
             float o[4];
-            if (force_heavy_wave(entry, part, (int)hw, lane, s_p, s_v, spos, svel, srho, rec, skeys,
+            if (force_heavy_wave<CULL>(entry, part, (int)hw, lane, s_p, s_v, spos, svel, srho, rec, skeys,
                                  n, g, cstart, cell_grp, K, stride, skip_tag, epoch, o)) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) hpart[hpart_at(slot, hw, part, c, lane)] = o[c];
@@ -1444,7 +1549,7 @@ __global__ __launch_bounds__(kWave) void k_force_pass(
 // the sums do not depend on which items got slots.  The result goes to the item's slab plane
 // like a light item's.  Launched only when the context has fewer slots than items.
 constexpr uint32_t kSpillGrid = 1024;
-template <uint32_t HW>
+template <uint32_t HW, bool CULL>
 __global__ __launch_bounds__(kWave * HW) void k_density_spill(
     const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
@@ -1462,7 +1567,7 @@ __global__ __launch_bounds__(kWave * HW) void k_density_spill(
         if (slot < hslot_cap) continue;  // the pass kernel's parts have it
         float acc = 0.0f;
         // false in every part or in none (only group members are skipped)
-        const bool any = density_heavy_wave(entry, part, (int)HW, lane, s_p[part], spos, skeys,
+        const bool any = density_heavy_wave<CULL>(entry, part, (int)HW, lane, s_p[part], spos, skeys,
                                             n, g, cstart, cell_grp, h2, skip_tag, epoch, acc);
         s_sum[part][lane] = acc;
         __syncthreads();
@@ -1478,7 +1583,7 @@ __global__ __launch_bounds__(kWave * HW) void k_density_spill(
     }
 }
 
-template <uint32_t HW>
+template <uint32_t HW, bool CULL>
 __global__ __launch_bounds__(kWave * HW) void k_force_spill(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
     const float* __restrict__ srho, const float4* __restrict__ rec,
@@ -1498,7 +1603,7 @@ __global__ __launch_bounds__(kWave * HW) void k_force_spill(
         const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
         if (slot < hslot_cap) continue;
         float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const bool any = force_heavy_wave(entry, part, (int)HW, lane, s_p[part], s_v[part], spos,
+        const bool any = force_heavy_wave<CULL>(entry, part, (int)HW, lane, s_p[part], s_v[part], spos,
                                           svel, srho, rec, skeys, n, g, cstart, cell_grp, K,
                                           stride, skip_tag, epoch, o);
 #pragma unroll
@@ -1623,7 +1728,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     }
     sout[2u * s] = make_float4(npx, npy, npz, rho);
     sout[2u * s + 1u] = make_float4(nvx, nvy, nvz, v.w);  // .w: the particle id
-    if (keys_out) keys_out[s] = cell_of(npx, npy, npz, g);  // the next resident substep's keys
+    if (keys_out) keys_out[s] = sort_key_of(npx, npy, npz, g);  // the next resident substep's keys
     if (want_accel) sout[2 * (size_t)stride + s] = make_float4(ax, ay, az, 0.0f);
 }
 
@@ -1701,14 +1806,20 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     tbeg(c, KID_DENSITY);
     const uint32_t hgrid = heavy_grid(items);
     const uint32_t hw = heavy_parts(c);
-    const auto kernel = hw == 8u ? k_density_pass<8> : k_density_pass<kHeavyWaves>;
+    // the heavy walks skip far chunks only where the cells are ordered by sub-cell (g.sb > 0)
+    const bool cull = a.g.sb != 0u;
+    const auto kernel = hw == 8u ? (cull ? k_density_pass<8, true> : k_density_pass<8, false>)
+                                 : (cull ? k_density_pass<kHeavyWaves, true>
+                                         : k_density_pass<kHeavyWaves, false>);
     kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
         items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
         c->heavy_cap, c->hpart, hgrid, c->hslot_cap);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && c->hslot_cap < kHeavyLists * c->heavy_cap) {  // items may lack slots
-        const auto spill = hw == 8u ? k_density_spill<8> : k_density_spill<kHeavyWaves>;
+        const auto spill = hw == 8u ? (cull ? k_density_spill<8, true> : k_density_spill<8, false>)
+                                    : (cull ? k_density_spill<kHeavyWaves, true>
+                                            : k_density_spill<kHeavyWaves, false>);
         spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
             c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
             c->skip_tag, c->ctl, c->heavy, c->heavy_cap, c->hslot_cap);
@@ -1755,14 +1866,19 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     tbeg(c, KID_FORCE);
     const uint32_t hgrid = heavy_grid(items);
     const uint32_t hw = heavy_parts(c);
-    const auto kernel = hw == 8u ? k_force_pass<8> : k_force_pass<kHeavyWaves>;
+    const bool cull = a.g.sb != 0u;  // as in launch_density_fast
+    const auto kernel = hw == 8u ? (cull ? k_force_pass<8, true> : k_force_pass<8, false>)
+                                 : (cull ? k_force_pass<kHeavyWaves, true>
+                                         : k_force_pass<kHeavyWaves, false>);
     kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
         c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
         c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid, c->hslot_cap);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && c->hslot_cap < kHeavyLists * c->heavy_cap) {  // items may lack slots
-        const auto spill = hw == 8u ? k_force_spill<8> : k_force_spill<kHeavyWaves>;
+        const auto spill = hw == 8u ? (cull ? k_force_spill<8, true> : k_force_spill<8, false>)
+                                    : (cull ? k_force_spill<kHeavyWaves, true>
+                                            : k_force_spill<kHeavyWaves, false>);
         spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
             c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
             c->fpart, c->wpart, c->max_n, c->skip_tag, c->ctl, c->heavy, c->heavy_cap,

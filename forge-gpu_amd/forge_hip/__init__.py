@@ -9,6 +9,7 @@ none.
 from ._lib import (FH_EINVAL, FH_ENODEV, FH_EPI_BOX, FH_EPI_GRAVITY, FH_EPI_INTEGRATE,
                    FH_ERANGE, FH_ESTATE, FH_OK, FH_OPT_DIRECT_ITEMS, FH_OPT_EPOCH_PERIOD,
                    FH_OPT_HEAVY_PARTS, FH_OPT_HEAVY_SLOTS, FH_OPT_HEAVY_WORK, FH_OPT_SPH_EXACT,
+                   FH_OPT_SUBCELL,
                    FH_OPT_SPIN_LIMIT,
                    ForgeError, LibraryNotBuilt, load)
 from .hashgrid import HashGrid, RadixSorter, cell_start_csr, find_cell_boundaries
@@ -22,7 +23,7 @@ __all__ = [
     "FH_OK", "FH_EINVAL", "FH_ERANGE", "FH_ESTATE", "FH_ENODEV", "FH_EPI_GRAVITY",
     "FH_EPI_INTEGRATE", "FH_EPI_BOX", "FH_OPT_SPH_EXACT", "FH_OPT_HEAVY_WORK",
     "FH_OPT_DIRECT_ITEMS", "FH_OPT_HEAVY_PARTS", "FH_OPT_EPOCH_PERIOD", "FH_OPT_SPIN_LIMIT",
-    "FH_OPT_HEAVY_SLOTS",
+    "FH_OPT_HEAVY_SLOTS", "FH_OPT_SUBCELL",
     "ForgeError", "LibraryNotBuilt", "load", "HashGrid",
     "RadixSorter", "find_cell_boundaries", "cell_start_csr", "FieldSet", "SimModule", "Pipeline",
     "SphDensityModule", "SphFusedModule", "SphPressureModule", "SphViscosityModule",

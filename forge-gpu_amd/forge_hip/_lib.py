@@ -31,6 +31,7 @@ FH_OPT_HEAVY_PARTS = 4
 FH_OPT_EPOCH_PERIOD = 5
 FH_OPT_SPIN_LIMIT = 6
 FH_OPT_HEAVY_SLOTS = 7
+FH_OPT_SUBCELL = 8
 
 
 class LibraryNotBuilt(RuntimeError):

@@ -35,6 +35,7 @@ pub const FH_OPT_HEAVY_PARTS: c_int = 4;
 pub const FH_OPT_EPOCH_PERIOD: c_int = 5;
 pub const FH_OPT_SPIN_LIMIT: c_int = 6;
 pub const FH_OPT_HEAVY_SLOTS: c_int = 7;
+pub const FH_OPT_SUBCELL: c_int = 8;
 
 pub const FH_NOALLOC_MAX_N: u32 = 1_048_576;
 pub const FH_NOALLOC_SCRATCH_BYTES: u32 = 19_939_328;

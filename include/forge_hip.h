@@ -311,6 +311,16 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * the context's captured graph is dropped and any graph captured on its stream before must be
  * captured again. */
 #define FH_OPT_HEAVY_SLOTS 7
+/* FH_OPT_SUBCELL = 8: sub-cells per axis (0: off, the default; 2, 4 or 8) by which the fused
+ * module's fast rebuilds order the particles inside each cell (Morton order of the sub-cells:
+ * 3, 6 or 9 more key bits, so more sort passes where the keys then need them).  A run of
+ * consecutive candidates then covers a small box: the heavy items skip the 64-candidate chunks
+ * with no candidate within h of their particles' box and pass only the near candidates of the
+ * others to the pair loop.  Dense clumps gain (configs[4] with 8: 98 -> 63 ms); moderate
+ * densities lose more in the extra sort passes than they gain (configs[3]: 414 -> 425 us with
+ * 2).  Results differ only by rounding (the summation order); fh_sph_density and the bit-exact
+ * mode are not affected. */
+#define FH_OPT_SUBCELL 8
 int fh_set_option(fh_ctx* ctx, int option, int value);
 
 /* GravityModule (gravity.rs:31-34): v += g * dt. */

@@ -46,16 +46,21 @@ def set_mode(fh, f, cfg, mode):
     whose partials are added afterwards; light: none of them (one wavefront per item, shared
     stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; spill,
     spill8: as heavy and heavy8 with 5 partial-sum slots (FH_OPT_HEAVY_SLOTS), so nearly every
-    item is walked by the spill kernels; direct: every item walked lane by lane; exact: the
-    bit-exact passes."""
+    item is walked by the spill kernels; subcell, subcell2, subcell8: as fast with the cells
+    ordered by 4, 2 or 8 sub-cells per axis (FH_OPT_SUBCELL), so that heavy items skip far
+    candidate chunks and compact the others to their near candidates;
+    subheavy: every item heavy, with 4 sub-cells per axis; direct: every item walked lane by
+    lane; exact: the bit-exact passes."""
     ctx = f.context(cfg.num_cells)
-    heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1}
+    heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1, "subheavy": 1}
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, heavy.get(mode, 1 << 30 if mode == "light" else 0))
     ctx.set_option(fh.FH_OPT_DIRECT_ITEMS,
                    0 if mode in heavy or mode == "light" else 2 if mode == "direct" else 1)
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode in ("heavy8", "spill8") else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 5 if mode in ("spill", "spill8") else 0)
+    ctx.set_option(fh.FH_OPT_SUBCELL,
+                   {"subcell": 4, "subcell2": 2, "subcell8": 8, "subheavy": 4}.get(mode, 0))
 
 
 def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast", visible=None):
@@ -139,8 +144,8 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "spill", "light",
-                                  "direct"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "spill", "subcell",
+                                  "subheavy", "light", "direct"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
     from forge_hip import workloads
@@ -160,8 +165,8 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "light",
-                                  "direct"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "subcell",
+                                  "subcell2", "subcell8", "subheavy", "light", "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
@@ -221,8 +226,8 @@ def colocated_cfg(n=40_000, seed=33):
     return cfg, vel
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "light",
-                                  "direct"])
+@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "subcell",
+                                  "subcell8", "subheavy", "light", "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
@@ -272,7 +277,8 @@ def viscosity_cfg(case):
 
 
 @pytest.mark.parametrize("case", ["lattice", "groups", "colocated"])
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "subheavy", "light",
+                                  "direct"])
 def test_viscosity_without_pressure_matches_oracle(fh, gpu_ctx, oracle, case, mode):
     """The fused force's viscosity half (sph_fused.rs:617-623) on its own, in every work split:
     plain lattice particles, and members of co-located groups, which are finished from their
@@ -314,14 +320,15 @@ def test_fused_epilogue_equals_separate_modules(fh, gpu_ctx):
         assert np.array_equal(outs[0][k], outs[1][k]), k
 
 
-@pytest.mark.parametrize("resident,case", [(True, "small"), (False, "small"), (True, "c3")])
+@pytest.mark.parametrize("resident,case", [(True, "small"), (False, "small"), (True, "c3"),
+                                           (True, "c3_subcell")])
 def test_graph_replay_matches_eager(fh, gpu_ctx, resident, case):
     """10 captured substeps replayed twice == the same 10 substeps run eagerly twice, bit for
     bit; each replay is checked after eager work and synchronisation in between (graph nodes
     must not go stale).  resident: one fh_sph_fused_steps call of 10 substeps; otherwise 10
     fh_sph_fused calls.  c3: the full 1M-particle dam break (co-located corner groups, heavy
     and transposed items, both streams), whose heavy-list order varies from run to run while
-    every item's sums must not."""
+    every item's sums must not.  c3_subcell: the same with 4 sub-cells per axis."""
     from forge_hip import workloads
     cfg = workloads.small_sph(n=16384, cols=32) if case == "small" else workloads.config3()
     print(f"graph replay {case} resident={resident}", flush=True)
@@ -330,14 +337,19 @@ def test_graph_replay_matches_eager(fh, gpu_ctx, resident, case):
     p_e = sph_pipeline(fh, cfg)
     p_g = sph_pipeline(fh, cfg)
     p_e.resident = p_g.resident = resident
-    torch.cuda.synchronize()
-    p_g.capture(f_g, cfg.dt, 10)
-    for rep in range(2):
-        p_e.run(f_e, cfg.dt, 10)
-        p_g.replay(1)
-        f_g.context().sync()
-        for k in f_e.f32_fields:
-            assert torch.equal(f_e.f32_fields[k], f_g.f32_fields[k]), (rep, k)
+    ctx = f_g.context(cfg.num_cells)
+    ctx.set_option(fh.FH_OPT_SUBCELL, 4 if case == "c3_subcell" else 0)
+    try:
+        torch.cuda.synchronize()
+        p_g.capture(f_g, cfg.dt, 10)
+        for rep in range(2):
+            p_e.run(f_e, cfg.dt, 10)
+            p_g.replay(1)
+            f_g.context().sync()
+            for k in f_e.f32_fields:
+                assert torch.equal(f_e.f32_fields[k], f_g.f32_fields[k]), (rep, k)
+    finally:
+        ctx.set_option(fh.FH_OPT_SUBCELL, 0)
 
 
 def test_density_module_matches_oracle(fh, gpu_ctx, oracle):
@@ -379,8 +391,8 @@ def test_standalone_modules_match_oracle(fh, gpu_ctx, oracle):
         assert np.array_equal(gpu, o), nm
 
 
-@pytest.mark.parametrize("parts", [4, 8])
-def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts):
+@pytest.mark.parametrize("parts,sub", [(4, 0), (8, 0), (8, 4), (8, 8)])
+def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, sub):
     """configs[4] at full size (8,388,608 particles, 64 Gaussian clumps + 10 % uniform, cells of
     0 to ~27,000 particles): one HashGrid build (bit-exact), then one fused SPH pass.  The full
     CPU passes would take ~1.3e11 candidate tests each, so the oracle evaluates a sample: 4096
@@ -388,7 +400,8 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts):
     is checked against or_sph_density_at (rel 1e-4); the acceleration against
     or_sph_force_f64_at evaluated on the GPU's densities (themselves checked on the sample),
     within 1e-4 * sum|pair terms|.  Random velocities make the viscosity term non-zero.
-    parts: wavefronts per heavy item (FH_OPT_HEAVY_PARTS), the default and the bench's."""
+    parts: wavefronts per heavy item (FH_OPT_HEAVY_PARTS); sub: sub-cells per axis
+    (FH_OPT_SUBCELL); (8, 8) is the bench's setting."""
     from forge_hip import workloads
     cfg = workloads.config4()
     n = cfg.n
@@ -411,14 +424,16 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts):
     m.accel = accel
     p.add(m)
     torch.cuda.synchronize()
-    print(f"c4 fused pass ({parts} parts): max occupancy {occ.max()}, "
+    print(f"c4 fused pass ({parts} parts, {sub} sub-cells): max occupancy {occ.max()}, "
           f"p99 {np.percentile(occ, 99):.0f}", flush=True)
     ctx = f.context(cfg.num_cells)
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, parts)
+    ctx.set_option(fh.FH_OPT_SUBCELL, sub)
     try:
         p.step(f, cfg.dt)
     finally:
         ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
+        ctx.set_option(fh.FH_OPT_SUBCELL, 0)
     rho = f.f32_fields["density"].cpu().numpy()
     acc = accel.cpu().numpy().astype(np.float64)
     dense = int(np.argmax(occ))
@@ -475,8 +490,12 @@ def resident_case(case):
     return cfg, vel, 4
 
 
-@pytest.mark.parametrize("case", ["small", "colocated", "c0", "lattice_k0", "groups_k0", "c3"])
-def test_resident_substeps_match_oracle(fh, gpu_ctx, oracle, case):
+@pytest.mark.parametrize("case,mode", [("small", "fast"), ("colocated", "fast"), ("c0", "fast"),
+                                       ("lattice_k0", "fast"), ("groups_k0", "fast"),
+                                       ("c3", "fast"), ("small", "subheavy"),
+                                       ("colocated", "subcell"), ("groups_k0", "subheavy"),
+                                       ("c3", "subcell")])
+def test_resident_substeps_match_oracle(fh, gpu_ctx, oracle, case, mode):
     """Resident substeps (fh_sph_fused_steps: the state stays in sorted order on the device
     between substeps, sorted by the previous substep's slots) against the oracle, particle by
     particle.  A call of k substeps repeats the first k - 1 substeps of the call of k - 1
@@ -485,18 +504,22 @@ def test_resident_substeps_match_oracle(fh, gpu_ctx, oracle, case):
     first runs resident.  c3: the full 1,048,576-particle dam break, whose second substep
     (resident) already moves most particles to other cells.  _k0 cases: gas_constant = 0 (the viscosity term alone, non-chaotic
     motion), where the K-substep result is also compared with K chained oracle steps from the
-    initial fields, within K times the one-step bound."""
+    initial fields, within K times the one-step bound.  mode: the work split (set_mode); the
+    sub-cell modes carry the sub-cell order from substep to substep in the resident keys."""
     cfg, vel, K = resident_case(case)
-    print(f"resident substeps vs oracle: {case} n={cfg.n} K={K}", flush=True)
+    print(f"resident substeps vs oracle: {case} ({mode}) n={cfg.n} K={K}", flush=True)
     states = [({"pos_x": cfg.x, "pos_y": cfg.y, "pos_z": cfg.z}, vel)]
     for k in range(1, K + 1):
         acc = torch.zeros((3, cfg.n), dtype=torch.float32, device="cuda")
         f = fields_from(fh, cfg, vel)
         p = sph_pipeline(fh, cfg, accel=acc)
         p.resident = True
-        set_mode(fh, f, cfg, "fast")
+        set_mode(fh, f, cfg, mode)
         torch.cuda.synchronize()
-        p.run(f, cfg.dt, k)
+        try:
+            p.run(f, cfg.dt, k)
+        finally:
+            set_mode(fh, f, cfg, "fast")
         got = {nm: t.cpu().numpy() for nm, t in f.f32_fields.items()}
         prev, pvel = states[-1]
         fr = assert_oracle_step(oracle, cfg, (prev["pos_x"], prev["pos_y"], prev["pos_z"]),
@@ -569,6 +592,16 @@ def test_heavy_parts_option(fh, gpu_ctx):
         with pytest.raises(fh.ForgeError):
             gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, bad)
     gpu_ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
+
+
+def test_subcell_option(fh, gpu_ctx):
+    """FH_OPT_SUBCELL takes 0 (default), 2, 4 or 8; other values are refused."""
+    for v in (0, 2, 4, 8):
+        gpu_ctx.set_option(fh.FH_OPT_SUBCELL, v)
+    for bad in (1, 3, 16, -1):
+        with pytest.raises(fh.ForgeError):
+            gpu_ctx.set_option(fh.FH_OPT_SUBCELL, bad)
+    gpu_ctx.set_option(fh.FH_OPT_SUBCELL, 0)
 
 
 def test_heavy_slots_option(fh, gpu_ctx):
