@@ -235,6 +235,96 @@ def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
+def outside_cfg():
+    """Particles the grid does not hold as they are: NaN / +inf / -inf coordinates, a clump of
+    50 at x ~ -0.2 (clamped into the cells of x = 0, within h of each other and of no particle
+    inside), one at x = -0.004 within h of an inside particle, and two beyond the far corner of
+    the grid (x, y, z ~ 1.4)."""
+    from forge_hip import workloads
+    cfg = workloads.small_sph(n=20_000, cols=24)
+    rng = np.random.default_rng(41)
+    cfg.x[0] = np.nan
+    cfg.y[1] = np.inf
+    cfg.z[2] = -np.inf
+    cfg.x[3:53] = (-0.2 + rng.uniform(-0.004, 0.004, 50)).astype(np.float32)
+    cfg.y[3:53] = (0.3 + rng.uniform(-0.004, 0.004, 50)).astype(np.float32)
+    cfg.z[3:53] = (0.2 + rng.uniform(-0.004, 0.004, 50)).astype(np.float32)
+    inside = int(np.argmin(cfg.x[60:])) + 60  # the particle nearest the x = 0 face
+    cfg.x[53] = np.float32(-0.004)
+    cfg.y[53] = cfg.y[inside]
+    cfg.z[53] = cfg.z[inside] + np.float32(0.003)
+    cfg.x[54:56] = np.float32(1.4)
+    cfg.y[54:56] = np.float32(1.41)
+    cfg.z[54:56] = np.array([1.4, 1.405], np.float32)
+    vel = [rng.uniform(-0.5, 0.5, cfg.n).astype(np.float32) for _ in range(3)]
+    return cfg, vel
+
+
+@pytest.mark.parametrize("mode", ["fast", "exact", "subcell", "subheavy", "heavy", "light",
+                                  "direct"])
+def test_nonfinite_and_outside_positions_match_oracle(fh, gpu_ctx, oracle, mode):
+    """One fused step over outside_cfg against the oracle: every output field has NaN and
+    +-inf in the same places as the oracle's; the three non-finite particles have no neighbour
+    (density 0, no force); the particles with finite inputs meet the one-step bar of
+    assert_oracle_step (densities rel 1e-4, accelerations against the fp64 sums, velocities and
+    positions except where the box's clamp decision is ill-conditioned); exact: every finite
+    output bit-identical."""
+    cfg, vel = outside_cfg()
+    print(f"non-finite and outside positions ({mode})", flush=True)
+    accel = torch.zeros((3, cfg.n), dtype=torch.float32, device="cuda")
+    f = fields_from(fh, cfg, vel)
+    set_mode(fh, f, cfg, mode)
+    p = sph_pipeline(fh, cfg, accel=accel)
+    torch.cuda.synchronize()
+    try:
+        p.step(f, cfg.dt)
+    finally:
+        set_mode(fh, f, cfg, "fast")
+    got = {k: f.f32_fields[k].cpu().numpy() for k in f.f32_fields}
+    gacc = accel.cpu().numpy()
+    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity)
+    out = oracle.sph_step(prm, 7, cfg.gravity, cfg.box_min, cfg.box_max, cfg.restitution,
+                          cfg.x, cfg.y, cfg.z, *vel, cfg.dt)
+    names = ("pos_x", "pos_y", "pos_z", "vel_x", "vel_y", "vel_z", "density")
+    ref = dict(zip(names, out[:7]))
+    for k in names:
+        assert np.array_equal(np.isnan(got[k]), np.isnan(ref[k])), k
+        assert np.array_equal(np.isinf(got[k]), np.isinf(ref[k])), k
+    assert np.array_equal(np.isnan(gacc), np.isnan(out[7]))
+    fin = np.isfinite(cfg.x) & np.isfinite(cfg.y) & np.isfinite(cfg.z)
+    assert (~fin).sum() == 3
+    # the non-finite particles: no neighbours, so density 0 and no force, as in the oracle
+    assert np.all(got["density"][~fin] == 0.0) and np.all(ref["density"][~fin] == 0.0)
+    assert np.all(gacc[:, ~fin] == 0.0)
+    assert rel_err(got["density"][fin], ref["density"][fin]).max() <= REL
+    ocs, osi, _ = oracle.hashgrid_build(cfg.x, cfg.y, cfg.z, cfg.cell_size, (0, 0, 0), cfg.dims)
+    a64, s64, e64 = oracle.sph_force_f64(prm, cfg.x, cfg.y, cfg.z, *vel, ref["density"], ocs, osi)
+    atol = REL * s64 + e64 + 1e-30
+    ga = gacc.astype(np.float64)
+    assert np.all((np.abs(ga - a64) <= atol)[:, fin])
+    # the outside clump and the particle beside the x = 0 face do have neighbours
+    assert np.all(got["density"][3:54] > 0.0)
+    pre = oracle.sph_step(prm, 3, cfg.gravity, cfg.box_min, cfg.box_max, cfg.restitution,
+                          cfg.x, cfg.y, cfg.z, *vel, cfg.dt)  # the same step without the box
+    ok = fin.copy()
+    for a, o in enumerate(pre[:3]):
+        ptol = REL * np.abs(o) + cfg.dt * cfg.dt * atol[a]
+        ok &= ~((np.abs(o - cfg.box_min[a]) <= ptol) | (np.abs(o - cfg.box_max[a]) <= ptol))
+    for a, k in enumerate(("pos_x", "pos_y", "pos_z")):
+        tol = REL * np.abs(ref[k]) + cfg.dt * cfg.dt * atol[a]
+        assert np.all((np.abs(got[k] - ref[k]) <= tol)[ok]), k
+    for a, k in enumerate(("vel_x", "vel_y", "vel_z")):
+        tol = REL * np.abs(ref[k]) + cfg.dt * atol[a]
+        assert np.all((np.abs(got[k] - ref[k]) <= tol)[ok]), k
+    print(f"finite particles checked {int(ok.sum())} of {int(fin.sum())} (ambiguous clamps "
+          f"{int((fin & ~ok).sum())})", flush=True)
+    if mode == "exact":
+        for k in names:
+            assert np.array_equal(got[k][fin], ref[k][fin]), k
+        assert np.array_equal(gacc[:, fin], out[7][:, fin])
+
+
 def interior_groups_cfg(seed=36):
     """Co-located groups inside the lattice block (x, y in [0, 0.3), z in [0, 0.87)): every
     group's 27 cells hold lattice particles, the z +-1 slabs included, and every member has a
