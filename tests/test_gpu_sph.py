@@ -49,18 +49,20 @@ def set_mode(fh, f, cfg, mode):
     item is walked by the spill kernels; subcell, subcell2, subcell8: as fast with the cells
     ordered by 4, 2 or 8 sub-cells per axis (FH_OPT_SUBCELL), so that heavy items skip far
     candidate chunks and compact the others to their near candidates;
-    subheavy: every item heavy, with 4 sub-cells per axis; direct: every item walked lane by
+    subheavy: every item heavy, with 4 sub-cells per axis; subspill: as subheavy with 5
+    partial-sum slots (the spill kernels with chunk culling); direct: every item walked lane by
     lane; exact: the bit-exact passes."""
     ctx = f.context(cfg.num_cells)
-    heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1, "subheavy": 1}
+    heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1, "subheavy": 1, "subspill": 1}
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, heavy.get(mode, 1 << 30 if mode == "light" else 0))
     ctx.set_option(fh.FH_OPT_DIRECT_ITEMS,
                    0 if mode in heavy or mode == "light" else 2 if mode == "direct" else 1)
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode in ("heavy8", "spill8") else 0)
-    ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 5 if mode in ("spill", "spill8") else 0)
+    ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 5 if mode in ("spill", "spill8", "subspill") else 0)
     ctx.set_option(fh.FH_OPT_SUBCELL,
-                   {"subcell": 4, "subcell2": 2, "subcell8": 8, "subheavy": 4}.get(mode, 0))
+                   {"subcell": 4, "subcell2": 2, "subcell8": 8, "subheavy": 4,
+                    "subspill": 4}.get(mode, 0))
 
 
 def check_step(fh, oracle, cfg, vel=None, fuse=True, mode="fast", visible=None):
@@ -166,7 +168,8 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
 
 
 @pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "subcell",
-                                  "subcell2", "subcell8", "subheavy", "light", "direct"])
+                                  "subcell2", "subcell8", "subheavy", "subspill", "light",
+                                  "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
@@ -227,7 +230,7 @@ def colocated_cfg(n=40_000, seed=33):
 
 
 @pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "subcell",
-                                  "subcell8", "subheavy", "light", "direct"])
+                                  "subcell8", "subheavy", "subspill", "light", "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
@@ -713,8 +716,9 @@ def test_heavy_slots_option(fh, gpu_ctx):
 def test_heavy_slot_cap_is_bit_identical(fh, gpu_ctx, case):
     """With a few partial-sum slots (FH_OPT_HEAVY_SLOTS) most heavy items are walked part after
     part by the spill kernels, whose parts are added in the order the slotted items' are: three
-    substeps equal the uncapped ones bit for bit, for the default split and for every item
-    heavy with 4 and 8 parts.  A graph captured with a cap replays to the eager fields, and a
+    substeps equal the uncapped ones bit for bit, for the default split, for every item heavy
+    with 4 and 8 parts, and for every item heavy with 4 sub-cells per axis (the culling
+    instantiations of both kernels).  A graph captured with a cap replays to the eager fields, and a
     later change of the cap drops the context's graph: the replay is refused rather than run on
     the freed buffer.  c3: the 1M-particle dam break (co-located corner groups, transposed
     items)."""
@@ -723,7 +727,7 @@ def test_heavy_slot_cap_is_bit_identical(fh, gpu_ctx, case):
         cfg, vel = workloads.config3(), None
     else:
         cfg, vel = colocated_cfg()
-    for mode, cap in (("fast", 3), ("heavy", 1), ("heavy8", 17)):
+    for mode, cap in (("fast", 3), ("heavy", 1), ("heavy8", 17), ("subheavy", 2)):
         print(f"heavy slot cap {case} {mode} cap={cap}", flush=True)
         outs = []
         for slots in (0, cap):
