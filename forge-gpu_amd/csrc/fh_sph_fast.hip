@@ -141,6 +141,8 @@ constexpr uint32_t kTransLightRatio = FH_TRANS_LIGHT_RATIO, kTransLightOffset = 
 #define FH_HGRID 4096
 #endif
 constexpr uint32_t kHeavyGrid = FH_HGRID;  // heavy workgroups (grid-stride over the list)
+// candidates per step of the heavy force walk with chunk culling (twice as many without it,
+// where the registers allow: the culling instantiation would spill)
 #ifndef FH_HU
 #define FH_HU 2
 #endif
@@ -1383,7 +1385,7 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
             window_rows(L, w0, jb, je);
 #pragma unroll
             for (int r = 0; r < 3; r++)
-                if (jb[r] < je[r]) force_run<2>(bp, bv, w0, jb[r], je[r], pi, p_i, K, ax, ay, az, wv);
+                if (jb[r] < je[r]) force_run<4>(bp, bv, w0, jb[r], je[r], pi, p_i, K, ax, ay, az, wv);
         }
     }
     if (in) {
@@ -1479,8 +1481,9 @@ __device__ __forceinline__ bool force_heavy_wave(
                 bv[lane] = w;
                 __builtin_amdgcn_wave_barrier();
                 if (mine)
-                    force_run<FH_HU>(bp, bv, c0, max(pick3(b, r), c0), min(pick3(e, r), c0 + m),
-                                     pi, p_i, K, ax, ay, az, wv);
+                    force_run<CULL ? FH_HU : 2 * FH_HU>(bp, bv, c0, max(pick3(b, r), c0),
+                                                        min(pick3(e, r), c0 + m), pi, p_i, K, ax,
+                                                        ay, az, wv);
             }
             t += (uint32_t)hw;
             r = nr;
@@ -1501,10 +1504,11 @@ __device__ __forceinline__ bool force_heavy_wave(
 }
 
 // Force pass, one launch: heavy parts first, then one light item per wave (as k_density_pass).
-// With the chunk tests (CULL) at least 6 waves per SIMD (80 registers): held to 7 it spills 2
-// registers to scratch, which was 3 % slower on configs[4].
+// Held to 6 waves per SIMD (80 registers): the light rows take 4 candidates per step (4 loads in
+// flight; 2 per step at 7 waves: c3's fixed state 167.9 instead of 163.6 us), and the chunk tests
+// (CULL) fit without spilling (at 7 waves they spill 2 registers: 3 % slower on configs[4]).
 template <uint32_t HW, bool CULL>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(CULL ? 6 : 1, 8))) void k_force_pass(
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_force_pass(
     const float4* __restrict__ spos, const float4* __restrict__ svel,
     const float* __restrict__ srho, const float4* __restrict__ rec,
     const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
