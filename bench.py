@@ -116,6 +116,10 @@ def read_traffic(kernel_pass: str):
 
 
 VALU_PEAK_INSTS = 256 * 2.4e9  # MI355X: one non-packed VALU wave instruction per cycle per CU
+# The highest VALU wave-instruction rate measured on this GPU (SQ_INSTS_VALU over the kernel
+# trace's duration): the configs[4] force pass, profiles/sph_c4_kernel_stats.md.  It is above
+# VALU_PEAK_INSTS, so that figure is not the counter's ceiling.
+VALU_MEASURED_INSTS = 7.63e11
 
 
 def read_valu(kernel_pass: str):
@@ -557,7 +561,10 @@ def valu_block(insts, us):
         return None
     return {"insts_per_launch": insts, "peak_insts_per_s": VALU_PEAK_INSTS,
             "achieved_insts_per_s": insts / (us * 1e-6),
-            "frac": insts / (us * 1e-6) / VALU_PEAK_INSTS, "source": "profiles/valu_c3.txt"}
+            "frac": insts / (us * 1e-6) / VALU_PEAK_INSTS,
+            "measured_ceiling_insts_per_s": VALU_MEASURED_INSTS,
+            "frac_of_measured_ceiling": insts / (us * 1e-6) / VALU_MEASURED_INSTS,
+            "source": "profiles/valu_c3.txt"}
 
 
 # Survey bytes per particle of each neighbour pass: density reads the
