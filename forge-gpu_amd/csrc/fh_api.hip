@@ -231,11 +231,12 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     // partial sums of the heavy parts: a slot for every item by default (FH_OPT_HEAVY_SLOTS
     // caps it), kHeavyWaves parts x kHeavyComps x 64 lanes each (room for kHeavyWavesMax parts
-    // is made when FH_OPT_HEAVY_PARTS asks for it)
-    c->hpart_parts = kHeavyWaves;
+    // is made when FH_OPT_HEAVY_PARTS asks for it, and from the start for small contexts, whose
+    // default is kHeavyWavesMax parts)
+    c->hpart_parts = max_n < kSmallSystemN ? (uint32_t)kHeavyWavesMax : (uint32_t)kHeavyWaves;
     c->hslot_cap = kHeavyLists * c->heavy_cap;
     if (e == hipSuccess)
-        e = alloc(&c->hpart, (size_t)c->hslot_cap * kHeavyWaves * kHeavyComps * 64u, &tot);
+        e = alloc(&c->hpart, (size_t)c->hslot_cap * c->hpart_parts * kHeavyComps * 64u, &tot);
     if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
     if (e == hipSuccess)
         e = alloc(&c->lstream, 3 * (size_t)ceil_div(max_n, 64u) * kLightCacheWords, &tot);

@@ -70,9 +70,13 @@ constexpr int kHeavyLists = 8;
 #ifndef FH_HW
 #define FH_HW 4
 #endif
-// single-wave parts of a heavy SPH item: kHeavyWaves by default, up to kHeavyWavesMax (the
-// partial-sum slots are sized for the maximum) with FH_OPT_HEAVY_PARTS
+// single-wave parts of a heavy SPH item: kHeavyWaves by default, kHeavyWavesMax with
+// FH_OPT_HEAVY_PARTS or for small systems (the partial-sum slots then have room for it)
 constexpr int kHeavyWaves = FH_HW, kHeavyWavesMax = 8;
+// Systems of fewer particles have too few (sub-tile, slab) items to fill the GPU (configs[0]'s
+// 50,000: 2,346 items for 1,024 SIMDs): by default the fast passes split more of their items,
+// into kHeavyWavesMax parts (contexts of smaller max_n make room for them at creation).
+constexpr uint32_t kSmallSystemN = 1u << 18;
 constexpr int kHeavyComps = 4;      // partial sums per lane and part: a_x, a_y, a_z, w (density: 1)
 // A light item's candidate stream as the density pass leaves it for the force pass: per lane
 // and row, (stream start << 16 | count), then the sorted indices of the first two windows'

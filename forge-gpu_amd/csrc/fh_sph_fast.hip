@@ -104,6 +104,7 @@ __device__ __forceinline__ void slab_ranges(const CellXYZ& c, bool live, const G
 // items.  The plan is made once per substep and serves both passes.
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
 constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
+constexpr uint32_t kSmallHeavyWork = 32;  // the default below kSmallSystemN particles
 constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
 constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transposed
 constexpr uint32_t kEntryFlags = kCutFlag | kTransFlag;
@@ -1074,9 +1075,37 @@ __device__ __forceinline__ uint32_t heavy_entry_slot(const uint32_t* __restrict_
 // kHeavyGrid) follows the item count, so that a small system does not dispatch thousands of
 // idle parts (c0's 50,000 particles: 2,346 items).
 static_assert(kHeavyGrid % 8 == 0, "heavy part numbering");
-// The pass kernels are compiled for the default part count and for 8.
-static uint32_t heavy_parts(const fh_ctx* c) {
-    return c->heavy_parts == 8u ? 8u : (uint32_t)kHeavyWaves;
+// Partial-sum slots of hw parts each in the context's buffer (sized for hslot_cap slots of
+// hpart_parts parts): more slots when fewer parts are in use, fewer when more.
+static uint32_t slot_cap(const fh_ctx* c, uint32_t hw) {
+    const uint64_t room = (uint64_t)c->hslot_cap * c->hpart_parts / hw;
+    const uint32_t all = kHeavyLists * c->heavy_cap;
+    return room < all ? (uint32_t)room : all;
+}
+// The largest slot a call of n particles can number (list k, position i: 8i + k), plus one:
+// plan workgroup b (kPlanThreads particles, 3 items per 64) appends to list b % kHeavyLists.
+static uint32_t slots_needed(uint32_t n) {
+    const uint32_t per_list = 3u * (kPlanThreads / 64u) *
+                              ceil_div(ceil_div(n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
+    return per_list * kHeavyLists;
+}
+// The pass kernels are compiled for the default part count and for 8.  Unless
+// FH_OPT_HEAVY_PARTS fixes it, a call of fewer than kSmallSystemN particles takes 8 when the
+// context's uncapped buffer would hold 8 parts for every slot the call can number (its few
+// items then make 8 times as many waves): always in a context made for small systems, and in a
+// large one, whose buffer for 4 parts of all its items holds 8 parts of a small call's.  The
+// choice does not depend on FH_OPT_HEAVY_SLOTS (a cap only moves items to the spill kernels),
+// so capped and uncapped runs split the same way.
+static uint32_t heavy_parts(const fh_ctx* c, uint32_t n) {
+    if (c->heavy_parts) return c->heavy_parts == 8u ? 8u : (uint32_t)kHeavyWaves;
+    const uint64_t room = (uint64_t)kHeavyLists * c->heavy_cap * c->hpart_parts;
+    return n < kSmallSystemN && room >= 8ull * slots_needed(n) ? 8u : (uint32_t)kHeavyWaves;
+}
+// Candidates per particle and slab above which an item is split: FH_OPT_HEAVY_WORK, else 32 for
+// small systems (configs[0]: 120 -> 90 us per substep with 8 parts; 24, 28, 36, 40 gave 102, 96,
+// 92 and 100 us, every item split 195 us) and 384 otherwise.
+static uint32_t heavy_work(const fh_ctx* c, uint32_t n) {
+    return c->heavy_work ? c->heavy_work : n < kSmallSystemN ? kSmallHeavyWork : kHeavyWork;
 }
 static uint32_t heavy_grid(uint32_t items) {
     const uint32_t g = (items / 8u + 7u) / 8u * 8u;
@@ -1797,8 +1826,9 @@ hipError_t launch_group_plan(fh_ctx* c, const SphArgs& a, bool with_vel) {
                                 c->spos, with_vel ? c->svel : nullptr, c->sidx, c->rank, c->ka,
                                 c->cell_grp, c->vrep, c->skip_tag, a.g, c->run_tag,
                                 c->heavy_flag, c->heavy, c->heavy_cap,
-                                c->heavy_work ? c->heavy_work : kHeavyWork, c->direct_mode,
-                                c->ctl, c->lstream, c->lstream_t, c->hslot, c->hslot_cap);
+                                heavy_work(c, a.n), c->direct_mode,
+                                c->ctl, c->lstream, c->lstream_t, c->hslot,
+                                slot_cap(c, heavy_parts(c, a.n)));
     tend(c, KID_PLAN);
     return hipGetLastError();
 }
@@ -1809,7 +1839,7 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_DENSITY);
     const uint32_t hgrid = heavy_grid(items);
-    const uint32_t hw = heavy_parts(c);
+    const uint32_t hw = heavy_parts(c, a.n);
     // the heavy walks skip far chunks only where the cells are ordered by sub-cell (g.sb > 0)
     const bool cull = a.g.sb != 0u;
     const auto kernel = hw == 8u ? (cull ? k_density_pass<8, true> : k_density_pass<8, false>)
@@ -1818,15 +1848,15 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
     kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
         items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
-        c->heavy_cap, c->hpart, hgrid, c->hslot_cap);
+        c->heavy_cap, c->hpart, hgrid, slot_cap(c, hw));
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && c->hslot_cap < kHeavyLists * c->heavy_cap) {  // items may lack slots
+    if (e == hipSuccess && slot_cap(c, hw) < slots_needed(a.n)) {  // items may lack slots
         const auto spill = hw == 8u ? (cull ? k_density_spill<8, true> : k_density_spill<8, false>)
                                     : (cull ? k_density_spill<kHeavyWaves, true>
                                             : k_density_spill<kHeavyWaves, false>);
         spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
             c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
-            c->skip_tag, c->ctl, c->heavy, c->heavy_cap, c->hslot_cap);
+            c->skip_tag, c->ctl, c->heavy, c->heavy_cap, slot_cap(c, hw));
         e = hipGetLastError();
     }
     tend(c, KID_DENSITY);
@@ -1854,7 +1884,7 @@ hipError_t launch_prep(fh_ctx* c, const SphArgs& a) {
     if (a.n == 0) return hipSuccess;
     const FastForce K = fast_force(a);
     tbeg(c, KID_PREP);
-    const auto kernel = heavy_parts(c) == 8u ? k_prep<8> : k_prep<kHeavyWaves>;
+    const auto kernel = heavy_parts(c, a.n) == 8u ? k_prep<8> : k_prep<kHeavyWaves>;
     kernel<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->vrep, c->dpart, a.n,
                                                        c->max_n, K.mc, a.k, a.rho0, K.fp, K.fv,
                                                        c->srho, c->sout, c->hslot, c->hpart);
@@ -1869,7 +1899,7 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     const uint32_t grid = wave_grid(a.n, &items);
     tbeg(c, KID_FORCE);
     const uint32_t hgrid = heavy_grid(items);
-    const uint32_t hw = heavy_parts(c);
+    const uint32_t hw = heavy_parts(c, a.n);
     const bool cull = a.g.sb != 0u;  // as in launch_density_fast
     const auto kernel = hw == 8u ? (cull ? k_force_pass<8, true> : k_force_pass<8, false>)
                                  : (cull ? k_force_pass<kHeavyWaves, true>
@@ -1877,16 +1907,16 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
     kernel<<<hgrid * hw + grid, kWave, 0, c->stream>>>(
         c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
         c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
-        c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid, c->hslot_cap);
+        c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid, slot_cap(c, hw));
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && c->hslot_cap < kHeavyLists * c->heavy_cap) {  // items may lack slots
+    if (e == hipSuccess && slot_cap(c, hw) < slots_needed(a.n)) {  // items may lack slots
         const auto spill = hw == 8u ? (cull ? k_force_spill<8, true> : k_force_spill<8, false>)
                                     : (cull ? k_force_spill<kHeavyWaves, true>
                                             : k_force_spill<kHeavyWaves, false>);
         spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
             c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
             c->fpart, c->wpart, c->max_n, c->skip_tag, c->ctl, c->heavy, c->heavy_cap,
-            c->hslot_cap);
+            slot_cap(c, hw));
         e = hipGetLastError();
     }
     tend(c, KID_FORCE);
@@ -1921,7 +1951,7 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     }
     F.e = epi ? epi->restitution : 0.0f;
     tbeg(c, KID_FINAL);
-    const auto fin = heavy_parts(c) == 8u ? k_finalize<8> : k_finalize<kHeavyWaves>;
+    const auto fin = heavy_parts(c, a.n) == 8u ? k_finalize<8> : k_finalize<kHeavyWaves>;
     fin<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
                                                            c->wpart, a.n, c->max_n, F,
                                                            accel != nullptr, c->sout, a.g,

@@ -269,9 +269,9 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
 #define FH_OPT_SPH_EXACT 1
 /* FH_OPT_HEAVY_WORK = 2: work split of the fast passes.  A (64-particle, z-slab) item whose
  * particles face more than `value` candidates (a co-located group counting as one) is processed
- * by 4 wavefronts that split its candidates instead of one wavefront; value 0 restores the
- * default (384).
- * Results differ only by rounding. */
+ * by 4 (or 8: FH_OPT_HEAVY_PARTS) wavefronts that split its candidates instead of one
+ * wavefront; value 0 restores the default: 384, or 32 for calls of fewer than 2^18 particles,
+ * whose few items would not fill the GPU otherwise.  Results differ only by rounding. */
 #define FH_OPT_HEAVY_WORK 2
 /* FH_OPT_DIRECT_ITEMS = 3: items whose particles' candidate ranges barely overlap (sparse
  * particles along a row, or beside a dense one) are walked transposed: one particle at a time,
@@ -280,12 +280,14 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * lengths (default), 2: every item.  Results differ only by rounding. */
 #define FH_OPT_DIRECT_ITEMS 3
 /* FH_OPT_HEAVY_PARTS = 4: wavefronts (4 or 8) that split each heavy item of the fast passes; 0
- * restores the default (4).  More parts shorten the longest items (dense clumps: c4 is ~8 %
- * faster with 8), fewer cost less per item (c3 is ~2 % faster with 4).  Results differ only by
- * rounding.  The context holds the parts' partial sums for 4 parts; the first time 8 are set
- * it makes room for 8 (one allocation, twice the FH_OPT_HEAVY_SLOTS buffer below, so set it
- * outside capture; fh_scratch_bytes counts it; the context's captured graph is dropped and any
- * graph captured on its stream before must be captured again). */
+ * restores the default: 4, or 8 for calls of fewer than 2^18 particles where the context has
+ * room for them.  More parts shorten the longest items (dense clumps: c4 is ~8 % faster with
+ * 8) and give small systems more waves; fewer cost less per item (c3 is ~2 % faster with 4).
+ * Results differ only by rounding.  A context of max_n >= 2^18 holds the parts' partial sums
+ * for 4 parts; the first time 8 are set it makes room for 8 (one allocation, twice the
+ * FH_OPT_HEAVY_SLOTS buffer below, so set it outside capture; fh_scratch_bytes counts it; the
+ * context's captured graph is dropped and any graph captured on its stream before must be
+ * captured again).  A smaller context has room for 8 from its creation. */
 #define FH_OPT_HEAVY_PARTS 4
 /* FH_OPT_EPOCH_PERIOD = 5: the work tags of the SPH rebuilds (co-located groups, skipped
  * sub-tiles, candidate group cells) compare a 30-bit epoch that every sort / rebuild start

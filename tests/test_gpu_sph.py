@@ -42,7 +42,9 @@ def rel_err(a, b):
 
 
 def set_mode(fh, f, cfg, mode):
-    """fast: default work split; heavy: every (sub-tile, slab) item split into single-wave parts
+    """fast: default work split (below 2^18 particles: items of more than 32 candidates per
+    particle split into 8 parts); fast384: the default split of larger systems (384 candidates,
+    4 parts) at any size; heavy: every (sub-tile, slab) item split into 4 single-wave parts
     whose partials are added afterwards; light: none of them (one wavefront per item, shared
     stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; spill,
     spill8: as heavy and heavy8 with 5 partial-sum slots (FH_OPT_HEAVY_SLOTS), so nearly every
@@ -55,10 +57,12 @@ def set_mode(fh, f, cfg, mode):
     ctx = f.context(cfg.num_cells)
     heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1, "subheavy": 1, "subspill": 1}
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
-    ctx.set_option(fh.FH_OPT_HEAVY_WORK, heavy.get(mode, 1 << 30 if mode == "light" else 0))
+    ctx.set_option(fh.FH_OPT_HEAVY_WORK, heavy.get(mode, 1 << 30 if mode == "light" else
+                                                   384 if mode == "fast384" else 0))
     ctx.set_option(fh.FH_OPT_DIRECT_ITEMS,
                    0 if mode in heavy or mode == "light" else 2 if mode == "direct" else 1)
-    ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode in ("heavy8", "spill8") else 0)
+    ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode in ("heavy8", "spill8") else
+                   4 if mode in heavy or mode == "fast384" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 5 if mode in ("spill", "spill8", "subspill") else 0)
     ctx.set_option(fh.FH_OPT_SUBCELL,
                    {"subcell": 4, "subcell2": 2, "subcell8": 8, "subheavy": 4,
@@ -146,8 +150,8 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "spill", "subcell",
-                                  "subheavy", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "fast384", "exact", "heavy", "heavy8", "spill",
+                                  "subcell", "subheavy", "light", "direct"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
     from forge_hip import workloads
@@ -167,9 +171,9 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "subcell",
-                                  "subcell2", "subcell8", "subheavy", "subspill", "light",
-                                  "direct"])
+@pytest.mark.parametrize("mode", ["fast", "fast384", "heavy", "heavy8", "spill", "spill8",
+                                  "subcell", "subcell2", "subcell8", "subheavy", "subspill",
+                                  "light", "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
     """Hundreds of particles per cell and particles pinned to the walls (the state c3 reaches
     after a few substeps): many staging chunks per row and empty / skipped rows."""
@@ -229,8 +233,9 @@ def colocated_cfg(n=40_000, seed=33):
     return cfg, vel
 
 
-@pytest.mark.parametrize("mode", ["fast", "heavy", "heavy8", "spill", "spill8", "subcell",
-                                  "subcell8", "subheavy", "subspill", "light", "direct"])
+@pytest.mark.parametrize("mode", ["fast", "fast384", "heavy", "heavy8", "spill", "spill8",
+                                  "subcell", "subcell8", "subheavy", "subspill", "light",
+                                  "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
     cfg, vel = colocated_cfg()
     print(f"co-located cells ({mode})", flush=True)
@@ -370,8 +375,8 @@ def viscosity_cfg(case):
 
 
 @pytest.mark.parametrize("case", ["lattice", "groups", "colocated"])
-@pytest.mark.parametrize("mode", ["fast", "exact", "heavy", "heavy8", "subheavy", "light",
-                                  "direct"])
+@pytest.mark.parametrize("mode", ["fast", "fast384", "exact", "heavy", "heavy8", "subheavy",
+                                  "light", "direct"])
 def test_viscosity_without_pressure_matches_oracle(fh, gpu_ctx, oracle, case, mode):
     """The fused force's viscosity half (sph_fused.rs:617-623) on its own, in every work split:
     plain lattice particles, and members of co-located groups, which are finished from their
