@@ -19,7 +19,7 @@
 // pass.  Light workgroups are renumbered so that runs of kXcdChunk consecutive items share one
 // XCD's L2 (neighbouring sub-tiles read mostly the same cells).
 //
-// Heavy items.  An item whose particles face more than kHeavyWork (384) candidates in the slab,
+// Heavy items.  An item whose particles face more than kHeavyWork (192) candidates in the slab,
 // or that touches a co-located group, is listed by the plan (k_group_plan) and split into
 // kHeavyWaves (4) parts: single-wave workgroups that hold the same 64 particles and take the
 // 64-candidate chunks of each segment row round-robin (part p: chunks p, p + 4, ...).  Each part
@@ -103,7 +103,7 @@ __device__ __forceinline__ void slab_ranges(const CellXYZ& c, bool live, const G
 // same 64 particles; their partial sums are added in part order.  The light items skip those
 // items.  The plan is made once per substep and serves both passes.
 constexpr int kSub = 64;                // particles per sub-tile (one wavefront)
-constexpr uint32_t kHeavyWork = 384;   // default: candidates per particle and slab
+constexpr uint32_t kHeavyWork = 192;   // default: candidates per particle and slab
 constexpr uint32_t kSmallHeavyWork = 32;  // the default below kSmallSystemN particles
 constexpr uint32_t kCutFlag = 1u << 31;  // heavy list entry: the item touches a co-located group
 constexpr uint32_t kTransFlag = 1u << 30;  // heavy list entry: walked transposed
@@ -1103,7 +1103,10 @@ static uint32_t heavy_parts(const fh_ctx* c, uint32_t n) {
 }
 // Candidates per particle and slab above which an item is split: FH_OPT_HEAVY_WORK, else 32 for
 // small systems (configs[0]: 120 -> 90 us per substep with 8 parts; 24, 28, 36, 40 gave 102, 96,
-// 92 and 100 us, every item split 195 us) and 384 otherwise.
+// 92 and 100 us, every item split 195 us) and 192 otherwise (configs[3]'s trajectory: 412.9 ->
+// 406.1 us per substep against 384; 160: 407.8; its fixed state with 96, 128, 224, 256: 418.7,
+// 423.5, 410.0, 411.9 us; above 384 a light item's stream no longer fits the two windows kept
+// for the force pass: 512 took 729 us).
 static uint32_t heavy_work(const fh_ctx* c, uint32_t n) {
     return c->heavy_work ? c->heavy_work : n < kSmallSystemN ? kSmallHeavyWork : kHeavyWork;
 }

@@ -270,7 +270,7 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
 /* FH_OPT_HEAVY_WORK = 2: work split of the fast passes.  A (64-particle, z-slab) item whose
  * particles face more than `value` candidates (a co-located group counting as one) is processed
  * by 4 (or 8: FH_OPT_HEAVY_PARTS) wavefronts that split its candidates instead of one
- * wavefront; value 0 restores the default: 384, or 32 for calls of fewer than 2^18 particles,
+ * wavefront; value 0 restores the default: 192, or 32 for calls of fewer than 2^18 particles,
  * whose few items would not fill the GPU otherwise.  Results differ only by rounding. */
 #define FH_OPT_HEAVY_WORK 2
 /* FH_OPT_DIRECT_ITEMS = 3: items whose particles' candidate ranges barely overlap (sparse

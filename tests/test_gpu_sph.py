@@ -43,9 +43,9 @@ def rel_err(a, b):
 
 def set_mode(fh, f, cfg, mode):
     """fast: default work split (below 2^18 particles: items of more than 32 candidates per
-    particle split into 8 parts); fast384: the default split of larger systems (384 candidates,
-    4 parts) at any size; heavy: every (sub-tile, slab) item split into 4 single-wave parts
-    whose partials are added afterwards; light: none of them (one wavefront per item, shared
+    particle split into 8 parts); fastlarge: the default split of larger systems (192
+    candidates, 4 parts) at any size; heavy: every (sub-tile, slab) item split into 4
+    single-wave parts whose partials are added afterwards; light: none of them (one wavefront per item, shared
     stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; spill,
     spill8: as heavy and heavy8 with 5 partial-sum slots (FH_OPT_HEAVY_SLOTS), so nearly every
     item is walked by the spill kernels; subcell, subcell2, subcell8: as fast with the cells
@@ -58,11 +58,11 @@ def set_mode(fh, f, cfg, mode):
     heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1, "subheavy": 1, "subspill": 1}
     ctx.set_option(fh.FH_OPT_SPH_EXACT, 1 if mode == "exact" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, heavy.get(mode, 1 << 30 if mode == "light" else
-                                                   384 if mode == "fast384" else 0))
+                                                   192 if mode == "fastlarge" else 0))
     ctx.set_option(fh.FH_OPT_DIRECT_ITEMS,
                    0 if mode in heavy or mode == "light" else 2 if mode == "direct" else 1)
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8 if mode in ("heavy8", "spill8") else
-                   4 if mode in heavy or mode == "fast384" else 0)
+                   4 if mode in heavy or mode == "fastlarge" else 0)
     ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 5 if mode in ("spill", "spill8", "subspill") else 0)
     ctx.set_option(fh.FH_OPT_SUBCELL,
                    {"subcell": 4, "subcell2": 2, "subcell8": 8, "subheavy": 4,
@@ -150,7 +150,7 @@ def test_c0_step1_matches_oracle(fh, gpu_ctx, oracle, mode):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "fast384", "exact", "heavy", "heavy8", "spill",
+@pytest.mark.parametrize("mode", ["fast", "fastlarge", "exact", "heavy", "heavy8", "spill",
                                   "subcell", "subheavy", "light", "direct"])
 def test_step_with_velocities_matches_oracle(fh, gpu_ctx, oracle, mode):
     """v != 0 exercises the viscosity term (zero at c0's initial state)."""
@@ -171,7 +171,7 @@ def test_c3_step1_matches_oracle(fh, gpu_ctx, oracle):
     print("bit-exact fractions", exact)
 
 
-@pytest.mark.parametrize("mode", ["fast", "fast384", "heavy", "heavy8", "spill", "spill8",
+@pytest.mark.parametrize("mode", ["fast", "fastlarge", "heavy", "heavy8", "spill", "spill8",
                                   "subcell", "subcell2", "subcell8", "subheavy", "subspill",
                                   "light", "direct"])
 def test_dense_clumps_match_oracle(fh, gpu_ctx, oracle, mode):
@@ -233,7 +233,7 @@ def colocated_cfg(n=40_000, seed=33):
     return cfg, vel
 
 
-@pytest.mark.parametrize("mode", ["fast", "fast384", "heavy", "heavy8", "spill", "spill8",
+@pytest.mark.parametrize("mode", ["fast", "fastlarge", "heavy", "heavy8", "spill", "spill8",
                                   "subcell", "subcell8", "subheavy", "subspill", "light",
                                   "direct"])
 def test_colocated_cells_match_oracle(fh, gpu_ctx, oracle, mode):
@@ -375,7 +375,7 @@ def viscosity_cfg(case):
 
 
 @pytest.mark.parametrize("case", ["lattice", "groups", "colocated"])
-@pytest.mark.parametrize("mode", ["fast", "fast384", "exact", "heavy", "heavy8", "subheavy",
+@pytest.mark.parametrize("mode", ["fast", "fastlarge", "exact", "heavy", "heavy8", "subheavy",
                                   "light", "direct"])
 def test_viscosity_without_pressure_matches_oracle(fh, gpu_ctx, oracle, case, mode):
     """The fused force's viscosity half (sph_fused.rs:617-623) on its own, in every work split:
@@ -489,8 +489,8 @@ def test_standalone_modules_match_oracle(fh, gpu_ctx, oracle):
         assert np.array_equal(gpu, o), nm
 
 
-@pytest.mark.parametrize("parts,sub", [(4, 0), (8, 0), (8, 4), (8, 8)])
-def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, sub):
+@pytest.mark.parametrize("parts,sub,work", [(4, 0, 0), (8, 0, 0), (8, 4, 0), (8, 8, 384)])
+def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, sub, work):
     """configs[4] at full size (8,388,608 particles, 64 Gaussian clumps + 10 % uniform, cells of
     0 to ~27,000 particles): one HashGrid build (bit-exact), then one fused SPH pass.  The full
     CPU passes would take ~1.3e11 candidate tests each, so the oracle evaluates a sample: 4096
@@ -499,7 +499,8 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, su
     or_sph_force_f64_at evaluated on the GPU's densities (themselves checked on the sample),
     within 1e-4 * sum|pair terms|.  Random velocities make the viscosity term non-zero.
     parts: wavefronts per heavy item (FH_OPT_HEAVY_PARTS); sub: sub-cells per axis
-    (FH_OPT_SUBCELL); (8, 8) is the bench's setting."""
+    (FH_OPT_SUBCELL); work: candidates per particle above which an item is split
+    (FH_OPT_HEAVY_WORK, 0: the default); (8, 8, 384) is the bench's setting."""
     from forge_hip import workloads
     cfg = workloads.config4()
     n = cfg.n
@@ -522,16 +523,18 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, su
     m.accel = accel
     p.add(m)
     torch.cuda.synchronize()
-    print(f"c4 fused pass ({parts} parts, {sub} sub-cells): max occupancy {occ.max()}, "
-          f"p99 {np.percentile(occ, 99):.0f}", flush=True)
+    print(f"c4 fused pass ({parts} parts, {sub} sub-cells, work {work}): max occupancy "
+          f"{occ.max()}, p99 {np.percentile(occ, 99):.0f}", flush=True)
     ctx = f.context(cfg.num_cells)
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, parts)
     ctx.set_option(fh.FH_OPT_SUBCELL, sub)
+    ctx.set_option(fh.FH_OPT_HEAVY_WORK, work)
     try:
         p.step(f, cfg.dt)
     finally:
         ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
         ctx.set_option(fh.FH_OPT_SUBCELL, 0)
+        ctx.set_option(fh.FH_OPT_HEAVY_WORK, 0)
     rho = f.f32_fields["density"].cpu().numpy()
     acc = accel.cpu().numpy().astype(np.float64)
     dense = int(np.argmax(occ))
