@@ -179,9 +179,12 @@ __global__ __launch_bounds__(kWave) void k_nbr_stream(const float4* __restrict__
                 const uint32_t jb = max(L.S[r], w0);
                 const uint32_t je = min(L.S[r] + L.cnt[r], w0 + (uint32_t)kQueryWin);
                 // two candidates per step of the LDS address
+                // (the bounds are formed from the count, never before the buffer: an address
+                // below the LDS buffer's start would wrap around in 32-bit LDS addressing)
+                const uint32_t m = je > jb ? je - jb : 0u;
                 const float4* c = s_p + (jb - w0);
-                const float4* const ce = c + (je > jb ? je - jb : 0u);
-                const float4* const cu = ce - 1;
+                const float4* const ce = c + m;
+                const float4* const cu = c + (m > 1u ? m - 1u : 0u);
                 if (c < cu) {
                     do {
                         const float4 p0 = c[0], p1 = c[1];

@@ -156,10 +156,14 @@ __device__ __forceinline__ float density_run(const float4* __restrict__ sp, uint
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     // pointer-stepped: one address and one compare per four candidates.  Callers may pass an
     // empty range with je < jb (a lane whose range ends before the chunk): the count is clamped
-    // at 0, since je - c0 would wrap around.
+    // at 0, since je - c0 would wrap around.  The loop bounds are formed from the count, never
+    // before the buffer: an address below the LDS buffer's start (at address 0 in the pass
+    // kernels) would wrap around in 32-bit LDS addressing and the loop would run on for ~2^26
+    // steps.
+    const uint32_t m = je > jb ? je - jb : 0u;
     const float4* p = sp + (jb - c0);
-    const float4* const pe = p + (je > jb ? je - jb : 0u);
-    const float4* const pu = pe - 3;  // p < pu: four more candidates
+    const float4* const pe = p + m;
+    const float4* const pu = p + (m > 3u ? m - 3u : 0u);  // p < pu: four more candidates
     if (p < pu) {
         do {
             const float4 q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
@@ -384,9 +388,10 @@ __device__ __forceinline__ float density_run_w(const float4* __restrict__ sp, ui
                                                uint32_t jb, uint32_t je, float4 pi, float h2,
                                                float acc) {
     float a0 = 0.0f, a1 = 0.0f;
+    const uint32_t m = je > jb ? je - jb : 0u;  // empty when je <= jb
     const float4* p = sp + (jb - c0);
-    const float4* const pe = p + (je > jb ? je - jb : 0u);  // empty when je <= jb
-    const float4* const pu = pe - 1;  // p < pu: two more candidates
+    const float4* const pe = p + m;
+    const float4* const pu = p + (m > 1u ? m - 1u : 0u);  // p < pu: two more (as density_run)
     if (p < pu) {
         do {
             const float4 q0 = p[0], q1 = p[1];
@@ -1274,11 +1279,13 @@ __device__ __forceinline__ void force_run(const float4* __restrict__ sp,
                                           float& wv) {
     // pointer-stepped: the loop keeps one address and one compare per U candidates; empty when
     // je <= jb (je may lie before the chunk, where je - c0 would wrap around)
+    const uint32_t m = je > jb ? je - jb : 0u;
     const float4* p = sp + (jb - c0);
     const float4* v = sv + (jb - c0);
-    const float4* const pe = p + (je > jb ? je - jb : 0u);
+    const float4* const pe = p + m;
     if (U > 1) {
-        const float4* const pu = pe - (U - 1);  // p < pu: U more candidates
+        // p < pu: U more candidates (bounds from the count, as in density_run)
+        const float4* const pu = p + (m > (uint32_t)(U - 1) ? m - (uint32_t)(U - 1) : 0u);
         if (p < pu) {
             do {
                 float4 q[U], w[U];
