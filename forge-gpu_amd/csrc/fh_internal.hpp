@@ -80,9 +80,8 @@ constexpr uint32_t kSmallSystemN = 1u << 18;
 constexpr int kHeavyComps = 4;      // partial sums per lane and part: a_x, a_y, a_z, w (density: 1)
 // A light item's candidate stream as the density pass leaves it for the force pass: per lane
 // and row, (stream start << 16 | count), then the sorted indices of the first two windows'
-// staging slots (192 each).  Streams longer than two windows (~2 % of c3's light items) are
-// rebuilt by the force pass.
-constexpr uint32_t kLightCacheWords = 3 * 64 + 2 * 192;
+// staging slots (256 each).  Streams longer than two windows are rebuilt by the force pass.
+constexpr uint32_t kLightCacheWords = 3 * 64 + 2 * 256;
 #ifndef FH_PLAN_THREADS
 #define FH_PLAN_THREADS 512
 #endif

@@ -48,8 +48,11 @@ __device__ __forceinline__ uint32_t xcd_chunked(uint32_t b, uint32_t nb) {
 // contiguous interval [S[r], S[r] + cnt[r]) of the stream.  The stream is staged through the
 // wave's LDS slice kWin candidates at a time, and all lanes (of every segment at once) evaluate
 // their own intervals clipped to the window: segments no longer take turns.
+// 256 candidates per window (c3 trajectory 407.4 -> 402.4 us per substep against 192; 128:
+// slower, 320: slower on the fixed state; the kept streams then cost 132 instead of 108 bytes
+// per particle)
 #ifndef FH_WIN
-#define FH_WIN 192
+#define FH_WIN 256
 #endif
 constexpr int kWin = FH_WIN;  // candidates staged per window
 constexpr int kWinLoads = kWin / kWave;
