@@ -492,11 +492,13 @@ def bench_sph_c4(args, fh, torch, log):
                             cfg.rest_density, cfg.viscosity))
     ctx = f.context(cfg.num_cells)
     # c4's dense clumps make long heavy items: 8 wavefronts per heavy item instead of 4 (~9 %),
-    # cells ordered by 8 sub-cells per axis, so that heavy items skip far candidates (~36 %), and
-    # items split above 384 candidates per particle rather than the default 192 (~1.5 %)
+    # cells ordered by 8 sub-cells per axis, so that heavy items skip far candidates (~36 %),
+    # items split above 384 candidates per particle rather than the default 192 (~1.5 %), and a
+    # partial-sum slot for every item (most of c4's items are heavy; the default has one per 8)
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 8)
     ctx.set_option(fh.FH_OPT_SUBCELL, 8)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, 384)
+    ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 2**31 - 1)
     torch.cuda.synchronize()
     p.step(f, cfg.dt)  # warm-up (positions do not move: every call is the same workload)
     reps = 3
@@ -524,7 +526,7 @@ def bench_sph_c4(args, fh, torch, log):
         "candidate_tests_per_s": 2 * cand / (ms * 1e-3),
         "occupancy_max": int(occ.max()), "occupancy_p99_nonempty": float(np.percentile(nz, 99)),
         "kernels_us": {k: round(v, 1) for k, v in kt.items()},
-        "heavy_parts": 8, "subcells_per_axis": 8, "heavy_work": 384, "reps": reps,
+        "heavy_parts": 8, "subcells_per_axis": 8, "heavy_work": 384, "heavy_slots": "every item", "reps": reps,
         "input_sha256": cfg.digest(),
     }
     log(f"c4: {ms:.2f} ms per build + density + force, max occupancy {occ.max()}")

@@ -89,6 +89,18 @@ hipError_t alloc(T** p, size_t count, size_t* total) {
     return hipMalloc((void**)p, bytes);
 }
 
+// Partial-sum slots of a context by default: one per item below kSmallSystemN particles (whose
+// default splits every heavy item 8 ways; a few MB), else one per kDefaultSlotShare items, 24
+// bytes per particle of max_n with 4 parts (configs[3]'s trajectory numbers fewer than 4,096 of
+// its 49,152 items' slots; a heavy item past the slots is walked part after part by one wave,
+// with the same results).
+constexpr uint32_t kDefaultSlotShare = 8;
+static uint32_t default_slots(const fh_ctx* c) {
+    return c->max_n < kSmallSystemN
+               ? kHeavyLists * c->heavy_cap
+               : kHeavyLists * ceil_div(c->heavy_cap, kDefaultSlotShare);
+}
+
 // Rebuild of the SPH grid from the positions: hash + digit histograms, the stable sort giving
 // skeys / sidx (ascending id within a cell) and rank (its inverse), the gather into sorted
 // float4 order, and the CSR cell_start from the sorted keys (with the candidate co-located
@@ -210,7 +222,11 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->kb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->vb, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sort_lb, (size_t)c->max_sort_tiles * kDigitSlots, &tot);
-    if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)kHistBlocks * kDigitSlots, &tot);
+    // a histogram row per kHistChunk keys, at most kHistBlocks rows (the histogram kernels'
+    // grid for a sort of n <= max_n keys)
+    const uint32_t hist_rows =
+        std::min(ceil_div(max_n, (uint32_t)kHistChunk), (uint32_t)kHistBlocks);
+    if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)hist_rows * kDigitSlots, &tot);
     if (e == hipSuccess)
         e = alloc(&c->sort_pre,
                   ((size_t)c->max_sort_tiles + ceil_div(c->max_sort_tiles, 4u)) * 1024u, &tot);
@@ -229,12 +245,12 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
                    ceil_div(ceil_div(max_n, (uint32_t)kPlanThreads), (uint32_t)kHeavyLists);
     if (e == hipSuccess) e = alloc(&c->heavy, (size_t)kHeavyLists * c->heavy_cap, &tot);
     if (e == hipSuccess) e = alloc(&c->heavy_flag, 3 * (size_t)ceil_div(max_n, 64u), &tot);
-    // partial sums of the heavy parts: a slot for every item by default (FH_OPT_HEAVY_SLOTS
-    // caps it), kHeavyWaves parts x kHeavyComps x 64 lanes each (room for kHeavyWavesMax parts
-    // is made when FH_OPT_HEAVY_PARTS asks for it, and from the start for small contexts, whose
-    // default is kHeavyWavesMax parts)
+    // partial sums of the heavy parts: default_slots() slots (FH_OPT_HEAVY_SLOTS sets them),
+    // kHeavyWaves parts x kHeavyComps x 64 lanes each (room for kHeavyWavesMax parts is made
+    // when FH_OPT_HEAVY_PARTS asks for it, and from the start for small contexts, whose default
+    // is kHeavyWavesMax parts)
     c->hpart_parts = max_n < kSmallSystemN ? (uint32_t)kHeavyWavesMax : (uint32_t)kHeavyWaves;
-    c->hslot_cap = kHeavyLists * c->heavy_cap;
+    c->hslot_cap = default_slots(c);
     if (e == hipSuccess)
         e = alloc(&c->hpart, (size_t)c->hslot_cap * c->hpart_parts * kHeavyComps * 64u, &tot);
     if (e == hipSuccess) e = alloc(&c->hslot, 3 * (size_t)ceil_div(max_n, 64u), &tot);
@@ -244,7 +260,10 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->cell_grp, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->big, (size_t)ceil_div(max_n, 64u) + 1u, &tot);
     if (e == hipSuccess) e = alloc(&c->skip_tag, (size_t)ceil_div(max_n, 64u), &tot);
-    if (e == hipSuccess) e = alloc(&c->wpart, 3 * (size_t)max_n, &tot);
+    // the representatives' viscosity weights share the density partials' planes: the force
+    // pass writes them after k_prep has read the last density partial, k_finalize reads them,
+    // and a call that computes density only reads the partials and writes no weights
+    c->wpart = c->dpart;
     if (e == hipSuccess) e = alloc(&c->vrep, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->rank, max_n, &tot);
     if (e == hipSuccess) e = alloc(&c->sout, 3 * (size_t)max_n, &tot);
@@ -298,7 +317,7 @@ int fh_destroy(fh_ctx* c) {
                     c->cell_start, c->skeys, c->sidx, c->spos, c->svel,
                     c->srho, c->dpart, c->fpart, c->heavy, c->heavy_flag, c->hpart, c->hslot, c->lstream, c->lstream_t, c->hist_part,
                     c->sort_pre,
-                    c->cell_grp, c->big, c->skip_tag, c->wpart, c->vrep, c->rank, c->sout,
+                    c->cell_grp, c->big, c->skip_tag, c->vrep, c->rank, c->sout,
                     c->sidx2};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -676,7 +695,9 @@ int fh_set_option(fh_ctx* c, int option, int value) {
         case FH_OPT_HEAVY_SLOTS: {
             if (value < 0) return fail(FH_EINVAL, "fh_set_option: heavy slots %d < 0", value);
             const uint32_t all = kHeavyLists * c->heavy_cap;
-            const uint32_t cap = value == 0 || (uint32_t)value > all ? all : (uint32_t)value;
+            const uint32_t cap = value == 0              ? default_slots(c)
+                                 : (uint32_t)value > all ? all
+                                                         : (uint32_t)value;
             if (cap != c->hslot_cap) {
                 const int rc2 = resize_hpart(c, cap, c->hpart_parts);
                 if (rc2) return rc2;

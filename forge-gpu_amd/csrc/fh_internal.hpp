@@ -78,10 +78,12 @@ constexpr int kHeavyWaves = FH_HW, kHeavyWavesMax = 8;
 // into kHeavyWavesMax parts (contexts of smaller max_n make room for them at creation).
 constexpr uint32_t kSmallSystemN = 1u << 18;
 constexpr int kHeavyComps = 4;      // partial sums per lane and part: a_x, a_y, a_z, w (density: 1)
-// A light item's candidate stream as the density pass leaves it for the force pass: per lane
-// and row, (stream start << 16 | count), then the sorted indices of the first two windows'
-// staging slots (256 each).  Streams longer than two windows are rebuilt by the force pass.
-constexpr uint32_t kLightCacheWords = 3 * 64 + 2 * 256;
+// A light item's candidate stream as the plan or the density pass leaves it for the passes: per
+// lane, its three row starts and three counts in the stream (10 bits each, two words), then the
+// sorted indices of the first two windows' staging slots (256 each) as 16-bit offsets from a
+// base at or below the stream's lowest index (two per word).  Streams longer than two windows,
+// or spanning more than 65,536 sorted slots, are rebuilt by each pass.
+constexpr uint32_t kLightCacheWords = 2 * 64 + 256;
 #ifndef FH_PLAN_THREADS
 #define FH_PLAN_THREADS 512
 #endif
@@ -203,11 +205,13 @@ struct fh_ctx {
     uint32_t* lstream;   // [3 * ceil(max_n / 64)][kLightCacheWords] light items' candidate streams
                          // (lane intervals and window indices) from the density pass, reused by
                          // the force pass
-    uint32_t* lstream_t; // [3 * ceil(max_n / 64)] stream length of each light item
+    uint2* lstream_t;    // [3 * ceil(max_n / 64)] stream length of each light item and its lowest
+                         // sorted index (~0u: the stream is not kept)
     uint64_t* cell_grp;  // [max_cells] epoch << 32 | number of co-located leading particles
     uint2* big;          // [ceil(max_n / 64) + 1] (first slot, sample offset) of group cells
     uint32_t* skip_tag;  // [ceil(max_n / 64)] epoch of the rebuild whose sub-tile holds only group members
-    float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives
+    float* wpart;        // [3][max_n] per-slab viscosity weight sums of representatives (the
+                         // planes of dpart, free once k_prep has read them)
     float4* vrep;        // [max_n] summed velocity of the group, at representative indices
     uint32_t* rank;      // [max_n] sorted position of each particle (inverse of sidx)
     uint32_t* sidx2;     // [max_n] resident substeps: previous slot of each new slot

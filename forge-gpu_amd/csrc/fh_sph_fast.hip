@@ -11,7 +11,7 @@
 // arrays.  Lanes of one home row (cy, cz) are consecutive (a "segment"), and for each of the
 // slab's three rows the union of a segment's ranges is again one contiguous range.  The wave
 // concatenates the rows of all its segments into one candidate stream and copies it, kWin
-// (192) candidates at a time, into its own LDS slice with coalesced 16-byte loads (no workgroup
+// (256) candidates at a time, into its own LDS slice with coalesced 16-byte loads (no workgroup
 // barrier); every lane then evaluates the intervals of its own rows that fall in the window
 // (fh_stream.hpp, shared with the neighbour query of fh_grid.hip).  The plan builds each light
 // item's stream once (the lanes' intervals and the first two windows' staging indices,
@@ -518,6 +518,72 @@ __device__ __forceinline__ float density_trans(const float4* __restrict__ spos,
 // plan's waves then run in one round, so the stream build would lengthen it one for one.
 constexpr uint32_t kPlanStreamMinN = 1u << 18;
 
+// Base of a light item's kept stream in slab dz: a sorted index at or below every index of the
+// stream, when every index lies within 65,536 slots of it (the kept stream holds 16-bit offsets
+// from it; an empty stream keeps with base 0), else kNoBase: the stream is not kept.  Every
+// candidate cell of a particle in cell id lies in [id - 1 - nx + nx ny dz, id + 1 + nx + nx ny dz]
+// (linear ids x + nx (y + ny z)) and the item's particles are sorted by cell id, so the cell
+// starts at its first particle's low end and past its last particle's high end (stream_bounds,
+// loaded beside the slab's ranges) bound the stream (the gaps a stream holds between lanes'
+// ranges lie inside those ranges' span).  Wave-uniform; call with the whole wave (the lanes in
+// the tile lead).
+constexpr uint32_t kNoBase = 0xFFFFFFFFu;
+__device__ __forceinline__ uint2 stream_bounds(uint32_t key, bool in, const GridDesc& g,
+                                               const uint32_t* __restrict__ cstart, int dz) {
+    const int last = __popcll(__ballot(in)) - 1;
+    const int64_t plane = (int64_t)g.nx * g.ny, cells = plane * g.nz;
+    const int64_t k0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)key);
+    const int64_t k1 = (uint32_t)__builtin_amdgcn_readlane((int)key, last);
+    const int64_t lo = k0 - 1 - (int64_t)g.nx + plane * dz;
+    const int64_t hi = k1 + 2 + (int64_t)g.nx + plane * dz;
+    return make_uint2(cstart[min(max(lo, (int64_t)0), cells)],
+                      cstart[min(max(hi, (int64_t)0), cells)]);
+}
+__device__ __forceinline__ uint32_t stream_base(uint2 bounds, uint32_t T) {
+    if (T == 0u) return 0u;
+    return bounds.y - bounds.x <= 65536u ? bounds.x : kNoBase;
+}
+
+// A kept stream's lane intervals: a kept stream has at most 2 kWin = 512 positions, so each
+// lane's three starts and three counts fit 10 bits each, in two words (lane l: words l and
+// 64 + l; the starts of lanes outside the tile, whose counts are 0, are masked).  The window
+// offsets follow (kLightHead words in).
+constexpr uint32_t kLightHead = 2 * kWave;
+static_assert(2 * kWin < 1024, "kept stream positions fit 10 bits");
+__device__ __forceinline__ void put_intervals(uint32_t* __restrict__ lc, int lane,
+                                              const LightStream& L) {
+    lc[lane] = (L.S[0] & 0x3FFu) | (L.S[1] & 0x3FFu) << 10 | (L.S[2] & 0x3FFu) << 20;
+    lc[kWave + lane] = L.cnt[0] | L.cnt[1] << 10 | L.cnt[2] << 20;
+}
+__device__ __forceinline__ void get_intervals(const uint32_t* __restrict__ lc, int lane,
+                                              LightStream& L) {
+    const uint32_t s = lc[lane], c = lc[kWave + lane];
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        L.S[r] = (s >> (10 * r)) & 0x3FFu;
+        L.cnt[r] = (c >> (10 * r)) & 0x3FFu;
+    }
+}
+
+// A kept window's staging indices as 16-bit offsets from the base, two per word: lane l's words
+// of the window at w0 hold slots (l, 64 + l) and (128 + l, 192 + l).
+static_assert(kWinLoads % 2 == 0, "window slots pair up");
+__device__ __forceinline__ void put_offsets(uint32_t* __restrict__ off, uint32_t w0, int lane,
+                                            const uint32_t j[kWinLoads], uint32_t base) {
+#pragma unroll
+    for (int k = 0; k < kWinLoads; k += 2)
+        off[w0 / 2u + (uint32_t)(k / 2 * kWave + lane)] = (j[k] - base) | ((j[k + 1] - base) << 16);
+}
+__device__ __forceinline__ void get_offsets(const uint32_t* __restrict__ off, uint32_t w0,
+                                            int lane, uint32_t j[kWinLoads], uint32_t base) {
+#pragma unroll
+    for (int k = 0; k < kWinLoads; k += 2) {
+        const uint32_t v = off[w0 / 2u + (uint32_t)(k / 2 * kWave + lane)];
+        j[k] = base + (v & 0xFFFFu);
+        j[k + 1] = base + (v >> 16);
+    }
+}
+
 // Plan, beside the co-located groups (the group part, which tags particles f+1 .. f+M-1 of a grouped
 // cell in spos[s].w with their representative f, f itself with kRepFlag | M, and marks the
 // sub-tiles made only of such non-representative particles in skip_tag: both passes skip them,
@@ -534,7 +600,7 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                                           uint32_t* __restrict__ heavy, uint32_t heavy_cap,
                                           uint32_t heavy_work, uint32_t direct_mode,
                                           Control* ctl, uint32_t* __restrict__ lstream,
-                                          uint32_t* __restrict__ lstream_t,
+                                          uint2* __restrict__ lstream_t,
                                           uint32_t* __restrict__ hslot, uint32_t hslot_cap) {
     constexpr int kWaves = kPlanThreads / kWave;
     __shared__ uint32_t s_item[kWaves * 3];
@@ -545,12 +611,14 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
     const bool live = s < n;
     uint32_t nh = 0;  // heavy items of this wave, kept in s_item[wave * 3 ...]
     if (sub * kSub < n) {  // wave-uniform
-        const CellXYZ ci = key_xyz(load_or(skeys, s, live, 0u), g);
+        const uint32_t key = load_or(skeys, s, live, 0u);
+        const CellXYZ ci = key_xyz(key, g);
         {
             const uint32_t epoch = ctl->epoch;
             for (int slab = 0; slab < 3; slab++) {
                 uint32_t b[3], e[3];
                 slab_ranges(ci, live, g, cstart, n, slab - 1, b, e);
+                const uint2 bounds = stream_bounds(key, live, g, cstart, slab - 1);
                 uint32_t cand = (e[0] - b[0]) + (e[1] - b[1]) + (e[2] - b[2]);
                 uint32_t excess = 0;
                 if (cand >= kCollapseMin) {  // a grouped cell holds at least kCollapseMin
@@ -575,20 +643,20 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
                 }
                 hv = hv || trans;
                 const uint32_t item = sub * 3u + (uint32_t)slab;
-                if (!hv && L.T <= 2u * kWin) {  // uniform: the light stream for both passes
+                // uniform: the light stream for both passes (L.T is ~0u when none was built)
+                const uint32_t base =
+                    !hv && L.T <= 2u * kWin ? stream_base(bounds, L.T) : kNoBase;
+                if (base != kNoBase) {
                     uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
-#pragma unroll
-                    for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
+                    put_intervals(lc, lane, L);
                     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // uniform
                         uint32_t j[kWinLoads];
                         window_indices(L, w0, lane, j);
-#pragma unroll
-                        for (int k = 0; k < kWinLoads; k++)
-                            lc[3 * kWave + w0 + k * kWave + lane] = j[k];
+                        put_offsets(lc + kLightHead, w0, lane, j, base);
                     }
                 }
                 if (lane == 0) {
-                    lstream_t[item] = hv ? ~0u : L.T;
+                    lstream_t[item] = make_uint2(hv ? ~0u : L.T, base);
                     flag[item] = hv ? kItemHeavy : kItemLight;
                     if (!hv) hslot[item] = kNoSlot;
                     if (hv)
@@ -603,7 +671,7 @@ __device__ __forceinline__ void plan_work(uint32_t bid, const uint32_t* __restri
     __syncthreads();
     // one append per workgroup, to sub-list blockIdx % kHeavyLists, in wave order; the entry
     // at position pos of list k has partial-sum slot heavy_slot(k, pos) if that is below
-    // hslot_cap, else none (kNoSlot: the spill kernels walk it)
+    // hslot_cap, else none (kNoSlot: the passes' part-0 wave walks every part of it)
     __shared__ uint32_t s_base;
     if (threadIdx.x == 0) {
         uint32_t tot = 0;
@@ -640,7 +708,7 @@ __global__ __launch_bounds__(kPlanThreads, 8) void k_group_plan(
     uint64_t* __restrict__ cell_grp, float4* __restrict__ vrep, uint32_t* __restrict__ skip_tag,
     GridDesc g, const uint64_t* __restrict__ cand_tag, uint8_t* __restrict__ flag,
     uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t heavy_work, uint32_t direct_mode,
-    Control* ctl, uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
+    Control* ctl, uint32_t* __restrict__ lstream, uint2* __restrict__ lstream_t,
     uint32_t* __restrict__ hslot, uint32_t hslot_cap) {
     if (blockIdx.x < kGroupBlocks)
         group_work(blockIdx.x, kGroupBlocks, big, cap, n, skeys, cstart, spos, svel, sidx, rank,
@@ -740,7 +808,7 @@ __device__ __forceinline__ int next_row(const uint32_t lo[3], const uint32_t hi[
     return r;
 }
 
-static_assert(kLightCacheWords == 3 * kWave + 2 * kWin, "light stream cache layout");
+static_assert(kLightCacheWords == kLightHead + kWin, "light stream cache layout");
 
 // Density partials: dpart[slab][s] = sum over the slab's neighbours j of (h^2 - r^2)^3, r^2 < h^2.
 // Light items hold no co-located group (the plan sends those to the heavy list).
@@ -754,7 +822,7 @@ __device__ __forceinline__ void density_light(uint32_t item, int lane, float4* b
                                               const uint32_t* __restrict__ skip_tag,
                                               const Control* __restrict__ ctl,
                                               uint32_t* __restrict__ lstream,
-                                              uint32_t* __restrict__ lstream_t) {
+                                              uint2* __restrict__ lstream_t) {
     if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
@@ -764,41 +832,36 @@ __device__ __forceinline__ void density_light(uint32_t item, int lane, float4* b
     // the candidate stream the plan built (short streams), else built here and, when short,
     // kept for the force pass (kLightCacheWords)
     LightStream L;
-    L.T = lstream_t[item];
-    const bool kept = L.T <= 2u * kWin;  // uniform
+    const uint2 tb = lstream_t[item];
+    L.T = tb.x;
+    uint32_t base = tb.y;
+    const bool kept = base != kNoBase;  // uniform
     bool keep = false;
     uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
     if (kept) {
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-            const uint32_t v = lc[r * kWave + lane];
-            L.S[r] = v >> 16;
-            L.cnt[r] = v & 0xFFFFu;
-        }
+        get_intervals(lc, lane, L);
     } else {
-        const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
+        const uint32_t key = load_or(skeys, s, in, 0u);
+        const CellXYZ ci = key_xyz(key, g);
         uint32_t b[3], e[3];
         slab_ranges(ci, in, g, cstart, n, (int)slab - 1, b, e);
+        const uint2 bounds = stream_bounds(key, in, g, cstart, (int)slab - 1);
         light_stream(L, b, e, home_row(ci, g), in, lane);
-        keep = L.T <= 2u * kWin;  // uniform
-        if (lane == 0) lstream_t[item] = L.T;
+        base = L.T <= 2u * kWin ? stream_base(bounds, L.T) : kNoBase;  // uniform
+        keep = base != kNoBase;
+        if (lane == 0) lstream_t[item] = make_uint2(L.T, base);
         if (keep) {
-#pragma unroll
-            for (int r = 0; r < 3; r++) lc[r * kWave + lane] = (L.S[r] << 16) | L.cnt[r];
+            put_intervals(lc, lane, L);
         }
     }
     float acc = 0.0f;
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
         if (kept) {
-#pragma unroll
-            for (int k = 0; k < kWinLoads; k++) j[k] = lc[3 * kWave + w0 + k * kWave + lane];
+            get_offsets(lc + kLightHead, w0, lane, j, base);
         } else {
             window_indices(L, w0, lane, j);
-            if (keep) {
-#pragma unroll
-                for (int k = 0; k < kWinLoads; k++) lc[3 * kWave + w0 + k * kWave + lane] = j[k];
-            }
+            if (keep) put_offsets(lc + kLightHead, w0, lane, j, base);
         }
         float4 v[kWinLoads];
 #pragma unroll
@@ -1099,7 +1162,7 @@ static uint32_t slots_needed(uint32_t n) {
 // context's uncapped buffer would hold 8 parts for every slot the call can number (its few
 // items then make 8 times as many waves): always in a context made for small systems, and in a
 // large one, whose buffer for 4 parts of all its items holds 8 parts of a small call's.  The
-// choice does not depend on FH_OPT_HEAVY_SLOTS (a cap only moves items to the spill kernels),
+// choice does not depend on FH_OPT_HEAVY_SLOTS (a cap only moves items to the slot-less walks),
 // so capped and uncapped runs split the same way.
 static uint32_t heavy_parts(const fh_ctx* c, uint32_t n) {
     if (c->heavy_parts) return c->heavy_parts == 8u ? 8u : (uint32_t)kHeavyWaves;
@@ -1135,7 +1198,7 @@ void k_density_pass(
     const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
     float* __restrict__ dpart, uint32_t stride, uint32_t items, const uint8_t* __restrict__ flag,
     const uint32_t* __restrict__ skip_tag, const Control* __restrict__ ctl,
-    uint32_t* __restrict__ lstream, uint32_t* __restrict__ lstream_t,
+    uint32_t* __restrict__ lstream, uint2* __restrict__ lstream_t,
     const uint32_t* __restrict__ heavy, uint32_t heavy_cap, float* __restrict__ hpart,
     uint32_t hgrid, uint32_t hslot_cap) {
     constexpr uint32_t hw = HW;
@@ -1147,14 +1210,40 @@ void k_density_pass(
         int part;
         heavy_part_of(b, hw, q0, part);
         const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-        for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
+        // one walk per step: (entry q, this wave's part) for an item with a partial-sum slot;
+        // an item without one (FH_OPT_HEAVY_SLOTS caps them) is walked by its part-0 wave
+        // alone, part after part (pn), the parts added in part order through the item's plane
+        // (each lane re-reads what it wrote), as k_prep adds a slotted item's (slab_part): the
+        // same sums, whichever items got slots
+        int pn = 0;
+        for (uint32_t q = q0; q < count;) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
-            if (slot >= hslot_cap) continue;  // uniform: no partial-sum slot (k_density_spill)
+            const bool slotted = slot < hslot_cap;
+            if (!slotted && part != 0) {
+                q += hgrid;
+                continue;
+            }
+            const int p = slotted ? part : pn;
             float acc;
-            if (density_heavy_wave<CULL>(entry, part, (int)hw, lane, s_p, spos, skeys, n, g, cstart,
-                                   cell_grp, h2, skip_tag, epoch, acc))
+            // false in every part or in none (only group members are skipped)
+            const bool any = density_heavy_wave<CULL>(entry, p, (int)hw, lane, s_p, spos, skeys,
+                                                      n, g, cstart, cell_grp, h2, skip_tag, epoch,
+                                                      acc);
+            if (any && slotted) {
                 hpart[hpart_at(slot, hw, part, 0, lane)] = acc;
+            } else if (any) {
+                const uint32_t item = entry & ~kEntryFlags;
+                const uint32_t s = (item / 3u) * kSub + (uint32_t)lane;
+                float* const d = dpart + (size_t)(item % 3u) * stride;
+                if (s < n) d[s] = (p == 0 ? 0.0f : d[s]) + acc;
+            }
+            if (slotted || !any || p + 1 == (int)hw) {
+                q += hgrid;
+                pn = 0;
+            } else {
+                pn = p + 1;
+            }
         }
         return;
     }
@@ -1367,7 +1456,7 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
                                             const uint32_t* __restrict__ skip_tag,
                                             const Control* __restrict__ ctl,
                                             const uint32_t* __restrict__ lstream,
-                                            const uint32_t* __restrict__ lstream_t) {
+                                            const uint2* __restrict__ lstream_t) {
     if (item >= items || flag[item] != kItemLight) return;  // whole wave
     const uint32_t sub = item / 3u, slab = item - 3u * (item / 3u);
     if (skip_tag[sub] == ctl->epoch) return;  // only group members (finished from the group)
@@ -1381,16 +1470,12 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
     const float p_i = K.k * (rho_i - K.rho0);
     // the candidate stream the density pass left (short streams), else rebuilt
     LightStream L;
-    L.T = lstream_t[item];
-    const bool kept = L.T <= 2u * kWin;  // uniform
+    const uint2 tb = lstream_t[item];
+    L.T = tb.x;
+    const bool kept = tb.y != kNoBase;  // uniform
     const uint32_t* lc = lstream + (size_t)item * kLightCacheWords;
     if (kept) {
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-            const uint32_t v = lc[r * kWave + lane];
-            L.S[r] = v >> 16;
-            L.cnt[r] = v & 0xFFFFu;
-        }
+        get_intervals(lc, lane, L);
     } else {
         const CellXYZ ci = key_xyz(load_or(skeys, s, in, 0u), g);
         uint32_t b[3], e[3];
@@ -1401,8 +1486,7 @@ __device__ __forceinline__ void force_light(uint32_t item, int lane, float4* bp,
     for (uint32_t w0 = 0; w0 < L.T; w0 += kWin) {  // wave-uniform
         uint32_t j[kWinLoads];
         if (kept) {
-#pragma unroll
-            for (int k = 0; k < kWinLoads; k++) j[k] = lc[3 * kWave + w0 + k * kWave + lane];
+            get_offsets(lc + kLightHead, w0, lane, j, tb.y);
         } else {
             window_indices(L, w0, lane, j);
         }
@@ -1555,7 +1639,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(6, 8))) v
     float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride, uint32_t items,
     const uint8_t* __restrict__ flag, const uint32_t* __restrict__ skip_tag,
     const Control* __restrict__ ctl, const uint32_t* __restrict__ lstream,
-    const uint32_t* __restrict__ lstream_t, const uint32_t* __restrict__ heavy,
+    const uint2* __restrict__ lstream_t, const uint32_t* __restrict__ heavy,
     uint32_t heavy_cap, float* __restrict__ hpart, uint32_t hgrid, uint32_t hslot_cap) {
     constexpr uint32_t hw = HW;
     __shared__ float4 s_p[kWin];  // x, y, z, p_j
@@ -1567,15 +1651,48 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(6, 8))) v
         int part;
         heavy_part_of(b, hw, q0, part);
         const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-        for (uint32_t q = q0; q < count; q += hgrid) {  // uniform
+        // one walk per step: (entry q, this wave's part) for an item with a partial-sum slot;
+        // an item without one (FH_OPT_HEAVY_SLOTS caps them) is walked by its part-0 wave
+        // alone, part after part (pn), the parts added in part order through the item's planes
+        // (each lane re-reads what it wrote), as k_finalize adds a slotted item's (slab_part):
+        // the same sums, whichever items got slots
+        int pn = 0;
+        for (uint32_t q = q0; q < count;) {  // uniform
             uint32_t slot;
             const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
-            if (slot >= hslot_cap) continue;  // uniform: no partial-sum slot (k_force_spill)
+            const bool slotted = slot < hslot_cap;
+            if (!slotted && part != 0) {
+                q += hgrid;
+                continue;
+            }
+            const int p = slotted ? part : pn;
             float o[4];
-            if (force_heavy_wave<CULL>(entry, part, (int)hw, lane, s_p, s_v, spos, svel, srho, rec, skeys,
-                                 n, g, cstart, cell_grp, K, stride, skip_tag, epoch, o)) {
+            // false in every part or in none (only group members are skipped)
+            const bool any = force_heavy_wave<CULL>(entry, p, (int)hw, lane, s_p, s_v, spos, svel,
+                                                    srho, rec, skeys, n, g, cstart, cell_grp, K,
+                                                    stride, skip_tag, epoch, o);
+            if (any && slotted) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) hpart[hpart_at(slot, hw, part, c, lane)] = o[c];
+            } else if (any) {
+                const uint32_t item = entry & ~kEntryFlags;
+                const uint32_t s = (item / 3u) * kSub + (uint32_t)lane;
+                float* const f = fpart + (size_t)(item % 3u) * 3u * stride;
+                float* const wp = wpart + (size_t)(item % 3u) * stride;
+                if (s < n) {
+                    const bool first = p == 0;
+                    f[s] = (first ? 0.0f : f[s]) + o[0];
+                    f[stride + s] = (first ? 0.0f : f[stride + s]) + o[1];
+                    f[2u * (size_t)stride + s] = (first ? 0.0f : f[2u * (size_t)stride + s]) + o[2];
+                    // read only for a group representative (k_finalize finishes its members)
+                    wp[s] = (first ? 0.0f : wp[s]) + o[3];
+                }
+            }
+            if (slotted || !any || p + 1 == (int)hw) {
+                q += hgrid;
+                pn = 0;
+            } else {
+                pn = p + 1;
             }
         }
         return;
@@ -1584,92 +1701,6 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(6, 8))) v
     force_light(xcd_chunked(b - hparts, nl), lane, s_p, s_v, spos, svel, srho, rec, skeys, n,
                 g, cstart, K, fpart, wpart, stride, items, flag, skip_tag, ctl, lstream,
                 lstream_t);
-}
-
-// Heavy items that got no partial-sum slot (FH_OPT_HEAVY_SLOTS caps the slots): one workgroup
-// of HW wavefronts per item, wave p computing part p as the pass kernels do; the parts meet in
-// LDS and are added in part order, as k_prep / k_finalize add a slotted item's (slab_part), so
-// the sums do not depend on which items got slots.  The result goes to the item's slab plane
-// like a light item's.  Launched only when the context has fewer slots than items.
-constexpr uint32_t kSpillGrid = 1024;
-template <uint32_t HW, bool CULL>
-__global__ __launch_bounds__(kWave * HW) void k_density_spill(
-    const float4* __restrict__ spos, const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
-    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, float h2,
-    float* __restrict__ dpart, uint32_t stride, const uint32_t* __restrict__ skip_tag,
-    const Control* __restrict__ ctl, const uint32_t* __restrict__ heavy, uint32_t heavy_cap,
-    uint32_t hslot_cap) {
-    __shared__ float4 s_p[HW][kWin];
-    __shared__ float s_sum[HW][kWave];
-    const int lane = threadIdx.x % kWave;
-    const int part = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform in the workgroup
-        uint32_t slot;
-        const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
-        if (slot < hslot_cap) continue;  // the pass kernel's parts have it
-        float acc = 0.0f;
-        // false in every part or in none (only group members are skipped)
-        const bool any = density_heavy_wave<CULL>(entry, part, (int)HW, lane, s_p[part], spos, skeys,
-                                            n, g, cstart, cell_grp, h2, skip_tag, epoch, acc);
-        s_sum[part][lane] = acc;
-        __syncthreads();
-        const uint32_t item = entry & ~kEntryFlags;
-        const uint32_t s = (item / 3u) * kSub + (uint32_t)lane;
-        if (part == 0 && any && s < n) {
-            float t = 0.0f;
-#pragma unroll
-            for (int p = 0; p < (int)HW; p++) t += s_sum[p][lane];
-            dpart[(size_t)(item % 3u) * stride + s] = t;
-        }
-        __syncthreads();
-    }
-}
-
-template <uint32_t HW, bool CULL>
-__global__ __launch_bounds__(kWave * HW) void k_force_spill(
-    const float4* __restrict__ spos, const float4* __restrict__ svel,
-    const float* __restrict__ srho, const float4* __restrict__ rec,
-    const uint32_t* __restrict__ skeys, uint32_t n, GridDesc g,
-    const uint32_t* __restrict__ cstart, const uint64_t* __restrict__ cell_grp, FastForce K,
-    float* __restrict__ fpart, float* __restrict__ wpart, uint32_t stride,
-    const uint32_t* __restrict__ skip_tag, const Control* __restrict__ ctl,
-    const uint32_t* __restrict__ heavy, uint32_t heavy_cap, uint32_t hslot_cap) {
-    __shared__ float4 s_p[HW][kWin];
-    __shared__ float4 s_v[HW][kWin];
-    __shared__ float s_sum[HW][kHeavyComps][kWave];
-    const int lane = threadIdx.x % kWave;
-    const int part = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const uint32_t count = heavy_total(ctl, heavy_cap), epoch = ctl->epoch;
-    for (uint32_t q = blockIdx.x; q < count; q += gridDim.x) {  // uniform in the workgroup
-        uint32_t slot;
-        const uint32_t entry = heavy_entry_slot(heavy, ctl, heavy_cap, q, slot);
-        if (slot < hslot_cap) continue;
-        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const bool any = force_heavy_wave<CULL>(entry, part, (int)HW, lane, s_p[part], s_v[part], spos,
-                                          svel, srho, rec, skeys, n, g, cstart, cell_grp, K,
-                                          stride, skip_tag, epoch, o);
-#pragma unroll
-        for (int c = 0; c < 4; c++) s_sum[part][c][lane] = o[c];
-        __syncthreads();
-        const uint32_t item = entry & ~kEntryFlags;
-        const uint32_t s = (item / 3u) * kSub + (uint32_t)lane;
-        if (part == 0 && any && s < n) {
-            float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int p = 0; p < (int)HW; p++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) t[c] += s_sum[p][c][lane];
-            const uint32_t slab = item % 3u;
-            float* f = fpart + (size_t)slab * 3u * stride;
-            f[s] = t[0];
-            f[stride + s] = t[1];
-            f[2u * (size_t)stride + s] = t[2];
-            // read only for a group representative (k_finalize finishes its members)
-            wpart[(size_t)slab * stride + s] = t[3];
-        }
-        __syncthreads();
-    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1860,15 +1891,6 @@ hipError_t launch_density_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell
         items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream, c->lstream_t, c->heavy,
         c->heavy_cap, c->hpart, hgrid, slot_cap(c, hw));
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && slot_cap(c, hw) < slots_needed(a.n)) {  // items may lack slots
-        const auto spill = hw == 8u ? (cull ? k_density_spill<8, true> : k_density_spill<8, false>)
-                                    : (cull ? k_density_spill<kHeavyWaves, true>
-                                            : k_density_spill<kHeavyWaves, false>);
-        spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
-            c->spos, c->skeys, a.n, a.g, cell_start, c->cell_grp, a.h * a.h, c->dpart, c->max_n,
-            c->skip_tag, c->ctl, c->heavy, c->heavy_cap, slot_cap(c, hw));
-        e = hipGetLastError();
-    }
     tend(c, KID_DENSITY);
     return e;
 }
@@ -1919,16 +1941,6 @@ hipError_t launch_force_fast(fh_ctx* c, const SphArgs& a, const uint32_t* cell_s
         c->fpart, c->wpart, c->max_n, items, c->heavy_flag, c->skip_tag, c->ctl, c->lstream,
         c->lstream_t, c->heavy, c->heavy_cap, c->hpart, hgrid, slot_cap(c, hw));
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && slot_cap(c, hw) < slots_needed(a.n)) {  // items may lack slots
-        const auto spill = hw == 8u ? (cull ? k_force_spill<8, true> : k_force_spill<8, false>)
-                                    : (cull ? k_force_spill<kHeavyWaves, true>
-                                            : k_force_spill<kHeavyWaves, false>);
-        spill<<<kSpillGrid, kWave * hw, 0, c->stream>>>(
-            c->spos, c->svel, c->srho, c->sout, c->skeys, a.n, a.g, cell_start, c->cell_grp, K,
-            c->fpart, c->wpart, c->max_n, c->skip_tag, c->ctl, c->heavy, c->heavy_cap,
-            slot_cap(c, hw));
-        e = hipGetLastError();
-    }
     tend(c, KID_FORCE);
     return e;
 }

@@ -304,14 +304,15 @@ int fh_sph_fused_steps(fh_ctx* ctx, const fh_sph_params* prm, const fh_epilogue*
  * fh_sync returns FH_ESTATE).  Synchronises the stream. */
 #define FH_OPT_SPIN_LIMIT 6
 /* FH_OPT_HEAVY_SLOTS = 7: partial-sum slots of the fast passes' heavy items (4 KB each with 4
- * parts, 8 KB with 8).  By default every (64-particle, z-slab) item of max_n has one (~192 bytes
- * per particle of max_n with 4 parts); a smaller number bounds the context's memory.  A heavy
- * item that gets no slot in a substep is walked by one wavefront of an extra kernel, part after
- * part, and its parts are added in the same order as a slotted item's: the results are the same
- * bit for bit, only that item is slower.  value = slots (0 or more than the items restores one
- * per item).  One allocation, made at once: set it outside capture; fh_scratch_bytes counts it;
- * the context's captured graph is dropped and any graph captured on its stream before must be
- * captured again. */
+ * parts, 8 KB with 8).  By default a context of max_n >= 2^18 has one per 8 (64-particle,
+ * z-slab) items of max_n (24 bytes per particle with 4 parts; a slot per item would take 192),
+ * a smaller context one per item.  A heavy item that gets no slot in a substep is walked by one
+ * wavefront, part after part, and its parts are added in the same order as a slotted item's:
+ * the results are the same bit for bit, only that item is slower (workloads whose items are
+ * mostly heavy, like dense clumps, want a slot per item).  value = slots (0 restores the
+ * default; more than the items gives every item one).  One allocation, made at once: set it
+ * outside capture; fh_scratch_bytes counts it; the context's captured graph is dropped and any
+ * graph captured on its stream before must be captured again. */
 #define FH_OPT_HEAVY_SLOTS 7
 /* FH_OPT_SUBCELL = 8: sub-cells per axis (0: off, the default; 2, 4 or 8) by which the fused
  * module's fast rebuilds order the particles inside each cell (Morton order of the sub-cells:

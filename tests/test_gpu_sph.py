@@ -48,11 +48,11 @@ def set_mode(fh, f, cfg, mode):
     single-wave parts whose partials are added afterwards; light: none of them (one wavefront per item, shared
     stream); heavy8: as heavy, with 8 parts per item (FH_OPT_HEAVY_PARTS) instead of 4; spill,
     spill8: as heavy and heavy8 with 5 partial-sum slots (FH_OPT_HEAVY_SLOTS), so nearly every
-    item is walked by the spill kernels; subcell, subcell2, subcell8: as fast with the cells
+    item is walked without slots (k_density_pass's part-0 wave, k_force_spill); subcell, subcell2, subcell8: as fast with the cells
     ordered by 4, 2 or 8 sub-cells per axis (FH_OPT_SUBCELL), so that heavy items skip far
     candidate chunks and compact the others to their near candidates;
     subheavy: every item heavy, with 4 sub-cells per axis; subspill: as subheavy with 5
-    partial-sum slots (the spill kernels with chunk culling); direct: every item walked lane by
+    partial-sum slots (the slot-less walks with chunk culling); direct: every item walked lane by
     lane; exact: the bit-exact passes."""
     ctx = f.context(cfg.num_cells)
     heavy = {"heavy": 1, "heavy8": 1, "spill": 1, "spill8": 1, "subheavy": 1, "subspill": 1}
@@ -500,7 +500,9 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, su
     within 1e-4 * sum|pair terms|.  Random velocities make the viscosity term non-zero.
     parts: wavefronts per heavy item (FH_OPT_HEAVY_PARTS); sub: sub-cells per axis
     (FH_OPT_SUBCELL); work: candidates per particle above which an item is split
-    (FH_OPT_HEAVY_WORK, 0: the default); (8, 8, 384) is the bench's setting."""
+    (FH_OPT_HEAVY_WORK, 0: the default); (8, 8, 384) is the bench's setting, which also gives
+    every item a partial-sum slot (FH_OPT_HEAVY_SLOTS); the others keep the default slots, one
+    per 8 items, so that most heavy items of this clumped workload are walked without one."""
     from forge_hip import workloads
     cfg = workloads.config4()
     n = cfg.n
@@ -529,12 +531,14 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, su
     ctx.set_option(fh.FH_OPT_HEAVY_PARTS, parts)
     ctx.set_option(fh.FH_OPT_SUBCELL, sub)
     ctx.set_option(fh.FH_OPT_HEAVY_WORK, work)
+    ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 2**31 - 1 if work == 384 else 0)
     try:
         p.step(f, cfg.dt)
     finally:
         ctx.set_option(fh.FH_OPT_HEAVY_PARTS, 0)
         ctx.set_option(fh.FH_OPT_SUBCELL, 0)
         ctx.set_option(fh.FH_OPT_HEAVY_WORK, 0)
+        ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 0)
     rho = f.f32_fields["density"].cpu().numpy()
     acc = accel.cpu().numpy().astype(np.float64)
     dense = int(np.argmax(occ))
@@ -706,24 +710,51 @@ def test_subcell_option(fh, gpu_ctx):
 
 
 def test_heavy_slots_option(fh, gpu_ctx):
-    """FH_OPT_HEAVY_SLOTS: a negative count is refused; a cap shrinks the context's scratch by
-    its partial-sum buffer and 0 (or more slots than items) restores it."""
-    full = gpu_ctx.scratch_bytes
+    """FH_OPT_HEAVY_SLOTS: a negative count is refused; more slots than items give every item
+    one, a cap shrinks the context's scratch by its partial-sum buffer, and 0 restores the
+    default: one slot per 8 items in a context of 2^18 particles or more (24 bytes per particle
+    of max_n), one per item below.  A context for 2^20 particles then takes at most 300 bytes
+    per particle beside its cells."""
+    default = gpu_ctx.scratch_bytes
     with pytest.raises(fh.ForgeError):
         gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, -1)
-    gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 1)
-    assert gpu_ctx.scratch_bytes < full
     gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 2**31 - 1)
-    assert gpu_ctx.scratch_bytes == full
+    full = gpu_ctx.scratch_bytes
+    gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 1)
+    one = gpu_ctx.scratch_bytes
+    items = slots_per_context(gpu_ctx.max_n)
+    slot = (full - one) // (items - 1)
+    assert (full - one) % (items - 1) == 0 and slot in (4 * 4 * 64 * 4, 8 * 4 * 64 * 4)
+    assert default - one == (items // 8 - 1) * slot
     gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 3)
     gpu_ctx.set_option(fh.FH_OPT_HEAVY_SLOTS, 0)
-    assert gpu_ctx.scratch_bytes == full
+    assert gpu_ctx.scratch_bytes == default
+    big = fh.Context(max_n=1 << 20, max_cells=1)
+    try:
+        assert big.scratch_bytes <= 300 * (1 << 20), big.scratch_bytes / (1 << 20)
+    finally:
+        big.close()
+    small = fh.Context(max_n=1 << 17, max_cells=1)
+    try:  # every item has a slot (8 parts of 4 KB per 3 items of 64 particles)
+        base = small.scratch_bytes
+        small.set_option(fh.FH_OPT_HEAVY_SLOTS, 2**31 - 1)
+        assert small.scratch_bytes == base
+    finally:
+        small.close()
+
+
+def slots_per_context(max_n):
+    """Heavy-list entries of a context, a slot each at most: 8 lists of
+    3 * 8 * ceil(ceil(max_n / 512) / 8) entries (a plan workgroup of 512 particles lists up to
+    24 items, on one of 8 lists)."""
+    return 8 * 24 * -(-(-(-max_n // 512)) // 8)
 
 
 @pytest.mark.parametrize("case", ["colocated", "c3"])
 def test_heavy_slot_cap_is_bit_identical(fh, gpu_ctx, case):
     """With a few partial-sum slots (FH_OPT_HEAVY_SLOTS) most heavy items are walked part after
-    part by the spill kernels, whose parts are added in the order the slotted items' are: three
+    part without slots (the density pass's part-0 wave, the force pass's spill kernel), the parts
+    added in the order the slotted items' are: three
     substeps equal the uncapped ones bit for bit, for the default split, for every item heavy
     with 4 and 8 parts, and for every item heavy with 4 sub-cells per axis (the culling
     instantiations of both kernels).  A graph captured with a cap replays to the eager fields, and a
@@ -738,7 +769,7 @@ def test_heavy_slot_cap_is_bit_identical(fh, gpu_ctx, case):
     for mode, cap in (("fast", 3), ("heavy", 1), ("heavy8", 17), ("subheavy", 2)):
         print(f"heavy slot cap {case} {mode} cap={cap}", flush=True)
         outs = []
-        for slots in (0, cap):
+        for slots in (2**31 - 1, cap):
             f = fields_from(fh, cfg, vel)
             p = sph_pipeline(fh, cfg)
             set_mode(fh, f, cfg, mode)
