@@ -229,7 +229,7 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)hist_rows * kDigitSlots, &tot);
     if (e == hipSuccess)
         e = alloc(&c->sort_pre,
-                  ((size_t)c->max_sort_tiles + ceil_div(c->max_sort_tiles, 4u)) * 1024u, &tot);
+                  ((size_t)c->max_sort_tiles + ceil_div(c->max_sort_tiles, (uint32_t)kTilesPerReduce)) * 1024u, &tot);
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
     if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);

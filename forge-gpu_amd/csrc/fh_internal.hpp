@@ -49,7 +49,16 @@ constexpr int kHistChunk = kHistThreads * kHistItems;  // keys per histogram chu
 #define FH_HIST_BLOCKS 1024
 #endif
 constexpr int kHistBlocks = FH_HIST_BLOCKS;  // rows of per-block partial histograms
-constexpr int kHistRowsPerReduce = 8;  // partial rows summed by one reduce workgroup
+#ifndef FH_HIST_ROWS_PER_REDUCE
+#define FH_HIST_ROWS_PER_REDUCE 64
+#endif
+// Partial rows summed by one reduce workgroup: 32 first-pass tiles of a small sort, whose first
+// pass adds the sums of the groups before its tile (c2's build, 512 tiles: 8 rows per group took
+// 0.110 ms, 16 0.104, 32 0.100, 64 0.0997, 128 0.102; the c3 trajectory 401.9, 400.3, 400.0,
+// 399.8, 402.7 us per substep)
+constexpr int kHistRowsPerReduce = FH_HIST_ROWS_PER_REDUCE;
+constexpr int kTilesPerReduce = kHistRowsPerReduce / 2;  // first-pass tiles of one reduce group
+constexpr int kHistRowsPlain = 8;  // rows per reduce workgroup of a sort without first-pass prefixes
 constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
 // Co-located particles: when at least kCollapseMin particles of a cell sit at one position (the
 // box corners of a dam break collect thousands, next to a few hundred others), the cell is
@@ -180,7 +189,7 @@ struct fh_ctx {
     uint32_t* sort_lb;   // [max_sort_tiles * kDigitSlots] 32-bit look-back words (pass-major)
     uint32_t* hist_part; // [kHistBlocks][kDigitSlots] per-block digit histograms
     uint32_t* sort_pre;  // first-pass tile prefixes of small sorts: [max_sort_tiles][1024] within
-                         // groups of 4 tiles, then [ceil(max_sort_tiles / 4)][1024] group sums
+                         // groups of kTilesPerReduce tiles, then [ceil(max_sort_tiles / kTilesPerReduce)][1024] group sums
                          // (null: the first pass looks back like the others)
     fh::Control* ctl;    // device control block
     // grid scratch

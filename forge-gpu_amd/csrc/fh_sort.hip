@@ -238,19 +238,20 @@ __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
 // boundary gives the visibility.)
 // First-pass prefixes (pre != null: a small sort, whose histogram rows are its 4096-key chunks,
 // two per 8192-key tile): for the first pass's digits (slots < nb0), this workgroup's rows are
-// the 4 tiles 4g .. 4g+3, and it also writes each tile's exclusive prefix within them,
+// the kTilesPerReduce tiles of group g, and it also writes each tile's exclusive prefix within them,
 // pre[t * nb0 + d], and their sum, pre[(tiles + g) * nb0 + d].  The first pass of the sort then
 // takes its tiles' global prefixes from these instead of a look-back across the tiles.
-static_assert(kSortTile == 2 * kHistChunk && kHistRowsPerReduce == 8,
-              "first-pass prefixes: two histogram chunks per tile, four tiles per reduce group");
+static_assert(kSortTile == 2 * kHistChunk && kHistRowsPerReduce % 2 == 0,
+              "first-pass prefixes: two histogram chunks per tile, whole tiles per reduce group");
 __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict__ part,
                                                      uint32_t rows, uint32_t slot_blocks,
                                                      Control* ctl, uint32_t* __restrict__ pre,
-                                                     uint32_t nb0, uint32_t tiles, uint32_t n) {
+                                                     uint32_t nb0, uint32_t tiles, uint32_t n,
+                                                     uint32_t rpr) {
     const uint32_t b = blockIdx.x % slot_blocks, g = blockIdx.x / slot_blocks;
-    const uint32_t r0 = g * kHistRowsPerReduce;
+    const uint32_t r0 = g * rpr;
     const uint32_t slot = b * 256u + threadIdx.x;
-    const uint32_t r1 = min(rows, r0 + (uint32_t)kHistRowsPerReduce);
+    const uint32_t r1 = min(rows, r0 + rpr);
     uint32_t s = 0;
     if (pre && slot < nb0) {  // uniform per workgroup (nb0 is a multiple of 256)
 #pragma unroll 8
@@ -301,11 +302,15 @@ static uint32_t* first_pass_pre(fh_ctx* c, uint32_t n) {
 
 hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots, uint32_t n,
                               uint32_t nb0) {
-    const uint32_t groups = ceil_div(rows, (uint32_t)kHistRowsPerReduce);
+    // groups of kHistRowsPerReduce rows where the first pass takes its prefixes from them, else
+    // of kHistRowsPlain rows (more workgroups for the plain sums)
+    uint32_t* const pre = first_pass_pre(c, n);
+    const uint32_t rpr = pre ? (uint32_t)kHistRowsPerReduce : (uint32_t)kHistRowsPlain;
+    const uint32_t groups = ceil_div(rows, rpr);
     const uint32_t slot_blocks = slots / 256u;  // slots = passes * bins, bins >= 256
     k_hist_reduce<<<groups * slot_blocks, 256, 0, c->stream>>>(
-        c->hist_part, rows, slot_blocks, c->ctl, first_pass_pre(c, n), nb0,
-        ceil_div(n, (uint32_t)kSortTile), n);
+        c->hist_part, rows, slot_blocks, c->ctl, pre, nb0, ceil_div(n, (uint32_t)kSortTile), n,
+        rpr);
     return hipGetLastError();
 }
 
@@ -675,11 +680,11 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
 #pragma unroll
     for (int k = 0; k < DPT; k++) prefix[k] = 0u;
     if (owner && tile > 0 && precomputed) {
-        // the first pass reads the input order: the tile's prefix within its group of 4 tiles
+        // the first pass reads the input order: the tile's prefix within its group of tiles
         // plus the sums of the groups before it (k_hist_reduce)
 #pragma unroll
         for (int k = 0; k < DPT; k++) prefix[k] = io.pre[(size_t)tile * NB + d0 + k];
-        const uint32_t groups = tile >> 2;
+        const uint32_t groups = tile / (uint32_t)kTilesPerReduce;
 #pragma unroll 8
         for (uint32_t q = 0; q < groups; q++)
 #pragma unroll
