@@ -227,9 +227,12 @@ int fh_create(int device, uint32_t max_n, uint32_t max_cells, void* stream, fh_c
     const uint32_t hist_rows =
         std::min(ceil_div(max_n, (uint32_t)kHistChunk), (uint32_t)kHistBlocks);
     if (e == hipSuccess) e = alloc(&c->hist_part, (size_t)hist_rows * kDigitSlots, &tot);
+    // first-pass prefixes (sorts of up to kHistBlocks * kHistChunk keys): at most a tile per row
+    // and a group sum per kHistRowsPerReduce / 2 tiles
     if (e == hipSuccess)
         e = alloc(&c->sort_pre,
-                  ((size_t)c->max_sort_tiles + ceil_div(c->max_sort_tiles, (uint32_t)kTilesPerReduce)) * 1024u, &tot);
+                  ((size_t)hist_rows + ceil_div(hist_rows, (uint32_t)kHistRowsPerReduce / 2u)) * 1024u,
+                  &tot);
     if (e == hipSuccess) e = alloc(&c->ctl, 1, &tot);
     if (e == hipSuccess) e = alloc(&c->run_tag, max_cells, &tot);
     if (e == hipSuccess) e = alloc(&c->cell_start, (size_t)max_cells + 1, &tot);

@@ -45,6 +45,7 @@ constexpr int kHistThreads = 256;
 #endif
 constexpr int kHistItems = FH_HIST_ITEMS;
 constexpr int kHistChunk = kHistThreads * kHistItems;  // keys per histogram chunk
+constexpr int kPreItems = kHistChunk / kSortThreads;     // keys per thread of a first pass with prefixes
 #ifndef FH_HIST_BLOCKS
 #define FH_HIST_BLOCKS 1024
 #endif
@@ -57,7 +58,12 @@ constexpr int kHistBlocks = FH_HIST_BLOCKS;  // rows of per-block partial histog
 // 0.110 ms, 16 0.104, 32 0.100, 64 0.0997, 128 0.102; the c3 trajectory 401.9, 400.3, 400.0,
 // 399.8, 402.7 us per substep)
 constexpr int kHistRowsPerReduce = FH_HIST_ROWS_PER_REDUCE;
-constexpr int kTilesPerReduce = kHistRowsPerReduce / 2;  // first-pass tiles of one reduce group
+// A first pass with prefixes runs on tiles of one histogram row (4096 keys: twice the workgroups)
+// up to kPreSmallMaxN keys, where the tiles then fill the GPU in about one round (c3: 396.7 against
+// 398.7 us per substep, c0 86.7 against 89.5 us), and on tiles of two rows above (c2's 4,194,304
+// keys: 0.100 against 0.108 ms with one-row tiles)
+constexpr uint32_t kPreSmallMaxN = 1u << 21;
+__host__ __device__ inline uint32_t pre_rows_per_tile(uint32_t n) { return n <= kPreSmallMaxN ? 1u : 2u; }
 constexpr int kHistRowsPlain = 8;  // rows per reduce workgroup of a sort without first-pass prefixes
 constexpr uint32_t kMaxSortN = 1u << 30;  // look-back words hold 30-bit counts
 // Co-located particles: when at least kCollapseMin particles of a cell sit at one position (the
@@ -188,8 +194,9 @@ struct fh_ctx {
     uint32_t* vb;        // [max_n]
     uint32_t* sort_lb;   // [max_sort_tiles * kDigitSlots] 32-bit look-back words (pass-major)
     uint32_t* hist_part; // [kHistBlocks][kDigitSlots] per-block digit histograms
-    uint32_t* sort_pre;  // first-pass tile prefixes of small sorts: [max_sort_tiles][1024] within
-                         // groups of kTilesPerReduce tiles, then [ceil(max_sort_tiles / kTilesPerReduce)][1024] group sums
+    uint32_t* sort_pre;  // first-pass tile prefixes of small sorts (tiles of pre_rows_per_tile
+                         // histogram rows): [tiles][1024] within groups of kHistRowsPerReduce rows,
+                         // then the groups' sums
                          // (null: the first pass looks back like the others)
     fh::Control* ctl;    // device control block
     // grid scratch

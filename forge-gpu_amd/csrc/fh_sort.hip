@@ -237,12 +237,16 @@ __global__ __launch_bounds__(kHistThreads) void k_hash_hist(
 // workgroup; the decision about the passes is a separate one-workgroup kernel, the kernel
 // boundary gives the visibility.)
 // First-pass prefixes (pre != null: a small sort, whose histogram rows are its 4096-key chunks,
-// two per 8192-key tile): for the first pass's digits (slots < nb0), this workgroup's rows are
-// the kTilesPerReduce tiles of group g, and it also writes each tile's exclusive prefix within them,
+// rpt of them per first-pass tile): for the first pass's digits (slots < nb0), this workgroup's
+// rows are the tiles of group g, and it also writes each tile's exclusive prefix within them,
 // pre[t * nb0 + d], and their sum, pre[(tiles + g) * nb0 + d].  The first pass of the sort then
 // takes its tiles' global prefixes from these instead of a look-back across the tiles.
-static_assert(kSortTile == 2 * kHistChunk && kHistRowsPerReduce % 2 == 0,
-              "first-pass prefixes: two histogram chunks per tile, whole tiles per reduce group");
+static_assert(kPreItems * kSortThreads == kHistChunk && kSortTile == 2 * kHistChunk &&
+                  kHistRowsPerReduce >= 2 && (kHistRowsPerReduce & (kHistRowsPerReduce - 1)) == 0,
+              "first-pass prefixes: one or two histogram chunks per tile, whole tiles per group");
+// RPT (rows per first-pass tile, 1 or 2) is a template argument: with a run-time one the
+// unrolled row loop no longer overlaps its loads (c2's build 0.100 -> 0.112 ms).
+template <uint32_t RPT>
 __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict__ part,
                                                      uint32_t rows, uint32_t slot_blocks,
                                                      Control* ctl, uint32_t* __restrict__ pre,
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(256) void k_hist_reduce(const uint32_t* __restrict_
     if (pre && slot < nb0) {  // uniform per workgroup (nb0 is a multiple of 256)
 #pragma unroll 8
         for (uint32_t r = r0; r < r1; r++) {
-            if (!((r - r0) & 1u)) pre[(size_t)(r >> 1) * nb0 + slot] = s;
+            if (!((r - r0) & (RPT - 1u))) pre[(size_t)(r / RPT) * nb0 + slot] = s;
             s += part[(size_t)r * kDigitSlots + slot];
         }
         pre[((size_t)tiles + g) * nb0 + slot] = s;
@@ -308,9 +312,10 @@ hipError_t launch_hist_reduce(fh_ctx* c, uint32_t rows, uint32_t slots, uint32_t
     const uint32_t rpr = pre ? (uint32_t)kHistRowsPerReduce : (uint32_t)kHistRowsPlain;
     const uint32_t groups = ceil_div(rows, rpr);
     const uint32_t slot_blocks = slots / 256u;  // slots = passes * bins, bins >= 256
-    k_hist_reduce<<<groups * slot_blocks, 256, 0, c->stream>>>(
-        c->hist_part, rows, slot_blocks, c->ctl, pre, nb0, ceil_div(n, (uint32_t)kSortTile), n,
-        rpr);
+    const auto kernel = pre_rows_per_tile(n) == 1u ? k_hist_reduce<1> : k_hist_reduce<2>;
+    kernel<<<groups * slot_blocks, 256, 0, c->stream>>>(
+        c->hist_part, rows, slot_blocks, c->ctl, pre, nb0,
+        ceil_div(n, (uint32_t)kHistChunk * pre_rows_per_tile(n)), n, rpr);
     return hipGetLastError();
 }
 
@@ -397,7 +402,8 @@ struct SortIO {
     uint32_t passes;     // passes of the sort
     uint32_t in_place;
     const uint32_t* pre; // first-pass tile prefixes (k_hist_reduce), or null
-    uint32_t tiles;      // tiles of a pass (the group sums follow them in pre)
+    uint32_t tiles;      // tiles of the first pass (the group sums follow them in pre)
+    uint32_t group_shift; // log2 of the first-pass tiles per group of pre
     uint32_t kshift;     // the last pass writes key >> kshift to kfin (sub-cell bits dropped)
 };
 
@@ -684,7 +690,7 @@ __global__ __launch_bounds__(kSortThreads, Items > kSortItems ? 2 : FH_SORT_MINB
         // plus the sums of the groups before it (k_hist_reduce)
 #pragma unroll
         for (int k = 0; k < DPT; k++) prefix[k] = io.pre[(size_t)tile * NB + d0 + k];
-        const uint32_t groups = tile / (uint32_t)kTilesPerReduce;
+        const uint32_t groups = tile >> io.group_shift;
 #pragma unroll 8
         for (uint32_t q = 0; q < groups; q++)
 #pragma unroll
@@ -749,13 +755,26 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     const bool in_place = kfin != nullptr && kfin == k0;
     if (in_place ? (vfin != v0 || v0 == nullptr) : (vfin == v0 && v0 != nullptr) || !vfin)
         return hipErrorInvalidValue;  // mixed in place / out of place is not supported
+    // a first pass that takes its prefixes from k_hist_reduce runs on tiles of pre_rows_per_tile
+    // histogram rows: one row (kPreItems keys per thread, twice the workgroups of the later
+    // passes) for up to kPreSmallMaxN keys
+    const uint32_t* const pre = large ? nullptr : first_pass_pre(c, n);
+    const bool one_row = pre_rows_per_tile(n) == 1u;
+    const uint32_t pre_tiles = ceil_div(n, (uint32_t)kHistChunk * pre_rows_per_tile(n));
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
-              large ? nullptr : first_pass_pre(c, n), tiles, kshift};
+              pre, pre_tiles, (uint32_t)__builtin_ctz(kHistRowsPerReduce / pre_rows_per_tile(n)),
+              kshift};
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t shift = L.bits * p, pbits = min(L.bits, num_bits - shift);
         uint32_t* lb = c->sort_lb + (size_t)p * tiles * nb;
         tbeg(c, KID_SORT);
-        if (L.bits == kWideDigitBits)
+        if (p == 0u && pre && one_row && L.bits == kWideDigitBits)
+            k_onesweep<kPreItems, kWideDigitBits><<<pre_tiles, kSortThreads, 0, c->stream>>>(
+                io, c->ctl, p, lb, n, shift, pbits);
+        else if (p == 0u && pre && one_row)
+            k_onesweep<kPreItems, 8><<<pre_tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb,
+                                                                               n, shift, pbits);
+        else if (L.bits == kWideDigitBits)
             k_onesweep<kSortItems, kWideDigitBits><<<tiles, kSortThreads, 0, c->stream>>>(
                 io, c->ctl, p, lb, n, shift, pbits);
         else if (large)
