@@ -764,14 +764,19 @@ hipError_t launch_sort_passes(fh_ctx* c, const uint32_t* k0, const uint32_t* v0,
     SortIO io{k0, v0, c->ka, c->va, c->kb, c->vb, kfin, vfin, rank, passes, in_place ? 1u : 0u,
               pre, pre_tiles, (uint32_t)__builtin_ctz(kHistRowsPerReduce / pre_rows_per_tile(n)),
               kshift};
+    // the second pass of such a two-pass sort takes one-row tiles as well, its look-back words
+    // from word 0 (the first pass uses none, and 2 x ceil(n / kSortTile) x nb words, what
+    // make_begin zeroes for two passes, hold ceil(n / kHistChunk) x nb)
+    const bool one_row_both = pre && one_row && passes == 2u;
     for (uint32_t p = 0; p < passes; p++) {
         const uint32_t shift = L.bits * p, pbits = min(L.bits, num_bits - shift);
-        uint32_t* lb = c->sort_lb + (size_t)p * tiles * nb;
+        const bool small_tiles = p == 0u ? pre && one_row : one_row_both;
+        uint32_t* lb = small_tiles ? c->sort_lb : c->sort_lb + (size_t)p * tiles * nb;
         tbeg(c, KID_SORT);
-        if (p == 0u && pre && one_row && L.bits == kWideDigitBits)
+        if (small_tiles && L.bits == kWideDigitBits)
             k_onesweep<kPreItems, kWideDigitBits><<<pre_tiles, kSortThreads, 0, c->stream>>>(
                 io, c->ctl, p, lb, n, shift, pbits);
-        else if (p == 0u && pre && one_row)
+        else if (small_tiles)
             k_onesweep<kPreItems, 8><<<pre_tiles, kSortThreads, 0, c->stream>>>(io, c->ctl, p, lb,
                                                                                n, shift, pbits);
         else if (L.bits == kWideDigitBits)
