@@ -558,6 +558,49 @@ def test_c4_skewed_density_and_force_match_oracle(fh, gpu_ctx, oracle, parts, su
           f"{rel_err(rho[which], orho).max():.3g}")
 
 
+def test_wide_rows_light_streams_match_oracle(fh, gpu_ctx, oracle):
+    """Light items whose candidate streams may span more than 65,536 sorted slots: a 2048 x 4 x 4
+    grid with ~20 uniform particles per cell (655,360), so the rows y - 1 and y + 1 of a slab lie
+    ~82,000 sorted slots apart and the plan's bound on every stream (its first particle's cell
+    - 1 - nx to its last one's + 1 + nx) exceeds the 16-bit offsets: no stream is kept, and each
+    pass rebuilds its own.  One fused pass against the oracle on a sample: 4096 random particles
+    and the 1024 first of a middle row (densities rel 1e-4; accelerations against the fp64
+    sums, as for configs[4])."""
+    from forge_hip import workloads
+    nx, ny, nz, per = 2048, 4, 4, 20
+    n = nx * ny * nz * per
+    h = 0.01
+    rng = np.random.default_rng(58)
+    x = rng.uniform(0.0, nx * h, n).astype(np.float32)
+    y = rng.uniform(0.0, ny * h, n).astype(np.float32)
+    z = rng.uniform(0.0, nz * h, n).astype(np.float32)
+    cfg = workloads.SphConfig("wide", n, x, y, z, h=h, cell_size=h, dims=(nx, ny, nz), mass=1e-3)
+    vel = [rng.uniform(-1, 1, n).astype(np.float32) for _ in range(3)]
+    accel = torch.zeros((3, n), dtype=torch.float32, device="cuda")
+    f = fields_from(fh, cfg, vel)
+    p = fh.Pipeline()
+    m = fh.SphFusedModule(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                          cfg.rest_density, cfg.viscosity)
+    m.accel = accel
+    p.add(m)
+    torch.cuda.synchronize()
+    print("wide rows: fused pass", flush=True)
+    p.step(f, cfg.dt)
+    rho = f.f32_fields["density"].cpu().numpy()
+    acc = accel.cpu().numpy().astype(np.float64)
+    ocs, osi, _ = oracle.hashgrid_build(x, y, z, cfg.cell_size, (0, 0, 0), cfg.dims)
+    row = nx // 2 + nx * (1 + ny * 2)  # cell (nx / 2, 1, 2): a middle row of a middle plane
+    which = np.unique(np.concatenate([rng.choice(n, 4096, replace=False),
+                                      osi[ocs[row]:ocs[row] + 1024]])).astype(np.uint32)
+    prm = oracle.sph_params(cfg.h, cfg.cell_size, cfg.dims, cfg.mass, cfg.gas_constant,
+                            cfg.rest_density, cfg.viscosity)
+    orho = oracle.sph_density_at(prm, x, y, z, ocs, osi, which)
+    assert rel_err(rho[which], orho).max() <= REL
+    a64, s64, e64 = oracle.sph_force_f64_at(prm, x, y, z, *vel, rho, ocs, osi, which)
+    assert np.all(np.abs(acc[:, which] - a64) <= REL * s64 + e64 + 1e-30)
+    print(f"wide rows: {which.size} particles checked", flush=True)
+
+
 @pytest.mark.parametrize("case", ["small", "colocated"])
 def test_one_resident_substep_is_fh_sph_fused(fh, gpu_ctx, case):
     """fh_sph_fused_steps with steps = 1 is fh_sph_fused, bit for bit."""
