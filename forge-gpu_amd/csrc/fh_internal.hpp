@@ -51,12 +51,12 @@ constexpr int kPreItems = kHistChunk / kSortThreads;     // keys per thread of a
 #endif
 constexpr int kHistBlocks = FH_HIST_BLOCKS;  // rows of per-block partial histograms
 #ifndef FH_HIST_ROWS_PER_REDUCE
-#define FH_HIST_ROWS_PER_REDUCE 64
+#define FH_HIST_ROWS_PER_REDUCE 32
 #endif
-// Partial rows summed by one reduce workgroup: 32 first-pass tiles of a small sort, whose first
-// pass adds the sums of the groups before its tile (c2's build, 512 tiles: 8 rows per group took
-// 0.110 ms, 16 0.104, 32 0.100, 64 0.0997, 128 0.102; the c3 trajectory 401.9, 400.3, 400.0,
-// 399.8, 402.7 us per substep)
+// Partial rows summed by one reduce workgroup of a small sort, whose first pass adds the sums of
+// the groups before its tile (c2's build, 512 two-row tiles: groups of 8 rows took 0.110 ms, 16
+// 0.104, 32 0.100, 64 0.0997, 128 0.102; with c3's one-row tiles 32 rows against 64: c3 396.2
+// against 397.2 us per substep, c2 0.098 against 0.100 ms)
 constexpr int kHistRowsPerReduce = FH_HIST_ROWS_PER_REDUCE;
 // A first pass with prefixes runs on tiles of one histogram row (4096 keys: twice the workgroups)
 // up to kPreSmallMaxN keys, where the tiles then fill the GPU in about one round (c3: 396.7 against
