@@ -1729,7 +1729,8 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
                                                   uint32_t* __restrict__ keys_out,
                                                   const uint32_t* __restrict__ hslot,
                                                   const float* __restrict__ hpart,
-                                                  const float* __restrict__ srho) {
+                                                  const float* __restrict__ srho,
+                                                  uint32_t* __restrict__ rank_out) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const float4 p = spos[s];
@@ -1803,6 +1804,9 @@ __global__ __launch_bounds__(256) void k_finalize(const float4* __restrict__ spo
     sout[2u * s] = make_float4(npx, npy, npz, rho);
     sout[2u * s + 1u] = make_float4(nvx, nvy, nvz, v.w);  // .w: the particle id
     if (keys_out) keys_out[s] = sort_key_of(npx, npy, npz, g);  // the next resident substep's keys
+    // the last of several resident substeps: the particle -> slot map for k_scatter (what
+    // k_rank_of would read back from the new state)
+    if (rank_out && __float_as_uint(v.w) < n) rank_out[__float_as_uint(v.w)] = s;
     if (want_accel) sout[2 * (size_t)stride + s] = make_float4(ax, ay, az, 0.0f);
 }
 
@@ -1973,14 +1977,18 @@ hipError_t launch_finalize(fh_ctx* c, const SphArgs& a, const fh_epilogue* epi, 
     }
     F.e = epi ? epi->restitution : 0.0f;
     tbeg(c, KID_FINAL);
+    // after resident substeps k_finalize itself writes the particle -> slot map (with forces: a
+    // density-only call returns before it has the particle id)
+    const bool rank_here = to_particles && rebuild_rank && !density_only;
     const auto fin = heavy_parts(c, a.n) == 8u ? k_finalize<8> : k_finalize<kHeavyWaves>;
     fin<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->spos, c->svel, c->dpart, c->fpart,
                                                            c->wpart, a.n, c->max_n, F,
                                                            accel != nullptr, c->sout, a.g,
                                                            density_only ? nullptr : next_keys,
-                                                           c->hslot, c->hpart, c->srho);
+                                                           c->hslot, c->hpart, c->srho,
+                                                           rank_here ? c->rank : nullptr);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && to_particles && rebuild_rank) {
+    if (e == hipSuccess && to_particles && rebuild_rank && !rank_here) {
         k_rank_of<<<ceil_div(a.n, 256u), 256, 0, c->stream>>>(c->sout, a.n, c->rank);
         e = hipGetLastError();
     }
